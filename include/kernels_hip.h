@@ -1,0 +1,132 @@
+/* kernels_hip.h — the MI355X (gfx950) drop-in for the reference's quantized
+ * kernel ABI.
+ *
+ * Part 1 repeats ingot's kernel entry points with identical names, argument
+ * meaning, layouts and return codes, so the reference's decoder
+ * (src/arch_qwen3.c:46, :64, :175) links against this library unchanged:
+ *   - `weights` is the row-major [rows][cols / block] array of GGUF blocks
+ *     exactly as stored (never repacked);
+ *   - matvec writes output[rows]; matmat reads input[tokens][cols] and writes
+ *     output[tokens][rows]; dequant writes output[rows * cols] f32;
+ *   - return 0 on success, -1 on a NULL pointer, rows == 0, cols == 0, a
+ *     partial block, overflow or an unsupported type; nothing is printed.
+ * The pointers are HOST pointers, as in the reference. Weights inside a range
+ * handed to mynah_hip_register() are read from their resident HBM copy; any
+ * other weights are staged to the device for the call. x and y cross PCIe on
+ * every call, so a decoder that wants device speed uses part 2.
+ *
+ * Type ids are ggml's on-disk ids: Q8_0 = 8, Q4_K = 12, Q6_K = 14
+ * (third_party/ingot/include/ingot/dtype.h:24-59).
+ *
+ * Part 2 is new API with no reference counterpart: device-pointer twins with a
+ * stream argument (the stream is a hipStream_t passed as void *, NULL = the
+ * library's own stream), host-range registration (the hook the reference's
+ * ingot_gguf_mapping exists for, third_party/ingot/include/ingot/gguf.h:86-88),
+ * plain device memory helpers, and a timing helper for the benchmark.
+ *
+ * Errors: every call returns 0 / -1 (or NULL); mynah_hip_last_error() gives
+ * the message of the calling thread's last failure.
+ *
+ * Thread safety: calls may come from several threads; host-pointer calls are
+ * serialised inside the library (one device, one staging area).
+ *
+ * SPDX-License-Identifier: MIT */
+#ifndef MYNAH_KERNELS_HIP_H
+#define MYNAH_KERNELS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── part 1: ingot's kernel ABI ────────────────────────────────────────── */
+
+/* third_party/ingot/include/ingot/quant.h:155-156 */
+int ingot_matvec(int type, const void *weights, size_t rows, size_t cols,
+                 const float *input, float *output);
+/* quant.h:157-158. Exact f32 for every width (no int8 activation path): */
+int ingot_matmat(int type, const void *weights, size_t rows, size_t cols,
+                 const float *input, float *output, size_t tokens);
+/* quant.h:159-160 — bit-identical to the reference decoders. */
+int ingot_dequant_matrix(int type, const void *weights, size_t rows, size_t cols,
+                         float *output);
+/* quant.h:161 — 1 for Q4_K, Q6_K, Q8_0. */
+int ingot_has_kernel(int type);
+/* quant.h:150 — always 1: every width here is an exact reorder. */
+int ingot_matmat_is_exact(size_t tokens);
+
+/* quant.h:64-73 */
+int ingot_q4_k_matvec(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output);
+int ingot_q4_k_dequant(const void *weights, size_t rows, size_t cols, float *output);
+int ingot_q4_k_matmat(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output, size_t tokens);
+/* quant.h:151-152 */
+int ingot_q4_k_matmat_exact(const void *weights, size_t rows, size_t cols,
+                            const float *input, float *output, size_t tokens);
+/* quant.h:83-88 */
+int ingot_q6_k_matvec(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output);
+int ingot_q6_k_dequant(const void *weights, size_t rows, size_t cols, float *output);
+int ingot_q6_k_matmat(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output, size_t tokens);
+/* quant.h:107-112 */
+int ingot_q8_0_matvec(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output);
+int ingot_q8_0_dequant(const void *weights, size_t rows, size_t cols, float *output);
+int ingot_q8_0_matmat(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output, size_t tokens);
+
+/* quant.h:175-176 (ingot_gguf_matvec). `g` and `t` are the reference's
+ * ingot_gguf / ingot_tensor (third_party/ingot/include/ingot/gguf.h:41-50);
+ * the tensor's bytes are located through the host process's
+ * ingot_gguf_data(), so this entry point needs ingot's GGUF reader linked in
+ * (it returns -1 otherwise). rows = ne[1] (1 for rank 1), cols = ne[0]. */
+int ingot_gguf_matvec(const void *g, const void *t, const float *input, float *output);
+
+/* ── part 2: device-resident API (no reference counterpart) ────────────── */
+
+/* Select and initialise a device (default: device 0 on first use, or the
+ * MYNAH_HIP_DEVICE environment variable). */
+int mynah_hip_init(int device);
+const char *mynah_hip_last_error(void);
+
+/* Upload [host, host + bytes) unchanged into HBM; host pointers inside it
+ * then resolve to the device copy (same address modulo 256). */
+int mynah_hip_register(const void *host, size_t bytes);
+int mynah_hip_unregister(const void *host);
+/* Device address of a registered host pointer, or NULL. */
+void *mynah_hip_device_ptr(const void *host);
+
+/* Device-pointer twins. Weights 16-byte aligned for Q4_K and 2-byte aligned
+ * for Q6_K / Q8_0 (GGUF data and whole-row offsets satisfy both); x 16-byte
+ * aligned. Asynchronous on `stream`. */
+int mynah_hip_matvec_dev(int type, const void *w, size_t rows, size_t cols,
+                         const float *x, float *y, void *stream);
+int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols,
+                         const float *x, float *y, size_t tokens, void *stream);
+int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols,
+                          float *y, void *stream);
+
+/* Plain device memory (256-byte aligned) and copies; *_async take a stream. */
+void *mynah_hip_alloc(size_t bytes);
+int   mynah_hip_free(void *p);
+int   mynah_hip_h2d(void *dst, const void *src, size_t bytes);
+int   mynah_hip_d2h(void *dst, const void *src, size_t bytes);
+int   mynah_hip_memset(void *dst, int value, size_t bytes);
+int   mynah_hip_sync(void *stream);
+void *mynah_hip_stream(void);           /* the library's own stream */
+
+/* Benchmark helper: `iters` launches of the matvec, cycling through the
+ * `n_copies` weight copies in w_copies[] (to stream from HBM rather than
+ * cache), timed with HIP events on the launch stream. *ms = total time. */
+int mynah_hip_time_matvec(int type, const void *const *w_copies, int n_copies,
+                          size_t rows, size_t cols, const float *x, float *y,
+                          int iters, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,5 @@
+// kernels.hip — the one gfx950 code object of the library (every kernel
+// translation unit is included here and compiled by a single hipcc --genco).
+//
+// SPDX-License-Identifier: MIT
+#include "gemv.hip"

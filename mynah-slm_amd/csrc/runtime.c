@@ -1,0 +1,571 @@
+/* runtime.c — C11 host side of the gfx950 kernels: module loading, launch
+ * geometry, the ingot-compatible entry points and the device-resident API
+ * declared in include/kernels_hip.h.
+ *
+ * The kernels are one code object (hipcc --genco, gfx950) embedded in this
+ * library; each device loads it with hipModuleLoadData on first use and the
+ * kernels run through hipModuleLaunchKernel. No C++ host code, no PyTorch.
+ *
+ * SPDX-License-Identifier: MIT */
+#define _GNU_SOURCE
+#include "kernels_hip.h"
+#include "runtime_internal.h"
+
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+extern const unsigned char mynah_codeobj[];
+
+static _Thread_local char last_error[512];
+
+void mynah_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(last_error, sizeof last_error, fmt, ap);
+    va_end(ap);
+}
+
+const char *mynah_hip_last_error(void) { return last_error; }
+
+#define HIP_OK(call, what)                                                            \
+    do {                                                                              \
+        hipError_t e_ = (call);                                                       \
+        if (e_ != hipSuccess) {                                                       \
+            mynah_set_error("%s: %s", what, hipGetErrorString(e_));                   \
+            return -1;                                                                \
+        }                                                                             \
+    } while (0)
+
+/* ── per-device state ────────────────────────────────────────────────────── */
+
+static const char *const kernel_names[MYNAH_K_COUNT] = {
+#define X(id, name) [id] = name,
+    MYNAH_KERNEL_LIST(X)
+#undef X
+};
+
+static mynah_device devices[MYNAH_MAX_DEVICES];
+static int current_device = -1;
+static pthread_mutex_t init_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_mutex_t host_mu = PTHREAD_MUTEX_INITIALIZER;
+
+static int load_device(int dev) {
+    mynah_device *d = &devices[dev];
+    if (d->loaded) return 0;
+    HIP_OK(hipSetDevice(dev), "hipSetDevice");
+    HIP_OK(hipModuleLoadData(&d->module, mynah_codeobj), "hipModuleLoadData");
+    for (int k = 0; k < MYNAH_K_COUNT; k++) {
+        if (kernel_names[k] == NULL) continue;
+        hipError_t e = hipModuleGetFunction(&d->fn[k], d->module, kernel_names[k]);
+        if (e != hipSuccess) {
+            mynah_set_error("kernel %s missing from the code object: %s", kernel_names[k],
+                            hipGetErrorString(e));
+            return -1;
+        }
+    }
+    HIP_OK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
+    d->loaded = 1;
+    return 0;
+}
+
+int mynah_hip_init(int device) {
+    pthread_mutex_lock(&init_mu);
+    int rc = 0;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        mynah_set_error("no HIP device visible");
+        rc = -1;
+    } else if (device < 0 || device >= count || device >= MYNAH_MAX_DEVICES) {
+        mynah_set_error("device %d out of range (have %d)", device, count);
+        rc = -1;
+    } else {
+        rc = load_device(device);
+        if (rc == 0) current_device = device;
+    }
+    pthread_mutex_unlock(&init_mu);
+    return rc;
+}
+
+mynah_device *mynah_dev(void) {
+    if (current_device < 0) {
+        const char *env = getenv("MYNAH_HIP_DEVICE");
+        if (mynah_hip_init(env ? atoi(env) : 0) != 0) return NULL;
+    }
+    mynah_device *d = &devices[current_device];
+    if (hipSetDevice(current_device) != hipSuccess) {
+        mynah_set_error("hipSetDevice(%d) failed", current_device);
+        return NULL;
+    }
+    return d;
+}
+
+hipStream_t mynah_stream_or_default(mynah_device *d, void *stream) {
+    return stream ? (hipStream_t)stream : d->stream;
+}
+
+int mynah_launch(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned block,
+                 size_t shmem, hipStream_t stream, void **args) {
+    hipError_t e = hipModuleLaunchKernel(d->fn[kernel], gx, gy, 1, block, 1, 1,
+                                         (unsigned)shmem, stream, args, NULL);
+    if (e != hipSuccess) {
+        mynah_set_error("launch of %s: %s", kernel_names[kernel], hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+/* ── geometry ────────────────────────────────────────────────────────────── */
+
+int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes) {
+    size_t elems, bytes;
+    switch (type) {
+    case MYNAH_Q4_K: elems = 256; bytes = 144; break;
+    case MYNAH_Q6_K: elems = 256; bytes = 210; break;
+    case MYNAH_Q8_0: elems = 32;  bytes = 34;  break;
+    default:
+        mynah_set_error("type %d has no kernel", type);
+        return -1;
+    }
+    if (rows == 0 || cols == 0 || cols % elems != 0) {
+        mynah_set_error("bad geometry rows=%zu cols=%zu for type %d", rows, cols, type);
+        return -1;
+    }
+    const size_t blocks = cols / elems;
+    if (blocks > SIZE_MAX / bytes || rows > SIZE_MAX / (blocks * bytes) ||
+        rows > SIZE_MAX / cols || rows > 0xffffffffu || cols > 0xffffffffu) {
+        mynah_set_error("size overflow");
+        return -1;
+    }
+    *row_bytes = blocks * bytes;
+    return 0;
+}
+
+/* ── GEMV launch ─────────────────────────────────────────────────────────── */
+
+#define GEMV_WG 256
+#define GEMV_LDS_MAX (64u * 1024u)
+
+static size_t gemv_lds_bytes(int type, size_t cols) {
+    switch (type) {
+    case MYNAH_Q4_K: return (cols + cols / 16 + cols / 16) * sizeof(float);
+    case MYNAH_Q6_K: return (cols + cols / 32 + cols / 8) * sizeof(float);
+    default:         return (cols + cols / 8 + cols / 32) * sizeof(float);
+    }
+}
+
+/* Rows per lane: enough waves to fill 256 CUs several times over first,
+ * then more rows per lane to reuse each x read. */
+static int gemv_rows_per_lane(size_t rows) {
+    if (rows >= 65536) return 4;
+    if (rows >= 16384) return 2;
+    return 1;
+}
+
+int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                      const float *x, float *y, hipStream_t stream) {
+    size_t rb;
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if (type != MYNAH_Q8_0 && cols % 256 != 0) {
+        mynah_set_error("cols must be a multiple of 256");
+        return -1;
+    }
+    if (((uintptr_t)x & 15u) != 0) {
+        mynah_set_error("x must be 16-byte aligned");
+        return -1;
+    }
+    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0) {
+        mynah_set_error("weights misaligned for type %d", type);
+        return -1;
+    }
+    const size_t lds = gemv_lds_bytes(type, cols);
+    if (lds > GEMV_LDS_MAX) {
+        mynah_set_error("cols=%zu needs %zu B of LDS (max %u)", cols, lds, GEMV_LDS_MAX);
+        return -1;
+    }
+    const int R = gemv_rows_per_lane(rows);
+    const size_t rows_per_wg = (size_t)4 * 8 * (size_t)R;
+    const unsigned grid = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
+    int k;
+    if (type == MYNAH_Q4_K) k = R == 4 ? MYNAH_K_Q4K_R4 : R == 2 ? MYNAH_K_Q4K_R2 : MYNAH_K_Q4K_R1;
+    else if (type == MYNAH_Q6_K) k = R == 4 ? MYNAH_K_Q6K_R4 : R == 2 ? MYNAH_K_Q6K_R2 : MYNAH_K_Q6K_R1;
+    else k = R == 4 ? MYNAH_K_Q80_R4 : R == 2 ? MYNAH_K_Q80_R2 : MYNAH_K_Q80_R1;
+    uint32_t rows32 = (uint32_t)rows;
+    uint32_t nb = (uint32_t)(type == MYNAH_Q8_0 ? cols / 32 : cols / 256);
+    void *args[] = {&w, &x, &y, &rows32, &nb};
+    return mynah_launch(d, k, grid, 1, GEMV_WG, lds, stream, args);
+}
+
+int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                         float *y, hipStream_t stream) {
+    size_t rb;
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    /* Like the reference (kernels.c:2096-2101, 2563-2567): matrix dequant
+     * works in 256-value units for every type, ragged Q8_0 rows included. */
+    if (cols % 256 != 0) {
+        mynah_set_error("cols must be a multiple of 256");
+        return -1;
+    }
+    const size_t units = rows * (cols / 32);
+    if (units / GEMV_WG + 1 > 0x7fffffffu) {
+        mynah_set_error("dequant too large");
+        return -1;
+    }
+    uint32_t t = (uint32_t)type, r = (uint32_t)rows, c = (uint32_t)cols;
+    void *args[] = {&w, &y, &t, &r, &c};
+    return mynah_launch(d, MYNAH_K_DEQUANT, (unsigned)((units + GEMV_WG - 1) / GEMV_WG), 1,
+                        GEMV_WG, 0, stream, args);
+}
+
+/* ── host-range registry ─────────────────────────────────────────────────── */
+
+#define MAX_RANGES 64
+typedef struct {
+    const unsigned char *host;
+    size_t bytes;
+    unsigned char *alloc;    /* hipMalloc result */
+    unsigned char *dev;      /* device address of host[0] */
+    int device;
+} range;
+static range ranges[MAX_RANGES];
+static pthread_mutex_t reg_mu = PTHREAD_MUTEX_INITIALIZER;
+
+int mynah_hip_register(const void *host, size_t bytes) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (host == NULL || bytes == 0) {
+        mynah_set_error("register: empty range");
+        return -1;
+    }
+    const size_t skew = (uintptr_t)host & 255u;
+    unsigned char *alloc = NULL;
+    HIP_OK(hipMalloc((void **)&alloc, bytes + skew), "hipMalloc(register)");
+    if (hipMemcpy(alloc + skew, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(alloc);
+        mynah_set_error("register: upload failed");
+        return -1;
+    }
+    pthread_mutex_lock(&reg_mu);
+    int slot = -1;
+    for (int i = 0; i < MAX_RANGES; i++)
+        if (ranges[i].host == NULL) { slot = i; break; }
+    if (slot >= 0) {
+        ranges[slot].host = (const unsigned char *)host;
+        ranges[slot].bytes = bytes;
+        ranges[slot].alloc = alloc;
+        ranges[slot].dev = alloc + skew;
+        ranges[slot].device = current_device;
+    }
+    pthread_mutex_unlock(&reg_mu);
+    if (slot < 0) {
+        (void)hipFree(alloc);
+        mynah_set_error("register: too many ranges (max %d)", MAX_RANGES);
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_unregister(const void *host) {
+    pthread_mutex_lock(&reg_mu);
+    int found = -1;
+    for (int i = 0; i < MAX_RANGES; i++)
+        if (ranges[i].host == (const unsigned char *)host) { found = i; break; }
+    range r = found >= 0 ? ranges[found] : (range){0};
+    if (found >= 0) memset(&ranges[found], 0, sizeof ranges[found]);
+    pthread_mutex_unlock(&reg_mu);
+    if (found < 0) {
+        mynah_set_error("unregister: unknown range");
+        return -1;
+    }
+    (void)hipSetDevice(r.device);
+    HIP_OK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    HIP_OK(hipFree(r.alloc), "hipFree(register)");
+    return 0;
+}
+
+/* Device address for [host, host + bytes) if it lies inside one range. */
+static const void *lookup(const void *host, size_t bytes) {
+    const unsigned char *p = (const unsigned char *)host;
+    const void *out = NULL;
+    pthread_mutex_lock(&reg_mu);
+    for (int i = 0; i < MAX_RANGES; i++) {
+        const range *r = &ranges[i];
+        if (r->host != NULL && r->device == current_device && p >= r->host &&
+            (size_t)(p - r->host) <= r->bytes && bytes <= r->bytes - (size_t)(p - r->host)) {
+            out = r->dev + (p - r->host);
+            break;
+        }
+    }
+    pthread_mutex_unlock(&reg_mu);
+    return out;
+}
+
+void *mynah_hip_device_ptr(const void *host) { return (void *)lookup(host, 1); }
+
+/* ── host-pointer entry points (the ingot ABI) ───────────────────────────── */
+
+/* Staging buffers reused across calls (grown, never shrunk). */
+static unsigned char *stage_w, *stage_x, *stage_y;
+static size_t cap_w, cap_x, cap_y;
+
+static int grow(unsigned char **buf, size_t *cap, size_t need) {
+    if (need <= *cap) return 0;
+    if (*buf) (void)hipFree(*buf);
+    *buf = NULL;
+    *cap = 0;
+    size_t n = need < 4096 ? 4096 : need + need / 4;
+    HIP_OK(hipMalloc((void **)buf, n), "hipMalloc(staging)");
+    *cap = n;
+    return 0;
+}
+
+typedef enum { OP_MATVEC, OP_MATMAT, OP_DEQUANT } host_op;
+
+static int host_call(host_op op, int type, const void *w, size_t rows, size_t cols,
+                     const float *x, float *y, size_t tokens) {
+    if (w == NULL || y == NULL || (op != OP_DEQUANT && x == NULL) || tokens == 0) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    size_t rb;
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if (op == OP_MATMAT && tokens > SIZE_MAX / (rows > cols ? rows : cols) / sizeof(float)) {
+        mynah_set_error("size overflow");
+        return -1;
+    }
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    pthread_mutex_lock(&host_mu);
+    int rc = -1;
+    const size_t wbytes = rows * rb;
+    const size_t xbytes = op == OP_DEQUANT ? 0 : tokens * cols * sizeof(float);
+    const size_t ybytes = (op == OP_DEQUANT ? rows * cols : tokens * rows) * sizeof(float);
+    const void *wd = lookup(w, wbytes);
+    hipStream_t s = d->stream;
+    if (wd == NULL) {
+        if (grow(&stage_w, &cap_w, wbytes) != 0) goto out;
+        if (hipMemcpyAsync(stage_w, w, wbytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+            mynah_set_error("weight upload failed");
+            goto out;
+        }
+        wd = stage_w;
+    }
+    if (grow(&stage_y, &cap_y, ybytes) != 0) goto out;
+    if (xbytes) {
+        if (grow(&stage_x, &cap_x, xbytes) != 0) goto out;
+        if (hipMemcpyAsync(stage_x, x, xbytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+            mynah_set_error("input upload failed");
+            goto out;
+        }
+    }
+    if (op == OP_MATVEC) rc = mynah_gemv_launch(d, type, wd, rows, cols, (const float *)stage_x,
+                                                (float *)stage_y, s);
+    else if (op == OP_MATMAT) rc = mynah_matmat_launch(d, type, wd, rows, cols,
+                                                       (const float *)stage_x, (float *)stage_y,
+                                                       tokens, s);
+    else rc = mynah_dequant_launch(d, type, wd, rows, cols, (float *)stage_y, s);
+    if (rc != 0) goto out;
+    rc = -1;
+    if (hipMemcpyAsync(y, stage_y, ybytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        mynah_set_error("result download failed");
+        goto out;
+    }
+    rc = 0;
+out:
+    pthread_mutex_unlock(&host_mu);
+    return rc;
+}
+
+int ingot_matvec(int type, const void *weights, size_t rows, size_t cols,
+                 const float *input, float *output) {
+    return host_call(OP_MATVEC, type, weights, rows, cols, input, output, 1);
+}
+
+int ingot_matmat(int type, const void *weights, size_t rows, size_t cols,
+                 const float *input, float *output, size_t tokens) {
+    return host_call(tokens == 1 ? OP_MATVEC : OP_MATMAT, type, weights, rows, cols, input,
+                     output, tokens);
+}
+
+int ingot_dequant_matrix(int type, const void *weights, size_t rows, size_t cols,
+                         float *output) {
+    return host_call(OP_DEQUANT, type, weights, rows, cols, NULL, output, 1);
+}
+
+int ingot_has_kernel(int type) {
+    return type == MYNAH_Q4_K || type == MYNAH_Q6_K || type == MYNAH_Q8_0;
+}
+
+int ingot_matmat_is_exact(size_t tokens) {
+    (void)tokens;
+    return 1;
+}
+
+#define PER_TYPE(prefix, id)                                                              \
+    int ingot_##prefix##_matvec(const void *w, size_t rows, size_t cols, const float *x,   \
+                                float *y) {                                                \
+        return ingot_matvec(id, w, rows, cols, x, y);                                      \
+    }                                                                                      \
+    int ingot_##prefix##_dequant(const void *w, size_t rows, size_t cols, float *y) {      \
+        return ingot_dequant_matrix(id, w, rows, cols, y);                                 \
+    }                                                                                      \
+    int ingot_##prefix##_matmat(const void *w, size_t rows, size_t cols, const float *x,   \
+                                float *y, size_t tokens) {                                 \
+        return ingot_matmat(id, w, rows, cols, x, y, tokens);                              \
+    }
+PER_TYPE(q4_k, MYNAH_Q4_K)
+PER_TYPE(q6_k, MYNAH_Q6_K)
+PER_TYPE(q8_0, MYNAH_Q8_0)
+#undef PER_TYPE
+
+int ingot_q4_k_matmat_exact(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                            size_t tokens) {
+    return ingot_matmat(MYNAH_Q4_K, w, rows, cols, x, y, tokens);
+}
+
+/* The reference's tensor descriptor (third_party/ingot/include/ingot/gguf.h:41-50)
+ * and data accessor (gguf.h:74-76), resolved from the host process. */
+typedef struct {
+    const char *name;
+    int type;
+    uint32_t rank;
+    uint64_t ne[8];
+    uint64_t nelem, nbytes, offset;
+    uint32_t shard;
+} ingot_tensor_view;
+extern const void *ingot_gguf_data(const void *g, const void *t) __attribute__((weak));
+
+int ingot_gguf_matvec(const void *g, const void *t, const float *input, float *output) {
+    if (g == NULL || t == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    if (ingot_gguf_data == NULL) {
+        mynah_set_error("ingot_gguf_data is not linked into this process");
+        return -1;
+    }
+    const ingot_tensor_view *tv = (const ingot_tensor_view *)t;
+    const void *data = ingot_gguf_data(g, t);
+    if (data == NULL) return -1;
+    const size_t cols = (size_t)tv->ne[0];
+    const size_t rows = tv->rank >= 2 ? (size_t)tv->ne[1] : 1;
+    return ingot_matvec(tv->type, data, rows, cols, input, output);
+}
+
+/* ── device-resident API ─────────────────────────────────────────────────── */
+
+int mynah_hip_matvec_dev(int type, const void *w, size_t rows, size_t cols, const float *x,
+                         float *y, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w == NULL || x == NULL || y == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    return mynah_gemv_launch(d, type, w, rows, cols, x, y, mynah_stream_or_default(d, stream));
+}
+
+int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols, const float *x,
+                         float *y, size_t tokens, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w == NULL || x == NULL || y == NULL || tokens == 0) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    hipStream_t s = mynah_stream_or_default(d, stream);
+    if (tokens == 1) return mynah_gemv_launch(d, type, w, rows, cols, x, y, s);
+    return mynah_matmat_launch(d, type, w, rows, cols, x, y, tokens, s);
+}
+
+int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols, float *y,
+                          void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w == NULL || y == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    return mynah_dequant_launch(d, type, w, rows, cols, y, mynah_stream_or_default(d, stream));
+}
+
+void *mynah_hip_alloc(size_t bytes) {
+    if (mynah_dev() == NULL) return NULL;
+    void *p = NULL;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        mynah_set_error("hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return NULL;
+    }
+    return p;
+}
+
+int mynah_hip_free(void *p) {
+    if (p == NULL) return 0;
+    if (mynah_dev() == NULL) return -1;
+    HIP_OK(hipFree(p), "hipFree");
+    return 0;
+}
+
+int mynah_hip_h2d(void *dst, const void *src, size_t bytes) {
+    if (mynah_dev() == NULL) return -1;
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    return 0;
+}
+
+int mynah_hip_d2h(void *dst, const void *src, size_t bytes) {
+    if (mynah_dev() == NULL) return -1;
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return 0;
+}
+
+int mynah_hip_memset(void *dst, int value, size_t bytes) {
+    if (mynah_dev() == NULL) return -1;
+    HIP_OK(hipMemset(dst, value, bytes), "hipMemset");
+    return 0;
+}
+
+int mynah_hip_sync(void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    HIP_OK(hipStreamSynchronize(mynah_stream_or_default(d, stream)), "hipStreamSynchronize");
+    return 0;
+}
+
+void *mynah_hip_stream(void) {
+    mynah_device *d = mynah_dev();
+    return d ? (void *)d->stream : NULL;
+}
+
+int mynah_hip_time_matvec(int type, const void *const *w_copies, int n_copies, size_t rows,
+                          size_t cols, const float *x, float *y, int iters, float *ms) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w_copies == NULL || n_copies <= 0 || iters <= 0 || ms == NULL) {
+        mynah_set_error("bad timing arguments");
+        return -1;
+    }
+    hipEvent_t a, b;
+    HIP_OK(hipEventCreate(&a), "hipEventCreate");
+    if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        mynah_set_error("hipEventCreate");
+        return -1;
+    }
+    int rc = 0;
+    if (hipEventRecord(a, d->stream) != hipSuccess) rc = -1;
+    for (int i = 0; i < iters && rc == 0; i++)
+        rc = mynah_gemv_launch(d, type, w_copies[i % n_copies], rows, cols, x, y, d->stream);
+    if (rc == 0 && (hipEventRecord(b, d->stream) != hipSuccess ||
+                    hipEventSynchronize(b) != hipSuccess ||
+                    hipEventElapsedTime(ms, a, b) != hipSuccess)) {
+        mynah_set_error("event timing failed");
+        rc = -1;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return rc;
+}

@@ -1,0 +1,192 @@
+"""ctypes binding of libmynah_hip.so (the gfx950 kernels behind include/kernels_hip.h).
+
+The library is C11 + HIP; this module only loads it and gives numpy-friendly
+wrappers to tests and the benchmark. It never falls back to anything: if the
+shared library is missing, importing it raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmynah_hip.so")
+
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built: run `make -C mynah-slm_amd` (or __graft_entry__.build())")
+    lib = C.CDLL(LIB_PATH)
+    sig = {
+        "ingot_matvec": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "ingot_matmat": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
+        "ingot_dequant_matrix": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P]),
+        "ingot_has_kernel": (C.c_int, [C.c_int]),
+        "ingot_matmat_is_exact": (C.c_int, [_SZ]),
+        "mynah_hip_init": (C.c_int, [C.c_int]),
+        "mynah_hip_last_error": (C.c_char_p, []),
+        "mynah_hip_register": (C.c_int, [_P, _SZ]),
+        "mynah_hip_unregister": (C.c_int, [_P]),
+        "mynah_hip_device_ptr": (_P, [_P]),
+        "mynah_hip_matvec_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _P]),
+        "mynah_hip_matmat_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _P]),
+        "mynah_hip_dequant_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "mynah_hip_alloc": (_P, [_SZ]),
+        "mynah_hip_free": (C.c_int, [_P]),
+        "mynah_hip_h2d": (C.c_int, [_P, _P, _SZ]),
+        "mynah_hip_d2h": (C.c_int, [_P, _P, _SZ]),
+        "mynah_hip_memset": (C.c_int, [_P, C.c_int, _SZ]),
+        "mynah_hip_sync": (C.c_int, [_P]),
+        "mynah_hip_stream": (_P, []),
+        "mynah_hip_time_matvec": (C.c_int, [C.c_int, _P, C.c_int, _SZ, _SZ, _P, _P, C.c_int,
+                                            C.POINTER(C.c_float)]),
+        "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
+        "mynah_synth_normal": (C.c_int, [C.c_uint64, _SZ, C.c_float, C.c_float, _P, C.c_int]),
+        "mynah_synth_uniform_u32": (C.c_int, [C.c_uint64, _SZ, C.c_uint32, _P]),
+        "mynah_synth_substream": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "mynah_synth_f32_to_f16": (C.c_uint16, [C.c_float]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        raise HipError(f"{what}: {lib.mynah_hip_last_error().decode(errors='replace')}")
+
+
+def ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def row_bytes(qtype: int, cols: int) -> int:
+    elems, nbytes = BLOCK[qtype]
+    return cols // elems * nbytes
+
+
+# ── synthetic inputs (shared generator, see include/mynah_synth.h) ──────────
+
+def synth_blocks(qtype: int, seed: int, rows: int, cols: int, row0: int = 0) -> np.ndarray:
+    out = np.empty(rows * row_bytes(qtype, cols), dtype=np.uint8)
+    if lib.mynah_synth_blocks(qtype, seed, row0, rows, cols, ptr(out), 0) != 0:
+        raise ValueError("synth_blocks: bad arguments")
+    return out
+
+
+def synth_normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    if lib.mynah_synth_normal(seed, n, mean, std, ptr(out), 0) != 0:
+        raise ValueError("synth_normal: bad arguments")
+    return out
+
+
+def substream(seed: int, k: int) -> int:
+    return int(lib.mynah_synth_substream(seed, k))
+
+
+# ── device memory ───────────────────────────────────────────────────────────
+
+class DeviceBuffer:
+    """A plain hipMalloc allocation owned by the library."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = lib.mynah_hip_alloc(self.nbytes)
+        if not p:
+            raise HipError(f"alloc({nbytes}): {lib.mynah_hip_last_error().decode()}")
+        self.ptr = int(p)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        check(lib.mynah_hip_h2d(b.ptr, ptr(a), a.nbytes), "h2d")
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib.mynah_hip_h2d(self.ptr + offset, ptr(a), a.nbytes), "h2d")
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib.mynah_hip_d2h(ptr(out), self.ptr + offset, out.nbytes), "d2h")
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib.mynah_hip_free(self.ptr), "free")
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def sync() -> None:
+    check(lib.mynah_hip_sync(None), "sync")
+
+
+# ── kernels through the drop-in (host pointer) ABI ──────────────────────────
+
+def matvec(qtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    y = np.empty(rows, dtype=np.float32)
+    check(lib.ingot_matvec(qtype, ptr(w), rows, cols, ptr(x), ptr(y)), "ingot_matvec")
+    return y
+
+
+def matmat(qtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, tokens: int) -> np.ndarray:
+    y = np.empty(tokens * rows, dtype=np.float32)
+    check(lib.ingot_matmat(qtype, ptr(w), rows, cols, ptr(x), ptr(y), tokens), "ingot_matmat")
+    return y
+
+
+def dequant(qtype: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    y = np.empty(rows * cols, dtype=np.float32)
+    check(lib.ingot_dequant_matrix(qtype, ptr(w), rows, cols, ptr(y)), "ingot_dequant_matrix")
+    return y
+
+
+# ── device-pointer twins ────────────────────────────────────────────────────
+
+def matvec_dev(qtype: int, w: int, rows: int, cols: int, x: int, y: int, stream=None) -> None:
+    check(lib.mynah_hip_matvec_dev(qtype, w, rows, cols, x, y, stream), "matvec_dev")
+
+
+def matmat_dev(qtype: int, w: int, rows: int, cols: int, x: int, y: int, tokens: int,
+               stream=None) -> None:
+    check(lib.mynah_hip_matmat_dev(qtype, w, rows, cols, x, y, tokens, stream), "matmat_dev")
+
+
+def dequant_dev(qtype: int, w: int, rows: int, cols: int, y: int, stream=None) -> None:
+    check(lib.mynah_hip_dequant_dev(qtype, w, rows, cols, y, stream), "dequant_dev")
+
+
+def time_matvec(qtype: int, w_ptrs, rows: int, cols: int, x: int, y: int, iters: int) -> float:
+    arr = (C.c_void_p * len(w_ptrs))(*w_ptrs)
+    ms = C.c_float(0.0)
+    check(lib.mynah_hip_time_matvec(qtype, C.cast(arr, C.c_void_p), len(w_ptrs), rows, cols,
+                                    x, y, iters, C.byref(ms)), "time_matvec")
+    return float(ms.value)

@@ -1,0 +1,159 @@
+"""Write the golden vectors under tests/golden/ from the COMPILED REFERENCE.
+
+Run in a container where /root/reference exists and `make -C oracle` has built
+oracle/_ref/libref.so (the reference's own C sources, compiled unchanged). The
+outputs are plain arrays (.npz without pickles) plus the ingot test fixtures
+(data files of the reference's own test suite, copied as data).
+
+    python tests/golden/make_golden.py
+
+Cases (inputs are regenerated from seeds by the shared generator; the npz also
+records a SHA-256 of the input bytes so generator drift is detected):
+  kernels_small.npz  per type: matvec, exact matmat (3 tokens), dequant on
+                     37 x 512 (Q8_0 also 37 x 96, a ragged block count)
+  c1.npz             configs[0]: Q4_K 1024 x 3072 matvec, seed 0
+  c2.npz             configs[1]: Q6_K / Q8_0 sweep; the 151936-row head as a
+                     SHA-256 of its output bits plus every 97th row
+  matmat.npz         batched exact order at prefill-like widths
+  qwen3_tiny.npz     3-layer model: 32 greedy steps, first-step logits
+  qwen3_06b.npz      configs[2]: 0.6B, KV prefill 512, 64 greedy steps,
+                     first-step logits' top 64 and the SHA-256 of all of them
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import shutil
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+sys.path.insert(0, os.path.join(ROOT, "mynah-slm_amd"))
+
+import configs as CF  # noqa: E402
+import oracle_lib as O  # noqa: E402
+
+REF_FIXTURES = "/root/reference/third_party/ingot/tests/fixtures"
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def ref_matvec(ref, t, w, rows, cols, x):
+    y = np.empty(rows, np.float32)
+    assert ref.ref_matvec(t, O.ptr(w), rows, cols, O.ptr(x), O.ptr(y)) == 0
+    return y
+
+
+def ref_matmat(ref, t, w, rows, cols, x, tokens):
+    y = np.empty(rows * tokens, np.float32)
+    assert ref.ref_matmat(t, O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+    return y
+
+
+def ref_dequant(ref, t, w, rows, cols):
+    y = np.empty(rows * cols, np.float32)
+    assert ref.ref_dequant_matrix(t, O.ptr(w), rows, cols, O.ptr(y)) == 0
+    return y
+
+
+def main() -> int:
+    ref = O.load_ref()
+    if ref is None:
+        print("oracle/_ref/libref.so is not built (needs /root/reference): nothing written")
+        return 1
+    assert ref.ref_matmat_is_exact(2) == 1, "reference build took the int8 batched lane"
+
+    # The reference's own fixtures, copied as data.
+    fx = os.path.join(HERE, "ingot_fixtures")
+    os.makedirs(fx, exist_ok=True)
+    for name in ("Q4_K", "Q6_K", "Q8_0"):
+        for ext in ("bin", "ref"):
+            shutil.copyfile(os.path.join(REF_FIXTURES, f"{name}.{ext}"),
+                            os.path.join(fx, f"{name}.{ext}"))
+    for name in ("manifest.txt", "geometry.txt"):
+        shutil.copyfile(os.path.join(REF_FIXTURES, name), os.path.join(fx, name))
+
+    out = {}
+    for t in (CF.Q4_K, CF.Q6_K, CF.Q8_0):
+        shapes = [(37, 512)] + ([(37, 96)] if t == CF.Q8_0 else [])
+        for rows, cols in shapes:
+            key = f"{CF.TYPE_NAME[t]}_{rows}x{cols}"
+            w = O.blocks(t, 100 + t, rows, cols)
+            x = O.normal(200 + t, 3 * cols)
+            out[f"{key}_w_sha"] = np.array(sha(w))
+            out[f"{key}_x_sha"] = np.array(sha(x))
+            out[f"{key}_matvec"] = ref_matvec(ref, t, w, rows, cols, x)
+            if cols % 256 == 0:
+                out[f"{key}_matmat3"] = ref_matmat(ref, t, w, rows, cols, x, 3)
+                out[f"{key}_dequant"] = ref_dequant(ref, t, w, rows, cols)
+            else:
+                # The reference's batched core and matrix dequant work in
+                # 256-wide units and refuse a ragged Q8_0 row (-1).
+                y = np.empty(rows * cols * 3, np.float32)
+                out[f"{key}_matmat3_rc"] = np.array(ref.ref_matmat(
+                    t, O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), 3))
+                out[f"{key}_dequant_rc"] = np.array(ref.ref_dequant_matrix(
+                    t, O.ptr(w), rows, cols, O.ptr(y)))
+    np.savez_compressed(os.path.join(HERE, "kernels_small.npz"), **out)
+
+    # configs[0]
+    m = CF.C1[0]
+    ws, xs = CF.matrix_seeds(O.substream, 0, 0)
+    w, x = O.blocks(m.qtype, ws, m.rows, m.cols), O.normal(xs, m.cols)
+    np.savez_compressed(os.path.join(HERE, "c1.npz"), w_sha=np.array(sha(w)),
+                        x_sha=np.array(sha(x)), y=ref_matvec(ref, m.qtype, w, m.rows, m.cols, x))
+
+    # configs[1]
+    out = {}
+    for i, m in enumerate(CF.C2):
+        ws, xs = CF.matrix_seeds(O.substream, 0, i)
+        w, x = O.blocks(m.qtype, ws, m.rows, m.cols), O.normal(xs, m.cols)
+        y = ref_matvec(ref, m.qtype, w, m.rows, m.cols, x)
+        out[f"{m.name}_w_sha"] = np.array(sha(w))
+        out[f"{m.name}_y_sha"] = np.array(sha(y))
+        out[f"{m.name}_y_every97"] = y[::97].copy()
+        if m.rows <= 4096:
+            out[f"{m.name}_y"] = y
+    np.savez_compressed(os.path.join(HERE, "c2.npz"), **out)
+
+    # batched exact order
+    out = {}
+    for t, rows, cols, tokens in ((CF.Q4_K, 64, 2048, 16), (CF.Q6_K, 32, 6144, 8),
+                                  (CF.Q8_0, 40, 1024, 5)):
+        key = f"{CF.TYPE_NAME[t]}_{rows}x{cols}_t{tokens}"
+        w = O.blocks(t, 300 + t, rows, cols)
+        x = O.normal(400 + t, tokens * cols)
+        out[f"{key}_y"] = ref_matmat(ref, t, w, rows, cols, x, tokens)
+        out[f"{key}_w_sha"] = np.array(sha(w))
+    np.savez_compressed(os.path.join(HERE, "matmat.npz"), **out)
+
+    # Qwen3: tiny (every step's logits) and the 0.6B config.
+    shape, npre, steps = CF.QWEN3_TINY, 16, 32
+    model = O.SynthModel(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    toks, lg = O.ref_greedy(ref, model, k, v, npre, first, steps, npre + steps + 1)
+    np.savez_compressed(os.path.join(HERE, "qwen3_tiny.npz"), tokens=np.array(toks, np.uint32),
+                        first=np.array(first), logits0=lg, blob_sha=np.array(sha(model.blob)))
+
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
+    model = O.SynthModel(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    toks, lg = O.ref_greedy(ref, model, k, v, npre, first, steps, npre + steps + 1)
+    top = np.argsort(-lg, kind="stable")[:64]
+    np.savez_compressed(os.path.join(HERE, "qwen3_06b.npz"), tokens=np.array(toks, np.uint32),
+                        first=np.array(first), logits0_sha=np.array(sha(lg)),
+                        top_ids=top.astype(np.uint32), top_vals=lg[top],
+                        blob_sha=np.array(sha(model.blob)))
+    print("golden vectors written to", HERE)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

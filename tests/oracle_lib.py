@@ -1,0 +1,273 @@
+"""ctypes access to the CPU checkers under oracle/ (test infrastructure only).
+
+  * liboracle.so    this repository's C11 restatement of the reference path
+  * _ref/libref.so  the reference compiled from its own sources (built here
+                    when /root/reference exists; optional everywhere else)
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import tempfile
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+
+_P, _SZ = C.c_void_p, C.c_size_t
+
+
+class OrcTensor(C.Structure):
+    _fields_ = [("type", C.c_int), ("rows", C.c_uint64), ("cols", C.c_uint64), ("data", _P)]
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [(n, OrcTensor) for n in ("attn_norm", "wq", "wk", "wv", "q_norm", "k_norm", "wo",
+                                         "ffn_norm", "gate", "up", "down")]
+
+
+class OrcConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_layers", "d_model", "d_ff", "n_heads", "n_kv_heads",
+                                          "head_dim", "vocab")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class SynthShape(C.Structure):
+    _fields_ = OrcConfig._fields_
+
+
+class SynthTensor(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("type", C.c_int), ("rank", C.c_uint32),
+                ("rows", C.c_uint64), ("cols", C.c_uint64), ("offset", C.c_uint64),
+                ("nbytes", C.c_uint64)]
+
+
+def _load_oracle() -> C.CDLL:
+    if not os.path.exists(ORACLE_SO):
+        raise ImportError(f"{ORACLE_SO} missing: run `make -C oracle`")
+    lib = C.CDLL(ORACLE_SO)
+    sig = {
+        "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+        "orc_dequant_matrix": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P]),
+        "orc_matvec": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "orc_matmat": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
+        "orc_matmat_mt": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
+        "orc_project": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "orc_threads_init": (C.c_int, [C.c_int]),
+        "orc_threads_count": (C.c_int, []),
+        "orc_threads_shutdown": (None, []),
+        "orc_qwen3_new": (_P, [C.POINTER(OrcConfig), C.POINTER(OrcTensor), C.POINTER(OrcTensor),
+                               C.POINTER(OrcLayer), C.c_uint32]),
+        "orc_qwen3_free": (None, [_P]),
+        "orc_qwen3_k_cache": (C.POINTER(C.c_float), [_P]),
+        "orc_qwen3_v_cache": (C.POINTER(C.c_float), [_P]),
+        "orc_qwen3_set_n_past": (None, [_P, C.c_uint32]),
+        "orc_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
+        "orc_argmax": (C.c_uint32, [_P, _SZ]),
+        "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
+        "mynah_synth_normal": (C.c_int, [C.c_uint64, _SZ, C.c_float, C.c_float, _P, C.c_int]),
+        "mynah_synth_uniform_u32": (C.c_int, [C.c_uint64, _SZ, C.c_uint32, _P]),
+        "mynah_synth_substream": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "mynah_synth_f32_to_f16": (C.c_uint16, [C.c_float]),
+        "mynah_synth_qwen3_layout": (C.c_int, [C.POINTER(SynthShape), C.POINTER(SynthTensor), _SZ,
+                                               C.POINTER(_SZ), C.POINTER(C.c_uint64)]),
+        "mynah_synth_qwen3_fill": (C.c_int, [C.POINTER(SynthShape), C.c_uint64,
+                                             C.POINTER(SynthTensor), _SZ, _P, C.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    return lib
+
+
+orc = _load_oracle()
+
+
+def load_ref():
+    """The compiled reference, or None when it was not built on this machine."""
+    if not os.path.exists(REF_SO):
+        return None
+    lib = C.CDLL(REF_SO)
+    sig = {
+        "ref_matvec": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "ref_matmat": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
+        "ref_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "ref_matmat_is_exact": (C.c_int, [_SZ]),
+        "ref_dequant_matrix": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P]),
+        "ref_dequant": (C.c_int, [C.c_int, _P, _SZ, _P]),
+        "ref_write_qwen3_gguf": (C.c_int, [C.c_char_p, C.POINTER(SynthShape),
+                                           C.POINTER(SynthTensor), _SZ, _P, C.c_uint32,
+                                           C.c_char_p, _SZ]),
+        "ref_qwen3_greedy": (C.c_int, [C.c_char_p, _P, _P, C.c_uint32, C.c_uint32, C.c_uint32,
+                                       C.c_uint32, C.c_int, _P, _P, C.c_char_p, _SZ]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    return lib
+
+
+BLOCK = {12: (256, 144), 14: (256, 210), 8: (32, 34)}
+
+
+def ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def substream(seed: int, k: int) -> int:
+    return int(orc.mynah_synth_substream(seed, k))
+
+
+def blocks(qtype: int, seed: int, rows: int, cols: int) -> np.ndarray:
+    e, b = BLOCK[qtype]
+    out = np.empty(rows * (cols // e) * b, np.uint8)
+    assert orc.mynah_synth_blocks(qtype, seed, 0, rows, cols, ptr(out), 0) == 0
+    return out
+
+
+def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    assert orc.mynah_synth_normal(seed, n, mean, std, ptr(out), 0) == 0
+    return out
+
+
+def matvec(qtype, w, rows, cols, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    assert orc.orc_matvec(qtype, ptr(w), rows, cols, ptr(x), ptr(y)) == 0
+    return y
+
+
+def project(qtype, w, rows, cols, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    assert orc.orc_project(qtype, ptr(w), rows, cols, ptr(x), ptr(y)) == 0
+    return y
+
+
+def matmat(qtype, w, rows, cols, x, tokens, threaded=False) -> np.ndarray:
+    y = np.empty(rows * tokens, np.float32)
+    fn = orc.orc_matmat_mt if threaded else orc.orc_matmat
+    assert fn(qtype, ptr(w), rows, cols, ptr(x), ptr(y), tokens) == 0
+    return y
+
+
+def dequant(qtype, w, rows, cols) -> np.ndarray:
+    y = np.empty(rows * cols, np.float32)
+    assert orc.orc_dequant_matrix(qtype, ptr(w), rows, cols, ptr(y)) == 0
+    return y
+
+
+# ── random-init Qwen3 (shared layout with the GPU library) ──────────────────
+
+class SynthModel:
+    """Host blob + tensor table of a random-init Qwen3 in the Q4_K_M mix."""
+
+    def __init__(self, shape, seed: int = 0):
+        self.shape = shape
+        self.c_shape = SynthShape(shape.n_layers, shape.d_model, shape.d_ff, shape.n_heads,
+                                  shape.n_kv_heads, shape.head_dim, shape.vocab,
+                                  shape.rms_eps, shape.rope_theta)
+        count, total = _SZ(0), C.c_uint64(0)
+        orc.mynah_synth_qwen3_layout(C.byref(self.c_shape), None, 0, C.byref(count),
+                                     C.byref(total))
+        self.table = (SynthTensor * count.value)()
+        assert orc.mynah_synth_qwen3_layout(C.byref(self.c_shape), self.table, count.value,
+                                            C.byref(count), C.byref(total)) == 0
+        self.count = count.value
+        self.blob = np.empty(total.value, np.uint8)
+        assert orc.mynah_synth_qwen3_fill(C.byref(self.c_shape), seed, self.table, self.count,
+                                          ptr(self.blob), 0) == 0
+        self.by_name = {self.table[i].name.decode(): self.table[i] for i in range(self.count)}
+
+    def tensor(self, name: str) -> OrcTensor:
+        t = self.by_name[name]
+        return OrcTensor(t.type, t.rows, t.cols, ptr(self.blob) + t.offset)
+
+
+class OracleQwen3:
+    """The restated decoder over a SynthModel (same bytes the GPU consumes)."""
+
+    def __init__(self, model: SynthModel, n_ctx: int):
+        s = model.shape
+        self.model, self.n_ctx = model, n_ctx
+        self.cfg = OrcConfig(s.n_layers, s.d_model, s.d_ff, s.n_heads, s.n_kv_heads, s.head_dim,
+                             s.vocab, s.rms_eps, s.rope_theta)
+        names = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_q_norm", "attn_k_norm",
+                 "attn_output", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")
+        self.layers = (OrcLayer * s.n_layers)()
+        for l in range(s.n_layers):
+            for field, nm in zip([f[0] for f in OrcLayer._fields_], names):
+                setattr(self.layers[l], field, model.tensor(f"blk.{l}.{nm}.weight"))
+        self.embed = model.tensor("token_embd.weight")
+        self.out_norm = model.tensor("output_norm.weight")
+        self.h = orc.orc_qwen3_new(C.byref(self.cfg), C.byref(self.embed), C.byref(self.out_norm),
+                                   self.layers, n_ctx)
+        assert self.h, "orc_qwen3_new failed"
+        self.kv_dim = s.n_kv_heads * s.head_dim
+
+    def prefill_kv(self, k: np.ndarray, v: np.ndarray, n: int) -> None:
+        """k, v: [layer][n][kv_dim] f32."""
+        s = self.model.shape
+        kc = np.ctypeslib.as_array(orc.orc_qwen3_k_cache(self.h),
+                                   shape=(s.n_layers, self.n_ctx, self.kv_dim))
+        vc = np.ctypeslib.as_array(orc.orc_qwen3_v_cache(self.h),
+                                   shape=(s.n_layers, self.n_ctx, self.kv_dim))
+        kc[:, :n] = k.reshape(s.n_layers, n, self.kv_dim)
+        vc[:, :n] = v.reshape(s.n_layers, n, self.kv_dim)
+        orc.orc_qwen3_set_n_past(self.h, n)
+
+    def forward(self, token: int) -> np.ndarray:
+        logits = np.empty(self.model.shape.vocab, np.float32)
+        assert orc.orc_qwen3_forward(self.h, token, ptr(logits)) == 0
+        return logits
+
+    def greedy(self, first: int, steps: int):
+        toks, tok, first_logits = [], first, None
+        for i in range(steps):
+            lg = self.forward(tok)
+            if i == 0:
+                first_logits = lg
+            tok = int(orc.orc_argmax(ptr(lg), lg.size))
+            toks.append(tok)
+        return toks, first_logits
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            orc.orc_qwen3_free(self.h)
+            self.h = None
+
+
+def kv_prefill(substream_fn, shape, config_seed: int, n: int):
+    """K and V prefill tensors [layer][n][kv_dim] of a config (see configs.py)."""
+    from_idx = 1 << 20
+    kv_seed = substream_fn(config_seed, from_idx)
+    kvd = shape.n_kv_heads * shape.head_dim
+    k = np.empty((shape.n_layers, n * kvd), np.float32)
+    v = np.empty((shape.n_layers, n * kvd), np.float32)
+    for l in range(shape.n_layers):
+        k[l] = normal(substream_fn(kv_seed, 2 * l), n * kvd)
+        v[l] = normal(substream_fn(kv_seed, 2 * l + 1), n * kvd)
+    return k, v
+
+
+def first_token(config_seed: int, vocab: int) -> int:
+    out = np.empty(1, np.uint32)
+    assert orc.mynah_synth_uniform_u32(substream(config_seed, 1 << 21), 1, vocab, ptr(out)) == 0
+    return int(out[0])
+
+
+def ref_greedy(ref, model: SynthModel, k, v, n_prefill, first, steps, n_ctx, threads=0):
+    """Run the compiled reference loader + decoder on the same model."""
+    tokens = np.zeros(steps, np.uint32)
+    logits = np.zeros(model.shape.vocab, np.float32)
+    err = C.create_string_buffer(512)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf").encode()
+        rc = ref.ref_write_qwen3_gguf(path, C.byref(model.c_shape), model.table, model.count,
+                                      ptr(model.blob), n_ctx, err, 512)
+        assert rc == 0, err.value
+        rc = ref.ref_qwen3_greedy(path, ptr(k), ptr(v), n_prefill, first, steps, n_ctx, threads,
+                                  ptr(tokens), ptr(logits), err, 512)
+        assert rc == 0, err.value
+    return [int(t) for t in tokens], logits
