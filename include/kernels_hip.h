@@ -110,6 +110,15 @@ int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols,
 int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols,
                           float *y, void *stream);
 
+/* Summation order of every GEMV (host and device entry points):
+ *   MYNAH_GEMV_EXACT (default): the reference's own f32 order, so outputs are
+ *     bit-identical to the as-built CPU kernels;
+ *   MYNAH_GEMV_REORDERED: lane-parallel partial sums (fewer instructions per
+ *     weight); differs from the reference by f32 rounding only. */
+enum { MYNAH_GEMV_EXACT = 0, MYNAH_GEMV_REORDERED = 1 };
+int mynah_hip_set_gemv_order(int order);
+int mynah_hip_gemv_order(void);
+
 /* Plain device memory (256-byte aligned) and copies; *_async take a stream. */
 void *mynah_hip_alloc(size_t bytes);
 int   mynah_hip_free(void *p);
@@ -118,6 +127,13 @@ int   mynah_hip_d2h(void *dst, const void *src, size_t bytes);
 int   mynah_hip_memset(void *dst, int value, size_t bytes);
 int   mynah_hip_sync(void *stream);
 void *mynah_hip_stream(void);           /* the library's own stream */
+
+/* HIP events on a stream (NULL = the library's stream), for timing kernels
+ * exactly where they are launched. Elapsed time in milliseconds. */
+void *mynah_hip_event_create(void);
+int   mynah_hip_event_record(void *event, void *stream);
+int   mynah_hip_event_elapsed(void *start, void *end, float *ms);
+int   mynah_hip_event_destroy(void *event);
 
 /* Benchmark helper: `iters` launches of the matvec, cycling through the
  * `n_copies` weight copies in w_copies[] (to stream from HBM rather than

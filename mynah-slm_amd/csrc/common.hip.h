@@ -15,7 +15,20 @@ MYNAH_DEV float f16_to_f32(uint32_t bits16) {
     return (float)h;
 }
 
-// Byte k of a dword as float; the backend selects v_cvt_f32_ubyte{k}.
+// Byte K of a dword as float: one v_cvt_f32_ubyte{K}. Written as inline asm
+// because the compiler otherwise folds a preceding nibble mask into a v_bfe
+// and converts byte 0, which costs an extra instruction per weight.
+template <int K>
+MYNAH_DEV float ubyte_f(uint32_t v) {
+    float r;
+    if (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Byte k of a dword as float (plain C; the backend picks the conversion).
 MYNAH_DEV float byte_f(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xffu); }
 
 // {hi:lo} >> (8 * shift), low dword (v_alignbyte_b32).

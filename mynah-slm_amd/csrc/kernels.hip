@@ -3,3 +3,4 @@
 //
 // SPDX-License-Identifier: MIT
 #include "gemv.hip"
+#include "gemv_exact.hip"

@@ -4,9 +4,10 @@
  * per-type batched kernels (kernels.c:1742-1751, 2627-2648). Exact f32 for
  * every width, like the reference's exact path.
  *
- * This first form runs one GEMV launch per token over the resident weights:
- * correct for any width, and the entry point the MFMA prefill kernel replaces
- * for wide batches.
+ * This form runs the exact GEMV once per token in the batched reference's own
+ * summation order (natural weight order per 256-value unit, kernels.c:1017-
+ * 1039 and 2635-2648), so every output is bit-identical to ingot's exact
+ * matmat; tokens == 1 is the matvec, as in the reference (kernels.c:1726).
  *
  * SPDX-License-Identifier: MIT */
 #include "runtime_internal.h"
@@ -22,7 +23,7 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
         return -1;
     }
     for (size_t t = 0; t < tokens; t++) {
-        if (mynah_gemv_launch(d, type, w, rows, cols, x + t * cols, y + t * rows, stream) != 0)
+        if (mynah_gemv_seq_launch(d, type, w, rows, cols, x + t * cols, y + t * rows, stream) != 0)
             return -1;
     }
     return 0;

@@ -156,12 +156,43 @@ static size_t gemv_lds_bytes(int type, size_t cols) {
     }
 }
 
-/* Rows per lane: enough waves to fill 256 CUs several times over first,
- * then more rows per lane to reuse each x read. */
+/* Rows per lane of the reordered kernels: enough waves to fill 256 CUs
+ * several times over first, then more rows per lane to reuse each x read. */
 static int gemv_rows_per_lane(size_t rows) {
     if (rows >= 65536) return 4;
     if (rows >= 16384) return 2;
     return 1;
+}
+
+static int gemv_order = MYNAH_GEMV_EXACT;
+
+int mynah_hip_set_gemv_order(int order) {
+    if (order != MYNAH_GEMV_EXACT && order != MYNAH_GEMV_REORDERED) {
+        mynah_set_error("unknown GEMV order %d", order);
+        return -1;
+    }
+    gemv_order = order;
+    return 0;
+}
+
+int mynah_hip_gemv_order(void) { return gemv_order; }
+
+/* Exact kernels: 64 rows per workgroup, W waves splitting the units of a
+ * row (W <= 16, balanced so every wave gets the same count). */
+static int gemv_exact_launch(mynah_device *d, int type, const void *w, size_t rows,
+                             size_t cols, size_t rb, const float *x, float *y,
+                             hipStream_t stream, int seq) {
+    const size_t units = (type == MYNAH_Q8_0 && !seq) ? cols / 32 : cols / 256;
+    const size_t per_wave = (units + 15) / 16;
+    const size_t waves = (units + per_wave - 1) / per_wave;
+    const unsigned grid = (unsigned)((rows + 63) / 64);
+    int k;
+    if (type == MYNAH_Q4_K) k = seq ? MYNAH_K_Q4K_EXACT_SEQ : MYNAH_K_Q4K_EXACT;
+    else if (type == MYNAH_Q6_K) k = MYNAH_K_Q6K_EXACT;
+    else k = seq ? MYNAH_K_Q80_EXACT_SEQ : MYNAH_K_Q80_EXACT;
+    uint32_t rows32 = (uint32_t)rows, units32 = (uint32_t)units, rb32 = (uint32_t)rb;
+    void *args[] = {&w, &x, &y, &rows32, &units32, &rb32};
+    return mynah_launch(d, k, grid, 1, (unsigned)(64 * waves), 0, stream, args);
 }
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -180,6 +211,12 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
         mynah_set_error("weights misaligned for type %d", type);
         return -1;
     }
+    if (rb > 0xffffffffu) {
+        mynah_set_error("row too long");
+        return -1;
+    }
+    if (gemv_order == MYNAH_GEMV_EXACT)
+        return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 0);
     const size_t lds = gemv_lds_bytes(type, cols);
     if (lds > GEMV_LDS_MAX) {
         mynah_set_error("cols=%zu needs %zu B of LDS (max %u)", cols, lds, GEMV_LDS_MAX);
@@ -196,6 +233,21 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     uint32_t nb = (uint32_t)(type == MYNAH_Q8_0 ? cols / 32 : cols / 256);
     void *args[] = {&w, &x, &y, &rows32, &nb};
     return mynah_launch(d, k, grid, 1, GEMV_WG, lds, stream, args);
+}
+
+int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                          const float *x, float *y, hipStream_t stream) {
+    size_t rb;
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if (cols % 256 != 0 || rb > 0xffffffffu) {
+        mynah_set_error("batched order needs cols to be a multiple of 256");
+        return -1;
+    }
+    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0) {
+        mynah_set_error("weights misaligned for type %d", type);
+        return -1;
+    }
+    return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 1);
 }
 
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -568,4 +620,32 @@ int mynah_hip_time_matvec(int type, const void *const *w_copies, int n_copies, s
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
     return rc;
+}
+
+void *mynah_hip_event_create(void) {
+    if (mynah_dev() == NULL) return NULL;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) {
+        mynah_set_error("hipEventCreate failed");
+        return NULL;
+    }
+    return (void *)e;
+}
+
+int mynah_hip_event_record(void *event, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    HIP_OK(hipEventRecord((hipEvent_t)event, mynah_stream_or_default(d, stream)), "hipEventRecord");
+    return 0;
+}
+
+int mynah_hip_event_elapsed(void *start, void *end, float *ms) {
+    HIP_OK(hipEventSynchronize((hipEvent_t)end), "hipEventSynchronize");
+    HIP_OK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end), "hipEventElapsedTime");
+    return 0;
+}
+
+int mynah_hip_event_destroy(void *event) {
+    HIP_OK(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
+    return 0;
 }

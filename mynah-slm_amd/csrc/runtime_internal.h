@@ -21,7 +21,12 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_Q80_R1, "mynah_q80_gemv_r1")            \
     X(MYNAH_K_Q80_R2, "mynah_q80_gemv_r2")            \
     X(MYNAH_K_Q80_R4, "mynah_q80_gemv_r4")            \
-    X(MYNAH_K_DEQUANT, "mynah_dequant")
+    X(MYNAH_K_DEQUANT, "mynah_dequant")                 \
+    X(MYNAH_K_Q4K_EXACT, "mynah_q4k_gemv_exact")        \
+    X(MYNAH_K_Q6K_EXACT, "mynah_q6k_gemv_exact")        \
+    X(MYNAH_K_Q80_EXACT, "mynah_q80_gemv_exact")        \
+    X(MYNAH_K_Q4K_EXACT_SEQ, "mynah_q4k_gemv_exact_seq") \
+    X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq")
 
 enum {
 #define X(id, name) id,
@@ -48,6 +53,10 @@ int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes);
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                       const float *x, float *y, hipStream_t stream);
+/* The exact GEMV in the batched reference's summation order (one token of
+ * the exact matmat). cols must be a multiple of 256. */
+int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                          const float *x, float *y, hipStream_t stream);
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                          float *y, hipStream_t stream);
 int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,

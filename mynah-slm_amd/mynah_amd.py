@@ -47,6 +47,12 @@ def _load() -> C.CDLL:
         "mynah_hip_memset": (C.c_int, [_P, C.c_int, _SZ]),
         "mynah_hip_sync": (C.c_int, [_P]),
         "mynah_hip_stream": (_P, []),
+        "mynah_hip_set_gemv_order": (C.c_int, [C.c_int]),
+        "mynah_hip_gemv_order": (C.c_int, []),
+        "mynah_hip_event_create": (_P, []),
+        "mynah_hip_event_record": (C.c_int, [_P, _P]),
+        "mynah_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
+        "mynah_hip_event_destroy": (C.c_int, [_P]),
         "mynah_hip_time_matvec": (C.c_int, [C.c_int, _P, C.c_int, _SZ, _SZ, _P, _P, C.c_int,
                                             C.POINTER(C.c_float)]),
         "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
@@ -190,3 +196,27 @@ def time_matvec(qtype: int, w_ptrs, rows: int, cols: int, x: int, y: int, iters:
     check(lib.mynah_hip_time_matvec(qtype, C.cast(arr, C.c_void_p), len(w_ptrs), rows, cols,
                                     x, y, iters, C.byref(ms)), "time_matvec")
     return float(ms.value)
+
+
+class Event:
+    """A HIP event on the library's stream (or a given one)."""
+
+    def __init__(self):
+        p = lib.mynah_hip_event_create()
+        if not p:
+            raise HipError(lib.mynah_hip_last_error().decode())
+        self.p = p
+
+    def record(self, stream=None) -> None:
+        check(lib.mynah_hip_event_record(self.p, stream), "event_record")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float(0.0)
+        check(lib.mynah_hip_event_elapsed(self.p, end.p, C.byref(ms)), "event_elapsed")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            lib.mynah_hip_event_destroy(self.p)
+        except Exception:
+            pass
