@@ -1,0 +1,61 @@
+/* mynah_decode.h — the resident Qwen3 decode step on one MI355X.
+ *
+ * The GPU twin of the reference decoder's state and step
+ * (src/arch_qwen3.h:21-62): init owns the KV cache and every scratch buffer,
+ * forward() advances one position, reset() drops the history. The model is
+ * described by a tensor table (names, ggml types and shapes of the GGUF the
+ * reference loads, src/model.c:142-228) over one byte blob that is uploaded
+ * unchanged; Q4_K, Q6_K and Q8_0 projections run through the bit-exact GEMVs
+ * of kernels_hip.h, the f32 operators follow src/kernels.c.
+ *
+ * SPDX-License-Identifier: MIT */
+#ifndef MYNAH_DECODE_H
+#define MYNAH_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mynah_synth.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mynah_qwen3 mynah_qwen3;
+
+/* src/arch_qwen3.h:52-53 (mynah_slm_state_init): bind the tensors of
+ * `table` (offsets into `blob`, blob_bytes long), upload the blob, allocate
+ * the state for n_ctx positions. Tied head when "output.weight" is absent.
+ * NULL on failure, with the reason in err. */
+mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *shape, const mynah_synth_tensor *table,
+                                 size_t count, const void *blob, uint64_t blob_bytes,
+                                 uint32_t n_ctx, char *err, size_t errsz);
+/* src/arch_qwen3.h:54 */
+void mynah_hip_qwen3_free(mynah_qwen3 *s);
+/* src/arch_qwen3.h:56-57 (mynah_slm_state_reset) */
+void mynah_hip_qwen3_reset(mynah_qwen3 *s);
+
+/* src/arch_qwen3.h:59-62 (mynah_slm_forward): one token at position n_past;
+ * logits (host, vocab floats) may be NULL. 0, or -1 with the context full. */
+int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits);
+
+/* Greedy decoding (src/generate.c:47-77 with src/sampler.c:122-129) of
+ * n_steps tokens from first_token, the whole loop resident on the GPU (one
+ * captured step replayed per token). tokens_out gets the n_steps sampled
+ * ids; *ms (optional) the GPU time of the loop. */
+int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
+                             uint32_t *tokens_out, float *ms);
+
+/* Fill positions [0, n_pos) of the KV cache from host arrays laid out
+ * [layer][n_pos][kv_dim] and set n_past = n_pos (the configs prefill the
+ * cache with synthetic values instead of running a prompt). */
+int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos);
+
+uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
+/* 1 when the step runs as a replayed hipGraph, 0 when launched directly. */
+int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

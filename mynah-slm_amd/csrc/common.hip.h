@@ -48,3 +48,34 @@ MYNAH_DEV float wave_sum(float v) {
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
     return v;
 }
+
+// Workgroup-wide double sum; every thread gets the result. `sh` holds one
+// double per wave (blockDim.x <= 1024).
+MYNAH_DEV double block_sum_d(double v, double *sh) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    const uint32_t nw = (blockDim.x + 63u) >> 6;
+    for (uint32_t k = 0; k < nw; k++) t += sh[k];
+    return t;
+}
+
+MYNAH_DEV unsigned long long wave_max_u64(unsigned long long v) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(v, m, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Key ordering logits like the reference's greedy choice (src/sampler.c:
+// 124-129): a larger value wins, and among equal values the smaller index
+// (hence ~index in the low word). -0 is folded onto +0 so they compare equal.
+MYNAH_DEV unsigned long long argmax_key(float v, uint32_t index) {
+    uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (unsigned long long)(~index);
+}

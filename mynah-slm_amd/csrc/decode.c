@@ -1,0 +1,490 @@
+/* decode.c — the resident Qwen3 decode step on one GPU (C11 host side).
+ *
+ * Mirrors the reference decoder's interface and state
+ * (src/arch_qwen3.h:21-62, src/arch_qwen3.c:89-252):
+ *   - the model's bytes are uploaded once, unchanged, and every tensor is
+ *     used in place (the GGUF block layout is never repacked);
+ *   - the state owns the f32 KV cache [layer][n_ctx][kv_dim] (a position is
+ *     contiguous), the RoPE tables built exactly like the reference's (angles
+ *     in double, rounded to f32 once), and every scratch buffer, all
+ *     allocated at init; nothing allocates in the token loop;
+ *   - forward(token, logits) advances one position and returns -1 when the
+ *     context is full, like mynah_slm_forward.
+ *
+ * One step is a fixed sequence of launches on the library stream: embedding
+ * row, then per layer the q/k/v GEMVs as one grouped launch that also
+ * computes the RMSNorm of their input (K and V written straight into the
+ * cache slot), attention scores (QK-norm and RoPE folded in), softmax and
+ * weighted V sum, the o GEMV with the residual add, gate/up as one paired
+ * launch (RMSNorm in front, SwiGLU behind), the down GEMV with the residual
+ * add; then the final RMSNorm, the tied head (each workgroup leaving the key
+ * of its largest logit) and the greedy argmax over those keys, which also
+ * advances the device-side position. The token and the position live in device memory, so the step is
+ * captured once as a hipGraph and replayed for every generated token.
+ *
+ * SPDX-License-Identifier: MIT */
+#define _GNU_SOURCE
+#include "kernels_hip.h"
+#include "mynah_decode.h"
+#include "runtime_internal.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct {
+    int type;
+    uint64_t rows, cols, row_bytes;
+    const unsigned char *dev;
+} dtensor;
+
+typedef struct {
+    dtensor attn_norm, wq, wk, wv, q_norm, k_norm, wo, ffn_norm, gate, up, down;
+} dlayer;
+
+struct mynah_qwen3 {
+    mynah_qwen3_shape c;
+    uint32_t n_ctx, n_past, q_dim, kv_dim;
+    float scale;
+    unsigned char *blob;            /* the model bytes, unchanged */
+    dtensor embed, out_norm, head;
+    dlayer *layers;
+    float *k_cache, *v_cache, *rope_cos, *rope_sin;
+    float *x, *h, *q, *attn, *act, *logits, *scores;
+    uint32_t *counters;             /* token, pos, step */
+    unsigned long long *keys;       /* head workgroups' argmax keys */
+    uint32_t *tokens;               /* [n_ctx] generated ids */
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    int graph_state;                /* 0 not tried, 1 ready, -1 unavailable */
+    int graph_order;                /* GEMV order the graph was captured with */
+};
+
+#define TOKEN(s) ((s)->counters + 0)
+#define POS(s) ((s)->counters + 1)
+#define STEP(s) ((s)->counters + 2)
+
+static int fail(char *err, size_t errsz, const char *msg, const char *detail) {
+    if (err && errsz) snprintf(err, errsz, "%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
+    mynah_set_error("%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
+    return -1;
+}
+
+static const mynah_synth_tensor *find(const mynah_synth_tensor *t, size_t n, const char *name) {
+    for (size_t i = 0; i < n; i++)
+        if (strncmp(t[i].name, name, sizeof t[i].name) == 0) return &t[i];
+    return NULL;
+}
+
+static int bind(dtensor *out, const mynah_synth_tensor *table, size_t count,
+                const unsigned char *blob, uint64_t blob_bytes, const char *name, int want_type,
+                uint64_t rows, uint64_t cols, char *err, size_t errsz) {
+    const mynah_synth_tensor *t = find(table, count, name);
+    if (t == NULL) return fail(err, errsz, "missing tensor", name);
+    if (t->rows != rows || t->cols != cols || (want_type >= 0 && t->type != want_type))
+        return fail(err, errsz, "tensor has the wrong shape or type", name);
+    if (t->offset > blob_bytes || t->nbytes > blob_bytes - t->offset)
+        return fail(err, errsz, "tensor outside the blob", name);
+    size_t rb = cols * 4;
+    if (t->type != 0 && mynah_geometry(t->type, rows, cols, &rb) != 0)
+        return fail(err, errsz, "tensor type has no kernel", name);
+    out->type = t->type;
+    out->rows = rows;
+    out->cols = cols;
+    out->row_bytes = rb;
+    out->dev = blob + t->offset;
+    return 0;
+}
+
+static void *dalloc(size_t bytes, int *ok) {
+    void *p = NULL;
+    if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+        *ok = 0;
+        return NULL;
+    }
+    return p;
+}
+
+void mynah_hip_qwen3_free(mynah_qwen3 *s) {
+    if (s == NULL) return;
+    if (s->exec) (void)hipGraphExecDestroy(s->exec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->h, s->q,
+                    s->attn, s->act, s->logits, s->scores, s->counters, s->tokens};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
+        if (bufs[i]) (void)hipFree(bufs[i]);
+    free(s->layers);
+    free(s);
+}
+
+mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_tensor *table,
+                                 size_t count, const void *blob, uint64_t blob_bytes,
+                                 uint32_t n_ctx, char *err, size_t errsz) {
+    if (c == NULL || table == NULL || blob == NULL || n_ctx == 0) {
+        fail(err, errsz, "null argument", NULL);
+        return NULL;
+    }
+    if (c->n_kv_heads == 0 || c->n_heads % c->n_kv_heads != 0 ||
+        c->n_heads / c->n_kv_heads > 8 || c->head_dim != 128 ||
+        c->d_model % 256 != 0 || c->d_ff % 256 != 0 || c->vocab % 4 != 0 ||
+        (size_t)(c->n_heads / c->n_kv_heads) * n_ctx * 4 > 30 * 1024) {
+        fail(err, errsz, "unsupported shape", NULL);
+        return NULL;
+    }
+    mynah_device *d = mynah_dev();
+    if (d == NULL) {
+        fail(err, errsz, "no device", mynah_hip_last_error());
+        return NULL;
+    }
+    mynah_qwen3 *s = (mynah_qwen3 *)calloc(1, sizeof *s);
+    if (s == NULL) return NULL;
+    s->c = *c;
+    s->n_ctx = n_ctx;
+    s->q_dim = c->n_heads * c->head_dim;
+    s->kv_dim = c->n_kv_heads * c->head_dim;
+    s->scale = 1.0f / sqrtf((float)c->head_dim);      /* src/kernels.c:233 */
+    s->layers = (dlayer *)calloc(c->n_layers, sizeof *s->layers);
+    int ok = s->layers != NULL;
+
+    s->blob = (unsigned char *)dalloc(blob_bytes, &ok);
+    if (ok && hipMemcpy(s->blob, blob, blob_bytes, hipMemcpyHostToDevice) != hipSuccess) ok = 0;
+    if (!ok) {
+        fail(err, errsz, "cannot upload the model", NULL);
+        mynah_hip_qwen3_free(s);
+        return NULL;
+    }
+
+    const uint64_t dm = c->d_model, ff = c->d_ff, hd = c->head_dim;
+    int rc = bind(&s->embed, table, count, s->blob, blob_bytes, "token_embd.weight", -1, c->vocab,
+                  dm, err, errsz);
+    rc = rc ? rc : bind(&s->out_norm, table, count, s->blob, blob_bytes, "output_norm.weight", 0,
+                        1, dm, err, errsz);
+    if (rc == 0 && find(table, count, "output.weight"))
+        rc = bind(&s->head, table, count, s->blob, blob_bytes, "output.weight", -1, c->vocab, dm,
+                  err, errsz);
+    else
+        s->head = s->embed;                              /* tied (src/model.c:200-203) */
+    for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
+        dlayer *L = &s->layers[l];
+        char n[64];
+#define B(field, suffix, ty, r, cc)                                                     \
+        if (rc == 0) {                                                                  \
+            snprintf(n, sizeof n, "blk.%u." suffix, l);                                 \
+            rc = bind(&L->field, table, count, s->blob, blob_bytes, n, ty, r, cc, err,  \
+                      errsz);                                                           \
+        }
+        B(attn_norm, "attn_norm.weight", 0, 1, dm)
+        B(wq, "attn_q.weight", -1, s->q_dim, dm)
+        B(wk, "attn_k.weight", -1, s->kv_dim, dm)
+        B(wv, "attn_v.weight", -1, s->kv_dim, dm)
+        B(q_norm, "attn_q_norm.weight", 0, 1, hd)
+        B(k_norm, "attn_k_norm.weight", 0, 1, hd)
+        B(wo, "attn_output.weight", -1, dm, s->q_dim)
+        B(ffn_norm, "ffn_norm.weight", 0, 1, dm)
+        B(gate, "ffn_gate.weight", -1, ff, dm)
+        B(up, "ffn_up.weight", -1, ff, dm)
+        B(down, "ffn_down.weight", -1, dm, ff)
+#undef B
+        if (rc == 0 && (L->gate.type != L->up.type || L->gate.type == 0 || L->wq.type == 0 ||
+                        L->wk.type == 0 || L->wv.type == 0 || L->wo.type == 0 ||
+                        L->down.type == 0))
+            rc = fail(err, errsz, "projection types must be quantized, gate/up alike", n);
+    }
+    if (rc == 0 && s->head.type == 0)
+        rc = fail(err, errsz, "the output head must be quantized", NULL);
+    if (rc != 0) {
+        mynah_hip_qwen3_free(s);
+        return NULL;
+    }
+
+    const size_t kv = (size_t)c->n_layers * n_ctx * s->kv_dim;
+    const size_t half = hd / 2;
+    s->k_cache = (float *)dalloc(kv * 4, &ok);
+    s->v_cache = (float *)dalloc(kv * 4, &ok);
+    s->rope_cos = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
+    s->rope_sin = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
+    s->x = (float *)dalloc(dm * 4, &ok);
+    s->h = (float *)dalloc(dm * 4, &ok);
+    s->q = (float *)dalloc((size_t)s->q_dim * 4, &ok);
+    s->attn = (float *)dalloc((size_t)s->q_dim * 4, &ok);
+    s->act = (float *)dalloc(ff * 4, &ok);
+    s->logits = (float *)dalloc((size_t)c->vocab * 4, &ok);
+    s->scores = (float *)dalloc((size_t)c->n_heads * n_ctx * 4, &ok);
+    s->counters = (uint32_t *)dalloc(16, &ok);
+    s->keys = (unsigned long long *)dalloc(((size_t)c->vocab / 8 + 64) * 8, &ok);
+    s->tokens = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
+    if (!ok) {
+        fail(err, errsz, "out of device memory for the state", NULL);
+        mynah_hip_qwen3_free(s);
+        return NULL;
+    }
+    /* src/kernels.c:141-164: angle p * theta^(-2i/hd) in double, cos/sin
+     * rounded to f32 once. */
+    float *cs = (float *)malloc((size_t)n_ctx * half * 4), *sn = (float *)malloc((size_t)n_ctx * half * 4);
+    if (cs == NULL || sn == NULL) ok = 0;
+    for (uint32_t i = 0; ok && i < half; i++) {
+        const double inv = 1.0 / pow((double)c->rope_theta, (2.0 * (double)i) / (double)hd);
+        for (uint32_t p = 0; p < n_ctx; p++) {
+            const double a = (double)p * inv;
+            cs[(size_t)p * half + i] = (float)cos(a);
+            sn[(size_t)p * half + i] = (float)sin(a);
+        }
+    }
+    if (ok && (hipMemcpy(s->rope_cos, cs, (size_t)n_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+               hipMemcpy(s->rope_sin, sn, (size_t)n_ctx * half * 4, hipMemcpyHostToDevice) != hipSuccess ||
+               hipMemset(s->counters, 0, 16) != hipSuccess ||
+               hipMemset(s->k_cache, 0, kv * 4) != hipSuccess ||
+               hipMemset(s->v_cache, 0, kv * 4) != hipSuccess))
+        ok = 0;
+    free(cs);
+    free(sn);
+    if (!ok) {
+        fail(err, errsz, "state initialisation failed", NULL);
+        mynah_hip_qwen3_free(s);
+        return NULL;
+    }
+    return s;
+}
+
+/* ── the step ────────────────────────────────────────────────────────────── */
+
+static int gemv_desc(mynah_gemv_desc *g, const dtensor *w, const float *x, float *y) {
+    return mynah_gemv_desc_init(g, w->type, w->dev, w->rows, w->cols, x, y);
+}
+
+static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
+    const mynah_qwen3_shape *c = &s->c;
+    const size_t per_layer = (size_t)s->n_ctx * s->kv_dim;
+    uint32_t *tok = TOKEN(s), *pos = POS(s), *step = STEP(s);
+    int rc = 0;
+    {
+        const unsigned char *tab = s->embed.dev;
+        float *x = s->x;
+        uint32_t dm = c->d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
+        void *args[] = {&tab, &tok, &x, &dm, &ty, &rb};
+        rc = mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, st, args);
+    }
+    for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
+        const dlayer *L = &s->layers[l];
+        float *kl = s->k_cache + l * per_layer, *vl = s->v_cache + l * per_layer;
+        mynah_gemv_group g;
+
+        memset(&g, 0, sizeof g);
+        g.n = 3;
+        rc = gemv_desc(&g.d[0], &L->wq, s->x, s->q);
+        rc = rc ? rc : gemv_desc(&g.d[1], &L->wk, s->x, kl);
+        rc = rc ? rc : gemv_desc(&g.d[2], &L->wv, s->x, vl);
+        if (rc) break;
+        for (int k = 0; k < 3; k++) {      /* src/arch_qwen3.c:201 folded in */
+            g.d[k].norm_w = (const float *)L->attn_norm.dev;
+            g.d[k].eps = c->rms_eps;
+        }
+        g.d[1].ypos = pos;
+        g.d[1].ystride = s->kv_dim;
+        g.d[2].ypos = pos;
+        g.d[2].ystride = s->kv_dim;
+        rc = mynah_gemv_group_launch(d, &g, st);
+        if (rc) break;
+        {
+            const float *q = s->q, *qn = (const float *)L->q_norm.dev;
+            const float *kn = (const float *)L->k_norm.dev;
+            const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+            float *sc = s->scores;
+            uint32_t nctx = s->n_ctx, hd = c->head_dim, kvd = s->kv_dim;
+            uint32_t group = c->n_heads / c->n_kv_heads;
+            float eps = c->rms_eps, scale = s->scale;
+            void *args[] = {&q, &kl, &qn, &kn, &rcos, &rsin, &pos, &sc, &nctx, &hd, &kvd, &group,
+                            &eps, &scale};
+            rc = mynah_launch(d, MYNAH_K_ATTN_SCORES, c->n_kv_heads, (s->n_ctx + 63) / 64,
+                              64 * group, 0, st, args);
+            if (rc) break;
+            float *out = s->attn;
+            const float *scc = s->scores;
+            void *args2[] = {&vl, &scc, &pos, &out, &nctx, &hd, &kvd, &group};
+            rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, hd / 16, 256,
+                              (size_t)group * s->n_ctx * 4, st, args2);
+        }
+        if (rc) break;
+        memset(&g, 0, sizeof g);
+        g.n = 1;
+        rc = gemv_desc(&g.d[0], &L->wo, s->attn, s->x);
+        g.d[0].res = s->x;
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+        if (rc) break;
+        memset(&g, 0, sizeof g);
+        g.n = 1;
+        rc = gemv_desc(&g.d[0], &L->gate, s->x, s->act);
+        g.d[0].w2 = L->up.dev;
+        g.d[0].norm_w = (const float *)L->ffn_norm.dev;     /* src/arch_qwen3.c:226 */
+        g.d[0].eps = c->rms_eps;
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+        if (rc) break;
+        memset(&g, 0, sizeof g);
+        g.n = 1;
+        rc = gemv_desc(&g.d[0], &L->down, s->act, s->x);
+        g.d[0].res = s->x;
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+    }
+    if (rc == 0) {                                          /* src/arch_qwen3.c:239 */
+        const float *x = s->x, *w = (const float *)s->out_norm.dev;
+        float *h = s->h;
+        uint32_t n = c->d_model;
+        float eps = c->rms_eps;
+        void *args[] = {&x, &w, &h, &n, &eps};
+        rc = mynah_launch(d, MYNAH_K_RMSNORM, 1, 1, 1024, 0, st, args);
+    }
+    if (rc == 0) {
+        mynah_gemv_group g;
+        memset(&g, 0, sizeof g);
+        g.n = 1;
+        rc = gemv_desc(&g.d[0], &s->head, s->h, s->logits);
+        g.d[0].keys = s->keys;                               /* src/sampler.c:124-129 */
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+    }
+    if (rc == 0) {
+        const unsigned long long *keys = s->keys;
+        uint32_t n = mynah_gemv_group_tiles(c->vocab, c->vocab), maxs = s->n_ctx;
+        uint32_t *toks = s->tokens;
+        void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs};
+        rc = mynah_launch(d, MYNAH_K_ARGMAX, 1, 1, 1024, 0, st, args);
+    }
+    return rc;
+}
+
+/* Capture the step once; fall back to direct launches if capture fails. */
+static int run_step(mynah_qwen3 *s, mynah_device *d) {
+    hipStream_t st = d->stream;
+    if (s->graph_state == 1 && s->graph_order != mynah_hip_gemv_order()) {
+        (void)hipGraphExecDestroy(s->exec);
+        (void)hipGraphDestroy(s->graph);
+        s->exec = NULL;
+        s->graph = NULL;
+        s->graph_state = 0;
+    }
+    if (s->graph_state == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
+        s->graph_state = -1;
+        if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+            const int rc = enqueue_step(s, d, st);
+            hipGraph_t g = NULL;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (rc == 0 && e == hipSuccess && g != NULL &&
+                hipGraphInstantiate(&s->exec, g, NULL, NULL, 0) == hipSuccess) {
+                s->graph = g;
+                s->graph_state = 1;
+                s->graph_order = mynah_hip_gemv_order();
+            } else if (g != NULL) {
+                (void)hipGraphDestroy(g);
+            }
+        }
+        (void)hipGetLastError();
+    }
+    if (s->graph_state == 1) {
+        if (hipGraphLaunch(s->exec, st) != hipSuccess) {
+            mynah_set_error("hipGraphLaunch failed");
+            return -1;
+        }
+        return 0;
+    }
+    return enqueue_step(s, d, st);
+}
+
+static int set_counters(mynah_qwen3 *s, mynah_device *d, uint32_t token, uint32_t step) {
+    uint32_t v[3] = {token, s->n_past, step};
+    if (hipMemcpyAsync(s->counters, v, sizeof v, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
+        hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("counter upload failed");
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL) return -1;
+    if (s->n_past >= s->n_ctx) {
+        mynah_set_error("context exhausted");
+        return -1;
+    }
+    if (token >= s->c.vocab) {
+        mynah_set_error("token %u out of range", token);
+        return -1;
+    }
+    if (set_counters(s, d, token, 0) != 0 || run_step(s, d) != 0) return -1;
+    s->n_past++;
+    if (logits && hipMemcpyAsync(logits, s->logits, (size_t)s->c.vocab * 4,
+                                 hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
+        mynah_set_error("logits download failed");
+        return -1;
+    }
+    if (hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("step failed");
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
+                             uint32_t *tokens_out, float *ms) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || tokens_out == NULL) return -1;
+    if (n_steps == 0 || n_steps > s->n_ctx - s->n_past) {
+        mynah_set_error("%u steps do not fit the context (%u of %u used)", n_steps, s->n_past,
+                        s->n_ctx);
+        return -1;
+    }
+    if (first_token >= s->c.vocab) {
+        mynah_set_error("token %u out of range", first_token);
+        return -1;
+    }
+    if (set_counters(s, d, first_token, 0) != 0) return -1;
+    hipEvent_t a = NULL, b = NULL;
+    if (ms && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) {
+        mynah_set_error("hipEventCreate failed");
+        return -1;
+    }
+    int rc = 0;
+    if (ms) (void)hipEventRecord(a, d->stream);
+    for (uint32_t i = 0; i < n_steps && rc == 0; i++) rc = run_step(s, d);
+    if (ms) (void)hipEventRecord(b, d->stream);
+    if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("decode failed");
+        rc = -1;
+    }
+    if (rc == 0 && ms) (void)hipEventElapsedTime(ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (rc != 0) return -1;
+    s->n_past += n_steps;
+    if (hipMemcpy(tokens_out, s->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        mynah_set_error("token download failed");
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || k == NULL || v == NULL || n_pos > s->n_ctx) {
+        mynah_set_error("bad KV prefill");
+        return -1;
+    }
+    const size_t row = (size_t)n_pos * s->kv_dim, per_layer = (size_t)s->n_ctx * s->kv_dim;
+    for (uint32_t l = 0; l < s->c.n_layers; l++) {
+        if (hipMemcpy(s->k_cache + l * per_layer, k + l * row, row * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(s->v_cache + l * per_layer, v + l * row, row * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            mynah_set_error("KV upload failed");
+            return -1;
+        }
+    }
+    s->n_past = n_pos;
+    return 0;
+}
+
+uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s) { return s ? s->n_past : 0; }
+
+void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
+    if (s) s->n_past = 0;
+}
+
+int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) { return s ? s->graph_state == 1 : 0; }

@@ -252,3 +252,123 @@ GEMV_EXACT_ENTRY(mynah_q6k_gemv_exact, 14, false)
 GEMV_EXACT_ENTRY(mynah_q80_gemv_exact, 8, false)
 GEMV_EXACT_ENTRY(mynah_q4k_gemv_exact_seq, 12, true)
 GEMV_EXACT_ENTRY(mynah_q80_gemv_exact_seq, 8, true)
+
+
+// ── grouped launches with fused epilogues (the resident decode step) ───────
+// One launch covers up to EX_GROUP_MAX matrices; workgroup t serves the
+// 64-row tile t - tile0 of the descriptor whose [tile0, next tile0) range
+// holds t. Epilogues, each the reference's own f32 operation on the exact
+// row sum: y = res + Wx (src/arch_qwen3.c:224, 234 — mynah_slm_add), and for
+// a paired matrix w2 (ffn_up next to ffn_gate) y = (g * sigmoid(g)) * u with
+// the reference's overflow-safe sigmoid (src/kernels.c:193-205). `ypos`
+// moves y by ypos[0] * ystride: the K / V projections write straight into
+// the cache slot of the current position (src/arch_qwen3.c:194-199).
+
+#define EX_GROUP_MAX 8
+
+struct GemvDesc {
+    const uint8_t *w;
+    const uint8_t *w2;
+    const float *x;
+    float *y;
+    const float *res;
+    const uint32_t *ypos;
+    const float *norm_w;
+    unsigned long long *keys;    // per-workgroup argmax keys of the rows (head)
+    uint32_t ystride, rows, units, row_bytes, type, tile0, cols;
+    float eps;
+    uint32_t pad;
+};
+
+struct GemvGroup {
+    uint32_t n, pad;
+    GemvDesc d[EX_GROUP_MAX];
+};
+
+MYNAH_DEV float sigmoid_ref(float v) {
+#pragma clang fp contract(off)
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+template <int FMT>
+MYNAH_DEV float unit_any(const GemvDesc &g, const uint8_t *r1, const uint8_t *r2, uint32_t u,
+                         const float *__restrict__ x) {
+    if (u < g.units) return unit_sum<FMT, false>(r1, u, x);
+    return unit_sum<FMT, false>(r2, u - g.units, x);
+}
+
+template <bool NORM>
+MYNAH_DEV void group_body(const GemvDesc &g, uint32_t t, const float *__restrict__ x) {
+#pragma clang fp contract(off)
+    __shared__ float part[EX_MAX_WAVES][EX_ROWS];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+    const uint32_t row = (t - g.tile0) * EX_ROWS + lane;
+    const size_t roff = (size_t)(row < g.rows ? row : g.rows - 1u) * g.row_bytes;
+    const uint8_t *r1 = g.w + roff;
+    const uint8_t *r2 = g.w2 ? g.w2 + roff : r1;
+    const uint32_t total_units = g.w2 ? 2u * g.units : g.units;
+    float t1 = 0.0f, t2 = 0.0f;
+    for (uint32_t p = 0; p < total_units; p += nw) {
+        const uint32_t u = p + wave;
+        float s = 0.0f;
+        if (u < total_units) {
+            if (g.type == 12u) s = unit_any<12>(g, r1, r2, u, x);
+            else if (g.type == 14u) s = unit_any<14>(g, r1, r2, u, x);
+            else s = unit_any<8>(g, r1, r2, u, x);
+        }
+        part[wave][lane] = s;
+        __syncthreads();
+        if (wave == 0) {
+            const uint32_t n = total_units - p < nw ? total_units - p : nw;
+            for (uint32_t k = 0; k < n; k++) {
+                if (p + k < g.units) t1 = t1 + part[k][lane];
+                else t2 = t2 + part[k][lane];
+            }
+        }
+        __syncthreads();
+    }
+    if (wave == 0) {
+        float v = t1;
+        if (g.w2) v = t1 * sigmoid_ref(t1) * t2;
+        else if (g.res && row < g.rows) v = g.res[row] + t1;
+        if (row < g.rows) {
+            float *y = g.y + (g.ypos ? (size_t)g.ypos[0] * g.ystride : 0);
+            y[row] = v;
+        }
+        if (g.keys) {
+            const unsigned long long k = wave_max_u64(row < g.rows ? argmax_key(v, row) : 0ull);
+            if (lane == 0) g.keys[t - g.tile0] = k;
+        }
+    }
+}
+
+// With norm_w set, the input is RMSNorm(x) * norm_w (src/kernels.c:118-128:
+// double sum of squares, s = (float)(1 / sqrt(sum / n + eps)), (x * s) * w),
+// computed by every workgroup into LDS before its GEMV; this replaces the
+// reference's separate rms_norm call feeding the projections
+// (src/arch_qwen3.c:201, 226, 239). Dynamic LDS: cols floats.
+extern "C" __global__ void __launch_bounds__(EX_ROWS * EX_MAX_WAVES)
+mynah_gemv_group(const GemvGroup grp) {
+#pragma clang fp contract(off)
+    extern __shared__ float hx[];
+    __shared__ double shd[EX_MAX_WAVES];
+    const uint32_t t = blockIdx.x;
+    uint32_t i = 0;
+    while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
+    const GemvDesc &g = grp.d[i];
+    if (g.norm_w == nullptr) {
+        group_body<false>(g, t, g.x);
+        return;
+    }
+    double acc = 0.0;
+    for (uint32_t k = threadIdx.x; k < g.cols; k += blockDim.x) acc += (double)g.x[k] * (double)g.x[k];
+    const double sum = block_sum_d(acc, shd);
+    const float s = (float)(1.0 / sqrt(sum / (double)g.cols + (double)g.eps));
+    for (uint32_t k = threadIdx.x; k < g.cols; k += blockDim.x) hx[k] = g.x[k] * s * g.norm_w[k];
+    __syncthreads();
+    group_body<true>(g, t, hx);
+}

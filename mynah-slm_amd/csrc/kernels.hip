@@ -2,5 +2,7 @@
 // translation unit is included here and compiled by a single hipcc --genco).
 //
 // SPDX-License-Identifier: MIT
-#include "gemv.hip"
+#include "dequant.hip"
 #include "gemv_exact.hip"
+#include "gemv_fast.hip"
+#include "decode.hip"

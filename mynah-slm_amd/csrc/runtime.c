@@ -146,23 +146,6 @@ int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes) {
 /* ── GEMV launch ─────────────────────────────────────────────────────────── */
 
 #define GEMV_WG 256
-#define GEMV_LDS_MAX (64u * 1024u)
-
-static size_t gemv_lds_bytes(int type, size_t cols) {
-    switch (type) {
-    case MYNAH_Q4_K: return (cols + cols / 16 + cols / 16) * sizeof(float);
-    case MYNAH_Q6_K: return (cols + cols / 32 + cols / 8) * sizeof(float);
-    default:         return (cols + cols / 8 + cols / 32) * sizeof(float);
-    }
-}
-
-/* Rows per lane of the reordered kernels: enough waves to fill 256 CUs
- * several times over first, then more rows per lane to reuse each x read. */
-static int gemv_rows_per_lane(size_t rows) {
-    if (rows >= 65536) return 4;
-    if (rows >= 16384) return 2;
-    return 1;
-}
 
 static int gemv_order = MYNAH_GEMV_EXACT;
 
@@ -217,22 +200,11 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     }
     if (gemv_order == MYNAH_GEMV_EXACT)
         return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 0);
-    const size_t lds = gemv_lds_bytes(type, cols);
-    if (lds > GEMV_LDS_MAX) {
-        mynah_set_error("cols=%zu needs %zu B of LDS (max %u)", cols, lds, GEMV_LDS_MAX);
-        return -1;
-    }
-    const int R = gemv_rows_per_lane(rows);
-    const size_t rows_per_wg = (size_t)4 * 8 * (size_t)R;
-    const unsigned grid = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
-    int k;
-    if (type == MYNAH_Q4_K) k = R == 4 ? MYNAH_K_Q4K_R4 : R == 2 ? MYNAH_K_Q4K_R2 : MYNAH_K_Q4K_R1;
-    else if (type == MYNAH_Q6_K) k = R == 4 ? MYNAH_K_Q6K_R4 : R == 2 ? MYNAH_K_Q6K_R2 : MYNAH_K_Q6K_R1;
-    else k = R == 4 ? MYNAH_K_Q80_R4 : R == 2 ? MYNAH_K_Q80_R2 : MYNAH_K_Q80_R1;
-    uint32_t rows32 = (uint32_t)rows;
-    uint32_t nb = (uint32_t)(type == MYNAH_Q8_0 ? cols / 32 : cols / 256);
-    void *args[] = {&w, &x, &y, &rows32, &nb};
-    return mynah_launch(d, k, grid, 1, GEMV_WG, lds, stream, args);
+    mynah_gemv_group g;
+    memset(&g, 0, sizeof g);
+    g.n = 1;
+    if (mynah_gemv_desc_init(&g.d[0], type, w, rows, cols, x, y) != 0) return -1;
+    return mynah_gemv_group_launch(d, &g, stream);
 }
 
 int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -248,6 +220,87 @@ int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows,
         return -1;
     }
     return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 1);
+}
+
+int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
+                         const float *x, float *y) {
+    size_t rb;
+    memset(g, 0, sizeof *g);
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if ((type != MYNAH_Q8_0 && cols % 256 != 0) || rb > 0xffffffffu) {
+        mynah_set_error("cols must be a multiple of 256");
+        return -1;
+    }
+    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0 ||
+        ((uintptr_t)x & 3u) != 0) {
+        mynah_set_error("misaligned operand for type %d", type);
+        return -1;
+    }
+    g->w = w;
+    g->x = x;
+    g->y = y;
+    g->rows = (uint32_t)rows;
+    g->cols = (uint32_t)cols;
+    g->units = (uint32_t)(type == MYNAH_Q8_0 ? cols / 32 : cols / 256);
+    g->row_bytes = (uint32_t)rb;
+    g->type = (uint32_t)type;
+    return 0;
+}
+
+static uint32_t fast_ks(uint32_t all_rows) {
+    return all_rows >= 32768u ? 1u : all_rows >= 8192u ? 2u : 4u;
+}
+
+uint32_t mynah_gemv_group_tiles(uint32_t rows, uint32_t all_rows) {
+    const uint32_t tile_rows = gemv_order == MYNAH_GEMV_EXACT ? 64u : 32u / fast_ks(all_rows);
+    return (rows + tile_rows - 1u) / tile_rows;
+}
+
+/* The grouped GEMV in the current order: exact (64-row tiles, W waves
+ * splitting the units) or reordered (32-row tiles of 4 waves, x in LDS). */
+int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream) {
+    if (grp->n == 0 || grp->n > MYNAH_GROUP_MAX) {
+        mynah_set_error("group of %u matrices", grp->n);
+        return -1;
+    }
+    const int exact = gemv_order == MYNAH_GEMV_EXACT;
+    /* Reordered: KS waves split the super-blocks of an 8-row tile; small
+     * launches use KS = 4 for more waves in flight, large ones KS = 1. */
+    uint32_t all_rows = 0;
+    for (uint32_t i = 0; i < grp->n; i++) all_rows += grp->d[i].rows;
+    const uint32_t ks = fast_ks(all_rows);
+    const uint32_t tile_rows = exact ? 64u : 32u / ks;
+    uint32_t tiles = 0, max_units = 1;
+    size_t lds = 0;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        mynah_gemv_desc *g = &grp->d[i];
+        size_t need = 0;
+        if (!exact) {
+            if (g->cols % 8 != 0 || ((uintptr_t)g->x & 15u) != 0 ||
+                ((uintptr_t)g->norm_w & 15u) != 0) {
+                mynah_set_error("reordered GEMV needs 16-byte aligned x and cols %% 8 == 0");
+                return -1;
+            }
+            need = ((size_t)g->cols + g->cols / 16 + g->cols / 8) * 4;
+        } else if (g->norm_w != NULL) {
+            need = (size_t)g->cols * 4;
+        }
+        if (need > lds) lds = need;
+        g->tile0 = tiles;
+        tiles += (g->rows + tile_rows - 1u) / tile_rows;
+        const uint32_t u = g->w2 ? 2u * g->units : g->units;
+        if (u > max_units) max_units = u;
+    }
+    if (lds > 56u * 1024u) {
+        mynah_set_error("input of this GEMV exceeds the LDS budget (%zu B)", lds);
+        return -1;
+    }
+    void *args[] = {grp};
+    grp->pad = exact ? 0u : ks;
+    if (!exact) return mynah_launch(d, MYNAH_K_GEMV_FAST_GROUP, tiles, 1, 256, lds, stream, args);
+    const uint32_t per_wave = (max_units + 15u) / 16u;
+    const uint32_t waves = (max_units + per_wave - 1u) / per_wave;
+    return mynah_launch(d, MYNAH_K_GEMV_GROUP, tiles, 1, 64u * waves, lds, stream, args);
 }
 
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,

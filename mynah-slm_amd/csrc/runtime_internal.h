@@ -12,21 +12,19 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
 
 /* Every kernel of the embedded code object: id and symbol name. */
 #define MYNAH_KERNEL_LIST(X)                          \
-    X(MYNAH_K_Q4K_R1, "mynah_q4k_gemv_r1")            \
-    X(MYNAH_K_Q4K_R2, "mynah_q4k_gemv_r2")            \
-    X(MYNAH_K_Q4K_R4, "mynah_q4k_gemv_r4")            \
-    X(MYNAH_K_Q6K_R1, "mynah_q6k_gemv_r1")            \
-    X(MYNAH_K_Q6K_R2, "mynah_q6k_gemv_r2")            \
-    X(MYNAH_K_Q6K_R4, "mynah_q6k_gemv_r4")            \
-    X(MYNAH_K_Q80_R1, "mynah_q80_gemv_r1")            \
-    X(MYNAH_K_Q80_R2, "mynah_q80_gemv_r2")            \
-    X(MYNAH_K_Q80_R4, "mynah_q80_gemv_r4")            \
     X(MYNAH_K_DEQUANT, "mynah_dequant")                 \
     X(MYNAH_K_Q4K_EXACT, "mynah_q4k_gemv_exact")        \
     X(MYNAH_K_Q6K_EXACT, "mynah_q6k_gemv_exact")        \
     X(MYNAH_K_Q80_EXACT, "mynah_q80_gemv_exact")        \
     X(MYNAH_K_Q4K_EXACT_SEQ, "mynah_q4k_gemv_exact_seq") \
-    X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq")
+    X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq") \
+    X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
+    X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
+    X(MYNAH_K_ATTN_SCORES, "mynah_attn_scores")        \
+    X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
+    X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
+    X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
+    X(MYNAH_K_EMBED, "mynah_embed_row")
 
 enum {
 #define X(id, name) id,
@@ -61,5 +59,34 @@ int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, 
                          float *y, hipStream_t stream);
 int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                         const float *x, float *y, size_t tokens, hipStream_t stream);
+
+/* Host mirror of the grouped exact GEMV launch (gemv_exact.hip GemvGroup). */
+#define MYNAH_GROUP_MAX 8
+typedef struct {
+    const void *w, *w2;
+    const float *x;
+    float *y;
+    const float *res;
+    const uint32_t *ypos;
+    const float *norm_w;     /* input = RMSNorm(x) * norm_w when set */
+    unsigned long long *keys; /* one argmax key per workgroup tile when set */
+    uint32_t ystride, rows, units, row_bytes, type, tile0, cols;
+    float eps;
+    uint32_t pad;
+} mynah_gemv_desc;
+
+typedef struct {
+    uint32_t n, pad;
+    mynah_gemv_desc d[MYNAH_GROUP_MAX];
+} mynah_gemv_group;
+
+/* Fill tile0 and launch. Each desc needs w, x, y, rows, type and (from
+ * cols) units / row_bytes, which mynah_gemv_desc_init sets. */
+int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
+                         const float *x, float *y);
+int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream);
+/* Tiles (workgroups) the group launch will use for a descriptor of `rows`
+ * rows under the current order (the length of its argmax key array). */
+uint32_t mynah_gemv_group_tiles(uint32_t rows, uint32_t all_rows);
 
 #endif

@@ -21,6 +21,18 @@ _P = C.c_void_p
 _SZ = C.c_size_t
 
 
+class Qwen3Shape(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_layers", "d_model", "d_ff", "n_heads", "n_kv_heads",
+                                          "head_dim", "vocab")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class SynthTensor(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("type", C.c_int), ("rank", C.c_uint32),
+                ("rows", C.c_uint64), ("cols", C.c_uint64), ("offset", C.c_uint64),
+                ("nbytes", C.c_uint64)]
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -60,6 +72,20 @@ def _load() -> C.CDLL:
         "mynah_synth_uniform_u32": (C.c_int, [C.c_uint64, _SZ, C.c_uint32, _P]),
         "mynah_synth_substream": (C.c_uint64, [C.c_uint64, C.c_uint64]),
         "mynah_synth_f32_to_f16": (C.c_uint16, [C.c_float]),
+        "mynah_synth_qwen3_layout": (C.c_int, [C.POINTER(Qwen3Shape), C.POINTER(SynthTensor), _SZ,
+                                               C.POINTER(_SZ), C.POINTER(C.c_uint64)]),
+        "mynah_synth_qwen3_fill": (C.c_int, [C.POINTER(Qwen3Shape), C.c_uint64,
+                                             C.POINTER(SynthTensor), _SZ, _P, C.c_int]),
+        "mynah_hip_qwen3_new": (_P, [C.POINTER(Qwen3Shape), C.POINTER(SynthTensor), _SZ, _P,
+                                     C.c_uint64, C.c_uint32, C.c_char_p, _SZ]),
+        "mynah_hip_qwen3_free": (None, [_P]),
+        "mynah_hip_qwen3_reset": (None, [_P]),
+        "mynah_hip_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
+        "mynah_hip_qwen3_generate": (C.c_int, [_P, C.c_uint32, C.c_uint32, _P,
+                                               C.POINTER(C.c_float)]),
+        "mynah_hip_qwen3_set_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
+        "mynah_hip_qwen3_n_past": (C.c_uint32, [_P]),
+        "mynah_hip_qwen3_uses_graph": (C.c_int, [_P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -218,5 +244,83 @@ class Event:
     def __del__(self):
         try:
             lib.mynah_hip_event_destroy(self.p)
+        except Exception:
+            pass
+
+
+# ── random-init Qwen3 and the resident decoder ──────────────────────────────
+
+class SynthQwen3:
+    """Tensor table + host blob of a random-init Qwen3 (include/mynah_synth.h)."""
+
+    def __init__(self, shape, seed: int = 0):
+        self.shape = shape
+        self.c_shape = Qwen3Shape(shape.n_layers, shape.d_model, shape.d_ff, shape.n_heads,
+                                  shape.n_kv_heads, shape.head_dim, shape.vocab, shape.rms_eps,
+                                  shape.rope_theta)
+        count, total = _SZ(0), C.c_uint64(0)
+        lib.mynah_synth_qwen3_layout(C.byref(self.c_shape), None, 0, C.byref(count), C.byref(total))
+        self.table = (SynthTensor * count.value)()
+        if lib.mynah_synth_qwen3_layout(C.byref(self.c_shape), self.table, count.value,
+                                        C.byref(count), C.byref(total)) != 0:
+            raise ValueError("bad Qwen3 shape")
+        self.count = count.value
+        self.blob = np.empty(total.value, np.uint8)
+        if lib.mynah_synth_qwen3_fill(C.byref(self.c_shape), seed, self.table, self.count,
+                                      ptr(self.blob), 0) != 0:
+            raise ValueError("synthesis failed")
+
+    def weight_bytes(self) -> int:
+        return int(sum(self.table[i].nbytes for i in range(self.count)))
+
+
+class Qwen3Decoder:
+    """The GPU decode state (include/mynah_decode.h) over a SynthQwen3."""
+
+    def __init__(self, model: SynthQwen3, n_ctx: int):
+        err = C.create_string_buffer(512)
+        self.model = model
+        self.h = lib.mynah_hip_qwen3_new(C.byref(model.c_shape), model.table, model.count,
+                                         ptr(model.blob), model.blob.nbytes, n_ctx, err, 512)
+        if not self.h:
+            raise HipError(f"qwen3_new: {err.value.decode()}")
+
+    def set_kv(self, k: np.ndarray, v: np.ndarray, n_pos: int) -> None:
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        check(lib.mynah_hip_qwen3_set_kv(self.h, ptr(k), ptr(v), n_pos), "set_kv")
+
+    def forward(self, token: int, want_logits: bool = True):
+        logits = np.empty(self.model.shape.vocab, np.float32) if want_logits else None
+        check(lib.mynah_hip_qwen3_forward(self.h, token, ptr(logits) if want_logits else None),
+              "forward")
+        return logits
+
+    def generate(self, first: int, steps: int):
+        out = np.empty(steps, np.uint32)
+        ms = C.c_float(0.0)
+        check(lib.mynah_hip_qwen3_generate(self.h, first, steps, ptr(out), C.byref(ms)),
+              "generate")
+        return [int(t) for t in out], float(ms.value)
+
+    @property
+    def n_past(self) -> int:
+        return int(lib.mynah_hip_qwen3_n_past(self.h))
+
+    @property
+    def uses_graph(self) -> bool:
+        return bool(lib.mynah_hip_qwen3_uses_graph(self.h))
+
+    def reset(self) -> None:
+        lib.mynah_hip_qwen3_reset(self.h)
+
+    def close(self) -> None:
+        if self.h:
+            lib.mynah_hip_qwen3_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass

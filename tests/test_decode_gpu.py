@@ -1,0 +1,139 @@
+"""GPU parity of the resident Qwen3 decode step (configs[2] and a tiny model).
+
+The GEMVs are bit-exact and the f32 operators follow the reference operation
+for operation, so the logits agree with the oracle (bit-identical to the
+compiled reference decoder) to |gpu - ref| / max(1, |ref|) <= 1e-4 — the only
+differences are last-bit expf results and the order of double sums — and
+the greedy token ids equal the golden ids the compiled reference produced.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import configs as CF
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def M():
+    import mynah_amd
+    mynah_amd.check(mynah_amd.lib.mynah_hip_init(0), "init")
+    mynah_amd.check(mynah_amd.lib.mynah_hip_set_gemv_order(0), "order")
+    O.orc.orc_threads_init(0)
+    return mynah_amd
+
+
+def rel_err(got, ref):
+    return float((np.abs(got.astype(np.float64) - ref) / np.maximum(1.0, np.abs(ref))).max())
+
+
+def setup(M, shape, n_prefill, steps):
+    print(f"[case] decode layers={shape.n_layers} d={shape.d_model} prefill={n_prefill}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, n_prefill)
+    first = O.first_token(0, shape.vocab)
+    n_ctx = n_prefill + steps + 1
+    dec = M.Qwen3Decoder(model, n_ctx)
+    dec.set_kv(k, v, n_prefill)
+    return model, k, v, first, n_ctx, dec
+
+
+def test_tiny_logits_and_tokens(M):
+    g = np.load(os.path.join(GOLDEN, "qwen3_tiny.npz"), allow_pickle=False)
+    shape, npre, steps = CF.QWEN3_TINY, 16, int(g["tokens"].size)
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    assert first == int(g["first"])
+    lg = dec.forward(first)
+    assert rel_err(lg, g["logits0"]) <= TOL
+    assert int(np.argmax(lg)) == int(g["tokens"][0])
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    toks, _ = dec.generate(first, steps)
+    assert toks == [int(t) for t in g["tokens"]]
+
+
+def test_tiny_every_step_against_oracle(M):
+    """Logits of every step, fed the same tokens, against the oracle."""
+    shape, npre, steps = CF.QWEN3_TINY, 16, 12
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    orc_model = O.SynthModel(shape, 0)
+    assert np.array_equal(orc_model.blob, model.blob)
+    ref = O.OracleQwen3(orc_model, n_ctx)
+    ref.prefill_kv(k, v, npre)
+    tok = first
+    for i in range(steps):
+        a = dec.forward(tok)
+        b = ref.forward(tok)
+        err = rel_err(a, b)
+        print(f"step {i}: max rel err {err:.2e}, bit-equal {np.array_equal(a.view(np.uint32), b.view(np.uint32))}")
+        assert err <= TOL
+        tok = int(np.argmax(b))
+
+
+def test_graph_replay_equals_step_by_step(M):
+    shape, npre, steps = CF.QWEN3_TINY, 8, 10
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    toks, _ = dec.generate(first, steps)
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    tok, stepwise = first, []
+    for _ in range(steps):
+        lg = dec.forward(tok)
+        tok = int(np.argmax(lg))      # first maximum, like the reference sampler
+        stepwise.append(tok)
+    assert stepwise == toks
+
+
+def test_context_exhaustion_returns_error(M):
+    shape = CF.QWEN3_TINY
+    model = M.SynthQwen3(shape, 0)
+    dec = M.Qwen3Decoder(model, 3)
+    for _ in range(3):
+        dec.forward(1, want_logits=False)
+    assert M.lib.mynah_hip_qwen3_forward(dec.h, 1, None) == -1
+    assert b"context" in M.lib.mynah_hip_last_error()
+
+
+def test_qwen3_06b_64_greedy_steps(M):
+    g = np.load(os.path.join(GOLDEN, "qwen3_06b.npz"), allow_pickle=False)
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    assert first == int(g["first"])
+    lg = dec.forward(first)
+    top = np.argsort(-lg, kind="stable")[:64]
+    assert list(top[:8]) == [int(t) for t in g["top_ids"][:8]]
+    assert rel_err(lg[g["top_ids"]], g["top_vals"]) <= TOL
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    toks, ms = dec.generate(first, steps)
+    print(f"0.6B decode: {steps} steps in {ms:.2f} ms = {steps / ms * 1e3:.0f} tok/s, "
+          f"graph={dec.uses_graph}")
+    assert toks == [int(t) for t in g["tokens"]]
+
+
+def test_fast_order_same_tokens(M):
+    """The reordered GEMV order: logits differ from the reference only by f32
+    rounding of the sums; the 64 greedy tokens are the reference's."""
+    g = np.load(os.path.join(GOLDEN, "qwen3_06b.npz"), allow_pickle=False)
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
+    M.check(M.lib.mynah_hip_set_gemv_order(1), "order")
+    try:
+        model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+        lg = dec.forward(first)
+        err = rel_err(lg[g["top_ids"]], g["top_vals"])
+        print(f"reordered: top-64 logits max rel err {err:.2e}")
+        assert err <= 1e-3
+        dec.reset()
+        dec.set_kv(k, v, npre)
+        toks, ms = dec.generate(first, steps)
+        print(f"0.6B decode (reordered GEMVs): {steps / ms * 1e3:.0f} tok/s")
+        assert toks == [int(t) for t in g["tokens"]]
+    finally:
+        M.check(M.lib.mynah_hip_set_gemv_order(0), "order")
