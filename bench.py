@@ -42,69 +42,38 @@ def algorithmic_bytes(m) -> int:
     return m.rows * M.row_bytes(m.qtype, m.cols) + 4 * m.cols + 4 * m.rows
 
 
-class Resident:
-    """Device copies of one matrix plus its x and y."""
-
-    def __init__(self, M, m, w, x, copies: int):
-        self.m = m
-        self.w = [M.DeviceBuffer.from_array(w) for _ in range(copies)]
-        self.x = M.DeviceBuffer.from_array(x)
-        self.y = M.DeviceBuffer(4 * m.rows)
-
-    def launch(self, M, step: int) -> None:
-        w = self.w[step % len(self.w)]
-        M.matvec_dev(self.m.qtype, w.ptr, self.m.rows, self.m.cols, self.x.ptr, self.y.ptr)
+def upload_copies(M, w, copies: int):
+    return [M.DeviceBuffer.from_array(w) for _ in range(copies)]
 
 
 def gpu_sweep(M, CF, steps: int, warmup: int):
+    """configs[1] sweep launched from C (no Python between launches)."""
     mats = CF.C2
-    inputs = []
-    for i, m in enumerate(mats):
-        ws, xs = CF.matrix_seeds(M.substream, 0, i)
-        inputs.append((M.synth_blocks(m.qtype, ws, m.rows, m.cols), M.synth_normal(xs, m.cols)))
     step_bytes = sum(algorithmic_bytes(m) for m in mats)
     copies = max(2, -(-2 * MALL_BYTES // step_bytes))
-    res = [Resident(M, m, w, x, copies) for m, (w, x) in zip(mats, inputs)]
+    ws, xs, ys = [], [], []
+    for i, m in enumerate(mats):
+        wseed, xseed = CF.matrix_seeds(M.substream, 0, i)
+        ws.append(upload_copies(M, M.synth_blocks(m.qtype, wseed, m.rows, m.cols), copies))
+        xs.append(M.DeviceBuffer.from_array(M.synth_normal(xseed, m.cols)))
+        ys.append(M.DeviceBuffer(4 * m.rows))
     head = len(mats) - 1
     assert mats[head].rows == 151936
+    w_ptrs = [b.ptr for copies_of in ws for b in copies_of]
+    x_ptrs, y_ptrs = [b.ptr for b in xs], [b.ptr for b in ys]
+    M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, max(1, warmup), -1)
+    total_ms, head_total = M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, steps, head)
+    head_ms = head_total / steps
 
-    for s in range(warmup):
-        for r in res:
-            r.launch(M, s)
-    M.sync()
-
-    start, end = M.Event(), M.Event()
-    hs = [(M.Event(), M.Event()) for _ in range(steps)]
-    start.record()
-    for s in range(steps):
-        for i, r in enumerate(res):
-            if i == head:
-                hs[s][0].record()
-                r.launch(M, s)
-                hs[s][1].record()
-            else:
-                r.launch(M, s)
-    end.record()
-    M.sync()
-    total_ms = start.elapsed_ms(end)
-    head_ms = sum(a.elapsed_ms(b) for a, b in hs) / steps
-
-    # Per-matrix averages, each timed alone over rotating copies (outside the
-    # timed region above; reported for the per-shape view).
+    # Per-matrix averages, each matrix alone over its rotating copies.
     per = {}
-    for r in res:
-        a, b = M.Event(), M.Event()
-        n = 4 * copies
-        a.record()
-        for s in range(n):
-            r.launch(M, s)
-        b.record()
-        M.sync()
-        ms = a.elapsed_ms(b) / n
-        per[r.m.name] = round(algorithmic_bytes(r.m) / (ms * 1e-3) / 1e9, 1)
-    for r in res:
-        for w in r.w:
-            w.free()
+    for i, m in enumerate(mats):
+        n = 8 * copies
+        ms = M.time_matvec(m.qtype, [b.ptr for b in ws[i]], m.rows, m.cols, x_ptrs[i],
+                           y_ptrs[i], n) / n
+        per[m.name] = round(algorithmic_bytes(m) / (ms * 1e-3) / 1e9, 1)
+    for b in [b for c in ws for b in c] + xs + ys:
+        b.free()
     return step_bytes, copies, total_ms, head_ms, algorithmic_bytes(mats[head]), per
 
 
@@ -112,24 +81,50 @@ def gpu_4b_classes(M, CF, launches: int = 64):
     """GB/s of each Qwen3-4B GEMV class, rotating copies totalling > 2x MALL."""
     out = {}
     for i, m in enumerate(CF.QWEN3_4B_GEMV):
-        w = M.synth_blocks(m.qtype, 1000 + i, m.rows, m.cols)
-        x = M.synth_normal(2000 + i, m.cols)
+        wseed, xseed = CF.matrix_seeds(M.substream, 4, i)
         nbytes = algorithmic_bytes(m)
         copies = max(2, -(-2 * MALL_BYTES // nbytes))
-        r = Resident(M, m, w, x, copies)
-        for s in range(copies):
-            r.launch(M, s)
-        n = max(launches, copies)
-        a, b = M.Event(), M.Event()
-        a.record()
-        for s in range(n):
-            r.launch(M, s)
-        b.record()
-        M.sync()
-        ms = a.elapsed_ms(b) / n
+        w = upload_copies(M, M.synth_blocks(m.qtype, wseed, m.rows, m.cols), copies)
+        x = M.DeviceBuffer.from_array(M.synth_normal(xseed, m.cols))
+        y = M.DeviceBuffer(4 * m.rows)
+        ptrs = [b.ptr for b in w]
+        n = max(launches, 4 * copies)
+        M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies)
+        ms = M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, n) / n
         out[m.name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
-        for buf in r.w:
-            buf.free()
+        for b in w + [x, y]:
+            b.free()
+    return out
+
+
+def gpu_decode(M, CF):
+    """Qwen3-0.6B batch-1 greedy decode, 512 prefilled positions,
+    64 steps, in both GEMV orders; tokens checked against the golden ids the
+    compiled reference produced."""
+    import numpy as np
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
+    model = M.SynthQwen3(shape, 0)
+    k, v = CF.kv_prefill(M.substream, M.synth_normal, shape, 0, npre)
+    first = M.first_token(0, shape.vocab)
+    golden = np.load(os.path.join(ROOT, "tests", "golden", "qwen3_06b.npz"), allow_pickle=False)
+    want = [int(t) for t in golden["tokens"]]
+    out = {"model": "Qwen3-0.6B random-init Q4_K_M mix", "prefill": npre, "steps": steps,
+           "weight_bytes": model.weight_bytes()}
+    old = M.lib.mynah_hip_gemv_order()
+    try:
+        for order, name in ((0, "exact"), (1, "reordered")):
+            M.check(M.lib.mynah_hip_set_gemv_order(order), "order")
+            dec = M.Qwen3Decoder(model, npre + steps + 1)
+            dec.set_kv(k, v, npre)
+            dec.generate(first, 4)                       # warm-up and graph capture
+            dec.reset()
+            dec.set_kv(k, v, npre)
+            toks, ms = dec.generate(first, steps)
+            out[name] = {"tok_s": round(steps / ms * 1e3, 1), "ms_per_token": round(ms / steps, 4),
+                         "tokens_match_reference": toks == want, "graph": dec.uses_graph}
+            dec.close()
+    finally:
+        M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
     return out
 
 
@@ -163,6 +158,26 @@ def cpu_baseline(CF, seconds: float = 10.0):
                       f"4*nth row chunks on {threads} threads"}
 
 
+def pmc_probe(M, CF, launches: int = 8) -> None:
+    """A short program for rocprofv3 --pmc runs: `launches` head GEMVs over two
+    weight copies in the current GEMV order, then four 256 MiB device copies
+    (mynah_copy16) whose known bytes calibrate FETCH_SIZE / WRITE_SIZE."""
+    m = CF.C2[-1]
+    wseed, xseed = CF.matrix_seeds(M.substream, 0, len(CF.C2) - 1)
+    w = upload_copies(M, M.synth_blocks(m.qtype, wseed, m.rows, m.cols), 2)
+    x = M.DeviceBuffer.from_array(M.synth_normal(xseed, m.cols))
+    y = M.DeviceBuffer(4 * m.rows)
+    M.time_matvec(m.qtype, [b.ptr for b in w], m.rows, m.cols, x.ptr, y.ptr, launches)
+    nbytes = 256 << 20
+    a, b = M.DeviceBuffer(nbytes), M.DeviceBuffer(nbytes)
+    M.check(M.lib.mynah_hip_memset(a.ptr, 1, nbytes), "memset")
+    for _ in range(4):
+        M.copy_dev(b.ptr, a.ptr, nbytes)
+    M.sync()
+    log(f"[pmc-probe] {launches} head launches ({algorithmic_bytes(m)} algorithmic bytes each), "
+        f"4 copies of {nbytes} bytes (mynah_copy16)")
+
+
 def traffic_for(name: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
@@ -176,11 +191,16 @@ def traffic_for(name: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-4b", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the configs[2] decode section, printed as one JSON line")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only the head GEMV + calibration copies, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported here "
@@ -191,6 +211,12 @@ def main() -> int:
     import mynah_amd as M
     M.check(M.lib.mynah_hip_init(0), "init")
     order = M.lib.mynah_hip_gemv_order()
+    if args.pmc_probe:
+        pmc_probe(M, CF)
+        return 0
+    if args.decode_only:
+        print(json.dumps({"decode": gpu_decode(M, CF)}), flush=True)
+        return 0
 
     log("[bench] configs[1] sweep")
     step_bytes, copies, total_ms, head_ms, head_bytes, per = gpu_sweep(M, CF, args.steps,
@@ -198,6 +224,11 @@ def main() -> int:
     ms_per_step = total_ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = head_bytes / (head_ms * 1e-3) / 1e9
+
+    decode = None
+    if not args.no_decode:
+        log("[bench] configs[2] decode")
+        decode = gpu_decode(M, CF)
 
     extra_4b = None
     if not args.no_4b:
@@ -230,7 +261,8 @@ def main() -> int:
             "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": "mynah_q6k_gemv_exact (151936x1024 head)",
+            "kernel": ("mynah_q6k_gemv_exact" if order == 0 else "mynah_gemv_fast_group")
+                      + " (Q6_K 151936x1024 head)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
@@ -241,6 +273,7 @@ def main() -> int:
             "avg_launch_ms": round(head_ms, 5),
         },
         "cpu_baseline": cpu,
+        "decode": decode,
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
     }

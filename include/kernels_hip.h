@@ -126,6 +126,9 @@ int   mynah_hip_h2d(void *dst, const void *src, size_t bytes);
 int   mynah_hip_d2h(void *dst, const void *src, size_t bytes);
 int   mynah_hip_memset(void *dst, int value, size_t bytes);
 int   mynah_hip_sync(void *stream);
+/* Device-to-device copy by a plain 16-byte-vector kernel (buffers 16-byte
+ * aligned, bytes a multiple of 16); the yardstick of the HBM counters. */
+int   mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 void *mynah_hip_stream(void);           /* the library's own stream */
 
 /* HIP events on a stream (NULL = the library's stream), for timing kernels
@@ -134,6 +137,16 @@ void *mynah_hip_event_create(void);
 int   mynah_hip_event_record(void *event, void *stream);
 int   mynah_hip_event_elapsed(void *start, void *end, float *ms);
 int   mynah_hip_event_destroy(void *event);
+
+/* Benchmark helper for a sweep of n matrices: `steps` passes, pass i
+ * launching matrix m on weight copy w[m * copies + i % copies] (all copies of
+ * one matrix share x[m] and y[m]). Launched from C on the library stream and
+ * timed with HIP events: *ms_total for all passes, and *ms_timed the summed
+ * duration of matrix `timed`'s launches (events around each). */
+int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copies,
+                         const size_t *rows, const size_t *cols, const float *const *x,
+                         float *const *y, int steps, int timed, float *ms_total,
+                         float *ms_timed);
 
 /* Benchmark helper: `iters` launches of the matvec, cycling through the
  * `n_copies` weight copies in w_copies[] (to stream from HBM rather than

@@ -86,3 +86,17 @@ PREFILL_X_INDEX = 1 << 22
 def matrix_seeds(substream, config_seed: int, i: int) -> tuple[int, int]:
     """(weight seed, activation seed) of matrix i of a config."""
     return substream(config_seed, 2 * i), substream(config_seed, 2 * i + 1)
+
+
+def kv_prefill(substream, normal, shape: Qwen3Shape, config_seed: int, n: int):
+    """K and V prefill [layer][n][kv_dim] f32 of a decode config (N(0, 1));
+    `normal(seed, count)` is the shared generator's f32 normal vector."""
+    import numpy as np
+    kv_seed = substream(config_seed, KV_SEED_INDEX)
+    kvd = shape.n_kv_heads * shape.head_dim
+    k = np.empty((shape.n_layers, n * kvd), np.float32)
+    v = np.empty((shape.n_layers, n * kvd), np.float32)
+    for layer in range(shape.n_layers):
+        k[layer] = normal(substream(kv_seed, 2 * layer), n * kvd)
+        v[layer] = normal(substream(kv_seed, 2 * layer + 1), n * kvd)
+    return k, v

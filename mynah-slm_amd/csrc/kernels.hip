@@ -6,3 +6,4 @@
 #include "gemv_exact.hip"
 #include "gemv_fast.hip"
 #include "decode.hip"
+#include "copy.hip"

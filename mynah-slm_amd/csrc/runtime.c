@@ -633,6 +633,22 @@ int mynah_hip_memset(void *dst, int value, size_t bytes) {
     return 0;
 }
 
+int mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (dst == NULL || src == NULL || bytes == 0 || bytes % 16 != 0 ||
+        ((uintptr_t)dst & 15u) != 0 || ((uintptr_t)src & 15u) != 0) {
+        mynah_set_error("copy needs 16-byte aligned buffers and a multiple of 16 bytes");
+        return -1;
+    }
+    uint64_t n16 = bytes / 16;
+    uint64_t want = (n16 + 255) / 256;
+    unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+    void *args[] = {&src, &dst, &n16};
+    return mynah_launch(d, MYNAH_K_COPY16, grid, 1, 256, 0, mynah_stream_or_default(d, stream),
+                        args);
+}
+
 int mynah_hip_sync(void *stream) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;
@@ -701,4 +717,50 @@ int mynah_hip_event_elapsed(void *start, void *end, float *ms) {
 int mynah_hip_event_destroy(void *event) {
     HIP_OK(hipEventDestroy((hipEvent_t)event), "hipEventDestroy");
     return 0;
+}
+
+int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copies,
+                         const size_t *rows, const size_t *cols, const float *const *x,
+                         float *const *y, int steps, int timed, float *ms_total,
+                         float *ms_timed) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (n <= 0 || copies <= 0 || steps <= 0 || types == NULL || w == NULL || rows == NULL ||
+        cols == NULL || x == NULL || y == NULL || ms_total == NULL || ms_timed == NULL ||
+        timed >= n) {
+        mynah_set_error("bad sweep arguments");
+        return -1;
+    }
+    hipEvent_t a = NULL, b = NULL;
+    hipEvent_t *ev = (hipEvent_t *)calloc((size_t)2 * steps, sizeof *ev);
+    int rc = ev ? 0 : -1;
+    if (rc == 0 && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) rc = -1;
+    for (int i = 0; rc == 0 && timed >= 0 && i < 2 * steps; i++)
+        if (hipEventCreate(&ev[i]) != hipSuccess) rc = -1;
+    if (rc == 0 && hipEventRecord(a, d->stream) != hipSuccess) rc = -1;
+    for (int i = 0; rc == 0 && i < steps; i++) {
+        for (int m = 0; rc == 0 && m < n; m++) {
+            if (m == timed) (void)hipEventRecord(ev[2 * i], d->stream);
+            rc = mynah_gemv_launch(d, types[m], w[(size_t)m * copies + (size_t)(i % copies)],
+                                   rows[m], cols[m], x[m], y[m], d->stream);
+            if (m == timed) (void)hipEventRecord(ev[2 * i + 1], d->stream);
+        }
+    }
+    if (rc == 0 && (hipEventRecord(b, d->stream) != hipSuccess ||
+                    hipEventSynchronize(b) != hipSuccess ||
+                    hipEventElapsedTime(ms_total, a, b) != hipSuccess))
+        rc = -1;
+    *ms_timed = 0.0f;
+    for (int i = 0; rc == 0 && timed >= 0 && i < steps; i++) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = -1;
+        *ms_timed += t;
+    }
+    if (rc != 0 && mynah_hip_last_error()[0] == 0) mynah_set_error("sweep timing failed");
+    for (int i = 0; ev && timed >= 0 && i < 2 * steps; i++)
+        if (ev[i]) (void)hipEventDestroy(ev[i]);
+    free(ev);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    return rc;
 }

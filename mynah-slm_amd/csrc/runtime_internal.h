@@ -24,7 +24,8 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
-    X(MYNAH_K_EMBED, "mynah_embed_row")
+    X(MYNAH_K_EMBED, "mynah_embed_row")                \
+    X(MYNAH_K_COPY16, "mynah_copy16")
 
 enum {
 #define X(id, name) id,

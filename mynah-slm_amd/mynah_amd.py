@@ -65,6 +65,9 @@ def _load() -> C.CDLL:
         "mynah_hip_event_record": (C.c_int, [_P, _P]),
         "mynah_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
         "mynah_hip_event_destroy": (C.c_int, [_P]),
+        "mynah_hip_copy_dev": (C.c_int, [_P, _P, _SZ, _P]),
+        "mynah_hip_time_sweep": (C.c_int, [C.c_int, _P, _P, C.c_int, _P, _P, _P, _P, C.c_int,
+                                           C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mynah_hip_time_matvec": (C.c_int, [C.c_int, _P, C.c_int, _SZ, _SZ, _P, _P, C.c_int,
                                             C.POINTER(C.c_float)]),
         "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
@@ -216,6 +219,26 @@ def dequant_dev(qtype: int, w: int, rows: int, cols: int, y: int, stream=None) -
     check(lib.mynah_hip_dequant_dev(qtype, w, rows, cols, y, stream), "dequant_dev")
 
 
+def copy_dev(dst: int, src: int, nbytes: int, stream=None) -> None:
+    check(lib.mynah_hip_copy_dev(dst, src, nbytes, stream), "copy_dev")
+
+
+def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int):
+    """Time `steps` passes over mats (launched from C); returns (total ms,
+    summed ms of matrix `timed`). w_ptrs is [matrix][copy] flattened."""
+    n = len(mats)
+    types = (C.c_int * n)(*[m.qtype for m in mats])
+    rows = (C.c_size_t * n)(*[m.rows for m in mats])
+    cols = (C.c_size_t * n)(*[m.cols for m in mats])
+    w = (C.c_void_p * len(w_ptrs))(*w_ptrs)
+    x = (C.c_void_p * n)(*x_ptrs)
+    y = (C.c_void_p * n)(*y_ptrs)
+    tot, tim = C.c_float(0.0), C.c_float(0.0)
+    check(lib.mynah_hip_time_sweep(n, types, w, copies, rows, cols, x, y, steps, timed,
+                                   C.byref(tot), C.byref(tim)), "time_sweep")
+    return float(tot.value), float(tim.value)
+
+
 def time_matvec(qtype: int, w_ptrs, rows: int, cols: int, x: int, y: int, iters: int) -> float:
     arr = (C.c_void_p * len(w_ptrs))(*w_ptrs)
     ms = C.c_float(0.0)
@@ -324,3 +347,12 @@ class Qwen3Decoder:
             self.close()
         except Exception:
             pass
+
+
+def first_token(config_seed: int, vocab: int) -> int:
+    """The first decode token of a config (uniform over the vocabulary)."""
+    import configs
+    out = np.empty(1, np.uint32)
+    check(lib.mynah_synth_uniform_u32(substream(config_seed, configs.TOKEN_SEED_INDEX), 1, vocab,
+                                      ptr(out)), "uniform")
+    return int(out[0])

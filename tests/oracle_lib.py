@@ -240,15 +240,8 @@ class OracleQwen3:
 
 def kv_prefill(substream_fn, shape, config_seed: int, n: int):
     """K and V prefill tensors [layer][n][kv_dim] of a config (see configs.py)."""
-    from_idx = 1 << 20
-    kv_seed = substream_fn(config_seed, from_idx)
-    kvd = shape.n_kv_heads * shape.head_dim
-    k = np.empty((shape.n_layers, n * kvd), np.float32)
-    v = np.empty((shape.n_layers, n * kvd), np.float32)
-    for l in range(shape.n_layers):
-        k[l] = normal(substream_fn(kv_seed, 2 * l), n * kvd)
-        v[l] = normal(substream_fn(kv_seed, 2 * l + 1), n * kvd)
-    return k, v
+    import configs
+    return configs.kv_prefill(substream_fn, normal, shape, config_seed, n)
 
 
 def first_token(config_seed: int, vocab: int) -> int:
