@@ -261,7 +261,7 @@ def main() -> int:
             "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": ("mynah_q6k_gemv_exact" if order == 0 else "mynah_gemv_fast_group")
+            "kernel": ("mynah_gemv_group" if order == 0 else "mynah_gemv_fast_group")
                       + " (Q6_K 151936x1024 head)",
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -54,6 +54,8 @@ struct mynah_qwen3 {
     float *x, *h, *q, *attn, *act, *logits, *scores;
     uint32_t *counters;             /* token, pos, step */
     unsigned long long *keys;       /* head workgroups' argmax keys */
+    uint32_t n_keys;
+    uint32_t sstride;               /* floats between the score rows of two heads */
     uint32_t *tokens;               /* [n_ctx] generated ids */
     hipGraph_t graph;
     hipGraphExec_t exec;
@@ -126,9 +128,9 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
         return NULL;
     }
     if (c->n_kv_heads == 0 || c->n_heads % c->n_kv_heads != 0 ||
-        c->n_heads / c->n_kv_heads > 8 || c->head_dim != 128 ||
+        c->n_heads / c->n_kv_heads > 8 || c->n_heads / c->n_kv_heads < 2 || c->head_dim != 128 ||
         c->d_model % 256 != 0 || c->d_ff % 256 != 0 || c->vocab % 4 != 0 ||
-        (size_t)(c->n_heads / c->n_kv_heads) * n_ctx * 4 > 30 * 1024) {
+        n_ctx > 4096 || (size_t)(c->n_heads / c->n_kv_heads) * ((n_ctx + 63) & ~63u) * 4 > 48 * 1024) {
         fail(err, errsz, "unsupported shape", NULL);
         return NULL;
     }
@@ -210,9 +212,11 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->attn = (float *)dalloc((size_t)s->q_dim * 4, &ok);
     s->act = (float *)dalloc(ff * 4, &ok);
     s->logits = (float *)dalloc((size_t)c->vocab * 4, &ok);
-    s->scores = (float *)dalloc((size_t)c->n_heads * n_ctx * 4, &ok);
+    s->sstride = (n_ctx + 63) & ~63u;
+    s->scores = (float *)dalloc((size_t)c->n_heads * s->sstride * 4, &ok);
     s->counters = (uint32_t *)dalloc(16, &ok);
-    s->keys = (unsigned long long *)dalloc(((size_t)c->vocab / 8 + 64) * 8, &ok);
+    s->n_keys = c->vocab / 8 + 64;
+    s->keys = (unsigned long long *)dalloc((size_t)s->n_keys * 8, &ok);
     s->tokens = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
     if (!ok) {
         fail(err, errsz, "out of device memory for the state", NULL);
@@ -257,14 +261,8 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
     const mynah_qwen3_shape *c = &s->c;
     const size_t per_layer = (size_t)s->n_ctx * s->kv_dim;
     uint32_t *tok = TOKEN(s), *pos = POS(s), *step = STEP(s);
+    uint32_t head_tiles = 0;
     int rc = 0;
-    {
-        const unsigned char *tab = s->embed.dev;
-        float *x = s->x;
-        uint32_t dm = c->d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
-        void *args[] = {&tab, &tok, &x, &dm, &ty, &rb};
-        rc = mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, st, args);
-    }
     for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
         const dlayer *L = &s->layers[l];
         float *kl = s->k_cache + l * per_layer, *vl = s->v_cache + l * per_layer;
@@ -284,33 +282,33 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[1].ystride = s->kv_dim;
         g.d[2].ypos = pos;
         g.d[2].ystride = s->kv_dim;
-        rc = mynah_gemv_group_launch(d, &g, st);
+        rc = mynah_gemv_group_launch(d, &g, st, NULL);
         if (rc) break;
         {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;
             const float *rcos = s->rope_cos, *rsin = s->rope_sin;
             float *sc = s->scores;
-            uint32_t nctx = s->n_ctx, hd = c->head_dim, kvd = s->kv_dim;
+            uint32_t nctx = s->n_ctx, kvd = s->kv_dim, sstride = s->sstride;
             uint32_t group = c->n_heads / c->n_kv_heads;
             float eps = c->rms_eps, scale = s->scale;
-            void *args[] = {&q, &kl, &qn, &kn, &rcos, &rsin, &pos, &sc, &nctx, &hd, &kvd, &group,
-                            &eps, &scale};
-            rc = mynah_launch(d, MYNAH_K_ATTN_SCORES, c->n_kv_heads, (s->n_ctx + 63) / 64,
-                              64 * group, 0, st, args);
+            void *args[] = {&q, &kl, &qn, &kn, &rcos, &rsin, &pos, &sc, &nctx, &sstride, &kvd,
+                            &group, &eps, &scale};
+            rc = mynah_launch(d, MYNAH_K_ATTN_SCORES, c->n_kv_heads, (s->n_ctx + 15) / 16, 256, 0,
+                              st, args);
             if (rc) break;
             float *out = s->attn;
             const float *scc = s->scores;
-            void *args2[] = {&vl, &scc, &pos, &out, &nctx, &hd, &kvd, &group};
-            rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, hd / 16, 256,
-                              (size_t)group * s->n_ctx * 4, st, args2);
+            void *args2[] = {&vl, &scc, &pos, &out, &sstride, &kvd, &group};
+            rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, 64 * group,
+                              (size_t)group * sstride * 4, st, args2);
         }
         if (rc) break;
         memset(&g, 0, sizeof g);
         g.n = 1;
         rc = gemv_desc(&g.d[0], &L->wo, s->attn, s->x);
         g.d[0].res = s->x;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
         if (rc) break;
         memset(&g, 0, sizeof g);
         g.n = 1;
@@ -318,38 +316,51 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[0].w2 = L->up.dev;
         g.d[0].norm_w = (const float *)L->ffn_norm.dev;     /* src/arch_qwen3.c:226 */
         g.d[0].eps = c->rms_eps;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
         if (rc) break;
         memset(&g, 0, sizeof g);
         g.n = 1;
         rc = gemv_desc(&g.d[0], &L->down, s->act, s->x);
         g.d[0].res = s->x;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
-    }
-    if (rc == 0) {                                          /* src/arch_qwen3.c:239 */
-        const float *x = s->x, *w = (const float *)s->out_norm.dev;
-        float *h = s->h;
-        uint32_t n = c->d_model;
-        float eps = c->rms_eps;
-        void *args[] = {&x, &w, &h, &n, &eps};
-        rc = mynah_launch(d, MYNAH_K_RMSNORM, 1, 1, 1024, 0, st, args);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
     }
     if (rc == 0) {
+        /* The final norm (src/arch_qwen3.c:239) runs inside the head GEMV. */
         mynah_gemv_group g;
         memset(&g, 0, sizeof g);
         g.n = 1;
-        rc = gemv_desc(&g.d[0], &s->head, s->h, s->logits);
+        rc = gemv_desc(&g.d[0], &s->head, s->x, s->logits);
+        g.d[0].norm_w = (const float *)s->out_norm.dev;
+        g.d[0].eps = c->rms_eps;
         g.d[0].keys = s->keys;                               /* src/sampler.c:124-129 */
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles);
+        if (rc == 0 && head_tiles > s->n_keys) {
+            mynah_set_error("head launch of %u workgroups exceeds the key buffer", head_tiles);
+            rc = -1;
+        }
     }
     if (rc == 0) {
         const unsigned long long *keys = s->keys;
-        uint32_t n = mynah_gemv_group_tiles(c->vocab, c->vocab), maxs = s->n_ctx;
+        uint32_t n = head_tiles, maxs = s->n_ctx;
         uint32_t *toks = s->tokens;
-        void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs};
+        const unsigned char *tab = s->embed.dev;
+        float *x = s->x;
+        uint32_t dm = c->d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
+        void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs, &tab, &x, &dm, &ty, &rb};
         rc = mynah_launch(d, MYNAH_K_ARGMAX, 1, 1, 1024, 0, st, args);
     }
     return rc;
+}
+
+/* The embedding of the current token (device counter) into x: the start of a
+ * sequence of steps; every step's argmax embeds the token it picks. */
+static int embed_current(mynah_qwen3 *s, mynah_device *d) {
+    const unsigned char *tab = s->embed.dev;
+    uint32_t *tok = TOKEN(s);
+    float *x = s->x;
+    uint32_t dm = s->c.d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
+    void *args[] = {&tab, &tok, &x, &dm, &ty, &rb};
+    return mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, d->stream, args);
 }
 
 /* Capture the step once; fall back to direct launches if capture fails. */
@@ -410,7 +421,8 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
         mynah_set_error("token %u out of range", token);
         return -1;
     }
-    if (set_counters(s, d, token, 0) != 0 || run_step(s, d) != 0) return -1;
+    if (set_counters(s, d, token, 0) != 0 || embed_current(s, d) != 0 || run_step(s, d) != 0)
+        return -1;
     s->n_past++;
     if (logits && hipMemcpyAsync(logits, s->logits, (size_t)s->c.vocab * 4,
                                  hipMemcpyDeviceToHost, d->stream) != hipSuccess) {
@@ -445,6 +457,7 @@ int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_st
     }
     int rc = 0;
     if (ms) (void)hipEventRecord(a, d->stream);
+    rc = embed_current(s, d);
     for (uint32_t i = 0; i < n_steps && rc == 0; i++) rc = run_step(s, d);
     if (ms) (void)hipEventRecord(b, d->stream);
     if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {

@@ -50,161 +50,221 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
     }
 }
 
-// Attention scores for one key head and a chunk of 64 positions
-// (src/kernels.c:228-250 first loop, with src/arch_qwen3.c:209-218 folded in):
-// every thread first fetches its key row k_t into registers; then wave g
+// Attention scores for one key head and a chunk of SC_POS positions
+// (src/kernels.c:228-250 first loop, with src/arch_qwen3.c:209-218 folded in).
+// Lane (r, l) of wave w handles position t = t0 + 4 w + r and the dot-product
+// lane l of the reference's 8-wide FMA dot (src/kernels.c:39-62): it holds
+// k_t[16 j + l] for j = 0..7 and accumulates fma(q[16 j + l], k_t[16 j + l])
+// over j, which is s0[l] for l < 8 and s1[l - 8] otherwise; the 16 lanes of a
+// position then combine exactly as the reference does: tt = s0 + s1, v[l] =
+// tt[l] + tt[l + 4], dot = (v0 + v1) + (v2 + v3). Before that, wave g
 // normalises and rotates query head kvh * group + g into LDS, and the
 // workgroup whose chunk holds `pos` normalises and rotates the new key in the
 // cache slot (the only writer of that slot; its own score uses the rotated
-// key from LDS); then thread (g, j) computes dot(q, k_t) * scale for
-// t = chunk * 64 + j. Grid (n_kv_heads, ceil(n_ctx / 64)), block 64 * group;
-// group <= 8, hd == 128.
-extern "C" __global__ void __launch_bounds__(512)
+// key from LDS). Scores rows are `sstride` floats apart. Grid (n_kv_heads,
+// ceil(n_ctx / SC_POS)), block 256; group <= 8, hd == 128.
+#define SC_POS 16
+extern "C" __global__ void __launch_bounds__(256)
 mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
                   const float *__restrict__ q_norm, const float *__restrict__ k_norm,
                   const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
                   const uint32_t *__restrict__ pos_ptr, float *__restrict__ scores,
-                  uint32_t n_ctx, uint32_t hd, uint32_t kv_dim, uint32_t group, float eps,
+                  uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group, float eps,
                   float scale) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float qn[8][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
     __shared__ float tmp[9][128];
     const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
-    const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * 64u;
+    const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * SC_POS;
     if (t0 >= n_kv) return;
-    const uint32_t g = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t t = t0 + lane;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t r = lane >> 4, l = lane & 15u;
+    const uint32_t t = t0 + 4u * wave + r;
     const bool live = t < pos;                      // the new key is rotated below
-    float4 kr[32];
-    const float4 *krow = (const float4 *)(k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u);
+    const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
+    float kv[8];
 #pragma unroll
-    for (int i = 0; i < 32; i++) kr[i] = krow[i];
-    const uint32_t half = 64u;
-    const float *cs = rope_cos + (size_t)pos * half, *sn = rope_sin + (size_t)pos * half;
-    head_norm_rope(q + (size_t)(kvh * group + g) * 128u, qn[g], q_norm, cs, sn, 128u, eps, tmp[g]);
-    float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
-    if (g == 0 && pos < t0 + 64u) {
-        head_norm_rope(kpos, kn, k_norm, cs, sn, 128u, eps, tmp[8]);
-        __builtin_amdgcn_wave_barrier();
-        for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
+    for (int j = 0; j < 8; j++) kv[j] = krow[16 * j];
+    const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
+    const bool has_pos = pos < t0 + SC_POS;
+    const uint32_t ntask = group + (has_pos ? 1u : 0u);
+    for (uint32_t task = wave; task < ntask; task += 4u) {
+        if (task < group) {
+            head_norm_rope(q + (size_t)(kvh * group + task) * 128u, qn[task], q_norm, cs, sn, 128u,
+                           eps, tmp[task]);
+        } else {
+            float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
+            head_norm_rope(kpos, kn, k_norm, cs, sn, 128u, eps, tmp[8]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
+        }
     }
     __syncthreads();
     if (t < n_kv) {
         if (!live) {
 #pragma unroll
-            for (int i = 0; i < 32; i++) kr[i] = *(const float4 *)(kn + 4 * i);
+            for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
         }
-        float s0[8], s1[8];
+        for (uint32_t h = 0; h < group; h++) {
+            float acc = 0.0f;
 #pragma unroll
-        for (int l = 0; l < 8; l++) { s0[l] = 0.0f; s1[l] = 0.0f; }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float kv[16] = {kr[4 * j].x, kr[4 * j].y, kr[4 * j].z, kr[4 * j].w,
-                                  kr[4 * j + 1].x, kr[4 * j + 1].y, kr[4 * j + 1].z, kr[4 * j + 1].w,
-                                  kr[4 * j + 2].x, kr[4 * j + 2].y, kr[4 * j + 2].z, kr[4 * j + 2].w,
-                                  kr[4 * j + 3].x, kr[4 * j + 3].y, kr[4 * j + 3].z, kr[4 * j + 3].w};
-            const float *qq = qn[g] + 16 * j;
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                s0[l] = __builtin_fmaf(qq[l], kv[l], s0[l]);
-                s1[l] = __builtin_fmaf(qq[8 + l], kv[8 + l], s1[l]);
-            }
+            for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kv[j], acc);
+            const float tt = acc + __shfl_down(acc, 8, 16);
+            const float v = tt + __shfl_down(tt, 4, 16);
+            const float w = v + __shfl_down(v, 1, 16);
+            const float dot = w + __shfl_down(w, 2, 16);
+            if (l == 0) scores[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
         }
-        // src/kernels.c:56-62: lanes s0 + s1, halves, two pair-adds.
-        float tt[8], v[4];
-#pragma unroll
-        for (int l = 0; l < 8; l++) tt[l] = s0[l] + s1[l];
-#pragma unroll
-        for (int l = 0; l < 4; l++) v[l] = tt[l] + tt[l + 4];
-        const float dot = (v[0] + v[1]) + (v[2] + v[3]);
-        scores[(size_t)(kvh * group + g) * n_ctx + t] = dot * scale;
     }
 }
 
-// Softmax and weighted sum of V for one key head and 16 output dimensions
-// (src/kernels.c:207-220, 244-249): wave g % 4 turns the scores of query
-// head kvh * group + g into probabilities in LDS (f32 max, expf, double sum,
-// times the f32 reciprocal); the V columns stream through LDS in chunks of
-// AO_CH positions, double-buffered (the whole workgroup loads chunk c + 1
-// while the chain threads consume chunk c); thread (g, j) accumulates
-// o = fma(v_t[d], p_t, o) for t = 0 .. n_kv - 1 in order, d = 16 * chunk + j.
-// Grid (n_kv_heads, hd / 16), block 256; group <= 16; dynamic LDS group *
-// n_ctx floats.
-#define AO_CH 256
-extern "C" __global__ void __launch_bounds__(256)
+// Softmax and weighted sum of V for one key head and AO_DV = 8 output
+// dimensions (src/kernels.c:207-220, 244-249). Wave g turns the scores of
+// query head kvh * group + g into probabilities: the scores are loaded into
+// registers (lane l holds positions 4 l + 256 k .. + 3), then the f32 max,
+// expf, the double sum and the product with the f32 reciprocal of the sum,
+// and the probabilities land in LDS. The V slice (32 contiguous bytes of each
+// position: two lanes per row) streams through LDS, transposed to
+// dimension-major, in chunks of AO_CH positions, chunk c + 1 fetched into
+// registers while chunk c is consumed; lane j < AO_DV of wave g accumulates
+// o = fma(v_t[d], p_t, o) for t = 0 .. n_kv - 1 in order, d = AO_DV *
+// blockIdx.y + j. Scores rows are `sstride` floats apart (a multiple of 4).
+// Grid (n_kv_heads, hd / AO_DV), block 64 * group, group in 2..8; n_kv <= 64
+// * 4 * AO_SK; dynamic LDS group * sstride floats.
+#define AO_DV 8
+#define AO_CH 1024
+#define AO_SK 16
+#define AO_VR (AO_CH * 2 / 128)
+
+// Chunk c of the V slice: row t = c * AO_CH + (i >> 1), half i & 1, for
+// i = threadIdx.x + nthr * k (nthr = blockDim.x >= 128); only the passes
+// that hold rows below n_kv are issued.
+MYNAH_DEV void ao_fetch(float4 *vr, const float *vcol, uint32_t c, uint32_t n_kv, uint32_t kv_dim,
+                        uint32_t nthr) {
+    const uint32_t rows = n_kv - c * AO_CH < AO_CH ? n_kv - c * AO_CH : AO_CH;
+    const uint32_t npass = (2u * rows + nthr - 1u) / nthr;
+#pragma unroll
+    for (int k = 0; k < AO_VR; k++) {
+        if ((uint32_t)k < npass) {
+            const uint32_t i = threadIdx.x + nthr * (uint32_t)k;
+            const uint32_t r = i >> 1;
+            vr[k] = r < rows ? *(const float4 *)(vcol + (size_t)(c * AO_CH + r) * kv_dim + 4u * (i & 1u))
+                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+}
+
+MYNAH_DEV float ao_fma4(float4 v, float4 p, float o) {
+    o = __builtin_fmaf(v.x, p.x, o);
+    o = __builtin_fmaf(v.y, p.y, o);
+    o = __builtin_fmaf(v.z, p.z, o);
+    return __builtin_fmaf(v.w, p.w, o);
+}
+
+extern "C" __global__ void __launch_bounds__(512)
 mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scores,
-               const uint32_t *__restrict__ pos_ptr, float *__restrict__ out, uint32_t n_ctx,
-               uint32_t hd, uint32_t kv_dim, uint32_t group) {
+               const uint32_t *__restrict__ pos_ptr, float *__restrict__ out, uint32_t sstride,
+               uint32_t kv_dim, uint32_t group) {
 #pragma clang fp contract(off)
-    extern __shared__ float p_all[];
-    __shared__ __attribute__((aligned(16))) float vb[2][AO_CH][16];
+    extern __shared__ __attribute__((aligned(16))) float p_all[];
+    __shared__ __attribute__((aligned(16))) float vt[AO_DV][AO_CH + 4];
     const uint32_t n_kv = pos_ptr[0] + 1u;
     const uint32_t kvh = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    for (uint32_t gw = wave; gw < group; gw += 4u) {
-        const uint32_t h = kvh * group + gw;
-        float *p = p_all + (size_t)gw * n_ctx;
-        const float *sc = scores + (size_t)h * n_ctx;
-        float m = -__builtin_inff();
-        for (uint32_t t = lane; t < n_kv; t += 64) m = fmaxf(m, sc[t]);
+    const uint32_t nthr = blockDim.x;
+    const float *vcol = v_layer + (size_t)kvh * 128u + AO_DV * blockIdx.y;
+    const uint32_t nc = (n_kv + AO_CH - 1u) / AO_CH;
+    float4 vr[AO_VR];
+    ao_fetch(vr, vcol, 0, n_kv, kv_dim, nthr);
+
+    // Softmax of head g = wave, in registers; positions >= n_kv read as -inf
+    // (they leave the max alone and their exponential is 0).
+    float *p = p_all + (size_t)wave * sstride;
+    {
+        const float4 *sc = (const float4 *)(scores + (size_t)(kvh * group + wave) * sstride);
+        const uint32_t n4 = (n_kv + 3u) / 4u, kmax = (n4 + 63u) / 64u;
+        const float ninf = -__builtin_inff();
+        float4 sv[AO_SK];
+#pragma unroll
+        for (int k = 0; k < AO_SK; k++) {
+            if ((uint32_t)k < kmax) {
+                const uint32_t i = lane + 64u * (uint32_t)k, t = 4u * i;
+                float4 v = i < n4 ? sc[i] : make_float4(ninf, ninf, ninf, ninf);
+                if (t + 1u >= n_kv) v.y = ninf;
+                if (t + 2u >= n_kv) v.z = ninf;
+                if (t + 3u >= n_kv) v.w = ninf;
+                sv[k] = v;
+            }
+        }
+        float m = ninf;
+#pragma unroll
+        for (int k = 0; k < AO_SK; k++)
+            if ((uint32_t)k < kmax)
+                m = fmaxf(fmaxf(fmaxf(m, sv[k].x), fmaxf(sv[k].y, sv[k].z)), sv[k].w);
         m = wave_max_f(m);
         double acc = 0.0;
-        for (uint32_t t = lane; t < n_kv; t += 64) {
-            const float e = expf(sc[t] - m);
-            p[t] = e;
-            acc += (double)e;
+#pragma unroll
+        for (int k = 0; k < AO_SK; k++) {
+            if ((uint32_t)k < kmax) {
+                float4 e;
+                e.x = expf(sv[k].x - m);
+                e.y = expf(sv[k].y - m);
+                e.z = expf(sv[k].z - m);
+                e.w = expf(sv[k].w - m);
+                acc += (double)e.x;
+                acc += (double)e.y;
+                acc += (double)e.z;
+                acc += (double)e.w;
+                sv[k] = e;
+            }
         }
         const double sum = wave_sum_d(acc);
         const float inv = (float)(1.0 / sum);
-        for (uint32_t t = lane; t < n_kv; t += 64) p[t] = p[t] * inv;
+#pragma unroll
+        for (int k = 0; k < AO_SK; k++) {
+            if ((uint32_t)k < kmax) {
+                const uint32_t i = lane + 64u * (uint32_t)k;
+                const float4 e = sv[k];
+                if (i < n4)
+                    *(float4 *)(p + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+            }
+        }
     }
-    // Chunk loader: row r of the chunk (16 floats = 4 float4) -> vb.
-    const float *vcol = v_layer + (size_t)kvh * hd + 16u * blockIdx.y;
-    const uint32_t nc = (n_kv + AO_CH - 1u) / AO_CH;
-    float4 reg[4];
-    auto fetch = [&](uint32_t c) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t idx = threadIdx.x + 256u * (uint32_t)k;   // float4 index in the chunk
-            const uint32_t t = c * AO_CH + idx / 4u;
-            reg[k] = t < n_kv ? *(const float4 *)(vcol + (size_t)t * kv_dim + 4u * (idx % 4u))
-                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-    };
-    auto stash = [&](uint32_t buf) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t idx = threadIdx.x + 256u * (uint32_t)k;
-            *(float4 *)(&vb[buf][idx / 4u][4u * (idx % 4u)]) = reg[k];
-        }
-    };
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    const uint32_t g = threadIdx.x >> 4, j = threadIdx.x & 15u;
-    const bool chain = g < group;
-    const float *p = p_all + (size_t)(chain ? g : 0u) * n_ctx;
+
+    const bool chain = lane < AO_DV;
     float o = 0.0f;
     for (uint32_t c = 0; c < nc; c++) {
-        if (c + 1 < nc) fetch(c + 1);
+        const uint32_t tn = n_kv - c * AO_CH < AO_CH ? n_kv - c * AO_CH : AO_CH;
+        const uint32_t npass = (2u * tn + nthr - 1u) / nthr;
+#pragma unroll
+        for (int k = 0; k < AO_VR; k++) {
+            const uint32_t i = threadIdx.x + nthr * (uint32_t)k;
+            const uint32_t r = i >> 1, d = 4u * (i & 1u);
+            if ((uint32_t)k < npass && r < AO_CH) {
+                vt[d][r] = vr[k].x; vt[d + 1][r] = vr[k].y; vt[d + 2][r] = vr[k].z; vt[d + 3][r] = vr[k].w;
+            }
+        }
+        __syncthreads();
+        if (c + 1 < nc) ao_fetch(vr, vcol, c + 1, n_kv, kv_dim, nthr);
         if (chain) {
-            const uint32_t tn = n_kv - c * AO_CH < AO_CH ? n_kv - c * AO_CH : AO_CH;
-            const float *pc = p + c * AO_CH;
-            const uint32_t b = c & 1u;
+            const float *pc = p + c * AO_CH, *vc = vt[lane];
             uint32_t t = 0;
             for (; t + 16 <= tn; t += 16) {
-                float vv[16], pp[16];
+                float4 va[4], pa[4];
 #pragma unroll
-                for (int k = 0; k < 16; k++) { vv[k] = vb[b][t + k][j]; pp[k] = pc[t + k]; }
+                for (int k = 0; k < 4; k++) {
+                    va[k] = *(const float4 *)(vc + t + 4 * k);
+                    pa[k] = *(const float4 *)(pc + t + 4 * k);
+                }
 #pragma unroll
-                for (int k = 0; k < 16; k++) o = __builtin_fmaf(vv[k], pp[k], o);
+                for (int k = 0; k < 4; k++) o = ao_fma4(va[k], pa[k], o);
             }
-            for (; t < tn; t++) o = __builtin_fmaf(vb[b][t][j], pc[t], o);
+            for (; t < tn; t++) o = __builtin_fmaf(vc[t], pc[t], o);
         }
-        if (c + 1 < nc) stash((c + 1) & 1u);
         __syncthreads();
     }
-    if (chain) out[(size_t)(kvh * group + g) * hd + 16u * blockIdx.y + j] = o;
+    if (chain) out[(size_t)(kvh * group + wave) * 128u + AO_DV * blockIdx.y + lane] = o;
 }
 
 // src/kernels.c:118-128 (the final norm before the head,
@@ -222,42 +282,13 @@ mynah_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float *_
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * s * w[i];
 }
 
-// src/sampler.c:122-129 finishes here: each workgroup of the head GEMV left
-// one 64-bit key (orderable logit << 32 | ~row) for the first maximum of its
-// rows; the largest key is the first index of the maximum logit. Writes the
-// token, appends it to tokens[step], and advances pos and step (the
-// reference's n_past++). One workgroup.
-extern "C" __global__ void __launch_bounds__(1024)
-mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_keys,
-                     uint32_t *__restrict__ token, uint32_t *__restrict__ tokens,
-                     uint32_t *__restrict__ pos, uint32_t *__restrict__ step, uint32_t max_steps) {
-    __shared__ unsigned long long wk[16];
-    unsigned long long best = 0ull;
-    for (uint32_t i = threadIdx.x; i < n_keys; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
-    best = wave_max_u64(best);
-    if ((threadIdx.x & 63u) == 0) wk[threadIdx.x >> 6] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (uint32_t k = 1; k < (blockDim.x + 63u) / 64u; k++) best = wk[k] > best ? wk[k] : best;
-        const uint32_t idx = ~(uint32_t)(best & 0xffffffffull);
-        token[0] = idx;
-        const uint32_t s = step[0];
-        if (s < max_steps) tokens[s] = idx;
-        step[0] = s + 1u;
-        pos[0] = pos[0] + 1u;
-    }
-}
-
-// src/arch_qwen3.c:160-176: dequantise embedding row `token` into x (no
-// scaling). type 0 = f32 rows; otherwise the exact block decoders. One
-// thread per 32 values.
-extern "C" __global__ void __launch_bounds__(DEC_WG)
-mynah_embed_row(const uint8_t *__restrict__ table, const uint32_t *__restrict__ token_ptr,
-                float *__restrict__ x, uint32_t d, uint32_t type, uint32_t row_bytes) {
+// src/arch_qwen3.c:160-176: dequantise the 32 values of group c of
+// embedding row `token` into x (no scaling). type 0 = f32 rows; otherwise
+// the exact block decoders.
+MYNAH_DEV void embed_group(const uint8_t *__restrict__ table, uint32_t token, float *__restrict__ x,
+                           uint32_t c, uint32_t type, uint32_t row_bytes) {
 #pragma clang fp contract(off)
-    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;   // 32-value group
-    if (c >= d / 32u) return;
-    const uint8_t *row = table + (size_t)token_ptr[0] * row_bytes;
+    const uint8_t *row = table + (size_t)token * row_bytes;
     float *dst = x + 32u * c;
     if (type == 0u) {
         const float *f = (const float *)row + 32u * c;
@@ -296,3 +327,47 @@ mynah_embed_row(const uint8_t *__restrict__ table, const uint32_t *__restrict__ 
     }
 }
 
+// src/sampler.c:122-129 finishes here: each workgroup of the head GEMV left
+// one 64-bit key (orderable logit << 32 | ~row) for the first maximum of its
+// rows; the largest key is the first index of the maximum logit. Writes the
+// token, appends it to tokens[step], advances pos and step (the reference's
+// n_past++), and dequantises the token's embedding row into x for the next
+// step (src/arch_qwen3.c:160-176). One workgroup.
+extern "C" __global__ void __launch_bounds__(1024)
+mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_keys,
+                     uint32_t *__restrict__ token, uint32_t *__restrict__ tokens,
+                     uint32_t *__restrict__ pos, uint32_t *__restrict__ step, uint32_t max_steps,
+                     const uint8_t *__restrict__ table, float *__restrict__ x, uint32_t d,
+                     uint32_t type, uint32_t row_bytes) {
+    __shared__ unsigned long long wk[16];
+    __shared__ uint32_t sidx;
+    unsigned long long best = 0ull;
+    for (uint32_t i = threadIdx.x; i < n_keys; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63u) == 0) wk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t k = 1; k < (blockDim.x + 63u) / 64u; k++) best = wk[k] > best ? wk[k] : best;
+        const uint32_t idx = ~(uint32_t)(best & 0xffffffffull);
+        token[0] = idx;
+        const uint32_t s = step[0];
+        if (s < max_steps) tokens[s] = idx;
+        step[0] = s + 1u;
+        pos[0] = pos[0] + 1u;
+        sidx = idx;
+    }
+    __syncthreads();
+    const uint32_t idx = sidx;
+    for (uint32_t c = threadIdx.x; c < d / 32u; c += blockDim.x) embed_group(table, idx, x, c, type, row_bytes);
+}
+
+// The embedding row of the current token into x (the first step of a
+// sequence; later steps get theirs from mynah_argmax_advance). One thread per
+// 32 values.
+extern "C" __global__ void __launch_bounds__(DEC_WG)
+mynah_embed_row(const uint8_t *__restrict__ table, const uint32_t *__restrict__ token_ptr,
+                float *__restrict__ x, uint32_t d, uint32_t type, uint32_t row_bytes) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;   // 32-value group
+    if (c >= d / 32u) return;
+    embed_group(table, token_ptr[0], x, c, type, row_bytes);
+}

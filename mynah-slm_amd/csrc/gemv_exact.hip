@@ -21,12 +21,15 @@
 // No product is ever fused with a sum here: the library is compiled with
 // -ffp-contract=off and every summing function repeats it as a pragma.
 //
-// Decomposition: lane = output row (64 rows per workgroup); a "unit" is one
-// super-block (Q4_K, Q6_K) or one 32-value block (Q8_0); wave w of the W waves
-// of a workgroup computes the unit sums of units w, w+W, ... of its 64 rows.
-// The unit index is wave-uniform, so x is read with scalar loads and fed to
-// the VALU as SGPR operands. Each phase of W units lands in LDS and wave 0
-// folds it into the running row sums in unit order.
+// Decomposition (grouped launch, mynah_gemv_group): a "unit" is one
+// super-block (Q4_K, Q6_K) or one 32-value block (Q8_0). Lane l of a wave
+// serves row l / K and unit slot l % K (K = 1..16 slots per row); WS waves
+// share the same rows and split the units, WR such row groups make a
+// workgroup. Each lane computes whole unit sums (the unit order inside a
+// unit is the reference's), stores them in LDS, and one thread per row folds
+// the unit sums in unit order. The input x is staged once per workgroup in
+// LDS, 256-value chunks padded by 4 floats so the K slots of a wave read
+// different banks.
 //
 // SPDX-License-Identifier: MIT
 #include "common.hip.h"
@@ -38,7 +41,7 @@
 
 template <int J>
 MYNAH_DEV void q4k_sm(uint32_t s0, uint32_t s1, uint32_t s2, float &sc, float &m) {
-    if (J < 4) {
+    if constexpr (J < 4) {
         sc = (float)((s0 >> (8 * J)) & 63u);
         m = (float)((s1 >> (8 * J)) & 63u);
     } else {
@@ -62,12 +65,15 @@ MYNAH_DEV float q4k_group(const uint32_t *q, float d, float dmin, uint32_t s0, u
         const uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
         const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
         const float qh[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
+        const float4 xa4 = *(const float4 *)(x + 64 * G + 4 * m);
+        const float4 xb4 = *(const float4 *)(x + 64 * G + 32 + 4 * m);
+        const float xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w}, xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const float wa = __builtin_fmaf(da, ql[t], -oa);
-            acc = acc + wa * x[64 * G + 4 * m + t];
+            acc = acc + wa * xa[t];
             const float wb = __builtin_fmaf(db, qh[t], -ob);
-            acc = acc + wb * x[64 * G + 32 + 4 * m + t];
+            acc = acc + wb * xb[t];
         }
     }
     return acc;
@@ -92,25 +98,22 @@ MYNAH_DEV float q4k_group_seq(const uint32_t *q, float d, float dmin, uint32_t s
             const uint32_t v = q[8 * G + m];
             const uint32_t n = half ? ((v >> 4) & 0x0f0f0f0fu) : (v & 0x0f0f0f0fu);
             const float qf[4] = {ubyte_f<0>(n), ubyte_f<1>(n), ubyte_f<2>(n), ubyte_f<3>(n)};
+            const float4 x4 = *(const float4 *)(x + 64 * G + 32 * half + 4 * m);
+            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const float w = __builtin_fmaf(dd, qf[t], -oo);
-                acc = acc + w * x[64 * G + 32 * half + 4 * m + t];
+                acc = acc + w * xv[t];
             }
         }
     }
     return acc;
 }
 
+// Raw block words in registers, loaded apart from the arithmetic so the
+// grouped kernel can issue a block's loads before it stages x.
 template <bool SEQ>
-MYNAH_DEV float q4k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
-    const uint4 *p = (const uint4 *)blk;
-    uint32_t v[36];
-#pragma unroll
-    for (int k = 0; k < 9; k++) {
-        const uint4 c = p[k];
-        v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
-    }
+MYNAH_DEV float q4k_sum(const uint32_t *v, const float *__restrict__ x) {
     const float d = f16_to_f32(v[0]), dmin = f16_to_f32(v[0] >> 16);
     const uint32_t s0 = v[1], s1 = v[2], s2 = v[3];
     const uint32_t *q = v + 4;
@@ -129,18 +132,36 @@ MYNAH_DEV float q4k_unit(const uint8_t *__restrict__ blk, const float *__restric
     return acc;
 }
 
+MYNAH_DEV void q4k_load(const uint8_t *__restrict__ blk, uint32_t *v) {
+    const uint4 *p = (const uint4 *)blk;
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        const uint4 c = p[k];
+        v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
+    }
+}
+
+template <bool SEQ>
+MYNAH_DEV float q4k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
+    uint32_t v[36];
+    q4k_load(blk, v);
+    return q4k_sum<SEQ>(v, x);
+}
+
 // ── Q6_K: 210-byte block, 2-byte aligned ───────────────────────────────────
 // Read as the 53 aligned dwords that hold it; realigned dword k (block bytes
 // 4k..4k+3) = alignbyte(raw[k+1], raw[k], s) with s = block address & 3.
 // d (bytes 208..209) sits in raw[52] at byte s.
 
-MYNAH_DEV float q6k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
-#pragma clang fp contract(off)
-    const uint32_t s = (uint32_t)(uintptr_t)blk & 3u;
+MYNAH_DEV void q6k_load(const uint8_t *__restrict__ blk, uint32_t *raw, uint32_t &s) {
+    s = (uint32_t)(uintptr_t)blk & 3u;
     const uint32_t *a = (const uint32_t *)(blk - s);
-    uint32_t raw[53];
 #pragma unroll
     for (int k = 0; k < 53; k++) raw[k] = a[k];
+}
+
+MYNAH_DEV float q6k_sum(const uint32_t *raw, uint32_t s, const float *__restrict__ x) {
+#pragma clang fp contract(off)
     uint32_t v[52];
 #pragma unroll
     for (int k = 0; k < 52; k++) v[k] = align_bytes(raw[k + 1], raw[k], s);
@@ -164,59 +185,78 @@ MYNAH_DEV float q6k_unit(const uint8_t *__restrict__ blk, const float *__restric
                 const uint32_t q6 = nib | (((qh >> (2 * k)) & 0x03030303u) << 4);
                 const int j = 8 * h + 2 * k + (m >= 4 ? 1 : 0);
                 const float qf[4] = {ubyte_f<0>(q6), ubyte_f<1>(q6), ubyte_f<2>(q6), ubyte_f<3>(q6)};
+                const float4 x4 = *(const float4 *)(x + 128 * h + 32 * k + 4 * m);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     const float w = __builtin_fmaf(dsc[j], qf[t], n32[j]);
-                    acc = acc + w * x[128 * h + 32 * k + 4 * m + t];
+                    acc = acc + w * xv[t];
                 }
             }
     return acc;
 }
 
+MYNAH_DEV float q6k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
+    uint32_t raw[53], s;
+    q6k_load(blk, raw, s);
+    return q6k_sum(raw, s, x);
+}
+
 // ── Q8_0: 34-byte block, 2-byte aligned ────────────────────────────────────
 
-MYNAH_DEV float q80_block(const uint8_t *__restrict__ blk, const float *__restrict__ x,
-                          float acc) {
-#pragma clang fp contract(off)
-    const uint32_t s = (uint32_t)(uintptr_t)blk & 3u;
+MYNAH_DEV void q80_load(const uint8_t *__restrict__ blk, uint32_t *raw, uint32_t &s) {
+    s = (uint32_t)(uintptr_t)blk & 3u;
     const uint32_t *a = (const uint32_t *)(blk - s);
-    uint32_t raw[9];
 #pragma unroll
     for (int k = 0; k < 9; k++) raw[k] = a[k];
+}
+
+MYNAH_DEV float q80_sum(const uint32_t *raw, uint32_t s, const float *__restrict__ x, float acc) {
+#pragma clang fp contract(off)
     const float d = f16_to_f32(s ? (raw[0] >> 16) : raw[0]);
     const float n128 = -128.0f * d;
 #pragma unroll
     for (int m = 0; m < 8; m++) {
         const uint32_t q = (s ? raw[m + 1] : align_bytes(raw[m + 1], raw[m], 2u)) ^ 0x80808080u;
         const float qf[4] = {ubyte_f<0>(q), ubyte_f<1>(q), ubyte_f<2>(q), ubyte_f<3>(q)};
+        const float4 x4 = *(const float4 *)(x + 4 * m);
+        const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const float w = __builtin_fmaf(d, qf[t], n128);
-            acc = acc + w * x[4 * m + t];
+            acc = acc + w * xv[t];
         }
     }
     return acc;
 }
 
-// ── driver ─────────────────────────────────────────────────────────────────
-// SEQ selects the batched reference's order (kernels.c:1053-1104): natural
-// weight order within a Q4_K block, and Q8_0 summed in 256-value units of
-// eight blocks (kernels.c:2635-2648). Q6_K is the same in both.
+MYNAH_DEV float q80_block(const uint8_t *__restrict__ blk, const float *__restrict__ x,
+                          float acc) {
+    uint32_t raw[9], s;
+    q80_load(blk, raw, s);
+    return q80_sum(raw, s, x, acc);
+}
 
-template <int FMT, bool SEQ>
-MYNAH_DEV float unit_sum(const uint8_t *__restrict__ row, uint32_t u, const float *__restrict__ x) {
-    if (FMT == 12) return q4k_unit<SEQ>(row + 144u * u, x + 256u * u);
+// ── batched-order driver ───────────────────────────────────────────────────
+// One token of the exact matmat (kernels.c:1053-1104): natural weight order
+// within a Q4_K block, Q8_0 summed in 256-value units of eight blocks
+// (kernels.c:2635-2648); Q6_K is the same as the matvec. Lane = row (64 rows
+// per workgroup), wave w of W sums units w, w + W, ...; x by scalar loads;
+// wave 0 folds each phase's unit sums in unit order.
+
+template <int FMT>
+MYNAH_DEV float seq_unit(const uint8_t *__restrict__ row, uint32_t u, const float *__restrict__ x) {
+    if (FMT == 12) return q4k_unit<true>(row + 144u * u, x + 256u * u);
     if (FMT == 14) return q6k_unit(row + 210u * u, x + 256u * u);
-    if (!SEQ) return q80_block(row + 34u * u, x + 32u * u, 0.0f);
     float acc = 0.0f;
 #pragma unroll
     for (int b = 0; b < 8; b++) acc = q80_block(row + 272u * u + 34u * b, x + 256u * u + 32u * b, acc);
     return acc;
 }
 
-template <int FMT, bool SEQ>
-MYNAH_DEV void gemv_exact(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                          float *__restrict__ y, uint32_t rows, uint32_t units, uint32_t row_bytes) {
+template <int FMT>
+MYNAH_DEV void gemv_seq(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                        float *__restrict__ y, uint32_t rows, uint32_t units, uint32_t row_bytes) {
 #pragma clang fp contract(off)
     __shared__ float part[EX_MAX_WAVES][EX_ROWS];
     const uint32_t lane = threadIdx.x & 63u;
@@ -228,7 +268,7 @@ MYNAH_DEV void gemv_exact(const uint8_t *__restrict__ w, const float *__restrict
     for (uint32_t p = 0; p < units; p += nw) {
         const uint32_t u = p + wave;
         float s = 0.0f;
-        if (u < units) s = unit_sum<FMT, SEQ>(wr, u, x);
+        if (u < units) s = seq_unit<FMT>(wr, u, x);
         part[wave][lane] = s;
         __syncthreads();
         if (wave == 0) {
@@ -240,29 +280,37 @@ MYNAH_DEV void gemv_exact(const uint8_t *__restrict__ w, const float *__restrict
     if (wave == 0 && row < rows) y[row] = total;
 }
 
-#define GEMV_EXACT_ENTRY(name, FMT, SEQ)                                                   \
+#define GEMV_SEQ_ENTRY(name, FMT)                                                          \
     extern "C" __global__ void __launch_bounds__(EX_ROWS * EX_MAX_WAVES)                  \
         name(const uint8_t *__restrict__ w, const float *__restrict__ x,                  \
              float *__restrict__ y, uint32_t rows, uint32_t units, uint32_t row_bytes) {  \
-        gemv_exact<FMT, SEQ>(w, x, y, rows, units, row_bytes);                             \
+        gemv_seq<FMT>(w, x, y, rows, units, row_bytes);                                    \
     }
 
-GEMV_EXACT_ENTRY(mynah_q4k_gemv_exact, 12, false)
-GEMV_EXACT_ENTRY(mynah_q6k_gemv_exact, 14, false)
-GEMV_EXACT_ENTRY(mynah_q80_gemv_exact, 8, false)
-GEMV_EXACT_ENTRY(mynah_q4k_gemv_exact_seq, 12, true)
-GEMV_EXACT_ENTRY(mynah_q80_gemv_exact_seq, 8, true)
+GEMV_SEQ_ENTRY(mynah_q4k_gemv_exact_seq, 12)
+GEMV_SEQ_ENTRY(mynah_q6k_gemv_exact_seq, 14)
+GEMV_SEQ_ENTRY(mynah_q80_gemv_exact_seq, 8)
 
 
-// ── grouped launches with fused epilogues (the resident decode step) ───────
+// ── grouped matvec with fused epilogues (every matvec, decode included) ────
 // One launch covers up to EX_GROUP_MAX matrices; workgroup t serves the
-// 64-row tile t - tile0 of the descriptor whose [tile0, next tile0) range
+// row tile t - tile0 of the descriptor whose [tile0, next tile0) range
 // holds t. Epilogues, each the reference's own f32 operation on the exact
 // row sum: y = res + Wx (src/arch_qwen3.c:224, 234 — mynah_slm_add), and for
 // a paired matrix w2 (ffn_up next to ffn_gate) y = (g * sigmoid(g)) * u with
 // the reference's overflow-safe sigmoid (src/kernels.c:193-205). `ypos`
 // moves y by ypos[0] * ystride: the K / V projections write straight into
 // the cache slot of the current position (src/arch_qwen3.c:194-199).
+// With norm_w set, the input is RMSNorm(x) * norm_w (src/kernels.c:118-128:
+// double sum of squares, s = (float)(1 / sqrt(sum / n + eps)), (x * s) * w),
+// computed by every workgroup while it stages x; this replaces the
+// reference's separate rms_norm call feeding the projections
+// (src/arch_qwen3.c:201, 226, 239).
+//
+// grp.shape = log2(K) | WS << 8 | WR << 16, with (64 / K) * WR <= 64 rows per
+// workgroup and 64 * WS * WR threads. Dynamic LDS (floats): the padded x,
+// (units | 1) unit sums per row of the workgroup, and with norm_w a copy of
+// the norm weights (cols).
 
 #define EX_GROUP_MAX 8
 
@@ -281,7 +329,7 @@ struct GemvDesc {
 };
 
 struct GemvGroup {
-    uint32_t n, pad;
+    uint32_t n, shape;
     GemvDesc d[EX_GROUP_MAX];
 };
 
@@ -292,83 +340,131 @@ MYNAH_DEV float sigmoid_ref(float v) {
     return e / (1.0f + e);
 }
 
+MYNAH_DEV uint32_t xpad_floats(uint32_t cols) { return cols + 4u * ((cols + 255u) >> 8); }
+
+template <int FMT> struct Raw;
+template <> struct Raw<12> {
+    static constexpr uint32_t BYTES = 144;
+    uint32_t v[36];
+    __device__ __forceinline__ void load(const uint8_t *b) { q4k_load(b, v); }
+    __device__ __forceinline__ float sum(const float *x) const { return q4k_sum<false>(v, x); }
+};
+template <> struct Raw<14> {
+    static constexpr uint32_t BYTES = 210;
+    uint32_t raw[53], s;
+    __device__ __forceinline__ void load(const uint8_t *b) { q6k_load(b, raw, s); }
+    __device__ __forceinline__ float sum(const float *x) const { return q6k_sum(raw, s, x); }
+};
+template <> struct Raw<8> {
+    static constexpr uint32_t BYTES = 34;
+    uint32_t raw[9], s;
+    __device__ __forceinline__ void load(const uint8_t *b) { q80_load(b, raw, s); }
+    __device__ __forceinline__ float sum(const float *x) const { return q80_sum(raw, s, x, 0.0f); }
+};
+
+// x position of unit u in the padded LDS copy.
 template <int FMT>
-MYNAH_DEV float unit_any(const GemvDesc &g, const uint8_t *r1, const uint8_t *r2, uint32_t u,
-                         const float *__restrict__ x) {
-    if (u < g.units) return unit_sum<FMT, false>(r1, u, x);
-    return unit_sum<FMT, false>(r2, u - g.units, x);
+MYNAH_DEV const float *unit_x(const float *lx, uint32_t u) {
+    if (FMT == 8) return lx + 260u * (u >> 3) + 32u * (u & 7u);
+    return lx + 260u * u;
 }
 
-template <bool NORM>
-MYNAH_DEV void group_body(const GemvDesc &g, uint32_t t, const float *__restrict__ x) {
+template <int FMT>
+MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float *lds, double *shd) {
 #pragma clang fp contract(off)
-    __shared__ float part[EX_MAX_WAVES][EX_ROWS];
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
-    const uint32_t row = (t - g.tile0) * EX_ROWS + lane;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t lk = shape & 31u, ws_n = (shape >> 8) & 31u, wr_n = (shape >> 16) & 31u;
+    const uint32_t k = 1u << lk, rpw = 64u >> lk, rpg = rpw * wr_n;
+    const uint32_t wr = wave / ws_n, wsi = wave - wr * ws_n;
+    const uint32_t rl = wr * rpw + (lane >> lk), j = lane & (k - 1u);
+    const uint32_t row0 = (t - g.tile0) * rpg, row = row0 + rl;
     const size_t roff = (size_t)(row < g.rows ? row : g.rows - 1u) * g.row_bytes;
     const uint8_t *r1 = g.w + roff;
     const uint8_t *r2 = g.w2 ? g.w2 + roff : r1;
-    const uint32_t total_units = g.w2 ? 2u * g.units : g.units;
-    float t1 = 0.0f, t2 = 0.0f;
-    for (uint32_t p = 0; p < total_units; p += nw) {
-        const uint32_t u = p + wave;
-        float s = 0.0f;
-        if (u < total_units) {
-            if (g.type == 12u) s = unit_any<12>(g, r1, r2, u, x);
-            else if (g.type == 14u) s = unit_any<14>(g, r1, r2, u, x);
-            else s = unit_any<8>(g, r1, r2, u, x);
+    const uint32_t U = g.units, Ut = g.w2 ? 2u * U : U, pstride = Ut | 1u;
+    const uint32_t step = k * ws_n;
+    constexpr uint32_t UB = Raw<FMT>::BYTES;
+    uint32_t u = j + k * wsi;
+    Raw<FMT> raw;
+    if (u < Ut) raw.load(u < U ? r1 + UB * u : r2 + UB * (u - U));
+
+    // Prefetch what the epilogue reads (residual row, cache slot).
+    const uint32_t frow = row0 + tid;
+    const bool folds = tid < rpg && frow < g.rows;
+    float resv = 0.0f;
+    if (folds && g.res) resv = g.res[frow];
+    const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
+
+    // Stage x (or RMSNorm(x) * norm_w) into the padded LDS copy; all x and
+    // norm-weight loads are issued before the first wait.
+    const uint32_t cols = g.cols, n4 = cols / 4u;
+    const float4 *x4 = (const float4 *)g.x;
+    float *lw = lds + xpad_floats(cols) + rpg * pstride;
+    if (g.norm_w) {
+        const float4 *w4 = (const float4 *)g.norm_w;
+        double acc = 0.0;
+#pragma unroll 4
+        for (uint32_t q = tid; q < n4; q += blockDim.x) {
+            const float4 v = x4[q], w = w4[q];
+            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = v;
+            *(float4 *)(lw + 4u * q) = w;
+            acc += (double)v.x * (double)v.x;
+            acc += (double)v.y * (double)v.y;
+            acc += (double)v.z * (double)v.z;
+            acc += (double)v.w * (double)v.w;
         }
-        part[wave][lane] = s;
-        __syncthreads();
-        if (wave == 0) {
-            const uint32_t n = total_units - p < nw ? total_units - p : nw;
-            for (uint32_t k = 0; k < n; k++) {
-                if (p + k < g.units) t1 = t1 + part[k][lane];
-                else t2 = t2 + part[k][lane];
-            }
+        const double sum = block_sum_d(acc, shd);
+        const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)g.eps));
+        for (uint32_t q = tid; q < n4; q += blockDim.x) {
+            float4 *px = (float4 *)(lds + 4u * q + 4u * (q >> 6));
+            float4 v = *px;
+            const float4 w = *(const float4 *)(lw + 4u * q);
+            v.x = v.x * sc * w.x; v.y = v.y * sc * w.y; v.z = v.z * sc * w.z; v.w = v.w * sc * w.w;
+            *px = v;
         }
-        __syncthreads();
+    } else {
+#pragma unroll 4
+        for (uint32_t q = tid; q < n4; q += blockDim.x)
+            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = x4[q];
     }
-    if (wave == 0) {
-        float v = t1;
-        if (g.w2) v = t1 * sigmoid_ref(t1) * t2;
-        else if (g.res && row < g.rows) v = g.res[row] + t1;
-        if (row < g.rows) {
-            float *y = g.y + (g.ypos ? (size_t)g.ypos[0] * g.ystride : 0);
-            y[row] = v;
+    __syncthreads();
+
+    float *part = lds + xpad_floats(cols);
+    while (u < Ut) {
+        const uint32_t uu = u < U ? u : u - U;
+        part[rl * pstride + u] = raw.sum(unit_x<FMT>(lds, uu));
+        u += step;
+        if (u < Ut) raw.load(u < U ? r1 + UB * u : r2 + UB * (u - U));
+    }
+    __syncthreads();
+
+    if (tid < 64u) {
+        float t1 = 0.0f, t2 = 0.0f, v = 0.0f;
+        if (folds) {
+            const float *pr = part + tid * pstride;
+            for (uint32_t q = 0; q < U; q++) t1 = t1 + pr[q];
+            for (uint32_t q = U; q < Ut; q++) t2 = t2 + pr[q];
+            v = t1;
+            if (g.w2) v = t1 * sigmoid_ref(t1) * t2;
+            else if (g.res) v = resv + t1;
+            g.y[yoff + frow] = v;
         }
         if (g.keys) {
-            const unsigned long long k = wave_max_u64(row < g.rows ? argmax_key(v, row) : 0ull);
-            if (lane == 0) g.keys[t - g.tile0] = k;
+            const unsigned long long key = wave_max_u64(folds ? argmax_key(v, frow) : 0ull);
+            if (tid == 0) g.keys[t - g.tile0] = key;
         }
     }
 }
 
-// With norm_w set, the input is RMSNorm(x) * norm_w (src/kernels.c:118-128:
-// double sum of squares, s = (float)(1 / sqrt(sum / n + eps)), (x * s) * w),
-// computed by every workgroup into LDS before its GEMV; this replaces the
-// reference's separate rms_norm call feeding the projections
-// (src/arch_qwen3.c:201, 226, 239). Dynamic LDS: cols floats.
-extern "C" __global__ void __launch_bounds__(EX_ROWS * EX_MAX_WAVES)
+extern "C" __global__ void __launch_bounds__(1024)
 mynah_gemv_group(const GemvGroup grp) {
-#pragma clang fp contract(off)
-    extern __shared__ float hx[];
-    __shared__ double shd[EX_MAX_WAVES];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ double shd[16];
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
     const GemvDesc &g = grp.d[i];
-    if (g.norm_w == nullptr) {
-        group_body<false>(g, t, g.x);
-        return;
-    }
-    double acc = 0.0;
-    for (uint32_t k = threadIdx.x; k < g.cols; k += blockDim.x) acc += (double)g.x[k] * (double)g.x[k];
-    const double sum = block_sum_d(acc, shd);
-    const float s = (float)(1.0 / sqrt(sum / (double)g.cols + (double)g.eps));
-    for (uint32_t k = threadIdx.x; k < g.cols; k += blockDim.x) hx[k] = g.x[k] * s * g.norm_w[k];
-    __syncthreads();
-    group_body<true>(g, t, hx);
+    if (g.type == 12u) group_split<12>(g, t, grp.shape, lds, shd);
+    else if (g.type == 14u) group_split<14>(g, t, grp.shape, lds, shd);
+    else group_split<8>(g, t, grp.shape, lds, shd);
 }

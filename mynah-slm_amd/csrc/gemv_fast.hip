@@ -254,7 +254,7 @@ MYNAH_DEV void fast_tile(const GemvDesc &g, uint32_t t, uint32_t ks, float *lx, 
     }
 }
 
-// grp.pad carries KS. Dynamic LDS: cols * 17/16 + cols / 8 floats.
+// grp.shape carries KS. Dynamic LDS: cols * 17/16 + cols / 8 floats.
 extern "C" __global__ void __launch_bounds__(FG_WG)
 mynah_gemv_fast_group(const GemvGroup grp) {
     extern __shared__ float lds_f[];
@@ -266,7 +266,7 @@ mynah_gemv_fast_group(const GemvGroup grp) {
     const GemvDesc &g = grp.d[i];
     float *lx = lds_f;
     float *ls = lds_f + g.cols + g.cols / 16u;
-    const uint32_t ks = grp.pad;
+    const uint32_t ks = grp.shape;
     if (g.type == 12u) fast_tile<RawQ4K>(g, t, ks, lx, ls, shd, wp);
     else if (g.type == 14u) fast_tile<RawQ6K>(g, t, ks, lx, ls, shd, wp);
     else fast_tile<RawQ80>(g, t, ks, lx, ls, shd, wp);

@@ -162,17 +162,16 @@ int mynah_hip_gemv_order(void) { return gemv_order; }
 
 /* Exact kernels: 64 rows per workgroup, W waves splitting the units of a
  * row (W <= 16, balanced so every wave gets the same count). */
-static int gemv_exact_launch(mynah_device *d, int type, const void *w, size_t rows,
-                             size_t cols, size_t rb, const float *x, float *y,
-                             hipStream_t stream, int seq) {
-    const size_t units = (type == MYNAH_Q8_0 && !seq) ? cols / 32 : cols / 256;
+/* One token of the exact matmat: the batched reference's summation order. */
+static int gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                           size_t rb, const float *x, float *y, hipStream_t stream) {
+    const size_t units = cols / 256;
     const size_t per_wave = (units + 15) / 16;
     const size_t waves = (units + per_wave - 1) / per_wave;
     const unsigned grid = (unsigned)((rows + 63) / 64);
-    int k;
-    if (type == MYNAH_Q4_K) k = seq ? MYNAH_K_Q4K_EXACT_SEQ : MYNAH_K_Q4K_EXACT;
-    else if (type == MYNAH_Q6_K) k = MYNAH_K_Q6K_EXACT;
-    else k = seq ? MYNAH_K_Q80_EXACT_SEQ : MYNAH_K_Q80_EXACT;
+    const int k = type == MYNAH_Q4_K   ? MYNAH_K_Q4K_EXACT_SEQ
+                  : type == MYNAH_Q6_K ? MYNAH_K_Q6K_EXACT_SEQ
+                                       : MYNAH_K_Q80_EXACT_SEQ;
     uint32_t rows32 = (uint32_t)rows, units32 = (uint32_t)units, rb32 = (uint32_t)rb;
     void *args[] = {&w, &x, &y, &rows32, &units32, &rb32};
     return mynah_launch(d, k, grid, 1, (unsigned)(64 * waves), 0, stream, args);
@@ -198,13 +197,11 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
         mynah_set_error("row too long");
         return -1;
     }
-    if (gemv_order == MYNAH_GEMV_EXACT)
-        return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 0);
     mynah_gemv_group g;
     memset(&g, 0, sizeof g);
     g.n = 1;
     if (mynah_gemv_desc_init(&g.d[0], type, w, rows, cols, x, y) != 0) return -1;
-    return mynah_gemv_group_launch(d, &g, stream);
+    return mynah_gemv_group_launch(d, &g, stream, NULL);
 }
 
 int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -219,7 +216,7 @@ int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows,
         mynah_set_error("weights misaligned for type %d", type);
         return -1;
     }
-    return gemv_exact_launch(d, type, w, rows, cols, rb, x, y, stream, 1);
+    return gemv_seq_launch(d, type, w, rows, cols, rb, x, y, stream);
 }
 
 int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
@@ -251,56 +248,88 @@ static uint32_t fast_ks(uint32_t all_rows) {
     return all_rows >= 32768u ? 1u : all_rows >= 8192u ? 2u : 4u;
 }
 
-uint32_t mynah_gemv_group_tiles(uint32_t rows, uint32_t all_rows) {
-    const uint32_t tile_rows = gemv_order == MYNAH_GEMV_EXACT ? 64u : 32u / fast_ks(all_rows);
-    return (rows + tile_rows - 1u) / tile_rows;
+/* Exact-order layout of a grouped launch: K unit slots per row in a wave
+ * (64 / K rows per wave), WS waves sharing rows, WR row groups per
+ * workgroup. Small launches spread one unit per lane over as many
+ * workgroups as possible (they are latency-bound); large ones keep every
+ * lane busy (K divides the units) and group rows to share the staged x. */
+static void exact_shape(uint32_t all_rows, uint32_t units, uint32_t *lk, uint32_t *ws,
+                        uint32_t *wr) {
+    uint32_t k = 1;
+    if (all_rows >= 16384u) {
+        while (k < 16u && units % (2u * k) == 0) k *= 2u;
+    } else {
+        while (k < 16u && k < units) k *= 2u;
+    }
+    uint32_t w = (units + k - 1u) / k;
+    if (w > 16u) w = 16u;
+    const uint32_t rpw = 64u / k;
+    uint32_t r = 1, tiles = (all_rows + rpw - 1u) / rpw;
+    while (w * r * 2u <= 4u && rpw * r * 2u <= 64u && tiles / (r * 2u) >= 1024u) r *= 2u;
+    uint32_t l = 0;
+    while ((1u << l) < k) l++;
+    *lk = l;
+    *ws = w;
+    *wr = r;
 }
 
-/* The grouped GEMV in the current order: exact (64-row tiles, W waves
- * splitting the units) or reordered (32-row tiles of 4 waves, x in LDS). */
-int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream) {
+/* The grouped GEMV in the current order: exact (lane = row x unit slot,
+ * unit sums folded in order) or reordered (8-lane row blocks, KS waves
+ * splitting the super-blocks of a tile). */
+int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
+                            uint32_t *tiles_out) {
     if (grp->n == 0 || grp->n > MYNAH_GROUP_MAX) {
         mynah_set_error("group of %u matrices", grp->n);
         return -1;
     }
     const int exact = gemv_order == MYNAH_GEMV_EXACT;
-    /* Reordered: KS waves split the super-blocks of an 8-row tile; small
-     * launches use KS = 4 for more waves in flight, large ones KS = 1. */
-    uint32_t all_rows = 0;
-    for (uint32_t i = 0; i < grp->n; i++) all_rows += grp->d[i].rows;
-    const uint32_t ks = fast_ks(all_rows);
-    const uint32_t tile_rows = exact ? 64u : 32u / ks;
-    uint32_t tiles = 0, max_units = 1;
+    uint32_t all_rows = 0, max_units = 1;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        mynah_gemv_desc *g = &grp->d[i];
+        all_rows += g->rows;
+        const uint32_t u = g->w2 ? 2u * g->units : g->units;
+        if (u > max_units) max_units = u;
+        if (g->cols % 8 != 0 || ((uintptr_t)g->x & 15u) != 0 ||
+            ((uintptr_t)g->norm_w & 15u) != 0) {
+            mynah_set_error("grouped GEMV needs 16-byte aligned x and norm weights, cols %% 8 == 0");
+            return -1;
+        }
+    }
+    uint32_t lk = 0, ws = 1, wr = 1, ks = 1, tile_rows;
+    if (exact) {
+        exact_shape(all_rows, max_units, &lk, &ws, &wr);
+        tile_rows = (64u >> lk) * wr;
+    } else {
+        /* Reordered: small launches use KS = 4 for more waves in flight,
+         * large ones KS = 1. */
+        ks = fast_ks(all_rows);
+        tile_rows = 32u / ks;
+    }
+    uint32_t tiles = 0;
     size_t lds = 0;
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
-        size_t need = 0;
-        if (!exact) {
-            if (g->cols % 8 != 0 || ((uintptr_t)g->x & 15u) != 0 ||
-                ((uintptr_t)g->norm_w & 15u) != 0) {
-                mynah_set_error("reordered GEMV needs 16-byte aligned x and cols %% 8 == 0");
-                return -1;
-            }
-            need = ((size_t)g->cols + g->cols / 16 + g->cols / 8) * 4;
-        } else if (g->norm_w != NULL) {
-            need = (size_t)g->cols * 4;
-        }
+        const uint32_t ut = g->w2 ? 2u * g->units : g->units;
+        const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
+                                     (size_t)tile_rows * (ut | 1u) +
+                                     (g->norm_w ? (size_t)g->cols : 0u)) * 4u
+                                  : ((size_t)g->cols + g->cols / 16 + g->cols / 8) * 4u;
         if (need > lds) lds = need;
         g->tile0 = tiles;
         tiles += (g->rows + tile_rows - 1u) / tile_rows;
-        const uint32_t u = g->w2 ? 2u * g->units : g->units;
-        if (u > max_units) max_units = u;
     }
-    if (lds > 56u * 1024u) {
+    if (lds > 60u * 1024u) {
         mynah_set_error("input of this GEMV exceeds the LDS budget (%zu B)", lds);
         return -1;
     }
+    if (tiles_out) *tiles_out = tiles;
     void *args[] = {grp};
-    grp->pad = exact ? 0u : ks;
-    if (!exact) return mynah_launch(d, MYNAH_K_GEMV_FAST_GROUP, tiles, 1, 256, lds, stream, args);
-    const uint32_t per_wave = (max_units + 15u) / 16u;
-    const uint32_t waves = (max_units + per_wave - 1u) / per_wave;
-    return mynah_launch(d, MYNAH_K_GEMV_GROUP, tiles, 1, 64u * waves, lds, stream, args);
+    if (!exact) {
+        grp->shape = ks;
+        return mynah_launch(d, MYNAH_K_GEMV_FAST_GROUP, tiles, 1, 256, lds, stream, args);
+    }
+    grp->shape = lk | (ws << 8) | (wr << 16);
+    return mynah_launch(d, MYNAH_K_GEMV_GROUP, tiles, 1, 64u * ws * wr, lds, stream, args);
 }
 
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,

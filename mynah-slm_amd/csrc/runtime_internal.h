@@ -13,10 +13,8 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
 /* Every kernel of the embedded code object: id and symbol name. */
 #define MYNAH_KERNEL_LIST(X)                          \
     X(MYNAH_K_DEQUANT, "mynah_dequant")                 \
-    X(MYNAH_K_Q4K_EXACT, "mynah_q4k_gemv_exact")        \
-    X(MYNAH_K_Q6K_EXACT, "mynah_q6k_gemv_exact")        \
-    X(MYNAH_K_Q80_EXACT, "mynah_q80_gemv_exact")        \
     X(MYNAH_K_Q4K_EXACT_SEQ, "mynah_q4k_gemv_exact_seq") \
+    X(MYNAH_K_Q6K_EXACT_SEQ, "mynah_q6k_gemv_exact_seq") \
     X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq") \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
@@ -77,7 +75,7 @@ typedef struct {
 } mynah_gemv_desc;
 
 typedef struct {
-    uint32_t n, pad;
+    uint32_t n, shape;        /* shape: set by the launch */
     mynah_gemv_desc d[MYNAH_GROUP_MAX];
 } mynah_gemv_group;
 
@@ -85,9 +83,9 @@ typedef struct {
  * cols) units / row_bytes, which mynah_gemv_desc_init sets. */
 int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
                          const float *x, float *y);
-int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream);
-/* Tiles (workgroups) the group launch will use for a descriptor of `rows`
- * rows under the current order (the length of its argmax key array). */
-uint32_t mynah_gemv_group_tiles(uint32_t rows, uint32_t all_rows);
+/* *tiles (optional) receives the number of workgroups, which is also the
+ * length of a descriptor's argmax key array when the group has one member. */
+int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
+                            uint32_t *tiles);
 
 #endif
