@@ -112,9 +112,12 @@ def gpu_decode(M, CF):
            "weight_bytes": model.weight_bytes()}
     old = M.lib.mynah_hip_gemv_order()
     try:
-        for order, name in ((0, "exact"), (1, "reordered")):
+        for order, attn, name in ((0, M.ATTN_EXACT, "exact"),
+                                  (0, M.ATTN_SPLIT, "exact_gemv_split_attention"),
+                                  (1, M.ATTN_SPLIT, "reordered_gemv_split_attention")):
             M.check(M.lib.mynah_hip_set_gemv_order(order), "order")
             dec = M.Qwen3Decoder(model, npre + steps + 1)
+            dec.set_attention(attn)
             dec.set_kv(k, v, npre)
             dec.generate(first, 4)                       # warm-up and graph capture
             dec.reset()

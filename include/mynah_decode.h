@@ -55,6 +55,17 @@ uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
 /* 1 when the step runs as a replayed hipGraph, 0 when launched directly. */
 int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);
 
+/* Attention of the decode step (no reference counterpart; the reference's
+ * attention is src/kernels.c:228-293):
+ *   MYNAH_ATTN_EXACT (default): the reference's operations in its order — the
+ *     full softmax over all positions, then o = fma(v_t, p_t, o) for t in
+ *     order; two launches per layer;
+ *   MYNAH_ATTN_SPLIT: positions split across workgroups, per-chunk softmax
+ *     partials combined by a second small launch; short FMA chains; differs
+ *     from the reference by f32 rounding only. */
+enum { MYNAH_ATTN_EXACT = 0, MYNAH_ATTN_SPLIT = 1 };
+int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,7 +51,7 @@ struct mynah_qwen3 {
     dtensor embed, out_norm, head;
     dlayer *layers;
     float *k_cache, *v_cache, *rope_cos, *rope_sin;
-    float *x, *h, *q, *attn, *act, *logits, *scores;
+    float *x, *q, *attn, *act, *logits, *scores;
     uint32_t *counters;             /* token, pos, step */
     unsigned long long *keys;       /* head workgroups' argmax keys */
     uint32_t n_keys;
@@ -61,6 +61,11 @@ struct mynah_qwen3 {
     hipGraphExec_t exec;
     int graph_state;                /* 0 not tried, 1 ready, -1 unavailable */
     int graph_order;                /* GEMV order the graph was captured with */
+    int attn_mode;                  /* MYNAH_ATTN_EXACT or MYNAH_ATTN_SPLIT */
+    int graph_attn;                 /* attention mode the graph was captured with */
+    uint32_t nch_max;               /* position chunks of the split attention */
+    float *pm, *po;                 /* split-attention partials: chunk max, weighted V */
+    double *pl;                     /* split-attention partials: chunk exp sums */
 };
 
 #define TOKEN(s) ((s)->counters + 0)
@@ -112,8 +117,9 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
     if (s->exec) (void)hipGraphExecDestroy(s->exec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
-    void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->h, s->q,
-                    s->attn, s->act, s->logits, s->scores, s->counters, s->tokens};
+    void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->q,
+                    s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->pm, s->pl,
+                    s->po};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
     free(s->layers);
@@ -207,7 +213,6 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->rope_cos = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
     s->rope_sin = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
     s->x = (float *)dalloc(dm * 4, &ok);
-    s->h = (float *)dalloc(dm * 4, &ok);
     s->q = (float *)dalloc((size_t)s->q_dim * 4, &ok);
     s->attn = (float *)dalloc((size_t)s->q_dim * 4, &ok);
     s->act = (float *)dalloc(ff * 4, &ok);
@@ -215,6 +220,13 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->sstride = (n_ctx + 63) & ~63u;
     s->scores = (float *)dalloc((size_t)c->n_heads * s->sstride * 4, &ok);
     s->counters = (uint32_t *)dalloc(16, &ok);
+    {
+        const size_t parts = (size_t)c->n_kv_heads * ((n_ctx + 31) / 32) * (c->n_heads / c->n_kv_heads);
+        s->nch_max = (n_ctx + 31) / 32;
+        s->pm = (float *)dalloc(parts * 4, &ok);
+        s->pl = (double *)dalloc(parts * 8, &ok);
+        s->po = (float *)dalloc(parts * 128 * 4, &ok);
+    }
     s->n_keys = c->vocab / 8 + 64;
     s->keys = (unsigned long long *)dalloc((size_t)s->n_keys * 8, &ok);
     s->tokens = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
@@ -282,9 +294,27 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[1].ystride = s->kv_dim;
         g.d[2].ypos = pos;
         g.d[2].ystride = s->kv_dim;
-        rc = mynah_gemv_group_launch(d, &g, st, NULL);
+        rc = mynah_gemv_group_launch(d, &g, st, NULL, -1);
         if (rc) break;
-        {
+        if (s->attn_mode == MYNAH_ATTN_SPLIT) {
+            const float *q = s->q, *qn = (const float *)L->q_norm.dev;
+            const float *kn = (const float *)L->k_norm.dev;
+            const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+            float *pm = s->pm, *po = s->po, *out = s->attn;
+            double *pl = s->pl;
+            uint32_t nchm = s->nch_max, kvd = s->kv_dim;
+            uint32_t group = c->n_heads / c->n_kv_heads;
+            float eps = c->rms_eps, scale = s->scale;
+            void *args[] = {&q, &kl, &vl, &qn, &kn, &rcos, &rsin, &pos, &pm, &pl, &po, &nchm, &kvd,
+                            &group, &eps, &scale};
+            rc = mynah_launch(d, MYNAH_K_ATTN_SPLIT, c->n_kv_heads, s->nch_max, 128 * group, 0, st,
+                              args);
+            if (rc) break;
+            const float *cpm = pm, *cpo = po;
+            const double *cpl = pl;
+            void *args2[] = {&pos, &cpm, &cpl, &cpo, &out, &nchm, &group};
+            rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_kv_heads, 1, 128 * group, 0, st, args2);
+        } else {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;
             const float *rcos = s->rope_cos, *rsin = s->rope_sin;
@@ -308,7 +338,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.n = 1;
         rc = gemv_desc(&g.d[0], &L->wo, s->attn, s->x);
         g.d[0].res = s->x;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL, -1);
         if (rc) break;
         memset(&g, 0, sizeof g);
         g.n = 1;
@@ -316,13 +346,13 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[0].w2 = L->up.dev;
         g.d[0].norm_w = (const float *)L->ffn_norm.dev;     /* src/arch_qwen3.c:226 */
         g.d[0].eps = c->rms_eps;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL, -1);
         if (rc) break;
         memset(&g, 0, sizeof g);
         g.n = 1;
         rc = gemv_desc(&g.d[0], &L->down, s->act, s->x);
         g.d[0].res = s->x;
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL);
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL, -1);
     }
     if (rc == 0) {
         /* The final norm (src/arch_qwen3.c:239) runs inside the head GEMV. */
@@ -333,7 +363,10 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[0].norm_w = (const float *)s->out_norm.dev;
         g.d[0].eps = c->rms_eps;
         g.d[0].keys = s->keys;                               /* src/sampler.c:124-129 */
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles);
+        /* The exact kernel is also the faster one for the head (its fused
+         * norm costs the reordered kernel more), so the head always runs in
+         * the reference's order. */
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles, MYNAH_GEMV_EXACT);
         if (rc == 0 && head_tiles > s->n_keys) {
             mynah_set_error("head launch of %u workgroups exceeds the key buffer", head_tiles);
             rc = -1;
@@ -366,7 +399,8 @@ static int embed_current(mynah_qwen3 *s, mynah_device *d) {
 /* Capture the step once; fall back to direct launches if capture fails. */
 static int run_step(mynah_qwen3 *s, mynah_device *d) {
     hipStream_t st = d->stream;
-    if (s->graph_state == 1 && s->graph_order != mynah_hip_gemv_order()) {
+    if (s->graph_state == 1 &&
+        (s->graph_order != mynah_hip_gemv_order() || s->graph_attn != s->attn_mode)) {
         (void)hipGraphExecDestroy(s->exec);
         (void)hipGraphDestroy(s->graph);
         s->exec = NULL;
@@ -384,6 +418,7 @@ static int run_step(mynah_qwen3 *s, mynah_device *d) {
                 s->graph = g;
                 s->graph_state = 1;
                 s->graph_order = mynah_hip_gemv_order();
+                s->graph_attn = s->attn_mode;
             } else if (g != NULL) {
                 (void)hipGraphDestroy(g);
             }
@@ -501,3 +536,12 @@ void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
 }
 
 int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) { return s ? s->graph_state == 1 : 0; }
+
+int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode) {
+    if (s == NULL || (mode != MYNAH_ATTN_EXACT && mode != MYNAH_ATTN_SPLIT)) {
+        mynah_set_error("attention mode %d", mode);
+        return -1;
+    }
+    s->attn_mode = mode;
+    return 0;
+}

@@ -267,6 +267,216 @@ mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scor
     if (chain) out[(size_t)(kvh * group + wave) * 128u + AO_DV * blockIdx.y + lane] = o;
 }
 
+// ── attention with the positions split across workgroups ───────────────────
+// The same operations as mynah_attn_scores + mynah_attn_out, except that the
+// softmax is taken per chunk of AS_CH positions and the chunks are combined
+// afterwards (the split form of src/kernels.c:228-250). mynah_attn_split:
+// workgroup (kvh, c) computes the scores of positions c * AS_CH .. for the
+// group's query heads (same lane order as the reference dot), its chunk max
+// m_c, e_t = expf(s_t - m_c), the double sum l_c of the e_t and the partial
+// o_c = sum e_t v_t (fma chain in t order), and stores (m_c, l_c, o_c).
+// mynah_attn_combine: M = max m_c, w_c = expf(m_c - M), inv = (float)(1 /
+// sum_c w_c l_c), o = sum_c (w_c * inv) o_c in chunk order. Differences from
+// the reference are f32 rounding of the exponentials and of the order of the
+// weighted sum. Split: grid (n_kv_heads, ceil(n_ctx / AS_CH)), block 128 *
+// group; group <= 8, hd == 128. Partials: pm, pl [n_kv][nch_max][group], po
+// [n_kv][nch_max][group][128].
+#define AS_CH 32
+#define AS_MAXP 1024                                // group * chunks (n_ctx <= 4096)
+// Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
+// x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
+// head_norm_rope, with the pair (i, i + 64) rotated in registers.
+MYNAH_DEV void norm_rope_reg(float x0, float x1, float w0, float w1, float c, float sn, float eps,
+                             float &y0, float &y1) {
+#pragma clang fp contract(off)
+    const double sum = wave_sum_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
+    const float s = (float)(1.0 / sqrt(sum / 128.0 + (double)eps));
+    const float a = x0 * (s * w0), b = x1 * (s * w1);
+    y0 = a * c - b * sn;
+    y1 = b * c + a * sn;
+}
+
+extern "C" __global__ void __launch_bounds__(1024)
+mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
+                 const float *__restrict__ v_layer, const float *__restrict__ q_norm,
+                 const float *__restrict__ k_norm, const float *__restrict__ rope_cos,
+                 const float *__restrict__ rope_sin, const uint32_t *__restrict__ pos_ptr,
+                 float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po,
+                 uint32_t nch_max, uint32_t kv_dim, uint32_t group, float eps, float scale) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float qn[8][128];
+    __shared__ __attribute__((aligned(16))) float kn[128];
+    __shared__ __attribute__((aligned(16))) float vs[AS_CH][128];
+    __shared__ __attribute__((aligned(16))) float es[8][AS_CH];
+    __shared__ __attribute__((aligned(16))) float ee[8][AS_CH];
+    const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
+    const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * AS_CH;
+    if (t0 >= n_kv) return;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nthr = blockDim.x;
+    const uint32_t nw = nthr >> 6;                  // 2 * group waves
+    const bool has_pos = pos < t0 + AS_CH;
+    // Every load of the workgroup is issued before the first wait: K for the
+    // dot lanes, the V rows of the chunk, and for wave w < group query head w
+    // (wave group: the new key when this chunk holds pos) with its norm
+    // weights and the rotation of position pos.
+    const uint32_t r = lane >> 4, l = lane & 15u;
+    const uint32_t ppp = 4u * nw;                   // positions per pass
+    float kv[2][8];
+#pragma unroll
+    for (int ps = 0; ps < 2; ps++) {
+        const uint32_t t = t0 + ppp * (uint32_t)ps + 4u * wave + r;
+        const bool live = t < pos && ppp * (uint32_t)ps < AS_CH;
+        const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[ps][j] = krow[16 * j];
+    }
+    float4 vr[(AS_CH * 32 + 255) / 256];
+#pragma unroll
+    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
+        const uint32_t i = tid + nthr * (uint32_t)k;
+        const uint32_t tr = i >> 5, q4 = i & 31u, t = t0 + tr;
+        vr[k] = (i < AS_CH * 32u && t < n_kv)
+                    ? *(const float4 *)(v_layer + (size_t)t * kv_dim + (size_t)kvh * 128u + 4u * q4)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const bool qwave = wave < group, kwave = wave == group && has_pos;
+    float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
+    float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    if (qwave || kwave) {
+        const float *src = qwave ? q + (size_t)(kvh * group + wave) * 128u : kpos;
+        const float *w = qwave ? q_norm : k_norm;
+        x0 = src[lane];
+        x1 = src[lane + 64u];
+        w0 = w[lane];
+        w1 = w[lane + 64u];
+        cs = rope_cos[(size_t)pos * 64u + lane];
+        sn = rope_sin[(size_t)pos * 64u + lane];
+    }
+#pragma unroll
+    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
+        const uint32_t i = tid + nthr * (uint32_t)k;
+        if (i < AS_CH * 32u) *(float4 *)(&vs[i >> 5][4u * (i & 31u)]) = vr[k];
+    }
+    if (qwave || kwave) {
+        float y0, y1;
+        norm_rope_reg(x0, x1, w0, w1, cs, sn, eps, y0, y1);
+        float *dst = qwave ? qn[wave] : kn;
+        dst[lane] = y0;
+        dst[lane + 64u] = y1;
+        if (kwave) {
+            kpos[lane] = y0;
+            kpos[lane + 64u] = y1;
+        }
+    }
+    __syncthreads();
+    // Scores, reference dot order, into es[h][t - t0].
+#pragma unroll
+    for (int ps = 0; ps < 2; ps++) {
+        const uint32_t tl = ppp * (uint32_t)ps + 4u * wave + r, t = t0 + tl;
+        if (tl < AS_CH && t < n_kv) {
+            float kk[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) kk[j] = t < pos ? kv[ps][j] : kn[16 * j + l];
+            for (uint32_t h = 0; h < group; h++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kk[j], acc);
+                const float tt = acc + __shfl_down(acc, 8, 16);
+                const float v = tt + __shfl_down(tt, 4, 16);
+                const float w = v + __shfl_down(v, 1, 16);
+                const float dot = w + __shfl_down(w, 2, 16);
+                if (l == 0) es[h][tl] = dot * scale;
+            }
+        }
+    }
+    __syncthreads();
+    // Chunk softmax: thread (h, d) with d < AS_CH turns position d into e.
+    const uint32_t h = tid >> 7, d = tid & 127u;
+    const uint32_t tn = n_kv - t0 < AS_CH ? n_kv - t0 : AS_CH;
+    float m = -__builtin_inff();
+    if (h < group) {
+#pragma unroll
+        for (int k = 0; k < AS_CH / 4; k++) {
+            const float4 v = *(const float4 *)(&es[h][4 * k]);
+            if ((uint32_t)(4 * k) < tn) m = fmaxf(m, v.x);
+            if ((uint32_t)(4 * k + 1) < tn) m = fmaxf(m, v.y);
+            if ((uint32_t)(4 * k + 2) < tn) m = fmaxf(m, v.z);
+            if ((uint32_t)(4 * k + 3) < tn) m = fmaxf(m, v.w);
+        }
+        if (d < AS_CH) ee[h][d] = d < tn ? expf(es[h][d] - m) : 0.0f;
+    }
+    __syncthreads();
+    // Partial weighted sum (fma chain in t order) and the chunk's exp sum.
+    if (h < group) {
+        float e[AS_CH], vv[AS_CH];
+#pragma unroll
+        for (int k = 0; k < AS_CH / 4; k++) {
+            const float4 v = *(const float4 *)(&ee[h][4 * k]);
+            e[4 * k] = v.x; e[4 * k + 1] = v.y; e[4 * k + 2] = v.z; e[4 * k + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < AS_CH; t++) vv[t] = vs[t][d];
+        float o = 0.0f;
+        double lsum = 0.0;
+#pragma unroll
+        for (int t = 0; t < AS_CH; t++) {
+            if ((uint32_t)t < tn) {
+                o = __builtin_fmaf(vv[t], e[t], o);
+                lsum += (double)e[t];
+            }
+        }
+        const size_t slot = ((size_t)kvh * nch_max + c) * group + h;
+        po[slot * 128u + d] = o;
+        if (d == 0) {
+            pm[slot] = m;
+            pl[slot] = lsum;
+        }
+    }
+}
+
+// Grid n_kv_heads, block 128 * group: thread (h, d) combines the partials of
+// query head kvh * group + h, dimension d.
+extern "C" __global__ void __launch_bounds__(1024)
+mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
+                   const double *__restrict__ pl, const float *__restrict__ po,
+                   float *__restrict__ out, uint32_t nch_max, uint32_t group) {
+#pragma clang fp contract(off)
+    __shared__ float sm[AS_MAXP];
+    __shared__ double sl[AS_MAXP];
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
+    const uint32_t kvh = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t h = tid >> 7, d = tid & 127u;
+    const size_t base0 = (size_t)kvh * nch_max * group;
+    const float *pob = po + (base0 + h) * 128u + d;
+    // The first weighted partials are in flight while the maxima are reduced.
+    float pv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) pv[u] = (uint32_t)u < nch ? pob[(size_t)u * group * 128u] : 0.0f;
+    for (uint32_t i = tid; i < group * nch; i += nthr) {
+        sm[i] = pm[base0 + i];
+        sl[i] = pl[base0 + i];
+    }
+    __syncthreads();
+    float M = -__builtin_inff();
+    for (uint32_t k = 0; k < nch; k++) M = fmaxf(M, sm[k * group + h]);
+    double L = 0.0;
+    for (uint32_t k = 0; k < nch; k++) L += (double)expf(sm[k * group + h] - M) * sl[k * group + h];
+    const float inv = (float)(1.0 / L);
+    float o = 0.0f;
+    uint32_t k = 0;
+    for (; k < 8 && k < nch; k++) o = __builtin_fmaf(expf(sm[k * group + h] - M) * inv, pv[k], o);
+    for (; k + 8 <= nch; k += 8) {
+        float pw[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) pw[u] = pob[(size_t)(k + u) * group * 128u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) o = __builtin_fmaf(expf(sm[(k + u) * group + h] - M) * inv, pw[u], o);
+    }
+    for (; k < nch; k++) o = __builtin_fmaf(expf(sm[k * group + h] - M) * inv, pob[(size_t)k * group * 128u], o);
+    out[(size_t)(kvh * group + h) * 128u + d] = o;
+}
+
+
 // src/kernels.c:118-128 (the final norm before the head,
 // src/arch_qwen3.c:239): s = (float)(1 / sqrt(sum(x^2) / n + eps)) with the
 // sum in double; out = (x * s) * w. One workgroup.

@@ -162,24 +162,50 @@ MYNAH_DEV float part(const RawQ80 &o, uint32_t u, const float *xb, const float *
 // Stage the (optionally RMS-normalised) input into LDS: lx padded, ls[i / 8]
 // = sum of x[i .. i + 7]. With norm_w the staged value is the reference's
 // (x * s) * w with s = (float)(1 / sqrt(sum x^2 / n + eps)), sum in double.
-MYNAH_DEV void fast_stage(const GemvDesc &g, float *lx, float *ls, double *shd) {
-    float s = 1.0f;
+// x (or RMSNorm(x) * norm_w) into the padded LDS copy plus the 8-value run
+// sums; every x and norm-weight load is issued before the first wait (the
+// norm weights wait in lw while the sum of squares is reduced).
+MYNAH_DEV void fast_stage(const GemvDesc &g, float *lx, float *ls, float *lw, double *shd) {
+#pragma clang fp contract(off)
+    const uint32_t n4 = g.cols / 4u;
+    const float4 *x4 = (const float4 *)g.x;
     if (g.norm_w != nullptr) {
+        const float4 *w4 = (const float4 *)g.norm_w;
         double acc = 0.0;
-        for (uint32_t k = threadIdx.x; k < g.cols; k += blockDim.x) acc += (double)g.x[k] * (double)g.x[k];
-        const double sum = block_sum_d(acc, shd);
-        s = (float)(1.0 / sqrt(sum / (double)g.cols + (double)g.eps));
-    }
-    for (uint32_t i = 4u * threadIdx.x; i < g.cols; i += 4u * blockDim.x) {
-        float4 v = *(const float4 *)(g.x + i);
-        if (g.norm_w != nullptr) {
-            const float4 w = *(const float4 *)(g.norm_w + i);
-            v.x = v.x * s * w.x; v.y = v.y * s * w.y; v.z = v.z * s * w.z; v.w = v.w * s * w.w;
+#pragma unroll 4
+        for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
+            const float4 v = x4[q], w = w4[q];
+            const uint32_t i = 4u * q;
+            *(float4 *)(lx + i + 4u * (i >> 6)) = v;
+            *(float4 *)(lw + i) = w;
+            acc += (double)v.x * (double)v.x;
+            acc += (double)v.y * (double)v.y;
+            acc += (double)v.z * (double)v.z;
+            acc += (double)v.w * (double)v.w;
         }
-        *(float4 *)(lx + i + 4u * (i >> 6)) = v;
-        float r = (v.x + v.y) + (v.z + v.w);
-        r += __shfl_xor(r, 1, 64);
-        if ((threadIdx.x & 1u) == 0) ls[i / 8u] = r;
+        const double sum = block_sum_d(acc, shd);
+        const float s = (float)(1.0 / sqrt(sum / (double)g.cols + (double)g.eps));
+        for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
+            const uint32_t i = 4u * q;
+            float4 *px = (float4 *)(lx + i + 4u * (i >> 6));
+            float4 v = *px;
+            const float4 w = *(const float4 *)(lw + i);
+            v.x = v.x * s * w.x; v.y = v.y * s * w.y; v.z = v.z * s * w.z; v.w = v.w * s * w.w;
+            *px = v;
+            float r = (v.x + v.y) + (v.z + v.w);
+            r += __shfl_xor(r, 1, 64);
+            if ((threadIdx.x & 1u) == 0) ls[i / 8u] = r;
+        }
+    } else {
+#pragma unroll 4
+        for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
+            const float4 v = x4[q];
+            const uint32_t i = 4u * q;
+            *(float4 *)(lx + i + 4u * (i >> 6)) = v;
+            float r = (v.x + v.y) + (v.z + v.w);
+            r += __shfl_xor(r, 1, 64);
+            if ((threadIdx.x & 1u) == 0) ls[i / 8u] = r;
+        }
     }
 }
 
@@ -203,7 +229,7 @@ MYNAH_DEV float lane_sum(const Raw *pre, const uint8_t *__restrict__ row, uint32
 
 template <class Raw>
 MYNAH_DEV void fast_tile(const GemvDesc &g, uint32_t t, uint32_t ks, float *lx, float *ls,
-                         double *shd, float (*wp)[2][8]) {
+                         float *lw, double *shd, float (*wp)[2][8]) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t u = lane & 7u, k0 = wave % ks, tile_wave = wave / ks;
     const uint32_t row = (t - g.tile0) * (32u / ks) + 8u * tile_wave + (lane >> 3);
@@ -219,7 +245,10 @@ MYNAH_DEV void fast_tile(const GemvDesc &g, uint32_t t, uint32_t ks, float *lx, 
             if (g.w2) load(p2[i], r2, s, u, g.units);
         }
     }
-    fast_stage(g, lx, ls, shd);
+    const bool folds = k0 == 0 && u == 0 && row < g.rows;
+    const float resv = (folds && g.res && !g.w2) ? g.res[row] : 0.0f;
+    const size_t yoff = g.ypos ? (size_t)g.ypos[0] * g.ystride : 0u;
+    fast_stage(g, lx, ls, lw, shd);
     __syncthreads();
     const float v1 = group8_sum(lane_sum(p1, r1, k0, ks, S, u, g.units, lx, ls));
     const float v2 = g.w2 ? group8_sum(lane_sum(p2, r2, k0, ks, S, u, g.units, lx, ls)) : 0.0f;
@@ -234,10 +263,9 @@ MYNAH_DEV void fast_tile(const GemvDesc &g, uint32_t t, uint32_t ks, float *lx, 
         }
         float v = a;
         if (g.w2) v = a * sigmoid_ref(a) * b;
-        else if (g.res && row < g.rows) v = g.res[row] + a;
+        else if (g.res) v = resv + a;
         if (row < g.rows) {
-            float *y = g.y + (g.ypos ? (size_t)g.ypos[0] * g.ystride : 0);
-            y[row] = v;
+            g.y[yoff + row] = v;
             key = argmax_key(v, row);
         }
     }
@@ -254,10 +282,11 @@ MYNAH_DEV void fast_tile(const GemvDesc &g, uint32_t t, uint32_t ks, float *lx, 
     }
 }
 
-// grp.shape carries KS. Dynamic LDS: cols * 17/16 + cols / 8 floats.
+// grp.shape carries KS. Dynamic LDS: cols * 17/16 + cols / 8 floats, plus
+// cols for the norm weights when norm_w is set.
 extern "C" __global__ void __launch_bounds__(FG_WG)
 mynah_gemv_fast_group(const GemvGroup grp) {
-    extern __shared__ float lds_f[];
+    extern __shared__ __attribute__((aligned(16))) float lds_f[];
     __shared__ double shd[4];
     __shared__ float wp[4][2][8];
     const uint32_t t = blockIdx.x;
@@ -266,8 +295,9 @@ mynah_gemv_fast_group(const GemvGroup grp) {
     const GemvDesc &g = grp.d[i];
     float *lx = lds_f;
     float *ls = lds_f + g.cols + g.cols / 16u;
+    float *lw = ls + g.cols / 8u;
     const uint32_t ks = grp.shape;
-    if (g.type == 12u) fast_tile<RawQ4K>(g, t, ks, lx, ls, shd, wp);
-    else if (g.type == 14u) fast_tile<RawQ6K>(g, t, ks, lx, ls, shd, wp);
-    else fast_tile<RawQ80>(g, t, ks, lx, ls, shd, wp);
+    if (g.type == 12u) fast_tile<RawQ4K>(g, t, ks, lx, ls, lw, shd, wp);
+    else if (g.type == 14u) fast_tile<RawQ6K>(g, t, ks, lx, ls, lw, shd, wp);
+    else fast_tile<RawQ80>(g, t, ks, lx, ls, lw, shd, wp);
 }

@@ -201,7 +201,7 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     memset(&g, 0, sizeof g);
     g.n = 1;
     if (mynah_gemv_desc_init(&g.d[0], type, w, rows, cols, x, y) != 0) return -1;
-    return mynah_gemv_group_launch(d, &g, stream, NULL);
+    return mynah_gemv_group_launch(d, &g, stream, NULL, -1);
 }
 
 int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -277,12 +277,12 @@ static void exact_shape(uint32_t all_rows, uint32_t units, uint32_t *lk, uint32_
  * unit sums folded in order) or reordered (8-lane row blocks, KS waves
  * splitting the super-blocks of a tile). */
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
-                            uint32_t *tiles_out) {
+                            uint32_t *tiles_out, int order) {
     if (grp->n == 0 || grp->n > MYNAH_GROUP_MAX) {
         mynah_set_error("group of %u matrices", grp->n);
         return -1;
     }
-    const int exact = gemv_order == MYNAH_GEMV_EXACT;
+    const int exact = (order < 0 ? gemv_order : order) == MYNAH_GEMV_EXACT;
     uint32_t all_rows = 0, max_units = 1;
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
@@ -313,7 +313,8 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
         const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
                                      (size_t)tile_rows * (ut | 1u) +
                                      (g->norm_w ? (size_t)g->cols : 0u)) * 4u
-                                  : ((size_t)g->cols + g->cols / 16 + g->cols / 8) * 4u;
+                                  : ((size_t)g->cols + g->cols / 16 + g->cols / 8 +
+                                     (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
         if (need > lds) lds = need;
         g->tile0 = tiles;
         tiles += (g->rows + tile_rows - 1u) / tile_rows;

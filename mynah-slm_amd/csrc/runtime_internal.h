@@ -20,6 +20,8 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
     X(MYNAH_K_ATTN_SCORES, "mynah_attn_scores")        \
     X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
+    X(MYNAH_K_ATTN_SPLIT, "mynah_attn_split")          \
+    X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
     X(MYNAH_K_EMBED, "mynah_embed_row")                \
@@ -84,8 +86,10 @@ typedef struct {
 int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
                          const float *x, float *y);
 /* *tiles (optional) receives the number of workgroups, which is also the
- * length of a descriptor's argmax key array when the group has one member. */
+ * length of a descriptor's argmax key array when the group has one member.
+ * order: MYNAH_GEMV_EXACT / MYNAH_GEMV_REORDERED, or -1 for the library's
+ * current order. */
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
-                            uint32_t *tiles);
+                            uint32_t *tiles, int order);
 
 #endif

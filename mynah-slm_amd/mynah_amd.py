@@ -89,6 +89,7 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_set_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
         "mynah_hip_qwen3_n_past": (C.c_uint32, [_P]),
         "mynah_hip_qwen3_uses_graph": (C.c_int, [_P]),
+        "mynah_hip_qwen3_set_attention": (C.c_int, [_P, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -297,6 +298,9 @@ class SynthQwen3:
         return int(sum(self.table[i].nbytes for i in range(self.count)))
 
 
+ATTN_EXACT, ATTN_SPLIT = 0, 1
+
+
 class Qwen3Decoder:
     """The GPU decode state (include/mynah_decode.h) over a SynthQwen3."""
 
@@ -329,6 +333,11 @@ class Qwen3Decoder:
     @property
     def n_past(self) -> int:
         return int(lib.mynah_hip_qwen3_n_past(self.h))
+
+    def set_attention(self, mode: int) -> None:
+        """ATTN_EXACT (the reference's order) or ATTN_SPLIT (positions split
+        across workgroups, per-chunk softmax partials combined)."""
+        check(lib.mynah_hip_qwen3_set_attention(self.h, mode), "set_attention")
 
     @property
     def uses_graph(self) -> bool:

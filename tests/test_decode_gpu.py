@@ -137,3 +137,55 @@ def test_fast_order_same_tokens(M):
         assert toks == [int(t) for t in g["tokens"]]
     finally:
         M.check(M.lib.mynah_hip_set_gemv_order(0), "order")
+
+
+def test_split_attention_every_step_against_oracle(M):
+    """Split attention (per-chunk softmax partials, one launch per layer):
+    logits within 1e-4 of the oracle on every step, over chunk boundaries."""
+    shape, npre, steps = CF.QWEN3_TINY, 60, 12          # positions 60..71 cross 64
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    dec.set_attention(M.ATTN_SPLIT)
+    orc_model = O.SynthModel(shape, 0)
+    ref = O.OracleQwen3(orc_model, n_ctx)
+    ref.prefill_kv(k, v, npre)
+    tok = first
+    worst = 0.0
+    for i in range(steps):
+        a = dec.forward(tok)
+        b = ref.forward(tok)
+        err = rel_err(a, b)
+        worst = max(worst, err)
+        assert err <= TOL, f"step {i}: {err:.2e}"
+        tok = int(np.argmax(b))
+    print(f"split attention: worst logit rel err {worst:.2e}")
+
+
+def test_split_attention_graph_equals_stepwise(M):
+    shape, npre, steps = CF.QWEN3_TINY, 30, 40
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    dec.set_attention(M.ATTN_SPLIT)
+    toks, _ = dec.generate(first, steps)
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    tok, stepwise = first, []
+    for _ in range(steps):
+        lg = dec.forward(tok)
+        tok = int(np.argmax(lg))
+        stepwise.append(tok)
+    assert stepwise == toks
+
+
+def test_qwen3_06b_split_attention_same_tokens(M):
+    g = np.load(os.path.join(GOLDEN, "qwen3_06b.npz"), allow_pickle=False)
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
+    model, k, v, first, n_ctx, dec = setup(M, shape, npre, steps)
+    dec.set_attention(M.ATTN_SPLIT)
+    lg = dec.forward(first)
+    err = rel_err(lg[g["top_ids"]], g["top_vals"])
+    print(f"split attention: top-64 logits max rel err {err:.2e}")
+    assert err <= TOL
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    toks, ms = dec.generate(first, steps)
+    print(f"0.6B decode (split attention): {steps / ms * 1e3:.0f} tok/s")
+    assert toks == [int(t) for t in g["tokens"]]
