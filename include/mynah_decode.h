@@ -52,6 +52,16 @@ int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_st
 int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos);
 
 uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
+/* src/generate.c:13-86 with greedy sampling: the prompt's tokens fill the
+ * cache (all but the last without logits, the head is skipped), then
+ * n_steps greedy steps start from the last prompt token; tokens_out gets the
+ * n_steps generated ids. *prefill_ms covers the n_prompt - 1 cache-filling
+ * steps, *decode_ms the greedy steps (either may be NULL). The position
+ * advances by n_prompt - 1 + n_steps. */
+int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_prompt,
+                           uint32_t n_steps, uint32_t *tokens_out, float *prefill_ms,
+                           float *decode_ms);
+
 /* 1 when the step runs as a replayed hipGraph, 0 when launched directly. */
 int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);
 

@@ -52,17 +52,20 @@ struct mynah_qwen3 {
     dlayer *layers;
     float *k_cache, *v_cache, *rope_cos, *rope_sin;
     float *x, *q, *attn, *act, *logits, *scores;
-    uint32_t *counters;             /* token, pos, step */
+    uint32_t *counters;             /* token, pos, step, forced-token count */
+    uint32_t *forced;               /* prompt tokens replayed before greedy steps */
     unsigned long long *keys;       /* head workgroups' argmax keys */
     uint32_t n_keys;
     uint32_t sstride;               /* floats between the score rows of two heads */
     uint32_t *tokens;               /* [n_ctx] generated ids */
-    hipGraph_t graph;
-    hipGraphExec_t exec;
-    int graph_state;                /* 0 not tried, 1 ready, -1 unavailable */
-    int graph_order;                /* GEMV order the graph was captured with */
+    /* Captured steps: [STEP_FULL] with the head and argmax, [STEP_PREFILL]
+     * without the head (a prompt token whose logits nobody reads). */
+    hipGraph_t graph[2];
+    hipGraphExec_t exec[2];
+    int graph_state[2];             /* 0 not tried, 1 ready, -1 unavailable */
+    int graph_order[2];             /* GEMV order the graph was captured with */
+    int graph_attn[2];              /* attention mode the graph was captured with */
     int attn_mode;                  /* MYNAH_ATTN_EXACT or MYNAH_ATTN_SPLIT */
-    int graph_attn;                 /* attention mode the graph was captured with */
     uint32_t nch_max;               /* position chunks of the split attention */
     float *pm, *po;                 /* split-attention partials: chunk max, weighted V */
     double *pl;                     /* split-attention partials: chunk exp sums */
@@ -71,6 +74,9 @@ struct mynah_qwen3 {
 #define TOKEN(s) ((s)->counters + 0)
 #define POS(s) ((s)->counters + 1)
 #define STEP(s) ((s)->counters + 2)
+#define NFORCED(s) ((s)->counters + 3)
+
+enum { STEP_FULL = 0, STEP_PREFILL = 1 };
 
 static int fail(char *err, size_t errsz, const char *msg, const char *detail) {
     if (err && errsz) snprintf(err, errsz, "%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
@@ -115,10 +121,12 @@ static void *dalloc(size_t bytes, int *ok) {
 
 void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
-    if (s->exec) (void)hipGraphExecDestroy(s->exec);
-    if (s->graph) (void)hipGraphDestroy(s->graph);
+    for (int v = 0; v < 2; v++) {
+        if (s->exec[v]) (void)hipGraphExecDestroy(s->exec[v]);
+        if (s->graph[v]) (void)hipGraphDestroy(s->graph[v]);
+    }
     void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->q,
-                    s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->pm, s->pl,
+                    s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->forced, s->pm, s->pl,
                     s->po};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
@@ -220,6 +228,7 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->sstride = (n_ctx + 63) & ~63u;
     s->scores = (float *)dalloc((size_t)c->n_heads * s->sstride * 4, &ok);
     s->counters = (uint32_t *)dalloc(16, &ok);
+    s->forced = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
     {
         const size_t parts = (size_t)c->n_kv_heads * ((n_ctx + 31) / 32) * (c->n_heads / c->n_kv_heads);
         s->nch_max = (n_ctx + 31) / 32;
@@ -269,7 +278,7 @@ static int gemv_desc(mynah_gemv_desc *g, const dtensor *w, const float *x, float
     return mynah_gemv_desc_init(g, w->type, w->dev, w->rows, w->cols, x, y);
 }
 
-static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
+static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int variant) {
     const mynah_qwen3_shape *c = &s->c;
     const size_t per_layer = (size_t)s->n_ctx * s->kv_dim;
     uint32_t *tok = TOKEN(s), *pos = POS(s), *step = STEP(s);
@@ -354,7 +363,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         g.d[0].res = s->x;
         rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, NULL, -1);
     }
-    if (rc == 0) {
+    if (rc == 0 && variant == STEP_FULL) {
         /* The final norm (src/arch_qwen3.c:239) runs inside the head GEMV. */
         mynah_gemv_group g;
         memset(&g, 0, sizeof g);
@@ -379,7 +388,10 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st) {
         const unsigned char *tab = s->embed.dev;
         float *x = s->x;
         uint32_t dm = c->d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
-        void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs, &tab, &x, &dm, &ty, &rb};
+        const uint32_t *forced = s->forced, *nforced = NFORCED(s);
+        uint32_t vocab = c->vocab;
+        void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs, &tab, &x, &dm, &ty, &rb,
+                        &forced, &nforced, &vocab};
         rc = mynah_launch(d, MYNAH_K_ARGMAX, 1, 1, 1024, 0, st, args);
     }
     return rc;
@@ -396,47 +408,49 @@ static int embed_current(mynah_qwen3 *s, mynah_device *d) {
     return mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, d->stream, args);
 }
 
-/* Capture the step once; fall back to direct launches if capture fails. */
-static int run_step(mynah_qwen3 *s, mynah_device *d) {
+/* Capture each step variant once; fall back to direct launches if capture
+ * fails. */
+static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
     hipStream_t st = d->stream;
-    if (s->graph_state == 1 &&
-        (s->graph_order != mynah_hip_gemv_order() || s->graph_attn != s->attn_mode)) {
-        (void)hipGraphExecDestroy(s->exec);
-        (void)hipGraphDestroy(s->graph);
-        s->exec = NULL;
-        s->graph = NULL;
-        s->graph_state = 0;
+    if (s->graph_state[v] == 1 &&
+        (s->graph_order[v] != mynah_hip_gemv_order() || s->graph_attn[v] != s->attn_mode)) {
+        (void)hipGraphExecDestroy(s->exec[v]);
+        (void)hipGraphDestroy(s->graph[v]);
+        s->exec[v] = NULL;
+        s->graph[v] = NULL;
+        s->graph_state[v] = 0;
     }
-    if (s->graph_state == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
-        s->graph_state = -1;
+    if (s->graph_state[v] == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
+        s->graph_state[v] = -1;
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-            const int rc = enqueue_step(s, d, st);
+            const int rc = enqueue_step(s, d, st, v);
             hipGraph_t g = NULL;
             const hipError_t e = hipStreamEndCapture(st, &g);
             if (rc == 0 && e == hipSuccess && g != NULL &&
-                hipGraphInstantiate(&s->exec, g, NULL, NULL, 0) == hipSuccess) {
-                s->graph = g;
-                s->graph_state = 1;
-                s->graph_order = mynah_hip_gemv_order();
-                s->graph_attn = s->attn_mode;
+                hipGraphInstantiate(&s->exec[v], g, NULL, NULL, 0) == hipSuccess) {
+                s->graph[v] = g;
+                s->graph_state[v] = 1;
+                s->graph_order[v] = mynah_hip_gemv_order();
+                s->graph_attn[v] = s->attn_mode;
             } else if (g != NULL) {
                 (void)hipGraphDestroy(g);
             }
         }
         (void)hipGetLastError();
     }
-    if (s->graph_state == 1) {
-        if (hipGraphLaunch(s->exec, st) != hipSuccess) {
+    if (s->graph_state[v] == 1) {
+        if (hipGraphLaunch(s->exec[v], st) != hipSuccess) {
             mynah_set_error("hipGraphLaunch failed");
             return -1;
         }
         return 0;
     }
-    return enqueue_step(s, d, st);
+    return enqueue_step(s, d, st, v);
 }
 
-static int set_counters(mynah_qwen3 *s, mynah_device *d, uint32_t token, uint32_t step) {
-    uint32_t v[3] = {token, s->n_past, step};
+static int set_counters(mynah_qwen3 *s, mynah_device *d, uint32_t token, uint32_t step,
+                        uint32_t n_forced) {
+    uint32_t v[4] = {token, s->n_past, step, n_forced};
     if (hipMemcpyAsync(s->counters, v, sizeof v, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
         hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("counter upload failed");
@@ -456,7 +470,8 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
         mynah_set_error("token %u out of range", token);
         return -1;
     }
-    if (set_counters(s, d, token, 0) != 0 || embed_current(s, d) != 0 || run_step(s, d) != 0)
+    if (set_counters(s, d, token, 0, 0) != 0 || embed_current(s, d) != 0 ||
+        run_step(s, d, STEP_FULL) != 0)
         return -1;
     s->n_past++;
     if (logits && hipMemcpyAsync(logits, s->logits, (size_t)s->c.vocab * 4,
@@ -471,44 +486,69 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
     return 0;
 }
 
-int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
-                             uint32_t *tokens_out, float *ms) {
+int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_prompt,
+                           uint32_t n_steps, uint32_t *tokens_out, float *prefill_ms,
+                           float *decode_ms) {
     mynah_device *d = mynah_dev();
-    if (d == NULL || s == NULL || tokens_out == NULL) return -1;
-    if (n_steps == 0 || n_steps > s->n_ctx - s->n_past) {
-        mynah_set_error("%u steps do not fit the context (%u of %u used)", n_steps, s->n_past,
-                        s->n_ctx);
+    if (d == NULL || s == NULL || prompt == NULL || tokens_out == NULL || n_prompt == 0) {
+        mynah_set_error("bad prompt arguments");
         return -1;
     }
-    if (first_token >= s->c.vocab) {
-        mynah_set_error("token %u out of range", first_token);
+    if (n_steps == 0 || n_prompt - 1u > s->n_ctx - s->n_past ||
+        n_steps > s->n_ctx - s->n_past - (n_prompt - 1u)) {
+        mynah_set_error("%u prompt tokens and %u steps do not fit the context (%u of %u used)",
+                        n_prompt, n_steps, s->n_past, s->n_ctx);
         return -1;
     }
-    if (set_counters(s, d, first_token, 0) != 0) return -1;
-    hipEvent_t a = NULL, b = NULL;
-    if (ms && (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)) {
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= s->c.vocab) {
+            mynah_set_error("token %u out of range", prompt[i]);
+            return -1;
+        }
+    if (n_prompt > 1 &&
+        hipMemcpy(s->forced, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        mynah_set_error("prompt upload failed");
+        return -1;
+    }
+    if (set_counters(s, d, prompt[0], 0, n_prompt > 1 ? n_prompt : 0) != 0) return -1;
+    hipEvent_t a = NULL, m = NULL, b = NULL;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&m) != hipSuccess ||
+        hipEventCreate(&b) != hipSuccess) {
         mynah_set_error("hipEventCreate failed");
+        if (a) (void)hipEventDestroy(a);
+        if (m) (void)hipEventDestroy(m);
         return -1;
     }
-    int rc = 0;
-    if (ms) (void)hipEventRecord(a, d->stream);
-    rc = embed_current(s, d);
-    for (uint32_t i = 0; i < n_steps && rc == 0; i++) rc = run_step(s, d);
-    if (ms) (void)hipEventRecord(b, d->stream);
+    (void)hipEventRecord(a, d->stream);
+    int rc = embed_current(s, d);
+    /* src/generate.c:33-36: every prompt token but the last only fills the
+     * cache; its logits are never produced. */
+    for (uint32_t i = 0; i + 1 < n_prompt && rc == 0; i++) rc = run_step(s, d, STEP_PREFILL);
+    (void)hipEventRecord(m, d->stream);
+    for (uint32_t i = 0; i < n_steps && rc == 0; i++) rc = run_step(s, d, STEP_FULL);
+    (void)hipEventRecord(b, d->stream);
     if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("decode failed");
         rc = -1;
     }
-    if (rc == 0 && ms) (void)hipEventElapsedTime(ms, a, b);
-    if (a) (void)hipEventDestroy(a);
-    if (b) (void)hipEventDestroy(b);
+    if (rc == 0 && prefill_ms) (void)hipEventElapsedTime(prefill_ms, a, m);
+    if (rc == 0 && decode_ms) (void)hipEventElapsedTime(decode_ms, m, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(m);
+    (void)hipEventDestroy(b);
     if (rc != 0) return -1;
-    s->n_past += n_steps;
-    if (hipMemcpy(tokens_out, s->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    s->n_past += n_prompt - 1u + n_steps;
+    if (hipMemcpy(tokens_out, s->tokens + (n_prompt - 1u), (size_t)n_steps * 4,
+                  hipMemcpyDeviceToHost) != hipSuccess) {
         mynah_set_error("token download failed");
         return -1;
     }
     return 0;
+}
+
+int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
+                             uint32_t *tokens_out, float *ms) {
+    return mynah_hip_qwen3_prompt(s, &first_token, 1, n_steps, tokens_out, NULL, ms);
 }
 
 int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos) {
@@ -535,7 +575,7 @@ void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
     if (s) s->n_past = 0;
 }
 
-int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) { return s ? s->graph_state == 1 : 0; }
+int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) { return s ? s->graph_state[STEP_FULL] == 1 : 0; }
 
 int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode) {
     if (s == NULL || (mode != MYNAH_ATTN_EXACT && mode != MYNAH_ATTN_SPLIT)) {

@@ -539,16 +539,19 @@ MYNAH_DEV void embed_group(const uint8_t *__restrict__ table, uint32_t token, fl
 
 // src/sampler.c:122-129 finishes here: each workgroup of the head GEMV left
 // one 64-bit key (orderable logit << 32 | ~row) for the first maximum of its
-// rows; the largest key is the first index of the maximum logit. Writes the
-// token, appends it to tokens[step], advances pos and step (the reference's
-// n_past++), and dequantises the token's embedding row into x for the next
-// step (src/arch_qwen3.c:160-176). One workgroup.
+// rows; the largest key is the first index of the maximum logit. Appends it
+// to tokens[step], advances pos and step (the reference's n_past++), picks
+// the next token — forced[step + 1] while step + 1 < n_forced[0] (a prompt
+// being prefilled, src/generate.c:13-86), the argmax after — and
+// dequantises its embedding row into x for the next step
+// (src/arch_qwen3.c:160-176). One workgroup.
 extern "C" __global__ void __launch_bounds__(1024)
 mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_keys,
                      uint32_t *__restrict__ token, uint32_t *__restrict__ tokens,
                      uint32_t *__restrict__ pos, uint32_t *__restrict__ step, uint32_t max_steps,
                      const uint8_t *__restrict__ table, float *__restrict__ x, uint32_t d,
-                     uint32_t type, uint32_t row_bytes) {
+                     uint32_t type, uint32_t row_bytes, const uint32_t *__restrict__ forced,
+                     const uint32_t *__restrict__ n_forced, uint32_t vocab) {
     __shared__ unsigned long long wk[16];
     __shared__ uint32_t sidx;
     unsigned long long best = 0ull;
@@ -559,12 +562,14 @@ mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_key
     if (threadIdx.x == 0) {
         for (uint32_t k = 1; k < (blockDim.x + 63u) / 64u; k++) best = wk[k] > best ? wk[k] : best;
         const uint32_t idx = ~(uint32_t)(best & 0xffffffffull);
-        token[0] = idx;
         const uint32_t s = step[0];
+        uint32_t next = s + 1u < n_forced[0] ? forced[s + 1u] : idx;
+        if (next >= vocab) next = 0u;       // no keys (a prefill step) and nothing forced
+        token[0] = next;
         if (s < max_steps) tokens[s] = idx;
         step[0] = s + 1u;
         pos[0] = pos[0] + 1u;
-        sidx = idx;
+        sidx = next;
     }
     __syncthreads();
     const uint32_t idx = sidx;

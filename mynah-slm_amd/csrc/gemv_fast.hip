@@ -172,7 +172,6 @@ MYNAH_DEV void fast_stage(const GemvDesc &g, float *lx, float *ls, float *lw, do
     if (g.norm_w != nullptr) {
         const float4 *w4 = (const float4 *)g.norm_w;
         double acc = 0.0;
-#pragma unroll 4
         for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
             const float4 v = x4[q], w = w4[q];
             const uint32_t i = 4u * q;
@@ -197,7 +196,6 @@ MYNAH_DEV void fast_stage(const GemvDesc &g, float *lx, float *ls, float *lw, do
             if ((threadIdx.x & 1u) == 0) ls[i / 8u] = r;
         }
     } else {
-#pragma unroll 4
         for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
             const float4 v = x4[q];
             const uint32_t i = 4u * q;

@@ -5,5 +5,6 @@
 #include "dequant.hip"
 #include "gemv_exact.hip"
 #include "gemv_fast.hip"
+#include "gemm_exact.hip"
 #include "decode.hip"
 #include "copy.hip"

@@ -2,12 +2,11 @@
  *
  * Replaces ingot_matmat (third_party/ingot/src/generic.c:107-124) and the
  * per-type batched kernels (kernels.c:1742-1751, 2627-2648). Exact f32 for
- * every width, like the reference's exact path.
- *
- * This form runs the exact GEMV once per token in the batched reference's own
- * summation order (natural weight order per 256-value unit, kernels.c:1017-
- * 1039 and 2635-2648), so every output is bit-identical to ingot's exact
- * matmat; tokens == 1 is the matvec, as in the reference (kernels.c:1726).
+ * every width, like the reference's exact path: the tiled kernel of
+ * gemm_exact.hip keeps the batched reference's own summation order (natural
+ * weight order per 256-value unit, kernels.c:1017-1039 and 2635-2648), so
+ * every output is bit-identical to ingot's exact matmat. tokens == 1 is the
+ * matvec, as in the reference (kernels.c:1726); the callers route it.
  *
  * SPDX-License-Identifier: MIT */
 #include "runtime_internal.h"
@@ -22,9 +21,20 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
         mynah_set_error("batched matmat needs cols to be a multiple of 256");
         return -1;
     }
-    for (size_t t = 0; t < tokens; t++) {
-        if (mynah_gemv_seq_launch(d, type, w, rows, cols, x + t * cols, y + t * rows, stream) != 0)
-            return -1;
+    if (tokens == 0 || tokens > 0xffffffffu || rb > 0xffffffffu) {
+        mynah_set_error("bad token count");
+        return -1;
     }
-    return 0;
+    if (((uintptr_t)x & 15u) != 0 || (type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) ||
+        ((uintptr_t)w & 1u) != 0) {
+        mynah_set_error("misaligned operand for the batched GEMM");
+        return -1;
+    }
+    const int k = type == MYNAH_Q4_K   ? MYNAH_K_Q4K_GEMM
+                  : type == MYNAH_Q6_K ? MYNAH_K_Q6K_GEMM
+                                       : MYNAH_K_Q80_GEMM;
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, t32 = (uint32_t)tokens, rb32 = (uint32_t)rb;
+    void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32};
+    return mynah_launch(d, k, (unsigned)((rows + 63) / 64), (unsigned)((tokens + 63) / 64), 256, 0,
+                        stream, args);
 }

@@ -16,6 +16,9 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_Q4K_EXACT_SEQ, "mynah_q4k_gemv_exact_seq") \
     X(MYNAH_K_Q6K_EXACT_SEQ, "mynah_q6k_gemv_exact_seq") \
     X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq") \
+    X(MYNAH_K_Q4K_GEMM, "mynah_q4k_gemm_exact")        \
+    X(MYNAH_K_Q6K_GEMM, "mynah_q6k_gemm_exact")        \
+    X(MYNAH_K_Q80_GEMM, "mynah_q80_gemm_exact")        \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
     X(MYNAH_K_ATTN_SCORES, "mynah_attn_scores")        \

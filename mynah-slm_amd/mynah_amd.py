@@ -90,6 +90,8 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_n_past": (C.c_uint32, [_P]),
         "mynah_hip_qwen3_uses_graph": (C.c_int, [_P]),
         "mynah_hip_qwen3_set_attention": (C.c_int, [_P, C.c_int]),
+        "mynah_hip_qwen3_prompt": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, _P,
+                                             C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -334,6 +336,16 @@ class Qwen3Decoder:
     def n_past(self) -> int:
         return int(lib.mynah_hip_qwen3_n_past(self.h))
 
+    def prompt(self, tokens, steps: int):
+        """Prefill the prompt (all but its last token, no head), then `steps`
+        greedy steps; returns (generated ids, prefill ms, decode ms)."""
+        p = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(steps, np.uint32)
+        pm, dm = C.c_float(0.0), C.c_float(0.0)
+        check(lib.mynah_hip_qwen3_prompt(self.h, ptr(p), p.size, steps, ptr(out), C.byref(pm),
+                                         C.byref(dm)), "prompt")
+        return [int(t) for t in out], float(pm.value), float(dm.value)
+
     def set_attention(self, mode: int) -> None:
         """ATTN_EXACT (the reference's order) or ATTN_SPLIT (positions split
         across workgroups, per-chunk softmax partials combined)."""
@@ -358,10 +370,14 @@ class Qwen3Decoder:
             pass
 
 
+def synth_uniform(seed: int, n: int, bound: int) -> np.ndarray:
+    """n integers uniform in [0, bound) from the shared generator."""
+    out = np.empty(n, np.uint32)
+    check(lib.mynah_synth_uniform_u32(seed, n, bound, ptr(out)), "uniform")
+    return out
+
+
 def first_token(config_seed: int, vocab: int) -> int:
     """The first decode token of a config (uniform over the vocabulary)."""
     import configs
-    out = np.empty(1, np.uint32)
-    check(lib.mynah_synth_uniform_u32(substream(config_seed, configs.TOKEN_SEED_INDEX), 1, vocab,
-                                      ptr(out)), "uniform")
-    return int(out[0])
+    return int(synth_uniform(substream(config_seed, configs.TOKEN_SEED_INDEX), 1, vocab)[0])

@@ -189,3 +189,33 @@ def test_qwen3_06b_split_attention_same_tokens(M):
     toks, ms = dec.generate(first, steps)
     print(f"0.6B decode (split attention): {steps / ms * 1e3:.0f} tok/s")
     assert toks == [int(t) for t in g["tokens"]]
+
+
+def test_prompt_prefill_equals_stepwise(M):
+    """Prompt prefill (cache-filling steps without the head) then greedy
+    steps gives the same ids as feeding the prompt through forward() and
+    generating from its last token, and the oracle's greedy run."""
+    shape, steps = CF.QWEN3_TINY, 12
+    model = M.SynthQwen3(shape, 0)
+    prompt = [int(t) for t in M.synth_uniform(M.substream(5, 1), 9, shape.vocab)]
+    n_ctx = len(prompt) + steps + 2
+    for attn in (M.ATTN_EXACT, M.ATTN_SPLIT):
+        dec = M.Qwen3Decoder(model, n_ctx)
+        dec.set_attention(attn)
+        got, pre_ms, dec_ms = dec.prompt(prompt, steps)
+        assert dec.n_past == len(prompt) - 1 + steps
+        dec.reset()
+        for t in prompt[:-1]:
+            dec.forward(t, want_logits=False)
+        ref, _ = dec.generate(prompt[-1], steps)
+        assert got == ref
+    orc_model = O.SynthModel(shape, 0)
+    orc = O.OracleQwen3(orc_model, n_ctx)
+    lg = None
+    for t in prompt:
+        lg = orc.forward(t)
+    tok, want = int(np.argmax(lg)), []
+    for _ in range(steps):
+        want.append(tok)
+        tok = int(np.argmax(orc.forward(tok)))
+    assert got == want

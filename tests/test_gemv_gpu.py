@@ -132,6 +132,31 @@ def test_matmat_against_oracle(M, qtype):
                           bits(M.matvec(qtype, w, rows, cols, x[:cols])))
 
 
+@pytest.mark.parametrize("qtype,rows,cols,tokens", [(12, 100, 2048, 70), (14, 72, 1536, 65),
+                                                    (8, 130, 512, 3), (12, 64, 256, 64),
+                                                    (14, 1, 256, 2)])
+def test_gemm_ragged_tiles(M, qtype, rows, cols, tokens):
+    """The tiled batched GEMM on shapes that leave partial row and token
+    tiles, bit-identical to the batched reference order."""
+    w, _ = case(M, qtype, rows, cols, seed=rows + tokens)
+    x = M.synth_normal(7 + tokens, tokens * cols)
+    assert same(M.matmat(qtype, w, rows, cols, x, tokens), O.matmat(qtype, w, rows, cols, x, tokens))
+
+
+@pytest.mark.parametrize("name", ["q4k_kv_2048x2048", "q6k_down_2048x6144"])
+def test_gemm_configs3_shapes(M, name):
+    """configs[3] prefill GEMMs (512 tokens) against the oracle's threaded
+    batched path, bit for bit."""
+    m = next(m for m in CF.C4 if m.name == name)
+    i = CF.C4.index(m)
+    ws, xs = CF.matrix_seeds(M.substream, 0, i)
+    w, _ = case(M, m.qtype, m.rows, m.cols, seed=ws)
+    x = M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i), CF.C4_TOKENS * m.cols)
+    O.orc.orc_threads_init(0)
+    ref = O.matmat(m.qtype, w, m.rows, m.cols, x, CF.C4_TOKENS, threaded=True)
+    assert same(M.matmat(m.qtype, w, m.rows, m.cols, x, CF.C4_TOKENS), ref)
+
+
 def test_matmat_golden(M):
     g = np.load(os.path.join(GOLDEN, "matmat.npz"), allow_pickle=False)
     for t, rows, cols, tokens in ((12, 64, 2048, 16), (14, 32, 6144, 8), (8, 40, 1024, 5)):
