@@ -15,6 +15,12 @@ rocprofv3 PMC counters (profiles/traffic.json), when present.
 as-built kernels with the reference's 4*nth row-chunk threading, bit-identical
 to it) on the same sweep on this host's cores.
 
+Beside the metric line's value: `decode` (configs[2], Qwen3-0.6B greedy
+decode tok/s in three numerics modes, tokens checked against the compiled
+reference's), `prefill_gemm` (configs[3], the exact batched GEMM at 512
+tokens), `qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
+greedy steps on Qwen3-4B) and `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 from __future__ import annotations
@@ -30,6 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "mynah-slm_amd"))
 
 METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak); Qwen3 batch-1 decode tok/s, 1 GPU"
 PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
 MALL_BYTES = 256 << 20
 
 
@@ -131,6 +138,71 @@ def gpu_decode(M, CF):
     return out
 
 
+def gpu_prefill_gemm(M, CF, reps: int = 5):
+    """the prefill GEMMs at Qwen3-1.7B shapes, 512 tokens, in the
+    exact batched order (bit-identical to the reference's exact matmat)."""
+    out, tot_flop, tot_ms = {}, 0, 0.0
+    for i, m in enumerate(CF.C4):
+        wseed, _ = CF.matrix_seeds(M.substream, 0, i)
+        w = M.DeviceBuffer.from_array(M.synth_blocks(m.qtype, wseed, m.rows, m.cols))
+        x = M.DeviceBuffer.from_array(M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i),
+                                                     CF.C4_TOKENS * m.cols))
+        y = M.DeviceBuffer(4 * m.rows * CF.C4_TOKENS)
+        M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
+        M.sync()
+        a, b = M.Event(), M.Event()
+        a.record()
+        for _ in range(reps):
+            M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
+        b.record()
+        M.sync()
+        ms = a.elapsed_ms(b) / reps
+        flop = 2 * m.rows * m.cols * CF.C4_TOKENS
+        tot_flop += flop
+        tot_ms += ms
+        out[m.name] = {"ms": round(ms, 4), "tflop_s": round(flop / ms / 1e9, 2)}
+        for buf in (w, x, y):
+            buf.free()
+    return {"workload": "configs[3]: Q4_K 4096/2048/2048/6144/6144 x 2048 and Q6_K 2048 x 6144, "
+                        "512 tokens, exact batched order",
+            "total_ms": round(tot_ms, 4), "flop": tot_flop,
+            "tflop_s": round(tot_flop / tot_ms / 1e9, 2),
+            "peak_tflop_s_fp32": PEAK_FP32_TFLOPS, "frac_of_fp32_peak": round(tot_flop / tot_ms / 1e9 / PEAK_FP32_TFLOPS, 4),
+            "note": "one mul and one add per product (the reference's roundings): the "
+                    "non-packed VALU issue rate bounds this order near 40 TFLOP/s",
+            "per_matrix": out}
+
+
+def gpu_qwen3_4b(M, CF):
+    """Qwen3-4B random-init Q4_K_M mix, a 2048-token prompt of
+    uniform ids prefilled step by step (no head on cache-filling steps, as the
+    reference), then 256 greedy steps; tok/s as the reference's timing.c
+    defines them (prompt tokens / prefill time, generated tokens / decode time)."""
+    shape = CF.QWEN3_4B
+    model = M.SynthQwen3(shape, 0)
+    prompt = CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)
+    out = {"model": "Qwen3-4B random-init Q4_K_M mix", "prompt": int(prompt.size),
+           "steps": CF.C5_STEPS, "weight_bytes": model.weight_bytes()}
+    old = M.lib.mynah_hip_gemv_order()
+    try:
+        for order, attn, name in ((0, M.ATTN_EXACT, "exact"),
+                                  (1, M.ATTN_SPLIT, "reordered_gemv_split_attention")):
+            M.check(M.lib.mynah_hip_set_gemv_order(order), "order")
+            dec = M.Qwen3Decoder(model, int(prompt.size) + CF.C5_STEPS + 1)
+            dec.set_attention(attn)
+            dec.prompt(prompt[:4], 4)                    # warm-up and graph captures
+            dec.reset()
+            toks, pre_ms, dec_ms = dec.prompt(prompt, CF.C5_STEPS)
+            out[name] = {"prefill_tok_s": round(prompt.size / (pre_ms * 1e-3), 1),
+                         "decode_tok_s": round(CF.C5_STEPS / (dec_ms * 1e-3), 1),
+                         "prefill_ms": round(pre_ms, 2), "decode_ms": round(dec_ms, 2),
+                         "first_tokens": toks[:4]}
+            dec.close()
+    finally:
+        M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
+    return out
+
+
 def cpu_baseline(CF, seconds: float = 10.0):
     """The CPU oracle on the same sweep, all of this host's cores (<= 16)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -200,6 +272,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-4b", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-4b-e2e", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the configs[2] decode section, printed as one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
@@ -232,6 +306,16 @@ def main() -> int:
     if not args.no_decode:
         log("[bench] configs[2] decode")
         decode = gpu_decode(M, CF)
+
+    prefill = None
+    if not args.no_prefill:
+        log("[bench] configs[3] prefill GEMM")
+        prefill = gpu_prefill_gemm(M, CF)
+
+    e2e_4b = None
+    if not args.no_4b_e2e:
+        log("[bench] configs[4] Qwen3-4B end to end")
+        e2e_4b = gpu_qwen3_4b(M, CF)
 
     extra_4b = None
     if not args.no_4b:
@@ -277,6 +361,8 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "decode": decode,
+        "prefill_gemm": prefill,
+        "qwen3_4b_end_to_end": e2e_4b,
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
     }

@@ -8,6 +8,7 @@ Seed scheme (all derived from a config seed s, 0 for every configuration):
   * Qwen3 KV prefill, layer l:   K from substream(kv, 2 l), V from substream(kv, 2 l + 1),
                                  kv = substream(s, 1 << 20)
   * Qwen3 first decode token:    uniform over the vocabulary from substream(s, 1 << 21)
+                                 (configs[4]'s prompt: the first 2048 values of that stream)
   * prefill activations (C4):    X from substream(s, 1 << 22 + i) for matrix i
 """
 from __future__ import annotations
@@ -77,6 +78,11 @@ QWEN3_TINY = Qwen3Shape(3, 512, 768, 4, 2, 128, 4096)
 C3_PREFILL = 512      # KV positions prefilled with N(0, 1)
 C3_STEPS = 64         # greedy steps the token parity covers
 
+C5_PROMPT = 2048      # prompt tokens, uniform over the vocabulary
+C5_STEPS = 256        # greedy steps after the prompt
+C5_GOLDEN_PROMPT = 8  # the prefix the compiled reference's golden run covers
+C5_GOLDEN_STEPS = 8
+
 MATRIX_SEED_STRIDE = 2
 KV_SEED_INDEX = 1 << 20
 TOKEN_SEED_INDEX = 1 << 21
@@ -100,3 +106,10 @@ def kv_prefill(substream, normal, shape: Qwen3Shape, config_seed: int, n: int):
         k[layer] = normal(substream(kv_seed, 2 * layer), n * kvd)
         v[layer] = normal(substream(kv_seed, 2 * layer + 1), n * kvd)
     return k, v
+
+
+def c5_prompt(uniform, substream, vocab: int, n: int = C5_PROMPT, config_seed: int = 0):
+    """configs[4]'s prompt: n ids uniform over the vocabulary (the stream whose
+    first value is the decode configs' first token); `uniform(seed, n, bound)`
+    is the shared generator's uniform vector."""
+    return uniform(substream(config_seed, TOKEN_SEED_INDEX), n, vocab)

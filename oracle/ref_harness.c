@@ -142,3 +142,42 @@ int ref_qwen3_greedy(const char *path, const float *k_prefill, const float *v_pr
     mynah_slm_free(m);
     return rc;
 }
+
+/* src/generate.c:13-86 with greedy sampling: the prompt's tokens but the
+ * last fill the cache without logits, then n_steps greedy steps start from
+ * the last prompt token. logits_first receives the logits of that first step
+ * (the last prompt token). */
+int ref_qwen3_prompt_greedy(const char *path, const uint32_t *prompt, uint32_t n_prompt,
+                            uint32_t n_steps, uint32_t n_ctx, int threads, uint32_t *tokens_out,
+                            float *logits_first, char *err, size_t errsz) {
+    mynah_slm_threads_init(threads);
+    mynah_slm_model_t *m = mynah_slm_load(path, err, errsz);
+    if (m == NULL) return -1;
+    mynah_slm_state st;
+    if (mynah_slm_state_init(&st, m, n_ctx, err, errsz) != 0) {
+        mynah_slm_free(m);
+        return -1;
+    }
+    const mynah_slm_config *c = mynah_slm_model_config(m);
+    mynah_slm_sampler_params p;
+    memset(&p, 0, sizeof p);
+    p.temp = 0.0f;
+    p.top_p = 1.0f;
+    p.repeat_penalty = 1.0f;
+    mynah_slm_sampler *sam = mynah_slm_sampler_new(&p, c->vocab_size);
+    int rc = sam ? 0 : -1;
+    for (uint32_t i = 0; i + 1 < n_prompt && rc == 0; i++)
+        if (mynah_slm_forward(&st, prompt[i], NULL) != 0) rc = -1;
+    uint32_t tok = prompt[n_prompt - 1];
+    for (uint32_t i = 0; i < n_steps && rc == 0; i++) {
+        if (mynah_slm_forward(&st, tok, st.logits) != 0) { rc = -1; break; }
+        if (i == 0 && logits_first) memcpy(logits_first, st.logits, c->vocab_size * sizeof(float));
+        tok = mynah_slm_sample(sam, st.logits);
+        tokens_out[i] = tok;
+    }
+    if (rc != 0) snprintf(err, errsz, "forward failed");
+    if (sam) mynah_slm_sampler_free(sam);
+    mynah_slm_state_free(&st);
+    mynah_slm_free(m);
+    return rc;
+}

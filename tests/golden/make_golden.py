@@ -18,6 +18,9 @@ records a SHA-256 of the input bytes so generator drift is detected):
   qwen3_tiny.npz     3-layer model: 32 greedy steps, first-step logits
   qwen3_06b.npz      configs[2]: 0.6B, KV prefill 512, 64 greedy steps,
                      first-step logits' top 64 and the SHA-256 of all of them
+  qwen3_4b_prompt.npz  configs[4]'s model (Qwen3-4B): the first 8 prompt ids,
+                     prefill + 8 greedy steps, the first step's logits' top 64
+                     (`--only c5` writes just this file)
 """
 from __future__ import annotations
 
@@ -59,6 +62,19 @@ def ref_dequant(ref, t, w, rows, cols):
     y = np.empty(rows * cols, np.float32)
     assert ref.ref_dequant_matrix(t, O.ptr(w), rows, cols, O.ptr(y)) == 0
     return y
+
+
+def golden_c5(ref) -> None:
+    shape = CF.QWEN3_4B
+    model = O.SynthModel(shape, 0)
+    prompt = CF.c5_prompt(O.uniform, O.substream, shape.vocab, CF.C5_GOLDEN_PROMPT)
+    steps = CF.C5_GOLDEN_STEPS
+    toks, lg = O.ref_prompt_greedy(ref, model, prompt, steps, CF.C5_GOLDEN_PROMPT + steps + 1)
+    top = np.argsort(-lg, kind="stable")[:64]
+    np.savez_compressed(os.path.join(HERE, "qwen3_4b_prompt.npz"), prompt=prompt.astype(np.uint32),
+                        tokens=np.array(toks, np.uint32), top_ids=top.astype(np.uint32),
+                        top_vals=lg[top], logits0_sha=np.array(sha(lg)),
+                        blob_sha=np.array(sha(model.blob)))
 
 
 def main() -> int:
@@ -156,4 +172,9 @@ def main() -> int:
 
 
 if __name__ == "__main__":
+    if sys.argv[1:] == ["--only", "c5"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_c5(r)
+        sys.exit(0)
     sys.exit(main())

@@ -102,6 +102,8 @@ def load_ref():
                                            C.c_char_p, _SZ]),
         "ref_qwen3_greedy": (C.c_int, [C.c_char_p, _P, _P, C.c_uint32, C.c_uint32, C.c_uint32,
                                        C.c_uint32, C.c_int, _P, _P, C.c_char_p, _SZ]),
+        "ref_qwen3_prompt_greedy": (C.c_int, [C.c_char_p, _P, C.c_uint32, C.c_uint32, C.c_uint32,
+                                              C.c_int, _P, _P, C.c_char_p, _SZ]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -124,6 +126,12 @@ def blocks(qtype: int, seed: int, rows: int, cols: int) -> np.ndarray:
     e, b = BLOCK[qtype]
     out = np.empty(rows * (cols // e) * b, np.uint8)
     assert orc.mynah_synth_blocks(qtype, seed, 0, rows, cols, ptr(out), 0) == 0
+    return out
+
+
+def uniform(seed: int, n: int, bound: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    assert orc.mynah_synth_uniform_u32(seed, n, bound, ptr(out)) == 0
     return out
 
 
@@ -248,6 +256,23 @@ def first_token(config_seed: int, vocab: int) -> int:
     out = np.empty(1, np.uint32)
     assert orc.mynah_synth_uniform_u32(substream(config_seed, 1 << 21), 1, vocab, ptr(out)) == 0
     return int(out[0])
+
+
+def ref_prompt_greedy(ref, model: SynthModel, prompt, steps, n_ctx, threads=0):
+    """The compiled reference's prompt prefill + greedy loop on the same model."""
+    p = np.ascontiguousarray(prompt, np.uint32)
+    tokens = np.zeros(steps, np.uint32)
+    logits = np.zeros(model.shape.vocab, np.float32)
+    err = C.create_string_buffer(512)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf").encode()
+        rc = ref.ref_write_qwen3_gguf(path, C.byref(model.c_shape), model.table, model.count,
+                                      ptr(model.blob), n_ctx, err, 512)
+        assert rc == 0, err.value
+        rc = ref.ref_qwen3_prompt_greedy(path, ptr(p), p.size, steps, n_ctx, threads,
+                                         ptr(tokens), ptr(logits), err, 512)
+        assert rc == 0, err.value
+    return [int(t) for t in tokens], logits
 
 
 def ref_greedy(ref, model: SynthModel, k, v, n_prefill, first, steps, n_ctx, threads=0):

@@ -219,3 +219,33 @@ def test_prompt_prefill_equals_stepwise(M):
         want.append(tok)
         tok = int(np.argmax(orc.forward(tok)))
     assert got == want
+
+
+def test_qwen3_4b_prompt_prefix(M):
+    """configs[4]'s model (Qwen3-4B, 36 layers, group 4): the first 8 prompt
+    ids, prefill + 8 greedy steps, against the compiled reference's run: the
+    first step's top-64 logits within 1e-4 and the same ids, in both
+    attention modes."""
+    g = np.load(os.path.join(GOLDEN, "qwen3_4b_prompt.npz"), allow_pickle=False)
+    shape = CF.QWEN3_4B
+    print(f"[case] Qwen3-4B prompt prefix", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    prompt = [int(t) for t in g["prompt"]]
+    assert prompt == [int(t) for t in CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab,
+                                                   CF.C5_GOLDEN_PROMPT)]
+    steps = int(g["tokens"].size)
+    want = [int(t) for t in g["tokens"]]
+    for attn in (M.ATTN_EXACT, M.ATTN_SPLIT):
+        dec = M.Qwen3Decoder(model, len(prompt) + steps + 1)
+        dec.set_attention(attn)
+        for t in prompt[:-1]:
+            dec.forward(t, want_logits=False)
+        lg = dec.forward(prompt[-1])
+        err = rel_err(lg[g["top_ids"]], g["top_vals"])
+        print(f"4B attention mode {attn}: top-64 logits max rel err {err:.2e}")
+        assert err <= TOL
+        assert int(np.argmax(lg)) == want[0]
+        dec.reset()
+        got, _, _ = dec.prompt(prompt, steps)
+        assert got == want
+        dec.close()

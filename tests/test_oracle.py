@@ -265,3 +265,26 @@ def test_argument_guards():
     assert f(12, O.ptr(w), 2, 0, O.ptr(x), O.ptr(y)) == -1
     assert f(12, O.ptr(w), 2, 100, O.ptr(x), O.ptr(y)) == -1
     assert f(99, O.ptr(w), 2, 256, O.ptr(x), O.ptr(y)) == -1
+
+
+@pytest.mark.skipif(not os.environ.get("MYNAH_SLOW_TESTS"),
+                    reason="2.5 GB model on the CPU: set MYNAH_SLOW_TESTS=1")
+def test_qwen3_4b_prompt_golden():
+    """The oracle's forward at Qwen3-4B scale (36 layers, 4 query heads per
+    key head) against the compiled reference's prompt prefill + greedy run:
+    the first step's top-64 logits bit for bit, then the greedy ids."""
+    g = np.load(os.path.join(GOLDEN, "qwen3_4b_prompt.npz"), allow_pickle=False)
+    O.orc.orc_threads_init(0)
+    model = O.SynthModel(CF.QWEN3_4B, 0)
+    prompt = [int(t) for t in g["prompt"]]
+    steps = int(g["tokens"].size)
+    orc = O.OracleQwen3(model, len(prompt) + steps + 1)
+    for t in prompt[:-1]:
+        orc.forward(t)
+    lg = orc.forward(prompt[-1])
+    assert np.array_equal(lg[g["top_ids"]].view(np.uint32), g["top_vals"].view(np.uint32))
+    tok, out = int(np.argmax(lg)), []
+    for _ in range(steps):
+        out.append(tok)
+        tok = int(np.argmax(orc.forward(tok)))
+    assert out == [int(t) for t in g["tokens"]]
