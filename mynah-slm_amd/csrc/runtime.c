@@ -263,6 +263,10 @@ static void exact_shape(uint32_t all_rows, uint32_t units, uint32_t *lk, uint32_
     }
     uint32_t w = (units + k - 1u) / k;
     if (w > 16u) w = 16u;
+    /* Large launches: at most two waves share rows, so each lane sums a few
+     * units (measured on the 151936 x 2560 head: 76 us against 117 us with
+     * one unit per lane over five waves). */
+    if (all_rows >= 16384u && w > 2u) w = 2u;
     const uint32_t rpw = 64u / k;
     uint32_t r = 1, tiles = (all_rows + rpw - 1u) / rpw;
     while (w * r * 2u <= 4u && rpw * r * 2u <= 64u && tiles / (r * 2u) >= 1024u) r *= 2u;
