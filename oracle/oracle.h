@@ -52,6 +52,16 @@ int  orc_project(int type, const void *w, size_t rows, size_t cols,
 int  orc_matmat_mt(int type, const void *w, size_t rows, size_t cols,
                    const float *x, float *y, size_t tokens);
 
+/* ── int8 activation lane of Q4_K (int8.c; kernels.c:636-788, 1120-1751) ── */
+/* One 256-value block: int8 quants, the eight 32-value integer sums, returns
+ * the activation scale amax / 127 (0 and zeros for an all-zero block). */
+float   orc_q8_quantize_block(const float *x, int8_t *q, int32_t sums[8]);
+/* Integer dot of sub-block j (0..7) of one Q4_K block with the quants. */
+int32_t orc_q4k_int8_dot(const unsigned char *blk, const int8_t *xq, int j);
+int     orc_q4k_matvec_int8(const void *w, size_t rows, size_t cols, const float *x, float *y);
+int     orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                            size_t tokens);
+
 /* ── Qwen3 decoder restatement (src/arch_qwen3.c:178-252) ───────────────── */
 typedef struct {
     uint32_t n_layers, d_model, d_ff, n_heads, n_kv_heads, head_dim, vocab;

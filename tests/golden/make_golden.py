@@ -21,6 +21,11 @@ records a SHA-256 of the input bytes so generator drift is detected):
   qwen3_4b_prompt.npz  configs[4]'s model (Qwen3-4B): the first 8 prompt ids,
                      prefill + 8 greedy steps, the first step's logits' top 64
                      (`--only c5` writes just this file)
+  int8.npz           the int8 activation lane of an AVX2 + FMA build of ingot
+                     (oracle/_ref/libref_int8.so, INGOT_SDOT=1): Q4_K matvec
+                     and batched outputs, incl. round-half-even ties, an
+                     all-zero block and token counts around the token tile
+                     (`--only int8` writes just this file)
 """
 from __future__ import annotations
 
@@ -75,6 +80,49 @@ def golden_c5(ref) -> None:
                         tokens=np.array(toks, np.uint32), top_ids=top.astype(np.uint32),
                         top_vals=lg[top], logits0_sha=np.array(sha(lg)),
                         blob_sha=np.array(sha(model.blob)))
+
+
+INT8_MATVEC = ((37, 512), (64, 3072))
+INT8_MATMAT = ((16, 2048, 16), (24, 2048, 70), (9, 512, 130), (8, 6144, 5), (4, 9728, 110),
+               (5, 512, 2), (3, 256, 3), (6, 1024, 1))
+
+
+def int8_special_x() -> np.ndarray:
+    """Three blocks that pin the quantiser: amax 127 with half-integer values
+    (x * 127 / amax = k + 0.5 exactly: ties to even), all zeros (scale 0),
+    and tiny values (a large finite inverse)."""
+    x = np.zeros(768, np.float32)
+    k = np.arange(256, dtype=np.float32)
+    x[:256] = (k % 254) - 126.5
+    x[0], x[1] = 127.0, -127.0
+    x[512:] = O.normal(77, 256) * np.float32(1e-30)
+    return x
+
+
+def golden_int8(ref8) -> None:
+    assert ref8.ingot_matmat_is_exact(2) == 0, "AVX2 build did not take the int8 lane"
+    out = {}
+    for rows, cols in INT8_MATVEC:
+        w, x = O.blocks(CF.Q4_K, 500 + rows, rows, cols), O.normal(600 + rows, cols)
+        y = np.empty(rows, np.float32)
+        assert ref8.ingot_q4_k_matvec(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y)) == 0
+        out[f"mv_{rows}x{cols}_y"] = y
+        out[f"mv_{rows}x{cols}_w_sha"] = np.array(sha(w))
+        out[f"mv_{rows}x{cols}_x_sha"] = np.array(sha(x))
+    w, x = O.blocks(CF.Q4_K, 700, 16, 768), int8_special_x()
+    y = np.empty(16, np.float32)
+    assert ref8.ingot_q4_k_matvec(O.ptr(w), 16, 768, O.ptr(x), O.ptr(y)) == 0
+    out["mv_special_y"] = y
+    out["mv_special_x"] = x
+    for rows, cols, tokens in INT8_MATMAT:
+        key = f"mm_{rows}x{cols}_t{tokens}"
+        w, x = O.blocks(CF.Q4_K, 800 + rows, rows, cols), O.normal(900 + tokens, tokens * cols)
+        y = np.empty(rows * tokens, np.float32)
+        assert ref8.ingot_q4_k_matmat(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+        out[f"{key}_y"] = y
+        out[f"{key}_w_sha"] = np.array(sha(w))
+        out[f"{key}_x_sha"] = np.array(sha(x))
+    np.savez_compressed(os.path.join(HERE, "int8.npz"), **out)
 
 
 def main() -> int:
@@ -167,11 +215,19 @@ def main() -> int:
                         first=np.array(first), logits0_sha=np.array(sha(lg)),
                         top_ids=top.astype(np.uint32), top_vals=lg[top],
                         blob_sha=np.array(sha(model.blob)))
+    r8 = O.load_ref_int8()
+    if r8 is not None:
+        golden_int8(r8)
     print("golden vectors written to", HERE)
     return 0
 
 
 if __name__ == "__main__":
+    if sys.argv[1:] == ["--only", "int8"]:
+        r8 = O.load_ref_int8()
+        assert r8 is not None, "oracle/_ref/libref_int8.so is missing: run make -C oracle"
+        golden_int8(r8)
+        sys.exit(0)
     if sys.argv[1:] == ["--only", "c5"]:
         r = O.load_ref()
         assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"

@@ -3,6 +3,8 @@
   * liboracle.so    this repository's C11 restatement of the reference path
   * _ref/libref.so  the reference compiled from its own sources (built here
                     when /root/reference exists; optional everywhere else)
+  * _ref/libref_int8.so  ingot's kernels built with AVX2 + FMA, the build in
+                    which the reference's int8 activation lane exists
 """
 from __future__ import annotations
 
@@ -15,6 +17,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+REF_INT8_SO = os.path.join(ROOT, "oracle", "_ref", "libref_int8.so")
 
 _P, _SZ = C.c_void_p, C.c_size_t
 
@@ -66,6 +69,10 @@ def _load_oracle() -> C.CDLL:
         "orc_qwen3_set_n_past": (None, [_P, C.c_uint32]),
         "orc_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
         "orc_argmax": (C.c_uint32, [_P, _SZ]),
+        "orc_q8_quantize_block": (C.c_float, [_P, _P, _P]),
+        "orc_q4k_int8_dot": (C.c_int32, [_P, _P, C.c_int]),
+        "orc_q4k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "orc_q4k_matmat_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
         "mynah_synth_normal": (C.c_int, [C.c_uint64, _SZ, C.c_float, C.c_float, _P, C.c_int]),
         "mynah_synth_uniform_u32": (C.c_int, [C.c_uint64, _SZ, C.c_uint32, _P]),
@@ -109,6 +116,59 @@ def load_ref():
         f = getattr(lib, name)
         f.restype, f.argtypes = res, args
     return lib
+
+
+def load_ref_int8():
+    """ingot's kernels from an AVX2 + FMA build of the reference sources, with
+    the int8 lane switched on for the matvec too (INGOT_SDOT=1, read once by
+    the library on its first call); None when not built on this machine."""
+    if not os.path.exists(REF_INT8_SO):
+        return None
+    os.environ["INGOT_SDOT"] = "1"
+    lib = C.CDLL(REF_INT8_SO)
+    sig = {
+        "ingot_q4_k_matvec": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_q4_k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_q4_k_matmat": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "ingot_matmat_is_exact": (C.c_int, [_SZ]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    return lib
+
+
+def q8_quantize(x: np.ndarray):
+    """Oracle quantisation of f32 activations [tokens][cols] (cols % 256 == 0):
+    int8 values, per-256 scales [tokens][cols/256], per-32 sums [tokens][cols/32]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, x.shape[-1])
+    tokens, cols = x.shape
+    nb = cols // 256
+    q = np.empty((tokens, cols), np.int8)
+    sc = np.empty((tokens, nb), np.float32)
+    sums = np.empty((tokens, nb * 8), np.int32)
+    for t in range(tokens):
+        for b in range(nb):
+            sc[t, b] = orc.orc_q8_quantize_block(x[t, 256 * b:].ctypes.data,
+                                                 q[t, 256 * b:].ctypes.data,
+                                                 sums[t, 8 * b:].ctypes.data)
+    return q, sc, sums
+
+
+def q4k_int8_dots(w: np.ndarray, rows: int, cols: int, q: np.ndarray) -> np.ndarray:
+    """Oracle integer dots: [rows][tokens][cols/32] of the Q4_K quants (0..15)
+    with the int8 activations, one per 32-value sub-block."""
+    q = np.ascontiguousarray(q, np.int8).reshape(-1, cols)
+    nb = cols // 256
+    wb = np.ascontiguousarray(w).view(np.uint8).reshape(rows, nb, 144)
+    nib = np.empty((rows, nb, 256), np.int32)
+    qs = wb[:, :, 16:].astype(np.int32).reshape(rows, nb, 4, 32)
+    nib.reshape(rows, nb, 4, 2, 32)[:, :, :, 0] = qs & 15
+    nib.reshape(rows, nb, 4, 2, 32)[:, :, :, 1] = qs >> 4
+    prod = np.einsum("rbk,tbk->rtbk", nib.reshape(rows, nb, 256),
+                     q.astype(np.int32).reshape(-1, nb, 256))
+    return prod.reshape(rows, q.shape[0], nb, 8, 32).sum(axis=-1).reshape(rows, q.shape[0], -1)
 
 
 BLOCK = {12: (256, 144), 14: (256, 210), 8: (32, 34)}
