@@ -46,7 +46,8 @@ extern "C" {
 /* third_party/ingot/include/ingot/quant.h:155-156 */
 int ingot_matvec(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output);
-/* quant.h:157-158. Exact f32 for every width (no int8 activation path): */
+/* quant.h:157-158. Exact f32 for every width unless the int8 lane is on
+ * (mynah_hip_set_int8 below), which then takes Q4_K from two tokens up. */
 int ingot_matmat(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output, size_t tokens);
 /* quant.h:159-160 — bit-identical to the reference decoders. */
@@ -54,7 +55,8 @@ int ingot_dequant_matrix(int type, const void *weights, size_t rows, size_t cols
                          float *output);
 /* quant.h:161 — 1 for Q4_K, Q6_K, Q8_0. */
 int ingot_has_kernel(int type);
-/* quant.h:150 — always 1: every width here is an exact reorder. */
+/* quant.h:149 (kernels.c:1714-1721): 1 when `tokens` takes the exact path —
+ * always for tokens <= 1, otherwise unless the int8 lane is on. */
 int ingot_matmat_is_exact(size_t tokens);
 
 /* quant.h:64-73 */
@@ -63,9 +65,16 @@ int ingot_q4_k_matvec(const void *weights, size_t rows, size_t cols,
 int ingot_q4_k_dequant(const void *weights, size_t rows, size_t cols, float *output);
 int ingot_q4_k_matmat(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output, size_t tokens);
-/* quant.h:151-152 */
+/* quant.h:151-152: the exact batched order whatever the int8 lane's mode
+ * (tokens == 1 is the matvec, kernels.c:1723-1726). */
 int ingot_q4_k_matmat_exact(const void *weights, size_t rows, size_t cols,
                             const float *input, float *output, size_t tokens);
+/* kernels.c:799-810 (exported by ingot's kernels, not declared in quant.h):
+ * the int8 matvec whatever the mode — activations quantised per 256 values
+ * (amax / 127, round half to even), integer dots per 32, the reference's f32
+ * epilogue; bit-identical to an AVX2 + FMA build of ingot. */
+int ingot_q4_k_matvec_int8(const void *weights, size_t rows, size_t cols,
+                           const float *input, float *output);
 /* quant.h:83-88 */
 int ingot_q6_k_matvec(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output);
@@ -118,6 +127,31 @@ int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols,
 enum { MYNAH_GEMV_EXACT = 0, MYNAH_GEMV_REORDERED = 1 };
 int mynah_hip_set_gemv_order(int order);
 int mynah_hip_gemv_order(void);
+
+/* The int8 activation lane of Q4_K products (the reference's lane of an
+ * AVX2 + FMA build of ingot, third_party/ingot/src/kernels.c:636-788,
+ * 1120-1751), bit-identical to that build:
+ *   MYNAH_INT8_OFF (default, like the as-built reference, which has no int8
+ *     lane): exact f32 everywhere;
+ *   MYNAH_INT8_BATCHED: Q4_K matmat with tokens >= 2 quantises its input
+ *     (that build's batched default);
+ *   MYNAH_INT8_ALL: the Q4_K matvec too (that build with INGOT_SDOT=1).
+ * INGOT_SDOT=1 in the environment, read at the first call that needs the
+ * mode, starts the library in MYNAH_INT8_ALL. Q6_K and Q8_0 stay exact, and
+ * the resident decode step (mynah_decode.h) always runs exact. */
+enum { MYNAH_INT8_OFF = 0, MYNAH_INT8_BATCHED = 1, MYNAH_INT8_ALL = 2 };
+int mynah_hip_set_int8(int mode);
+int mynah_hip_int8(void);
+/* The lane in two steps, for callers that reuse quantised activations:
+ * x[tokens][cols] (cols % 256 == 0, 16-byte aligned) to xq[tokens][cols]
+ * int8, xs[tokens][cols / 256] scales and xsum[tokens][cols / 32] int32 sums;
+ * then y[tokens][rows] from them (16-byte aligned xq and xsum). tokens == 1
+ * uses the matvec's epilogue, tokens >= 2 the batched one. Asynchronous. */
+int mynah_hip_q8_quantize_dev(const float *x, size_t tokens, size_t cols, int8_t *xq,
+                              float *xs, int32_t *xsum, void *stream);
+int mynah_hip_q4k_int8_dev(const void *w, size_t rows, size_t cols, const int8_t *xq,
+                           const float *xs, const int32_t *xsum, float *y, size_t tokens,
+                           void *stream);
 
 /* Plain device memory (256-byte aligned) and copies; *_async take a stream. */
 void *mynah_hip_alloc(size_t bytes);

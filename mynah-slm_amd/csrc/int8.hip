@@ -1,0 +1,388 @@
+// int8.hip — the int8 activation lane of Q4_K products: the activation
+// quantiser, the int8 matvec and the batched int8 GEMM on the matrix cores.
+//
+// The reference computes this lane in an AVX2 + FMA build of ingot
+// (third_party/ingot/src/kernels.c:636-788 for the matvec, 1120-1751 for the
+// batched form). Its arithmetic, which these kernels keep:
+//   * quantiser (kernels.c:675-708): per 256-value super-block of a token,
+//     amax = max |x|; scale = amax / 127, q = round-half-even(x * (127 / amax))
+//     as int8; the eight sums of q over 32-value sub-blocks (all zero when
+//     amax is 0);
+//   * integer dots: Q4_K quants (0..15) times q over each 32-value sub-block,
+//     exact in int32 whatever the order;
+//   * matvec epilogue (kernels.c:712-739): per super-block
+//     total = 0; per group g: total += d*sc*dot - dmin*m*sum for the low then
+//     the high sub-block (products and sums separately rounded); the block's
+//     value total * scale, summed over the row's super-blocks in order from 0;
+//   * batched epilogue (kernels.c:1495-1581): per super-block and
+//     (row, token), with scale_j = d*sc_j, offset_j = dmin*m_j:
+//     total = fma(dot_j, scale_j, total); total = fma(-sum_j, offset_j, total)
+//     for j = 0..7, for the tokens of a token tile that fall in whole groups
+//     of four; the tile's last (count % 4) tokens take
+//     total += scale_j*dot_j - offset_j*sum_j; then acc += total * scale,
+//     super-block after super-block. The token tile is
+//     clamp(4 MiB / (4 cols), 32, 128) rounded down to even (kernels.c:893-920).
+// So every output is bit-identical to that build of the reference.
+//
+// Quantised activations live in HBM as xq[token][cols] int8,
+// xs[token][cols / 256] f32 and xsum[token][cols / 32] int32.
+//
+// SPDX-License-Identifier: MIT
+#include "common.hip.h"
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// The (scale, min) pair of sub-block j from the 12 scale bytes s0..s2
+// (kernels.c:83-92, scale_min), selects only.
+MYNAH_DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j, uint32_t *sc,
+                             uint32_t *m) {
+    auto byte = [&](uint32_t k) -> uint32_t {
+        const uint32_t wd = k < 4u ? s0 : (k < 8u ? s1 : s2);
+        return (wd >> (8u * (k & 3u))) & 0xffu;
+    };
+    if (j < 4u) {
+        *sc = byte(j) & 63u;
+        *m = byte(j + 4u) & 63u;
+    } else {
+        *sc = (byte(j + 4u) & 15u) | ((byte(j - 4u) >> 6) << 4);
+        *m = (byte(j + 4u) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
+// ── quantiser ───────────────────────────────────────────────────────────
+// One wave per (token, super-block); lane l holds values 4l..4l+3, so the
+// lanes 8s..8s+7 hold sub-block s.
+extern "C" __global__ __launch_bounds__(256) void mynah_q8_quantize(
+    const float *__restrict__ x, int8_t *__restrict__ xq, float *__restrict__ xs,
+    int32_t *__restrict__ xsum, uint32_t n_units, uint32_t nb, uint32_t cols) {
+#pragma clang fp contract(off)
+    const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (u >= n_units) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = u / nb, b = u - t * nb;
+    const size_t off = (size_t)t * cols + 256u * b + 4u * lane;
+    const float4 v = *(const float4 *)(x + off);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    for (int m = 32; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    uint32_t packed = 0u;
+    int32_t s = 0;
+    float scale = 0.0f;
+    if (amax > 0.0f) {
+        scale = amax / 127.0f;
+        const float inv = 127.0f / amax;
+        const int32_t q0 = (int32_t)__builtin_rintf(v.x * inv);
+        const int32_t q1 = (int32_t)__builtin_rintf(v.y * inv);
+        const int32_t q2 = (int32_t)__builtin_rintf(v.z * inv);
+        const int32_t q3 = (int32_t)__builtin_rintf(v.w * inv);
+        s = q0 + q1 + q2 + q3;
+        // |q| <= 127 here (|x| <= amax), so the saturating packs are identities.
+        packed = ((uint32_t)q0 & 0xffu) | (((uint32_t)q1 & 0xffu) << 8) |
+                 (((uint32_t)q2 & 0xffu) << 16) | ((uint32_t)q3 << 24);
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    *(uint32_t *)(xq + off) = packed;
+    if ((lane & 7u) == 0u) xsum[(size_t)u * 8u + (lane >> 3)] = s;
+    if (lane == 0u) xs[u] = scale;
+}
+
+// ── int8 matvec (tokens == 1) ───────────────────────────────────────────
+// One thread per (row, super-block): a workgroup owns `rpw` whole rows
+// (rpw * nb <= 256 when nb <= 256), computes every block value into LDS, and
+// one thread per row sums its row's values in order.
+MYNAH_DEV float q4k_block_int8(const uint8_t *__restrict__ blk, const int8_t *__restrict__ q,
+                               float xscale, const int32_t *__restrict__ sums) {
+#pragma clang fp contract(off)
+    const uint4 hdr = *(const uint4 *)blk;
+    uint4 qs[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) qs[k] = ((const uint4 *)(blk + 16))[k];
+    uint4 xv[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) xv[k] = ((const uint4 *)q)[k];
+    const int4 s0 = ((const int4 *)sums)[0], s1 = ((const int4 *)sums)[1];
+    const int32_t sm[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const float d = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+    float total = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        // Group g: quant bytes 32g..32g+31 = qs[2g], qs[2g+1]; the low nibbles
+        // are sub-block 2g, the high ones 2g+1.
+        const uint32_t wq[8] = {qs[2 * g].x,     qs[2 * g].y,     qs[2 * g].z,     qs[2 * g].w,
+                                qs[2 * g + 1].x, qs[2 * g + 1].y, qs[2 * g + 1].z, qs[2 * g + 1].w};
+        const uint4 xl0 = xv[4 * g], xl1 = xv[4 * g + 1], xh0 = xv[4 * g + 2], xh1 = xv[4 * g + 3];
+        const uint32_t wl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+        const uint32_t wh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+        int32_t dl = 0, dh = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            dl = __builtin_amdgcn_sdot4((int)(wq[k] & 0x0f0f0f0fu), (int)wl[k], dl, false);
+            dh = __builtin_amdgcn_sdot4((int)((wq[k] >> 4) & 0x0f0f0f0fu), (int)wh[k], dh, false);
+        }
+        uint32_t sl, ml, sh, mh;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2u * g, &sl, &ml);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2u * g + 1u, &sh, &mh);
+        total += d * (float)sl * (float)dl - dmin * (float)ml * (float)sm[2 * g];
+        total += d * (float)sh * (float)dh - dmin * (float)mh * (float)sm[2 * g + 1];
+    }
+    return total * xscale;
+}
+
+extern "C" __global__ __launch_bounds__(256) void mynah_q4k_gemv_int8(
+    const uint8_t *__restrict__ w, const int8_t *__restrict__ xq, const float *__restrict__ xs,
+    const int32_t *__restrict__ xsum, float *__restrict__ y, uint32_t rows, uint32_t nb,
+    uint32_t rpw) {
+#pragma clang fp contract(off)
+    extern __shared__ float blockv[];   // rpw * nb values
+    const uint32_t r0 = blockIdx.x * rpw;
+    const uint32_t nrows = rows - r0 < rpw ? rows - r0 : rpw;
+    const uint32_t n = nrows * nb;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint32_t rr = i / nb, b = i - rr * nb;
+        const uint8_t *blk = w + ((size_t)(r0 + rr) * nb + b) * 144u;
+        blockv[i] = q4k_block_int8(blk, xq + 256u * b, xs[b], xsum + 8u * b);
+    }
+    __syncthreads();
+    for (uint32_t rr = threadIdx.x; rr < nrows; rr += blockDim.x) {
+        float s = 0.0f;
+        for (uint32_t b = 0; b < nb; b++) s += blockv[rr * nb + b];
+        y[r0 + rr] = s;
+    }
+}
+
+// ── batched int8 GEMM (tokens >= 2) ─────────────────────────────────────
+// A workgroup is 2 x 2 waves; wave (wr, wt) owns GI_TR 16-row tiles and GI_TT
+// 16-token tiles: rows R0 + 16 (GI_TR wr + i), tokens T0 + 16 (GI_TT wt + k).
+// Per super-block and sub-block j, one v_mfma_i32_16x16x32_i8 per tile gives
+// the tile's integer dots: lane l feeds row (l % 16) of the tile with the 8
+// quants 8 (l / 16) .. +7 of the sub-block (A operand) and token (l % 16) with
+// the same 8 activation positions (B operand), and receives the dots of rows
+// 4 (l / 16) + e, e = 0..3, for token l % 16. Sub-blocks 2g and 2g+1 are the
+// low and high nibbles of the same 8 quant bytes: one 8-byte load per group.
+// scale_j and offset_j of the workgroup's rows are computed once per
+// super-block into LDS (double buffered: one barrier per super-block), and
+// the next super-block's operands are fetched while the current one is
+// summed. The dots of sub-block j + 1 are issued before the epilogue of j.
+template <int GI_TR, int GI_TT>
+struct GiOps {
+    unsigned long long a[GI_TR][4];   // quant bytes of group g of each row tile
+    unsigned long long q[GI_TT][8];   // activations of sub-block j of each token tile
+    int4 s[GI_TT][2];                 // the 8 sub-block sums of each token tile
+    float xs[GI_TT];                  // activation scale of each token tile
+    uint4 hdr;                        // the header this thread stages
+};
+
+template <int GI_TR, int GI_TT>
+MYNAH_DEV void gi_load(GiOps<GI_TR, GI_TT> &o, const uint8_t *const *arow, const int8_t *const *btok,
+                       const float *const *xsp, const int32_t *const *xsump,
+                       const uint8_t *hrow, uint32_t b) {
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            o.a[i][g] = *(const unsigned long long *)(arow[i] + (size_t)b * 144u + 32u * g);
+#pragma unroll
+    for (int k = 0; k < GI_TT; k++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            o.q[k][j] = *(const unsigned long long *)(btok[k] + 256u * b + 32u * j);
+        o.s[k][0] = ((const int4 *)(xsump[k] + 8u * b))[0];
+        o.s[k][1] = ((const int4 *)(xsump[k] + 8u * b))[1];
+        o.xs[k] = xsp[k][b];
+    }
+    o.hdr = *(const uint4 *)(hrow + (size_t)b * 144u);
+}
+
+// Scale and offset of sub-blocks hj, hj + 1 of the staged row, into LDS.
+template <int GI_ROWS>
+MYNAH_DEV void gi_stage(float *buf, const uint4 hdr, uint32_t hj, uint32_t row) {
+#pragma clang fp contract(off)
+    const float d = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+    uint32_t s0, m0, s1, m1;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, hj, &s0, &m0);
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, hj + 1u, &s1, &m1);
+    buf[hj * GI_ROWS + row] = d * (float)s0;
+    buf[(hj + 1u) * GI_ROWS + row] = d * (float)s1;
+    buf[(8u + hj) * GI_ROWS + row] = dmin * (float)m0;
+    buf[(9u + hj) * GI_ROWS + row] = dmin * (float)m1;
+}
+
+template <int GI_TR, int GI_TT>
+MYNAH_DEV void gi_dots(i32x4 (&dt)[GI_TR][GI_TT], const GiOps<GI_TR, GI_TT> &o, int j) {
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++) {
+        const unsigned long long q =
+            ((j & 1) ? (o.a[i][j >> 1] >> 4) : o.a[i][j >> 1]) & 0x0f0f0f0f0f0f0f0full;
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++) {
+            const i32x4 zero = {0, 0, 0, 0};
+            dt[i][k] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)q, (long)o.q[k][j], zero, 0,
+                                                             0, 0);
+        }
+    }
+}
+
+// One super-block's epilogue: tot[i][k][e] over j = 0..7. MIXED: some lane
+// has a token outside the groups of four, which takes the plain form.
+template <bool MIXED, int GI_TR, int GI_TT>
+MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT> &o,
+                        const float4 *sbuf,
+                        uint32_t wr, uint32_t lk, const bool (&fma_path)[GI_TT]) {
+#pragma clang fp contract(off)
+    constexpr int GI_ROWS = 32 * GI_TR;
+    float xsm[GI_TT][8];
+#pragma unroll
+    for (int k = 0; k < GI_TT; k++) {
+        xsm[k][0] = (float)o.s[k][0].x; xsm[k][1] = (float)o.s[k][0].y;
+        xsm[k][2] = (float)o.s[k][0].z; xsm[k][3] = (float)o.s[k][0].w;
+        xsm[k][4] = (float)o.s[k][1].x; xsm[k][5] = (float)o.s[k][1].y;
+        xsm[k][6] = (float)o.s[k][1].z; xsm[k][7] = (float)o.s[k][1].w;
+    }
+    float tot[GI_TR][GI_TT][4];
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) tot[i][k][e] = 0.0f;
+    i32x4 cur[GI_TR][GI_TT], nxt[GI_TR][GI_TT];
+    gi_dots(cur, o, 0);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < 7) gi_dots(nxt, o, j + 1);
+#pragma unroll
+        for (int i = 0; i < GI_TR; i++) {
+            const uint32_t slot = (16u * (GI_TR * wr + i)) / 4u + lk;
+            const float4 sc = sbuf[j * (GI_ROWS / 4) + slot];
+            const float4 of = sbuf[(8 + j) * (GI_ROWS / 4) + slot];
+            const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+            const float ofv[4] = {of.x, of.y, of.z, of.w};
+#pragma unroll
+            for (int k = 0; k < GI_TT; k++) {
+                const float xsj = xsm[k][j];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float dv = (float)cur[i][k][e];
+                    float f = __builtin_fmaf(dv, scv[e], tot[i][k][e]);
+                    f = __builtin_fmaf(-xsj, ofv[e], f);
+                    if (MIXED) {
+                        const float p = tot[i][k][e] + (scv[e] * dv - ofv[e] * xsj);
+                        f = fma_path[k] ? f : p;
+                    }
+                    tot[i][k][e] = f;
+                }
+            }
+        }
+        if (j < 7) {
+#pragma unroll
+            for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+                for (int k = 0; k < GI_TT; k++) cur[i][k] = nxt[i][k];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][k][e] = acc[i][k][e] + tot[i][k][e] * o.xs[k];
+}
+
+template <int GI_TR, int GI_TT>
+MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,
+                         const float *__restrict__ xs, const int32_t *__restrict__ xsum,
+                         float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens,
+                         uint32_t nb, uint32_t tile) {
+    constexpr int GI_ROWS = 32 * GI_TR, GI_TOK = 32 * GI_TT;
+    __shared__ float4 so[2][16 * GI_ROWS / 4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t wr = wave & 1u, wt = wave >> 1;
+    const uint32_t R0 = blockIdx.x * GI_ROWS, T0 = blockIdx.y * GI_TOK;
+    const size_t rb = (size_t)nb * 144u;
+    const uint32_t lm = lane & 15u, lk = lane >> 4;
+
+    // Operand rows and tokens of this lane (clamped for loads; stores check).
+    const uint8_t *arow[GI_TR];
+    const int8_t *btok[GI_TT];
+    const float *xsp[GI_TT];
+    const int32_t *xsump[GI_TT];
+    uint32_t tok[GI_TT];
+    bool fma_path[GI_TT];
+    bool all_fma = true;
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++) {
+        uint32_t r = R0 + 16u * (GI_TR * wr + i) + lm;
+        r = r < rows ? r : rows - 1u;
+        arow[i] = w + (size_t)r * rb + 16u + 8u * lk;
+    }
+#pragma unroll
+    for (int k = 0; k < GI_TT; k++) {
+        const uint32_t t = T0 + 16u * (GI_TT * wt + k) + lm;
+        tok[k] = t;
+        const uint32_t tc = t < tokens ? t : tokens - 1u;
+        btok[k] = xq + (size_t)tc * cols + 8u * lk;
+        xsp[k] = xs + (size_t)tc * nb;
+        xsump[k] = xsum + (size_t)tc * nb * 8u;
+        const uint32_t t0 = tc - tc % tile;
+        const uint32_t cnt = tokens - t0 < tile ? tokens - t0 : tile;
+        fma_path[k] = tc - t0 < (cnt & ~3u);
+        all_fma = all_fma && fma_path[k];
+    }
+    const bool mixed = !__all(all_fma);
+    // Staging: thread tid owns row tid / 4 of the workgroup, sub-blocks
+    // 2 (tid % 4) and 2 (tid % 4) + 1 (threads beyond 4 GI_ROWS stage nothing).
+    const uint32_t srow = tid >> 2, hj = 2u * (tid & 3u);
+    const bool stager = srow < GI_ROWS;
+    uint32_t hr = R0 + (stager ? srow : 0u);
+    hr = hr < rows ? hr : rows - 1u;
+    const uint8_t *hrow = w + (size_t)hr * rb;
+
+    float acc[GI_TR][GI_TT][4];
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][k][e] = 0.0f;
+
+    GiOps<GI_TR, GI_TT> cur, nxt;
+    gi_load(cur, arow, btok, xsp, xsump, hrow, 0);
+    if (stager) gi_stage<GI_ROWS>((float *)so[0], cur.hdr, hj, srow);
+    __syncthreads();
+    for (uint32_t b = 0; b < nb; b++) {
+        const bool more = b + 1u < nb;
+        if (more) gi_load(nxt, arow, btok, xsp, xsump, hrow, b + 1u);
+        if (mixed) gi_block<true>(acc, cur, so[b & 1u], wr, lk, fma_path);
+        else gi_block<false>(acc, cur, so[b & 1u], wr, lk, fma_path);
+        if (more && stager) gi_stage<GI_ROWS>((float *)so[(b + 1u) & 1u], nxt.hdr, hj, srow);
+        __syncthreads();
+        if (more) cur = nxt;
+    }
+
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++) {
+            if (tok[k] >= tokens) continue;
+            float *yo = y + (size_t)tok[k] * rows;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t r = R0 + 16u * (GI_TR * wr + i) + 4u * lk + e;
+                if (r < rows) yo[r] = acc[i][k][e];
+            }
+        }
+}
+
+#define GEMM_INT8(TR, TT)                                                                    \
+    extern "C" __global__ __launch_bounds__(256) void mynah_q4k_gemm_int8_##TR##TT(          \
+        const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,                        \
+        const float *__restrict__ xs, const int32_t *__restrict__ xsum,                      \
+        float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t nb,   \
+        uint32_t tile) {                                                                     \
+        gemm_int8<TR, TT>(w, xq, xs, xsum, y, rows, cols, tokens, nb, tile);                 \
+    }
+GEMM_INT8(1, 1)
+GEMM_INT8(1, 2)
+GEMM_INT8(2, 1)
+GEMM_INT8(2, 2)

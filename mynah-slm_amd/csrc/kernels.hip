@@ -8,3 +8,4 @@
 #include "gemm_exact.hip"
 #include "decode.hip"
 #include "copy.hip"
+#include "int8.hip"

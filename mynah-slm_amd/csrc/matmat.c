@@ -2,19 +2,26 @@
  *
  * Replaces ingot_matmat (third_party/ingot/src/generic.c:107-124) and the
  * per-type batched kernels (kernels.c:1742-1751, 2627-2648). Exact f32 for
- * every width, like the reference's exact path: the tiled kernel of
+ * every width unless the int8 lane is on (int8.c), like the reference's exact
+ * path: the tiled kernel of
  * gemm_exact.hip keeps the batched reference's own summation order (natural
  * weight order per 256-value unit, kernels.c:1017-1039 and 2635-2648), so
  * every output is bit-identical to ingot's exact matmat. tokens == 1 is the
  * matvec, as in the reference (kernels.c:1726); the callers route it.
  *
  * SPDX-License-Identifier: MIT */
+#include "kernels_hip.h"
 #include "runtime_internal.h"
 
 int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                        const float *x, float *y, size_t tokens, hipStream_t stream) {
+                        const float *x, float *y, size_t tokens, int exact, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    /* The batched Q4_K product takes the int8 lane when it is on, exactly
+     * where the reference's does (kernels.c:1723-1751; only Q4_K of the
+     * types here, tokens >= 2). */
+    if (!exact && type == MYNAH_Q4_K && tokens >= 2 && mynah_int8_mode() != MYNAH_INT8_OFF)
+        return mynah_int8_product(d, w, rows, cols, x, y, tokens, stream);
     /* The reference's batched core works in 256-wide units for every type
      * and refuses anything else (kernels.c:1087-1088, 2641-2648). */
     if (cols % 256 != 0) {

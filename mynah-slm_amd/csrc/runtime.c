@@ -181,6 +181,10 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
                       const float *x, float *y, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    /* INGOT_SDOT=1 semantics: the Q4_K matvec quantises its input
+     * (third_party/ingot/src/kernels.c:819-834). */
+    if (type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
+        return mynah_int8_product(d, w, rows, cols, x, y, 1, stream);
     if (type != MYNAH_Q8_0 && cols % 256 != 0) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
@@ -460,7 +464,7 @@ static int grow(unsigned char **buf, size_t *cap, size_t need) {
     return 0;
 }
 
-typedef enum { OP_MATVEC, OP_MATMAT, OP_DEQUANT } host_op;
+typedef enum { OP_MATVEC, OP_MATVEC_INT8, OP_MATMAT, OP_MATMAT_EXACT, OP_DEQUANT } host_op;
 
 static int host_call(host_op op, int type, const void *w, size_t rows, size_t cols,
                      const float *x, float *y, size_t tokens) {
@@ -501,9 +505,12 @@ static int host_call(host_op op, int type, const void *w, size_t rows, size_t co
     }
     if (op == OP_MATVEC) rc = mynah_gemv_launch(d, type, wd, rows, cols, (const float *)stage_x,
                                                 (float *)stage_y, s);
-    else if (op == OP_MATMAT) rc = mynah_matmat_launch(d, type, wd, rows, cols,
-                                                       (const float *)stage_x, (float *)stage_y,
-                                                       tokens, s);
+    else if (op == OP_MATVEC_INT8) rc = mynah_int8_product(d, wd, rows, cols,
+                                                           (const float *)stage_x,
+                                                           (float *)stage_y, 1, s);
+    else if (op == OP_MATMAT || op == OP_MATMAT_EXACT)
+        rc = mynah_matmat_launch(d, type, wd, rows, cols, (const float *)stage_x,
+                                 (float *)stage_y, tokens, op == OP_MATMAT_EXACT, s);
     else rc = mynah_dequant_launch(d, type, wd, rows, cols, (float *)stage_y, s);
     if (rc != 0) goto out;
     rc = -1;
@@ -539,8 +546,8 @@ int ingot_has_kernel(int type) {
 }
 
 int ingot_matmat_is_exact(size_t tokens) {
-    (void)tokens;
-    return 1;
+    if (tokens <= 1) return 1;
+    return mynah_int8_mode() == MYNAH_INT8_OFF;
 }
 
 #define PER_TYPE(prefix, id)                                                              \
@@ -562,7 +569,12 @@ PER_TYPE(q8_0, MYNAH_Q8_0)
 
 int ingot_q4_k_matmat_exact(const void *w, size_t rows, size_t cols, const float *x, float *y,
                             size_t tokens) {
-    return ingot_matmat(MYNAH_Q4_K, w, rows, cols, x, y, tokens);
+    return host_call(tokens == 1 ? OP_MATVEC : OP_MATMAT_EXACT, MYNAH_Q4_K, w, rows, cols, x, y,
+                     tokens);
+}
+
+int ingot_q4_k_matvec_int8(const void *w, size_t rows, size_t cols, const float *x, float *y) {
+    return host_call(OP_MATVEC_INT8, MYNAH_Q4_K, w, rows, cols, x, y, 1);
 }
 
 /* The reference's tensor descriptor (third_party/ingot/include/ingot/gguf.h:41-50)
@@ -617,7 +629,7 @@ int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols, cons
     }
     hipStream_t s = mynah_stream_or_default(d, stream);
     if (tokens == 1) return mynah_gemv_launch(d, type, w, rows, cols, x, y, s);
-    return mynah_matmat_launch(d, type, w, rows, cols, x, y, tokens, s);
+    return mynah_matmat_launch(d, type, w, rows, cols, x, y, tokens, 0, s);
 }
 
 int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols, float *y,

@@ -28,7 +28,13 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
     X(MYNAH_K_EMBED, "mynah_embed_row")                \
-    X(MYNAH_K_COPY16, "mynah_copy16")
+    X(MYNAH_K_COPY16, "mynah_copy16")                  \
+    X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
+    X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \
+    X(MYNAH_K_Q4K_GEMM_INT8_11, "mynah_q4k_gemm_int8_11") \
+    X(MYNAH_K_Q4K_GEMM_INT8_12, "mynah_q4k_gemm_int8_12") \
+    X(MYNAH_K_Q4K_GEMM_INT8_21, "mynah_q4k_gemm_int8_21") \
+    X(MYNAH_K_Q4K_GEMM_INT8_22, "mynah_q4k_gemm_int8_22")
 
 enum {
 #define X(id, name) id,
@@ -61,8 +67,23 @@ int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows,
                           const float *x, float *y, hipStream_t stream);
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                          float *y, hipStream_t stream);
+/* exact != 0 keeps the exact batched order whatever the int8 lane's mode
+ * (ingot_q4_k_matmat_exact). */
 int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                        const float *x, float *y, size_t tokens, hipStream_t stream);
+                        const float *x, float *y, size_t tokens, int exact, hipStream_t stream);
+
+/* int8 activation lane (int8.c): the current mode (MYNAH_INT8_*), the
+ * quantiser, the product on quantised activations (tokens == 1: the matvec
+ * epilogue, else the batched one), and both behind one call with a
+ * stream-ordered workspace. */
+int mynah_int8_mode(void);
+int mynah_q8_quantize_launch(mynah_device *d, const float *x, size_t tokens, size_t cols,
+                             int8_t *xq, float *xs, int32_t *xsum, hipStream_t stream);
+int mynah_q4k_int8_launch(mynah_device *d, const void *w, size_t rows, size_t cols,
+                          const int8_t *xq, const float *xs, const int32_t *xsum, float *y,
+                          size_t tokens, hipStream_t stream);
+int mynah_int8_product(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
+                       float *y, size_t tokens, hipStream_t stream);
 
 /* Host mirror of the grouped exact GEMV launch (gemv_exact.hip GemvGroup). */
 #define MYNAH_GROUP_MAX 8

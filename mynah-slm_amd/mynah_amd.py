@@ -44,6 +44,12 @@ def _load() -> C.CDLL:
         "ingot_dequant_matrix": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P]),
         "ingot_has_kernel": (C.c_int, [C.c_int]),
         "ingot_matmat_is_exact": (C.c_int, [_SZ]),
+        "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "ingot_q4_k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "mynah_hip_set_int8": (C.c_int, [C.c_int]),
+        "mynah_hip_int8": (C.c_int, []),
+        "mynah_hip_q8_quantize_dev": (C.c_int, [_P, _SZ, _SZ, _P, _P, _P, _P]),
+        "mynah_hip_q4k_int8_dev": (C.c_int, [_P, _SZ, _SZ, _P, _P, _P, _P, _SZ, _P]),
         "mynah_hip_init": (C.c_int, [C.c_int]),
         "mynah_hip_last_error": (C.c_char_p, []),
         "mynah_hip_register": (C.c_int, [_P, _SZ]),
@@ -199,6 +205,39 @@ def matmat(qtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, token
     y = np.empty(tokens * rows, dtype=np.float32)
     check(lib.ingot_matmat(qtype, ptr(w), rows, cols, ptr(x), ptr(y), tokens), "ingot_matmat")
     return y
+
+
+INT8_OFF, INT8_BATCHED, INT8_ALL = 0, 1, 2
+
+
+def set_int8(mode: int) -> None:
+    """The int8 activation lane of Q4_K products (INT8_OFF, INT8_BATCHED,
+    INT8_ALL)."""
+    check(lib.mynah_hip_set_int8(mode), "set_int8")
+
+
+def matvec_int8(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    y = np.empty(rows, dtype=np.float32)
+    check(lib.ingot_q4_k_matvec_int8(ptr(w), rows, cols, ptr(x), ptr(y)), "q4_k_matvec_int8")
+    return y
+
+
+def matmat_exact(w: np.ndarray, rows: int, cols: int, x: np.ndarray, tokens: int) -> np.ndarray:
+    y = np.empty(tokens * rows, dtype=np.float32)
+    check(lib.ingot_q4_k_matmat_exact(ptr(w), rows, cols, ptr(x), ptr(y), tokens),
+          "q4_k_matmat_exact")
+    return y
+
+
+def q8_quantize_dev(x: int, tokens: int, cols: int, xq: int, xs: int, xsum: int,
+                    stream=None) -> None:
+    check(lib.mynah_hip_q8_quantize_dev(x, tokens, cols, xq, xs, xsum, stream), "q8_quantize")
+
+
+def q4k_int8_dev(w: int, rows: int, cols: int, xq: int, xs: int, xsum: int, y: int,
+                 tokens: int, stream=None) -> None:
+    check(lib.mynah_hip_q4k_int8_dev(w, rows, cols, xq, xs, xsum, y, tokens, stream),
+          "q4k_int8")
 
 
 def dequant(qtype: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
