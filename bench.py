@@ -18,7 +18,9 @@ to it) on the same sweep on this host's cores.
 Beside the metric line's value: `decode` (configs[2], Qwen3-0.6B greedy
 decode tok/s in three numerics modes, tokens checked against the compiled
 reference's), `prefill_gemm` (configs[3], the exact batched GEMM at 512
-tokens), `qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
+tokens), `prefill_gemm_int8` (the same with Q4_K on the int8 activation
+lane, the batched default of the reference's AVX2 build),
+`qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
 greedy steps on Qwen3-4B) and `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -37,6 +39,7 @@ sys.path.insert(0, os.path.join(ROOT, "mynah-slm_amd"))
 METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak); Qwen3 batch-1 decode tok/s, 1 GPU"
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
+PEAK_INT8_TOPS = 5000.0
 MALL_BYTES = 256 << 20
 
 
@@ -138,39 +141,61 @@ def gpu_decode(M, CF):
     return out
 
 
-def gpu_prefill_gemm(M, CF, reps: int = 5):
-    """the prefill GEMMs at Qwen3-1.7B shapes, 512 tokens, in the
-    exact batched order (bit-identical to the reference's exact matmat)."""
+def gpu_prefill_gemm(M, CF, reps: int = 5, int8: bool = False):
+    """the prefill GEMMs at Qwen3-1.7B shapes, 512 tokens.
+    int8=False: the exact batched order (bit-identical to the reference's
+    exact matmat). int8=True: the Q4_K products take the int8 activation lane
+    (bit-identical to the reference's AVX2 build, whose batched default it
+    is), quantisation included in the time; Q6_K stays exact, as there."""
     out, tot_flop, tot_ms = {}, 0, 0.0
-    for i, m in enumerate(CF.C4):
-        wseed, _ = CF.matrix_seeds(M.substream, 0, i)
-        w = M.DeviceBuffer.from_array(M.synth_blocks(m.qtype, wseed, m.rows, m.cols))
-        x = M.DeviceBuffer.from_array(M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i),
-                                                     CF.C4_TOKENS * m.cols))
-        y = M.DeviceBuffer(4 * m.rows * CF.C4_TOKENS)
-        M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
-        M.sync()
-        a, b = M.Event(), M.Event()
-        a.record()
-        for _ in range(reps):
+    M.set_int8(M.INT8_BATCHED if int8 else M.INT8_OFF)
+    try:
+        for i, m in enumerate(CF.C4):
+            wseed, _ = CF.matrix_seeds(M.substream, 0, i)
+            w = M.DeviceBuffer.from_array(M.synth_blocks(m.qtype, wseed, m.rows, m.cols))
+            x = M.DeviceBuffer.from_array(M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i),
+                                                         CF.C4_TOKENS * m.cols))
+            y = M.DeviceBuffer(4 * m.rows * CF.C4_TOKENS)
             M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
-        b.record()
-        M.sync()
-        ms = a.elapsed_ms(b) / reps
-        flop = 2 * m.rows * m.cols * CF.C4_TOKENS
-        tot_flop += flop
-        tot_ms += ms
-        out[m.name] = {"ms": round(ms, 4), "tflop_s": round(flop / ms / 1e9, 2)}
-        for buf in (w, x, y):
-            buf.free()
-    return {"workload": "configs[3]: Q4_K 4096/2048/2048/6144/6144 x 2048 and Q6_K 2048 x 6144, "
-                        "512 tokens, exact batched order",
-            "total_ms": round(tot_ms, 4), "flop": tot_flop,
-            "tflop_s": round(tot_flop / tot_ms / 1e9, 2),
-            "peak_tflop_s_fp32": PEAK_FP32_TFLOPS, "frac_of_fp32_peak": round(tot_flop / tot_ms / 1e9 / PEAK_FP32_TFLOPS, 4),
-            "note": "one mul and one add per product (the reference's roundings): the "
-                    "non-packed VALU issue rate bounds this order near 40 TFLOP/s",
-            "per_matrix": out}
+            M.sync()
+            a, b = M.Event(), M.Event()
+            n = reps * (8 if int8 else 1)
+            a.record()
+            for _ in range(n):
+                M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
+            b.record()
+            M.sync()
+            ms = a.elapsed_ms(b) / n
+            flop = 2 * m.rows * m.cols * CF.C4_TOKENS
+            tot_flop += flop
+            tot_ms += ms
+            lane = "int8" if (int8 and m.qtype == CF.Q4_K) else "exact"
+            out[m.name] = {"ms": round(ms, 4), "tflop_s": round(flop / ms / 1e9, 2), "lane": lane}
+            for buf in (w, x, y):
+                buf.free()
+    finally:
+        M.set_int8(M.INT8_OFF)
+    res = {"workload": "configs[3]: Q4_K 4096/2048/2048/6144/6144 x 2048 and Q6_K 2048 x 6144, "
+                       "512 tokens, " + ("Q4_K on the int8 activation lane" if int8
+                                         else "exact batched order"),
+           "total_ms": round(tot_ms, 4), "flop": tot_flop,
+           "tflop_s": round(tot_flop / tot_ms / 1e9, 2), "per_matrix": out}
+    if int8:
+        q4 = [v for v in out.values() if v["lane"] == "int8"]
+        q4_ms = sum(v["ms"] for v in q4)
+        q4_flop = sum(2 * m.rows * m.cols * CF.C4_TOKENS for m in CF.C4 if m.qtype == CF.Q4_K)
+        res.update({"q4k_int8_ms": round(q4_ms, 4),
+                    "q4k_int8_top_s": round(q4_flop / q4_ms / 1e9, 2),
+                    "peak_top_s_int8": PEAK_INT8_TOPS,
+                    "frac_of_int8_peak": round(q4_flop / q4_ms / 1e9 / PEAK_INT8_TOPS, 4),
+                    "note": "integer dots on v_mfma_i32_16x16x32_i8; the reference's f32 "
+                            "epilogue (a convert and two fma per dot) bounds it on the VALU"})
+    else:
+        res.update({"peak_tflop_s_fp32": PEAK_FP32_TFLOPS,
+                    "frac_of_fp32_peak": round(tot_flop / tot_ms / 1e9 / PEAK_FP32_TFLOPS, 4),
+                    "note": "one mul and one add per product (the reference's roundings): the "
+                            "non-packed VALU issue rate bounds this order near 40 TFLOP/s"})
+    return res
 
 
 def gpu_qwen3_4b(M, CF):
@@ -307,10 +332,12 @@ def main() -> int:
         log("[bench] configs[2] decode")
         decode = gpu_decode(M, CF)
 
-    prefill = None
+    prefill = prefill_int8 = None
     if not args.no_prefill:
         log("[bench] configs[3] prefill GEMM")
         prefill = gpu_prefill_gemm(M, CF)
+        log("[bench] configs[3] prefill GEMM, int8 lane")
+        prefill_int8 = gpu_prefill_gemm(M, CF, int8=True)
 
     e2e_4b = None
     if not args.no_4b_e2e:
@@ -362,6 +389,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode": decode,
         "prefill_gemm": prefill,
+        "prefill_gemm_int8": prefill_int8,
         "qwen3_4b_end_to_end": e2e_4b,
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
