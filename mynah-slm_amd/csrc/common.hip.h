@@ -49,10 +49,37 @@ MYNAH_DEV float wave_sum(float v) {
     return v;
 }
 
+// A double moved across lanes by one DPP control (both halves).
+template <int CTRL>
+MYNAH_DEV double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+MYNAH_DEV double readlane_d(double v, int lane) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+// Sum over the 64 lanes of a (fully active) wave in double, every lane
+// receiving the total: DPP within quads (xor 1, xor 2) and rows (rotate by
+// 4, 8), then the four row sums read as scalars.
+MYNAH_DEV double wave_sum_d(double v) {
+    v += dpp_d<0xB1>(v);     // quad_perm(1, 0, 3, 2)
+    v += dpp_d<0x4E>(v);     // quad_perm(2, 3, 0, 1)
+    v += dpp_d<0x124>(v);    // row_ror:4
+    v += dpp_d<0x128>(v);    // row_ror:8
+    return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
+}
+
 // Workgroup-wide double sum; every thread gets the result. `sh` holds one
 // double per wave (blockDim.x <= 1024).
 MYNAH_DEV double block_sum_d(double v, double *sh) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    v = wave_sum_d(v);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) sh[wave] = v;

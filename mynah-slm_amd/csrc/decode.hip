@@ -16,11 +16,6 @@
 #define DEC_WG 256
 
 // Wave-wide double sum / float max (all lanes get the result).
-MYNAH_DEV double wave_sum_d(double v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
-}
-
 MYNAH_DEV float wave_max_f(float v) {
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
     return v;

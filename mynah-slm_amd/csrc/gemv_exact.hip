@@ -307,8 +307,10 @@ GEMV_SEQ_ENTRY(mynah_q80_gemv_exact_seq, 8)
 // reference's separate rms_norm call feeding the projections
 // (src/arch_qwen3.c:201, 226, 239).
 //
-// grp.shape = log2(K) | WS << 8 | WR << 16, with (64 / K) * WR <= 64 rows per
-// workgroup and 64 * WS * WR threads. Dynamic LDS (floats): the padded x,
+// grp.shape = log2(K) | WS << 8 | WR << 16 | SPLIT << 24, with (64 / K) * WR
+// (SPLIT: (16 / K) * WR) rows per workgroup and 64 * WS * WR threads; SPLIT
+// (Q4_K and Q6_K only) shares each super-block among the four lanes of a
+// quad. Dynamic LDS (floats): the padded x,
 // (units | 1) unit sums per row of the workgroup, and with norm_w a copy of
 // the norm weights (cols).
 
@@ -362,6 +364,131 @@ template <> struct Raw<8> {
     __device__ __forceinline__ float sum(const float *x) const { return q80_sum(raw, s, x, 0.0f); }
 };
 
+// ── split super-blocks (small launches) ────────────────────────────────────
+// A decode-sized launch leaves most SIMDs idle, and one lane summing a whole
+// super-block issues ~1,100 VALU instructions in a row. In split mode four
+// lanes (a quad) share a super-block: lane s computes the 64 products of
+// segment s (weights 64 s .. 64 s + 63, in the reference's order) in
+// parallel, then the running sum is handed along the quad — segment 0 from
+// 0.0f, segment s from segment s - 1's total — so the sum is still the
+// reference's single chain over the 256 products, in its order.
+
+// (scale, min) of Q4_K sub-block j (runtime j), kernels.c:83-92.
+MYNAH_DEV void q4k_sm_rt(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j, float &sc, float &m) {
+    const uint32_t jl = 8u * (j & 3u);
+    const uint32_t a = (s0 >> jl) & 63u, b = (s1 >> jl) & 63u;
+    const uint32_t c = ((s2 >> jl) & 15u) | (((s0 >> (jl + 6u)) & 3u) << 4);
+    const uint32_t e = ((s2 >> (jl + 4u)) & 15u) | (((s1 >> (jl + 6u)) & 3u) << 4);
+    sc = (float)(j < 4u ? a : c);
+    m = (float)(j < 4u ? b : e);
+}
+
+template <int FMT> struct RawSeg;
+// Q4_K segment g = group g: the header and the 32 quant bytes of the group.
+template <> struct RawSeg<12> {
+    uint4 hdr, q0, q1;
+    __device__ __forceinline__ void load(const uint8_t *b, uint32_t g) {
+        hdr = *(const uint4 *)b;
+        const uint4 *p = (const uint4 *)(b + 16u + 32u * g);
+        q0 = p[0];
+        q1 = p[1];
+    }
+    __device__ __forceinline__ void products(const float *x, uint32_t g, float *p) const {
+#pragma clang fp contract(off)
+        const float d = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+        float sa, ma, sb, mb;
+        q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g, sa, ma);
+        q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g + 1u, sb, mb);
+        const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t lo = q[m] & 0x0f0f0f0fu, hi = (q[m] >> 4) & 0x0f0f0f0fu;
+            const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
+            const float qh[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
+            const float4 xa4 = *(const float4 *)(x + 4 * m);
+            const float4 xb4 = *(const float4 *)(x + 32 + 4 * m);
+            const float xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w}, xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                p[8 * m + 2 * t] = __builtin_fmaf(da, ql[t], -oa) * xa[t];
+                p[8 * m + 2 * t + 1] = __builtin_fmaf(db, qh[t], -ob) * xb[t];
+            }
+        }
+    }
+};
+// Q6_K segment s = (h, half) = (s >> 1, s & 1): weights 128 h + 32 k + 4 m + t
+// for k = 2 half, 2 half + 1; realigned words 16 h .. 16 h + 15 (ql),
+// 32 + 8 h .. + 7 (qh), 48 + 2 h + half (four scales) and d.
+template <> struct RawSeg<14> {
+    uint32_t ql[17], qh[9], sc[2], dw, s;
+    __device__ __forceinline__ void load(const uint8_t *b, uint32_t seg) {
+        s = (uint32_t)(uintptr_t)b & 3u;
+        const uint32_t *a = (const uint32_t *)(b - s);
+        const uint32_t h = seg >> 1, half = seg & 1u;
+#pragma unroll
+        for (int k = 0; k < 17; k++) ql[k] = a[16u * h + k];
+#pragma unroll
+        for (int k = 0; k < 9; k++) qh[k] = a[32u + 8u * h + k];
+        sc[0] = a[48u + 2u * h + half];
+        sc[1] = a[49u + 2u * h + half];
+        dw = a[52];
+    }
+    __device__ __forceinline__ void products(const float *x, uint32_t seg, float *p) const {
+#pragma clang fp contract(off)
+        const uint32_t half = seg & 1u;
+        const float d = f16_to_f32(dw >> (8u * s));
+        const uint32_t scw = align_bytes(sc[1], sc[0], s);
+        float dsc[4], n32[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            dsc[j] = d * (float)(int)(int8_t)(scw >> (8 * j));
+            n32[j] = -32.0f * dsc[j];
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const uint32_t lw = align_bytes(ql[8 * kk + m + 1], ql[8 * kk + m], s);
+                const uint32_t hw = align_bytes(qh[m + 1], qh[m], s);
+                const uint32_t nib = (half ? (lw >> 4) : lw) & 0x0f0f0f0fu;
+                const uint32_t q6 = nib | (((hw >> (4u * half + 2u * kk)) & 0x03030303u) << 4);
+                const int j = 2 * kk + (m >= 4 ? 1 : 0);
+                const float qf[4] = {ubyte_f<0>(q6), ubyte_f<1>(q6), ubyte_f<2>(q6), ubyte_f<3>(q6)};
+                const float4 x4 = *(const float4 *)(x + 32 * kk + 4 * m);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    p[32 * kk + 4 * m + t] = __builtin_fmaf(dsc[j], qf[t], n32[j]) * xv[t];
+            }
+    }
+};
+template <> struct RawSeg<8> {   // never launched: split mode is Q4_K / Q6_K only
+    __device__ __forceinline__ void load(const uint8_t *, uint32_t) {}
+    __device__ __forceinline__ void products(const float *, uint32_t, float *p) const {
+#pragma unroll
+        for (int i = 0; i < 64; i++) p[i] = 0.0f;
+    }
+};
+
+// The quad's running sum: step k extends the total handed over by lane
+// k - 1 of the quad (0.0f at step 0) with this lane's 64 products; lane k
+// keeps step k's result. Returns the unit sum on lane 3.
+MYNAH_DEV float quad_chain(const float *p, uint32_t seg) {
+#pragma clang fp contract(off)
+    float carry = 0.0f, res = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 4u; k++) {
+        float t = carry;
+#pragma unroll
+        for (int i = 0; i < 64; i++) t = t + p[i];
+        res = seg == k ? t : res;
+        // quad_perm(0, 0, 1, 2): lane i of the quad receives lane i - 1's t.
+        carry = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x90, 0xf, 0xf, false));
+    }
+    return res;
+}
+
 // x position of unit u in the padded LDS copy.
 template <int FMT>
 MYNAH_DEV const float *unit_x(const float *lx, uint32_t u) {
@@ -369,14 +496,16 @@ MYNAH_DEV const float *unit_x(const float *lx, uint32_t u) {
     return lx + 260u * u;
 }
 
-template <int FMT>
+template <int FMT, bool SEG>
 MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float *lds, double *shd) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t lk = shape & 31u, ws_n = (shape >> 8) & 31u, wr_n = (shape >> 16) & 31u;
-    const uint32_t k = 1u << lk, rpw = 64u >> lk, rpg = rpw * wr_n;
+    // SEG: lane = 4 * (unit lane) + segment; 16 unit lanes per wave.
+    const uint32_t ul = SEG ? lane >> 2 : lane, seg = lane & 3u;
+    const uint32_t k = 1u << lk, rpw = (SEG ? 16u : 64u) >> lk, rpg = rpw * wr_n;
     const uint32_t wr = wave / ws_n, wsi = wave - wr * ws_n;
-    const uint32_t rl = wr * rpw + (lane >> lk), j = lane & (k - 1u);
+    const uint32_t rl = wr * rpw + (ul >> lk), j = ul & (k - 1u);
     const uint32_t row0 = (t - g.tile0) * rpg, row = row0 + rl;
     const size_t roff = (size_t)(row < g.rows ? row : g.rows - 1u) * g.row_bytes;
     const uint8_t *r1 = g.w + roff;
@@ -386,7 +515,12 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     constexpr uint32_t UB = Raw<FMT>::BYTES;
     uint32_t u = j + k * wsi;
     Raw<FMT> raw;
-    if (u < Ut) raw.load(u < U ? r1 + UB * u : r2 + UB * (u - U));
+    RawSeg<FMT> rs;
+    if (u < Ut) {
+        const uint8_t *b = u < U ? r1 + UB * u : r2 + UB * (u - U);
+        if (SEG) rs.load(b, seg);
+        else raw.load(b);
+    }
 
     // Prefetch what the epilogue reads (residual row, cache slot).
     const uint32_t frow = row0 + tid;
@@ -408,10 +542,12 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
             const float4 v = x4[q], w = w4[q];
             *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = v;
             *(float4 *)(lw + 4u * q) = w;
-            acc += (double)v.x * (double)v.x;
-            acc += (double)v.y * (double)v.y;
-            acc += (double)v.z * (double)v.z;
-            acc += (double)v.w * (double)v.w;
+            // A float's square is exact in double, so one fma rounds
+            // exactly as the reference's multiply-then-add.
+            acc = __builtin_fma((double)v.x, (double)v.x, acc);
+            acc = __builtin_fma((double)v.y, (double)v.y, acc);
+            acc = __builtin_fma((double)v.z, (double)v.z, acc);
+            acc = __builtin_fma((double)v.w, (double)v.w, acc);
         }
         const double sum = block_sum_d(acc, shd);
         const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)g.eps));
@@ -432,9 +568,20 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     float *part = lds + xpad_floats(cols);
     while (u < Ut) {
         const uint32_t uu = u < U ? u : u - U;
-        part[rl * pstride + u] = raw.sum(unit_x<FMT>(lds, uu));
+        if (SEG) {
+            float pr[64];
+            rs.products(unit_x<FMT>(lds, uu) + 64u * seg, seg, pr);
+            const float r = quad_chain(pr, seg);
+            if (seg == 3u) part[rl * pstride + u] = r;
+        } else {
+            part[rl * pstride + u] = raw.sum(unit_x<FMT>(lds, uu));
+        }
         u += step;
-        if (u < Ut) raw.load(u < U ? r1 + UB * u : r2 + UB * (u - U));
+        if (u < Ut) {
+            const uint8_t *b = u < U ? r1 + UB * u : r2 + UB * (u - U);
+            if (SEG) rs.load(b, seg);
+            else raw.load(b);
+        }
     }
     __syncthreads();
 
@@ -464,7 +611,14 @@ mynah_gemv_group(const GemvGroup grp) {
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
     const GemvDesc &g = grp.d[i];
-    if (g.type == 12u) group_split<12>(g, t, grp.shape, lds, shd);
-    else if (g.type == 14u) group_split<14>(g, t, grp.shape, lds, shd);
-    else group_split<8>(g, t, grp.shape, lds, shd);
+    if (grp.shape & (1u << 24)) {
+        if (g.type == 12u) group_split<12, true>(g, t, grp.shape, lds, shd);
+        else group_split<14, true>(g, t, grp.shape, lds, shd);
+    } else if (g.type == 12u) {
+        group_split<12, false>(g, t, grp.shape, lds, shd);
+    } else if (g.type == 14u) {
+        group_split<14, false>(g, t, grp.shape, lds, shd);
+    } else {
+        group_split<8, false>(g, t, grp.shape, lds, shd);
+    }
 }

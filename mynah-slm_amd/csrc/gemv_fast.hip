@@ -177,10 +177,12 @@ MYNAH_DEV void fast_stage(const GemvDesc &g, float *lx, float *ls, float *lw, do
             const uint32_t i = 4u * q;
             *(float4 *)(lx + i + 4u * (i >> 6)) = v;
             *(float4 *)(lw + i) = w;
-            acc += (double)v.x * (double)v.x;
-            acc += (double)v.y * (double)v.y;
-            acc += (double)v.z * (double)v.z;
-            acc += (double)v.w * (double)v.w;
+            // A float's square is exact in double, so one fma rounds
+            // exactly as the reference's multiply-then-add.
+            acc = __builtin_fma((double)v.x, (double)v.x, acc);
+            acc = __builtin_fma((double)v.y, (double)v.y, acc);
+            acc = __builtin_fma((double)v.z, (double)v.z, acc);
+            acc = __builtin_fma((double)v.w, (double)v.w, acc);
         }
         const double sum = block_sum_d(acc, shd);
         const float s = (float)(1.0 / sqrt(sum / (double)g.cols + (double)g.eps));

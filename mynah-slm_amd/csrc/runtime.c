@@ -292,19 +292,41 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
     }
     const int exact = (order < 0 ? gemv_order : order) == MYNAH_GEMV_EXACT;
     uint32_t all_rows = 0, max_units = 1;
+    uint64_t all_units = 0;
+    int split = 1;
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
         all_rows += g->rows;
         const uint32_t u = g->w2 ? 2u * g->units : g->units;
         if (u > max_units) max_units = u;
+        all_units += (uint64_t)g->rows * u;
+        if (g->type == MYNAH_Q8_0) split = 0;
         if (g->cols % 8 != 0 || ((uintptr_t)g->x & 15u) != 0 ||
             ((uintptr_t)g->norm_w & 15u) != 0) {
             mynah_set_error("grouped GEMV needs 16-byte aligned x and norm weights, cols %% 8 == 0");
             return -1;
         }
     }
+    /* Split super-blocks across quads when the launch is small enough that
+     * four times the waves still fit the 1,024 SIMDs about twice. */
+    if (all_units > 32768u) split = 0;
+    const char *env = getenv("MYNAH_GEMV_SPLIT");
+    if (env != NULL) split = split && env[0] != '0';
     uint32_t lk = 0, ws = 1, wr = 1, ks = 1, tile_rows;
-    if (exact) {
+    if (exact && split) {
+        uint32_t k = 1;
+        while (k < 16u && k < max_units) k *= 2u;
+        ws = (max_units + k - 1u) / k;
+        if (ws > 16u) ws = 16u;
+        while ((1u << lk) < k) lk++;
+        /* Four (eight for a gate/up pair) row groups per workgroup: fewer
+         * workgroups each staging x (and its RMSNorm) with more threads. */
+        wr = 4u;
+        for (uint32_t i = 0; i < grp->n; i++)
+            if (grp->d[i].w2 != NULL) wr = 8u;
+        while (wr > 1u && ws * wr > 16u) wr /= 2u;
+        tile_rows = (16u >> lk) * wr;
+    } else if (exact) {
         exact_shape(all_rows, max_units, &lk, &ws, &wr);
         tile_rows = (64u >> lk) * wr;
     } else {
@@ -337,7 +359,7 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
         grp->shape = ks;
         return mynah_launch(d, MYNAH_K_GEMV_FAST_GROUP, tiles, 1, 256, lds, stream, args);
     }
-    grp->shape = lk | (ws << 8) | (wr << 16);
+    grp->shape = lk | (ws << 8) | (wr << 16) | ((uint32_t)(exact && split) << 24);
     return mynah_launch(d, MYNAH_K_GEMV_GROUP, tiles, 1, 64u * ws * wr, lds, stream, args);
 }
 
