@@ -230,8 +230,8 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->counters = (uint32_t *)dalloc(16, &ok);
     s->forced = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
     {
-        const size_t parts = (size_t)c->n_kv_heads * ((n_ctx + 31) / 32) * (c->n_heads / c->n_kv_heads);
-        s->nch_max = (n_ctx + 31) / 32;
+        s->nch_max = (n_ctx + MYNAH_AS_CH - 1) / MYNAH_AS_CH;
+        const size_t parts = (size_t)c->n_kv_heads * s->nch_max * (c->n_heads / c->n_kv_heads);
         s->pm = (float *)dalloc(parts * 4, &ok);
         s->pl = (double *)dalloc(parts * 8, &ok);
         s->po = (float *)dalloc(parts * 128 * 4, &ok);

@@ -276,7 +276,8 @@ mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scor
 // weighted sum. Split: grid (n_kv_heads, ceil(n_ctx / AS_CH)), block 128 *
 // group; group <= 8, hd == 128. Partials: pm, pl [n_kv][nch_max][group], po
 // [n_kv][nch_max][group][128].
-#define AS_CH 32
+#define AS_CH 32                                  // = MYNAH_AS_CH (runtime_internal.h)
+#define AS_PASS ((AS_CH + 15) / 16)                 // K passes of 16 positions (group >= 2)
 #define AS_MAXP 1024                                // group * chunks (n_ctx <= 4096)
 // Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
 // x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
@@ -316,9 +317,9 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     // weights and the rotation of position pos.
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t ppp = 4u * nw;                   // positions per pass
-    float kv[2][8];
+    float kv[AS_PASS][8];
 #pragma unroll
-    for (int ps = 0; ps < 2; ps++) {
+    for (int ps = 0; ps < AS_PASS; ps++) {
         const uint32_t t = t0 + ppp * (uint32_t)ps + 4u * wave + r;
         const bool live = t < pos && ppp * (uint32_t)ps < AS_CH;
         const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
@@ -366,7 +367,7 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     __syncthreads();
     // Scores, reference dot order, into es[h][t - t0].
 #pragma unroll
-    for (int ps = 0; ps < 2; ps++) {
+    for (int ps = 0; ps < AS_PASS; ps++) {
         const uint32_t tl = ppp * (uint32_t)ps + 4u * wave + r, t = t0 + tl;
         if (tl < AS_CH && t < n_kv) {
             float kk[8];

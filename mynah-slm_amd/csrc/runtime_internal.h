@@ -45,6 +45,9 @@ enum {
 
 #define MYNAH_MAX_DEVICES 16
 
+/* Positions per workgroup of the split attention (decode.hip AS_CH). */
+#define MYNAH_AS_CH 32
+
 typedef struct {
     int loaded;
     hipModule_t module;
