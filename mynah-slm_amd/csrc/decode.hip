@@ -430,46 +430,71 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     }
 }
 
-// Grid n_kv_heads, block 128 * group: thread (h, d) combines the partials of
-// query head kvh * group + h, dimension d.
-extern "C" __global__ void __launch_bounds__(1024)
+// Grid n_heads, block 64: one wave combines the chunks of one query head,
+// lane l holding dimensions l and l + 64. M = max m_c and the double sum
+// L = sum_c expf(m_c - M) l_c are wave reductions (lane c holds chunk c);
+// then o = fma(expf(m_c - M) * inv, o_c, o) in chunk order, inv =
+// (float)(1 / L).
+#define AC_MAXC 128                                 // chunks (n_ctx <= 4096)
+extern "C" __global__ void __launch_bounds__(64)
 mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                    const double *__restrict__ pl, const float *__restrict__ po,
                    float *__restrict__ out, uint32_t nch_max, uint32_t group) {
 #pragma clang fp contract(off)
-    __shared__ float sm[AS_MAXP];
-    __shared__ double sl[AS_MAXP];
+    __shared__ float wsc[AC_MAXC];
     const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
-    const uint32_t kvh = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
-    const uint32_t h = tid >> 7, d = tid & 127u;
-    const size_t base0 = (size_t)kvh * nch_max * group;
-    const float *pob = po + (base0 + h) * 128u + d;
-    // The first weighted partials are in flight while the maxima are reduced.
-    float pv[8];
+    const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
+    const uint32_t lane = threadIdx.x;
+    const size_t base = (size_t)kvh * nch_max * group + h;    // slot of chunk c: base + c * group
+    const float *pob = po + base * 128u + lane;
+    const size_t cstride = (size_t)group * 128u;
+    // The first weighted partials are in flight while M and L are reduced.
+    float pv[16][2];
 #pragma unroll
-    for (int u = 0; u < 8; u++) pv[u] = (uint32_t)u < nch ? pob[(size_t)u * group * 128u] : 0.0f;
-    for (uint32_t i = tid; i < group * nch; i += nthr) {
-        sm[i] = pm[base0 + i];
-        sl[i] = pl[base0 + i];
+    for (int u = 0; u < 16; u++) {
+        pv[u][0] = (uint32_t)u < nch ? pob[(size_t)u * cstride] : 0.0f;
+        pv[u][1] = (uint32_t)u < nch ? pob[(size_t)u * cstride + 64u] : 0.0f;
     }
-    __syncthreads();
     float M = -__builtin_inff();
-    for (uint32_t k = 0; k < nch; k++) M = fmaxf(M, sm[k * group + h]);
+    for (uint32_t c = lane; c < nch; c += 64u) M = fmaxf(M, pm[base + (size_t)c * group]);
+    M = wave_max_f(M);
     double L = 0.0;
-    for (uint32_t k = 0; k < nch; k++) L += (double)expf(sm[k * group + h] - M) * sl[k * group + h];
-    const float inv = (float)(1.0 / L);
-    float o = 0.0f;
-    uint32_t k = 0;
-    for (; k < 8 && k < nch; k++) o = __builtin_fmaf(expf(sm[k * group + h] - M) * inv, pv[k], o);
-    for (; k + 8 <= nch; k += 8) {
-        float pw[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) pw[u] = pob[(size_t)(k + u) * group * 128u];
-#pragma unroll
-        for (int u = 0; u < 8; u++) o = __builtin_fmaf(expf(sm[(k + u) * group + h] - M) * inv, pw[u], o);
+    for (uint32_t c = lane; c < nch; c += 64u) {
+        const float w = expf(pm[base + (size_t)c * group] - M);
+        wsc[c] = w;
+        L += (double)w * pl[base + (size_t)c * group];
     }
-    for (; k < nch; k++) o = __builtin_fmaf(expf(sm[k * group + h] - M) * inv, pob[(size_t)k * group * 128u], o);
-    out[(size_t)(kvh * group + h) * 128u + d] = o;
+    L = wave_sum_d(L);
+    const float inv = (float)(1.0 / L);
+    __syncthreads();
+    float o0 = 0.0f, o1 = 0.0f;
+    uint32_t c = 0;
+    for (; c < 16u && c < nch; c++) {
+        const float sc = wsc[c] * inv;
+        o0 = __builtin_fmaf(sc, pv[c][0], o0);
+        o1 = __builtin_fmaf(sc, pv[c][1], o1);
+    }
+    for (; c + 8u <= nch; c += 8u) {
+        float a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            a[u] = pob[(size_t)(c + u) * cstride];
+            b[u] = pob[(size_t)(c + u) * cstride + 64u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float sc = wsc[c + u] * inv;
+            o0 = __builtin_fmaf(sc, a[u], o0);
+            o1 = __builtin_fmaf(sc, b[u], o1);
+        }
+    }
+    for (; c < nch; c++) {
+        const float sc = wsc[c] * inv;
+        o0 = __builtin_fmaf(sc, pob[(size_t)c * cstride], o0);
+        o1 = __builtin_fmaf(sc, pob[(size_t)c * cstride + 64u], o1);
+    }
+    out[(size_t)head * 128u + lane] = o0;
+    out[(size_t)head * 128u + 64u + lane] = o1;
 }
 
 
