@@ -39,9 +39,11 @@ MYNAH_DEV void load(RawQ4K &o, const uint8_t *__restrict__ row, uint32_t s, uint
     o.q = *(const uint4 *)(blk + 16u + 16u * u);
 }
 
+// One dwordx3 load from the 4-byte aligned address at or below p (kernels
+// run in unaligned-access mode).
 MYNAH_DEV void load3(uint32_t *d, const uint8_t *p) {
     const uint32_t *a = (const uint32_t *)(p - ((uintptr_t)p & 3u));
-    d[0] = a[0]; d[1] = a[1]; d[2] = a[2];
+    __builtin_memcpy(d, a, 3 * sizeof(uint32_t));
 }
 
 MYNAH_DEV void load(RawQ6K &o, const uint8_t *__restrict__ row, uint32_t s, uint32_t u, uint32_t) {
@@ -62,8 +64,8 @@ MYNAH_DEV void load(RawQ80 &o, const uint8_t *__restrict__ row, uint32_t s, uint
     const uint8_t *blk = row + 34u * (o.ok ? j : 0u);
     o.sh = (uint32_t)(uintptr_t)blk & 3u;
     const uint32_t *a = (const uint32_t *)(blk - o.sh);
-#pragma unroll
-    for (int k = 0; k < 9; k++) o.r[k] = a[k];
+    __builtin_memcpy(o.r, a, 8 * sizeof(uint32_t));
+    o.r[8] = a[8];
 }
 
 // ── one lane's partial over one super-block ───────────────────────────────
