@@ -13,6 +13,23 @@
 // SPDX-License-Identifier: MIT
 #include "common.hip.h"
 
+// The value of lane i + N of the same 16-lane row (DPP row_shl:N; past the
+// row end 0, which no caller uses).
+template <int N>
+MYNAH_DEV float row_down(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xf, 0xf, false));
+}
+
+// Lane 0 of each 16-lane row: the sum of the row's 16 partial dots in the
+// horizontal order of the reference's AVX2 dot (src/kernels.c:39-62): the
+// two 8-lane halves, then 4, then 1, then 2 apart.
+MYNAH_DEV float row16_dot(float acc) {
+    const float tt = acc + row_down<8>(acc);
+    const float v = tt + row_down<4>(tt);
+    const float w = v + row_down<1>(v);
+    return w + row_down<2>(w);
+}
+
 #define DEC_WG 256
 
 // Wave-wide double sum / float max (all lanes get the result).
@@ -106,10 +123,7 @@ mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
             float acc = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kv[j], acc);
-            const float tt = acc + __shfl_down(acc, 8, 16);
-            const float v = tt + __shfl_down(tt, 4, 16);
-            const float w = v + __shfl_down(v, 1, 16);
-            const float dot = w + __shfl_down(w, 2, 16);
+            const float dot = row16_dot(acc);
             if (l == 0) scores[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
         }
     }
@@ -377,10 +391,7 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                 float acc = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kk[j], acc);
-                const float tt = acc + __shfl_down(acc, 8, 16);
-                const float v = tt + __shfl_down(tt, 4, 16);
-                const float w = v + __shfl_down(v, 1, 16);
-                const float dot = w + __shfl_down(w, 2, 16);
+                const float dot = row16_dot(acc);
                 if (l == 0) es[h][tl] = dot * scale;
             }
         }
@@ -412,15 +423,16 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         }
 #pragma unroll
         for (int t = 0; t < AS_CH; t++) vv[t] = vs[t][d];
+        // Positions past n_kv have e = 0 and v = 0, so they leave both sums
+        // unchanged; the exp sum runs as four interleaved double chains.
         float o = 0.0f;
-        double lsum = 0.0;
+        double l4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int t = 0; t < AS_CH; t++) {
-            if ((uint32_t)t < tn) {
-                o = __builtin_fmaf(vv[t], e[t], o);
-                lsum += (double)e[t];
-            }
+            o = __builtin_fmaf(vv[t], e[t], o);
+            l4[t & 3] += (double)e[t];
         }
+        const double lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
         const size_t slot = ((size_t)kvh * nch_max + c) * group + h;
         po[slot * 128u + d] = o;
         if (d == 0) {
