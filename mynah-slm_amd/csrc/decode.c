@@ -60,11 +60,11 @@ struct mynah_qwen3 {
     uint32_t *tokens;               /* [n_ctx] generated ids */
     /* Captured steps: [STEP_FULL] with the head and argmax, [STEP_PREFILL]
      * without the head (a prompt token whose logits nobody reads). */
-    hipGraph_t graph[2];
-    hipGraphExec_t exec[2];
-    int graph_state[2];             /* 0 not tried, 1 ready, -1 unavailable */
-    int graph_order[2];             /* GEMV order the graph was captured with */
-    int graph_attn[2];              /* attention mode the graph was captured with */
+    hipGraph_t graph[4];
+    hipGraphExec_t exec[4];
+    int graph_state[4];             /* 0 not tried, 1 ready, -1 unavailable */
+    int graph_order[4];             /* GEMV order the graph was captured with */
+    int graph_attn[4];              /* attention mode the graph was captured with */
     int attn_mode;                  /* MYNAH_ATTN_EXACT or MYNAH_ATTN_SPLIT */
     uint32_t nch_max;               /* position chunks of the split attention */
     float *pm, *po;                 /* split-attention partials: chunk max, weighted V */
@@ -76,7 +76,11 @@ struct mynah_qwen3 {
 #define STEP(s) ((s)->counters + 2)
 #define NFORCED(s) ((s)->counters + 3)
 
-enum { STEP_FULL = 0, STEP_PREFILL = 1 };
+/* STEP_MULTI + v: STEP_BATCH consecutive steps of variant v in one graph
+ * (the counters live on the device, so the steps are identical launches);
+ * it saves the per-launch gap between graphs. */
+enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_MULTI = 2 };
+#define STEP_BATCH 8u
 
 static int fail(char *err, size_t errsz, const char *msg, const char *detail) {
     if (err && errsz) snprintf(err, errsz, "%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
@@ -121,7 +125,7 @@ static void *dalloc(size_t bytes, int *ok) {
 
 void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
-    for (int v = 0; v < 2; v++) {
+    for (int v = 0; v < 4; v++) {
         if (s->exec[v]) (void)hipGraphExecDestroy(s->exec[v]);
         if (s->graph[v]) (void)hipGraphDestroy(s->graph[v]);
     }
@@ -408,9 +412,9 @@ static int embed_current(mynah_qwen3 *s, mynah_device *d) {
     return mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, d->stream, args);
 }
 
-/* Capture each step variant once; fall back to direct launches if capture
- * fails. */
-static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
+/* Capture step variant v once (or again after the GEMV order or attention
+ * mode changed); leaves graph_state[v] = -1 when capture is unavailable. */
+static void ensure_graph(mynah_qwen3 *s, mynah_device *d, int v) {
     hipStream_t st = d->stream;
     if (s->graph_state[v] == 1 &&
         (s->graph_order[v] != mynah_hip_gemv_order() || s->graph_attn[v] != s->attn_mode)) {
@@ -423,7 +427,9 @@ static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
     if (s->graph_state[v] == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
         s->graph_state[v] = -1;
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-            const int rc = enqueue_step(s, d, st, v);
+            int rc = enqueue_step(s, d, st, v % STEP_MULTI);
+            for (uint32_t r = 1; v >= STEP_MULTI && r < STEP_BATCH && rc == 0; r++)
+                rc = enqueue_step(s, d, st, v % STEP_MULTI);
             hipGraph_t g = NULL;
             const hipError_t e = hipStreamEndCapture(st, &g);
             if (rc == 0 && e == hipSuccess && g != NULL &&
@@ -438,6 +444,12 @@ static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
         }
         (void)hipGetLastError();
     }
+}
+
+/* One launch of variant v: its graph, or direct launches without one. */
+static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
+    hipStream_t st = d->stream;
+    ensure_graph(s, d, v);
     if (s->graph_state[v] == 1) {
         if (hipGraphLaunch(s->exec[v], st) != hipSuccess) {
             mynah_set_error("hipGraphLaunch failed");
@@ -445,7 +457,19 @@ static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
         }
         return 0;
     }
-    return enqueue_step(s, d, st, v);
+    int rc = enqueue_step(s, d, st, v % STEP_MULTI);
+    for (uint32_t r = 1; v >= STEP_MULTI && r < STEP_BATCH && rc == 0; r++)
+        rc = enqueue_step(s, d, st, v % STEP_MULTI);
+    return rc;
+}
+
+/* n steps of variant v: batches of STEP_BATCH, then single steps. */
+static int run_steps(mynah_qwen3 *s, mynah_device *d, int v, uint32_t n) {
+    int rc = 0;
+    uint32_t i = 0;
+    for (; i + STEP_BATCH <= n && rc == 0; i += STEP_BATCH) rc = run_step(s, d, STEP_MULTI + v);
+    for (; i < n && rc == 0; i++) rc = run_step(s, d, v);
+    return rc;
 }
 
 static int set_counters(mynah_qwen3 *s, mynah_device *d, uint32_t token, uint32_t step,
@@ -519,13 +543,20 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
         if (m) (void)hipEventDestroy(m);
         return -1;
     }
+    /* Capture before the clock starts: a capture leaves the device idle. */
+    if (n_prompt > 1) {
+        ensure_graph(s, d, n_prompt - 1u >= STEP_BATCH ? STEP_MULTI + STEP_PREFILL : STEP_PREFILL);
+        if ((n_prompt - 1u) % STEP_BATCH) ensure_graph(s, d, STEP_PREFILL);
+    }
+    ensure_graph(s, d, n_steps >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
+    if (n_steps % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
     (void)hipEventRecord(a, d->stream);
     int rc = embed_current(s, d);
     /* src/generate.c:33-36: every prompt token but the last only fills the
      * cache; its logits are never produced. */
-    for (uint32_t i = 0; i + 1 < n_prompt && rc == 0; i++) rc = run_step(s, d, STEP_PREFILL);
+    if (rc == 0 && n_prompt > 1) rc = run_steps(s, d, STEP_PREFILL, n_prompt - 1u);
     (void)hipEventRecord(m, d->stream);
-    for (uint32_t i = 0; i < n_steps && rc == 0; i++) rc = run_step(s, d, STEP_FULL);
+    if (rc == 0) rc = run_steps(s, d, STEP_FULL, n_steps);
     (void)hipEventRecord(b, d->stream);
     if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("decode failed");
@@ -575,7 +606,9 @@ void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
     if (s) s->n_past = 0;
 }
 
-int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) { return s ? s->graph_state[STEP_FULL] == 1 : 0; }
+int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) {
+    return s ? (s->graph_state[STEP_FULL] == 1 || s->graph_state[STEP_MULTI + STEP_FULL] == 1) : 0;
+}
 
 int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode) {
     if (s == NULL || (mode != MYNAH_ATTN_EXACT && mode != MYNAH_ATTN_SPLIT)) {
