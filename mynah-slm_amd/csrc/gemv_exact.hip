@@ -347,6 +347,49 @@ MYNAH_DEV float sigmoid_ref(float v) {
 
 MYNAH_DEV uint32_t xpad_floats(uint32_t cols) { return cols + 4u * ((cols + 255u) >> 8); }
 
+// Stage x (or RMSNorm(x) * norm_w, src/kernels.c:118-128: double sum of
+// squares, s = (float)(1 / sqrt(sum / n + eps)), (x * s) * w) into the
+// padded LDS copy lds[0 .. xpad_floats(cols)); x[i] sits at
+// lds[i + 4 * (i / 256)]. lw (cols floats of LDS) holds the norm weights
+// while they are applied. All x and norm-weight loads are issued before the
+// first wait. Every thread of the workgroup calls it (it has barriers when
+// norm_w is set); the caller synchronises before reading the copy.
+MYNAH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ norm_w,
+                       uint32_t cols, float eps, float *lds, float *lw, double *shd) {
+#pragma clang fp contract(off)
+    const uint32_t tid = threadIdx.x, n4 = cols / 4u;
+    const float4 *x4 = (const float4 *)x;
+    if (norm_w) {
+        const float4 *w4 = (const float4 *)norm_w;
+        double acc = 0.0;
+#pragma unroll 4
+        for (uint32_t q = tid; q < n4; q += blockDim.x) {
+            const float4 v = x4[q], w = w4[q];
+            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = v;
+            *(float4 *)(lw + 4u * q) = w;
+            // A float's square is exact in double, so one fma rounds
+            // exactly as the reference's multiply-then-add.
+            acc = __builtin_fma((double)v.x, (double)v.x, acc);
+            acc = __builtin_fma((double)v.y, (double)v.y, acc);
+            acc = __builtin_fma((double)v.z, (double)v.z, acc);
+            acc = __builtin_fma((double)v.w, (double)v.w, acc);
+        }
+        const double sum = block_sum_d(acc, shd);
+        const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)eps));
+        for (uint32_t q = tid; q < n4; q += blockDim.x) {
+            float4 *px = (float4 *)(lds + 4u * q + 4u * (q >> 6));
+            float4 v = *px;
+            const float4 w = *(const float4 *)(lw + 4u * q);
+            v.x = v.x * sc * w.x; v.y = v.y * sc * w.y; v.z = v.z * sc * w.z; v.w = v.w * sc * w.w;
+            *px = v;
+        }
+    } else {
+#pragma unroll 4
+        for (uint32_t q = tid; q < n4; q += blockDim.x)
+            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = x4[q];
+    }
+}
+
 template <int FMT> struct Raw;
 template <> struct Raw<12> {
     static constexpr uint32_t BYTES = 144;
@@ -498,7 +541,7 @@ MYNAH_DEV const float *unit_x(const float *lx, uint32_t u) {
     return lx + 260u * u;
 }
 
-template <int FMT, bool SEG>
+template <int FMT, bool SEG, class RawT = Raw<FMT>>
 MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float *lds, double *shd) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
@@ -514,9 +557,9 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     const uint8_t *r2 = g.w2 ? g.w2 + roff : r1;
     const uint32_t U = g.units, Ut = g.w2 ? 2u * U : U, pstride = Ut | 1u;
     const uint32_t step = k * ws_n;
-    constexpr uint32_t UB = Raw<FMT>::BYTES;
+    constexpr uint32_t UB = RawT::BYTES;
     uint32_t u = j + k * wsi;
-    Raw<FMT> raw;
+    RawT raw;
     RawSeg<FMT> rs;
     if (u < Ut) {
         const uint8_t *b = u < U ? r1 + UB * u : r2 + UB * (u - U);
@@ -531,40 +574,9 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     if (folds && g.res) resv = g.res[frow];
     const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
 
-    // Stage x (or RMSNorm(x) * norm_w) into the padded LDS copy; all x and
-    // norm-weight loads are issued before the first wait.
-    const uint32_t cols = g.cols, n4 = cols / 4u;
-    const float4 *x4 = (const float4 *)g.x;
-    float *lw = lds + xpad_floats(cols) + rpg * pstride;
-    if (g.norm_w) {
-        const float4 *w4 = (const float4 *)g.norm_w;
-        double acc = 0.0;
-#pragma unroll 4
-        for (uint32_t q = tid; q < n4; q += blockDim.x) {
-            const float4 v = x4[q], w = w4[q];
-            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = v;
-            *(float4 *)(lw + 4u * q) = w;
-            // A float's square is exact in double, so one fma rounds
-            // exactly as the reference's multiply-then-add.
-            acc = __builtin_fma((double)v.x, (double)v.x, acc);
-            acc = __builtin_fma((double)v.y, (double)v.y, acc);
-            acc = __builtin_fma((double)v.z, (double)v.z, acc);
-            acc = __builtin_fma((double)v.w, (double)v.w, acc);
-        }
-        const double sum = block_sum_d(acc, shd);
-        const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)g.eps));
-        for (uint32_t q = tid; q < n4; q += blockDim.x) {
-            float4 *px = (float4 *)(lds + 4u * q + 4u * (q >> 6));
-            float4 v = *px;
-            const float4 w = *(const float4 *)(lw + 4u * q);
-            v.x = v.x * sc * w.x; v.y = v.y * sc * w.y; v.z = v.z * sc * w.z; v.w = v.w * sc * w.w;
-            *px = v;
-        }
-    } else {
-#pragma unroll 4
-        for (uint32_t q = tid; q < n4; q += blockDim.x)
-            *(float4 *)(lds + 4u * q + 4u * (q >> 6)) = x4[q];
-    }
+    // Stage x (or RMSNorm(x) * norm_w) into the padded LDS copy.
+    const uint32_t cols = g.cols;
+    stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + rpg * pstride, shd);
     __syncthreads();
 
     float *part = lds + xpad_floats(cols);

@@ -67,6 +67,9 @@ static int load_device(int dev) {
         }
     }
     HIP_OK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
+    if (hipDeviceGetAttribute(&d->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        d->cus <= 0)
+        d->cus = 256;
     d->loaded = 1;
     return 0;
 }
@@ -281,9 +284,51 @@ static void exact_shape(uint32_t all_rows, uint32_t units, uint32_t *lk, uint32_
     *wr = r;
 }
 
+static long env_long(const char *name, long dflt) {
+    const char *e = getenv(name);
+    return (e != NULL && e[0] != '\0') ? strtol(e, NULL, 10) : dflt;
+}
+
+/* The streaming exact GEMV (gemv_stream.hip) for one large Q4_K / Q6_K
+ * matrix with long rows and no epilogue beyond the input RMSNorm and argmax
+ * keys: a persistent launch of four 4-wave workgroups per CU, each owning a
+ * balanced range of rows. Returns 1 when the launch does not qualify (the
+ * caller uses the grouped kernel), 0 launched, -1 error. Tuning switches:
+ * MYNAH_GEMV_STREAM=0 off, MYNAH_GEMV_MIX=1 the v_fma_mix_f32 form,
+ * MYNAH_STREAM_WGS, MYNAH_STREAM_MIN_UNITS, MYNAH_STREAM_MIN_ROW_UNITS. */
+static int gemv_stream_try(mynah_device *d, const mynah_gemv_group *grp, hipStream_t stream,
+                           uint32_t *tiles_out) {
+    if (grp->n != 1 || env_long("MYNAH_GEMV_STREAM", 1) == 0) return 1;
+    const mynah_gemv_desc *g = &grp->d[0];
+    if (g->w2 != NULL || g->res != NULL || g->ypos != NULL ||
+        (g->type != MYNAH_Q4_K && g->type != MYNAH_Q6_K))
+        return 1;
+    const uint64_t units = (uint64_t)g->rows * g->units;
+    /* Long rows only: with four super-blocks per row (the 0.6B head) the
+     * grouped kernel is faster. */
+    if (units < (uint64_t)env_long("MYNAH_STREAM_MIN_UNITS", 131072) ||
+        g->units < (uint32_t)env_long("MYNAH_STREAM_MIN_ROW_UNITS", 8))
+        return 1;
+    long wgs = env_long("MYNAH_STREAM_WGS", 4L * d->cus);
+    if (wgs < 1) wgs = 1;
+    if ((uint64_t)wgs > g->rows) wgs = (long)g->rows;
+    const uint64_t max_rows = ((uint64_t)g->rows + (uint64_t)wgs - 1u) / (uint64_t)wgs;
+    const uint64_t nf = (max_rows * g->units + 4u) & ~(uint64_t)3u;   /* + spare slot */
+    const size_t lds = ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) + nf +
+                        (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
+    if (lds > 64u * 1024u) return 1;
+    mynah_stream_desc sd = {g->w, g->x, g->y, g->norm_w, g->keys, g->rows, g->units,
+                            g->row_bytes, g->type, g->cols, g->eps};
+    if (tiles_out) *tiles_out = (uint32_t)wgs;
+    void *args[] = {&sd};
+    const int k = env_long("MYNAH_GEMV_MIX", 0) ? MYNAH_K_GEMV_STREAM : MYNAH_K_GEMV_STREAM_CVT;
+    return mynah_launch(d, k, (unsigned)wgs, 1, 256, lds, stream, args);
+}
+
 /* The grouped GEMV in the current order: exact (lane = row x unit slot,
  * unit sums folded in order) or reordered (8-lane row blocks, KS waves
- * splitting the super-blocks of a tile). */
+ * splitting the super-blocks of a tile). A single large matrix in the
+ * exact order takes the streaming kernel. */
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
                             uint32_t *tiles_out, int order) {
     if (grp->n == 0 || grp->n > MYNAH_GROUP_MAX) {
@@ -306,6 +351,10 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
             mynah_set_error("grouped GEMV needs 16-byte aligned x and norm weights, cols %% 8 == 0");
             return -1;
         }
+    }
+    if (exact) {
+        const int rc = gemv_stream_try(d, grp, stream, tiles_out);
+        if (rc != 1) return rc;
     }
     /* Split super-blocks across quads when the launch is small enough that
      * four times the waves still fit the 1,024 SIMDs about twice. */

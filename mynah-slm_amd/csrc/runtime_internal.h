@@ -20,6 +20,8 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_Q6K_GEMM, "mynah_q6k_gemm_exact")        \
     X(MYNAH_K_Q80_GEMM, "mynah_q80_gemm_exact")        \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
+    X(MYNAH_K_GEMV_STREAM, "mynah_gemv_stream")        \
+    X(MYNAH_K_GEMV_STREAM_CVT, "mynah_gemv_stream_cvt") \
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
     X(MYNAH_K_ATTN_SCORES, "mynah_attn_scores")        \
     X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
@@ -53,6 +55,7 @@ typedef struct {
     hipModule_t module;
     hipFunction_t fn[MYNAH_K_COUNT];
     hipStream_t stream;
+    int cus;                  /* compute units (sizes the persistent launches) */
 } mynah_device;
 
 void mynah_set_error(const char *fmt, ...);
@@ -102,6 +105,18 @@ typedef struct {
     float eps;
     uint32_t pad;
 } mynah_gemv_desc;
+
+/* Host mirror of the streaming GEMV's descriptor (gemv_stream.hip
+ * StreamDesc). */
+typedef struct {
+    const void *w;
+    const float *x;
+    float *y;
+    const float *norm_w;
+    unsigned long long *keys;
+    uint32_t rows, units, row_bytes, type, cols;
+    float eps;
+} mynah_stream_desc;
 
 typedef struct {
     uint32_t n, shape;        /* shape: set by the launch */

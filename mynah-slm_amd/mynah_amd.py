@@ -12,7 +12,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmynah_hip.so")
+# MYNAH_HIP_LIB names another build of the library (e.g. a tuning variant).
+LIB_PATH = os.environ.get("MYNAH_HIP_LIB") or os.path.join(HERE, "libmynah_hip.so")
 
 Q8_0, Q4_K, Q6_K = 8, 12, 14
 BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
