@@ -118,6 +118,16 @@ int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols,
                          const float *x, float *y, size_t tokens, void *stream);
 int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols,
                           float *y, void *stream);
+/* Y[tokens][rows] = X[tokens][cols] · W^T summed in the MATVEC order: every
+ * output bit-identical to mynah_hip_matvec_dev (and the reference's
+ * ingot_matvec, kernels.c:94-115, 319-337, 2525-2551) of its own token, at
+ * GEMM speed (the prompt prefill's projections). res (optional, may equal
+ * y): y = res + W x, the reference's residual add (src/arch_qwen3.c:224).
+ * No reference counterpart (the reference's batched product sums in its
+ * own batched order). cols % 256 == 0; device pointers; asynchronous. */
+int mynah_hip_matmat_mv_dev(int type, const void *w, size_t rows, size_t cols,
+                            const float *x, float *y, size_t tokens, const float *res,
+                            void *stream);
 
 /* Summation order of every GEMV (host and device entry points):
  *   MYNAH_GEMV_EXACT (default): the reference's own f32 order, so outputs are

@@ -51,6 +51,11 @@ int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_st
  * cache with synthetic values instead of running a prompt). */
 int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos);
 
+/* The mirror of set_kv: positions [0, n_pos) of the cache into host arrays
+ * [layer][n_pos][kv_dim] (the keys as the attention uses them: normalised
+ * and rotated). */
+int mynah_hip_qwen3_get_kv(const mynah_qwen3 *s, float *k, float *v, uint32_t n_pos);
+
 uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
 /* src/generate.c:13-86 with greedy sampling: the prompt's tokens fill the
  * cache (all but the last without logits, the head is skipped), then
@@ -61,6 +66,23 @@ uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
 int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_prompt,
                            uint32_t n_steps, uint32_t *tokens_out, float *prefill_ms,
                            float *decode_ms);
+
+/* Fill positions n_past .. n_past + n - 1 of the cache with n tokens and
+ * advance n_past by n, without logits — the same bits n calls of
+ * mynah_hip_qwen3_forward(s, token, NULL) leave in the exact GEMV order and
+ * the exact attention (no reference counterpart: the reference prefills
+ * token by token, src/arch_qwen3.c:3-7). Tokens run in chunks of up to 512
+ * (MYNAH_PREFILL_CHUNK) through matvec-order GEMMs, per-row RMSNorm and
+ * SwiGLU, and per-query attention; the chunk buffers are allocated on first
+ * use. 0, or -1 when the tokens do not fit the context. */
+int mynah_hip_qwen3_prefill(mynah_qwen3 *s, const uint32_t *tokens, uint32_t n);
+
+/* How mynah_hip_qwen3_prompt fills the cache with the prompt:
+ *   MYNAH_PREFILL_BATCHED (default): mynah_hip_qwen3_prefill;
+ *   MYNAH_PREFILL_STEPS: one decode step per token, in the current GEMV
+ *     order and attention mode (the reference's loop). */
+enum { MYNAH_PREFILL_BATCHED = 0, MYNAH_PREFILL_STEPS = 1 };
+int mynah_hip_qwen3_set_prefill(mynah_qwen3 *s, int mode);
 
 /* 1 when the step runs as a replayed hipGraph, 0 when launched directly. */
 int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);

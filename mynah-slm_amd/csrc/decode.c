@@ -69,6 +69,13 @@ struct mynah_qwen3 {
     uint32_t nch_max;               /* position chunks of the split attention */
     float *pm, *po;                 /* split-attention partials: chunk max, weighted V */
     double *pl;                     /* split-attention partials: chunk exp sums */
+    /* Batched prompt prefill (allocated on first use for pf_cap tokens):
+     * rows of X, normalised X, Q (rotated in place), attention output,
+     * gate (then SwiGLU) and up activations, scores, and the tokens. */
+    int prefill_mode;               /* MYNAH_PREFILL_BATCHED or MYNAH_PREFILL_STEPS */
+    uint32_t pf_cap;
+    float *pf_x, *pf_xn, *pf_q, *pf_att, *pf_g, *pf_u, *pf_s;
+    uint32_t *pf_tok;
 };
 
 #define TOKEN(s) ((s)->counters + 0)
@@ -131,7 +138,8 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     }
     void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->q,
                     s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->forced, s->pm, s->pl,
-                    s->po};
+                    s->po, s->pf_x, s->pf_xn, s->pf_q, s->pf_att, s->pf_g, s->pf_u, s->pf_s,
+                    s->pf_tok};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
     free(s->layers);
@@ -510,6 +518,251 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
     return 0;
 }
 
+/* ── batched prompt prefill ──────────────────────────────────────────────── */
+
+/* Tokens per prefill chunk: the GEMMs work in 64-token tiles, the scores
+ * buffer holds chunk x n_heads x sstride floats. */
+static uint32_t prefill_chunk_cap(void) {
+    const char *e = getenv("MYNAH_PREFILL_CHUNK");
+    long v = e ? strtol(e, NULL, 10) : 512;
+    if (v < 1) v = 1;
+    if (v > 4096) v = 4096;
+    return (uint32_t)v;
+}
+
+static int prefill_alloc(mynah_qwen3 *s, uint32_t cap) {
+    if (s->pf_cap >= cap) return 0;
+    void *bufs[] = {s->pf_x, s->pf_xn, s->pf_q, s->pf_att, s->pf_g, s->pf_u, s->pf_s, s->pf_tok};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
+        if (bufs[i]) (void)hipFree(bufs[i]);
+    const mynah_qwen3_shape *c = &s->c;
+    int ok = 1;
+    s->pf_x = (float *)dalloc((size_t)cap * c->d_model * 4, &ok);
+    s->pf_xn = (float *)dalloc((size_t)cap * c->d_model * 4, &ok);
+    s->pf_q = (float *)dalloc((size_t)cap * s->q_dim * 4, &ok);
+    s->pf_att = (float *)dalloc((size_t)cap * s->q_dim * 4, &ok);
+    s->pf_g = (float *)dalloc((size_t)cap * c->d_ff * 4, &ok);
+    s->pf_u = (float *)dalloc((size_t)cap * c->d_ff * 4, &ok);
+    s->pf_s = (float *)dalloc((size_t)cap * c->n_heads * s->sstride * 4, &ok);
+    s->pf_tok = (uint32_t *)dalloc((size_t)cap * 4, &ok);
+    if (!ok) {
+        mynah_set_error("out of device memory for a %u-token prefill chunk", cap);
+        s->pf_cap = 0;
+        return -1;
+    }
+    s->pf_cap = cap;
+    return 0;
+}
+
+/* The block size of the decode step's grouped launch whose fused RMSNorm
+ * the prefill's row norm must reproduce (the q/k/v group when gate is NULL,
+ * else the gate/up pair), always in the exact order. */
+static int norm_threads(const mynah_qwen3 *s, const dlayer *L, int ffn, uint32_t *thr) {
+    mynah_gemv_group g;
+    memset(&g, 0, sizeof g);
+    float *x = s->x;
+    int rc;
+    if (!ffn) {
+        g.n = 3;
+        rc = gemv_desc(&g.d[0], &L->wq, x, s->q);
+        rc = rc ? rc : gemv_desc(&g.d[1], &L->wk, x, s->q);
+        rc = rc ? rc : gemv_desc(&g.d[2], &L->wv, x, s->q);
+        for (int k = 0; k < 3; k++) g.d[k].norm_w = (const float *)L->attn_norm.dev;
+    } else {
+        g.n = 1;
+        rc = gemv_desc(&g.d[0], &L->gate, x, s->act);
+        g.d[0].w2 = L->up.dev;
+        g.d[0].norm_w = (const float *)L->ffn_norm.dev;
+    }
+    return rc ? rc : mynah_gemv_group_threads(&g, MYNAH_GEMV_EXACT, thr);
+}
+
+/* T tokens (already in pf_tok) at positions s->n_past .. + T - 1 through
+ * every layer, filling the cache; no head. */
+static int enqueue_prefill_chunk(mynah_qwen3 *s, mynah_device *d, hipStream_t st, uint32_t T) {
+    const mynah_qwen3_shape *c = &s->c;
+    const size_t per_layer = (size_t)s->n_ctx * s->kv_dim;
+    uint32_t p0 = s->n_past, dm = c->d_model;
+    const uint32_t group = c->n_heads / c->n_kv_heads;
+    int rc;
+    {
+        const unsigned char *tab = s->embed.dev;
+        const uint32_t *tk = s->pf_tok;
+        float *x = s->pf_x;
+        uint32_t ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
+        void *args[] = {&tab, &tk, &x, &dm, &ty, &rb};
+        rc = mynah_launch(d, MYNAH_K_EMBED_ROWS, (dm / 32 + 255) / 256, T, 256, 0, st, args);
+    }
+    for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
+        const dlayer *L = &s->layers[l];
+        float *kl = s->k_cache + l * per_layer, *vl = s->v_cache + l * per_layer;
+        uint32_t thr_attn = 0, thr_ffn = 0;
+        rc = norm_threads(s, L, 0, &thr_attn);
+        rc = rc ? rc : norm_threads(s, L, 1, &thr_ffn);
+        if (rc) break;
+        float eps = c->rms_eps;
+        {   /* src/arch_qwen3.c:201 */
+            const float *x = s->pf_x, *w = (const float *)L->attn_norm.dev;
+            float *o = s->pf_xn;
+            void *args[] = {&x, &w, &o, &dm, &eps};
+            rc = mynah_launch(d, MYNAH_K_RMSNORM_ROWS, T, 1, thr_attn, 0, st, args);
+        }
+        /* src/arch_qwen3.c:194-199: q, and k / v straight into the cache. */
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->wq.type, L->wq.dev, L->wq.rows, L->wq.cols,
+                                              s->pf_xn, s->pf_q, T, NULL, st);
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->wk.type, L->wk.dev, L->wk.rows, L->wk.cols,
+                                              s->pf_xn, kl + (size_t)p0 * s->kv_dim, T, NULL, st);
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->wv.type, L->wv.dev, L->wv.rows, L->wv.cols,
+                                              s->pf_xn, vl + (size_t)p0 * s->kv_dim, T, NULL, st);
+        if (rc) break;
+        {   /* src/arch_qwen3.c:209-218 */
+            float *q = s->pf_q;
+            const float *qn = (const float *)L->q_norm.dev, *kn = (const float *)L->k_norm.dev;
+            const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+            uint32_t nh = c->n_heads, kvd = s->kv_dim;
+            void *args[] = {&q, &kl, &qn, &kn, &rcos, &rsin, &p0, &nh, &kvd, &eps};
+            rc = mynah_launch(d, MYNAH_K_PREFILL_ROPE, T, c->n_heads + c->n_kv_heads, 64, 0, st,
+                              args);
+        }
+        if (rc) break;
+        {   /* src/kernels.c:228-293 (src/arch_qwen3.c:219-222) */
+            const float *qn = s->pf_q;
+            const float *kc = kl;
+            float *sc = s->pf_s, scale = s->scale;
+            uint32_t sstride = s->sstride, kvd = s->kv_dim, grp = group;
+            void *args[] = {&qn, &kc, &sc, &p0, &sstride, &kvd, &grp, &scale};
+            rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 15) / 16, T,
+                               256, 0, st, args);
+            if (rc) break;
+            const float *vc = vl, *scc = s->pf_s;
+            float *out = s->pf_att;
+            void *args2[] = {&vc, &scc, &out, &p0, &sstride, &kvd, &grp};
+            rc = mynah_launch3(d, MYNAH_K_PREFILL_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, T,
+                               64 * group, (size_t)group * s->sstride * 4, st, args2);
+        }
+        if (rc) break;
+        /* src/arch_qwen3.c:223-224: x += Wo attn */
+        rc = mynah_matmat_mv_launch(d, L->wo.type, L->wo.dev, L->wo.rows, L->wo.cols, s->pf_att,
+                                    s->pf_x, T, s->pf_x, st);
+        if (rc) break;
+        {   /* src/arch_qwen3.c:226 */
+            const float *x = s->pf_x, *w = (const float *)L->ffn_norm.dev;
+            float *o = s->pf_xn;
+            void *args[] = {&x, &w, &o, &dm, &eps};
+            rc = mynah_launch(d, MYNAH_K_RMSNORM_ROWS, T, 1, thr_ffn, 0, st, args);
+        }
+        /* src/arch_qwen3.c:227-233: gate, up, SwiGLU, down + residual */
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->gate.type, L->gate.dev, L->gate.rows,
+                                              L->gate.cols, s->pf_xn, s->pf_g, T, NULL, st);
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->up.type, L->up.dev, L->up.rows, L->up.cols,
+                                              s->pf_xn, s->pf_u, T, NULL, st);
+        if (rc) break;
+        {
+            const float *g = s->pf_g, *u = s->pf_u;
+            float *a = s->pf_g;
+            uint32_t n = T * c->d_ff;
+            void *args[] = {&g, &u, &a, &n};
+            rc = mynah_launch(d, MYNAH_K_SWIGLU_ROWS, (n + 255) / 256, 1, 256, 0, st, args);
+        }
+        rc = rc ? rc : mynah_matmat_mv_launch(d, L->down.type, L->down.dev, L->down.rows,
+                                              L->down.cols, s->pf_g, s->pf_x, T, s->pf_x, st);
+    }
+    return rc;
+}
+
+int mynah_hip_qwen3_prefill(mynah_qwen3 *s, const uint32_t *tokens, uint32_t n) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || (tokens == NULL && n > 0)) {
+        mynah_set_error("bad prefill arguments");
+        return -1;
+    }
+    if (n > s->n_ctx - s->n_past) {
+        mynah_set_error("%u prefill tokens do not fit the context (%u of %u used)", n, s->n_past,
+                        s->n_ctx);
+        return -1;
+    }
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= s->c.vocab) {
+            mynah_set_error("token %u out of range", tokens[i]);
+            return -1;
+        }
+    const uint32_t cap = prefill_chunk_cap();
+    if (n > 0 && prefill_alloc(s, n < cap ? n : cap) != 0) return -1;
+    hipStream_t st = d->stream;
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t T = n - done < s->pf_cap ? n - done : s->pf_cap;
+        if (hipMemcpyAsync(s->pf_tok, tokens + done, (size_t)T * 4, hipMemcpyHostToDevice, st) !=
+            hipSuccess) {
+            mynah_set_error("prefill token upload failed");
+            return -1;
+        }
+        if (enqueue_prefill_chunk(s, d, st, T) != 0) return -1;
+        s->n_past += T;
+        done += T;
+        /* the token buffer is reused by the next chunk */
+        if (done < n && hipStreamSynchronize(st) != hipSuccess) {
+            mynah_set_error("prefill failed");
+            return -1;
+        }
+    }
+    if (hipStreamSynchronize(st) != hipSuccess) {
+        mynah_set_error("prefill failed");
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_qwen3_set_prefill(mynah_qwen3 *s, int mode) {
+    if (s == NULL || (mode != MYNAH_PREFILL_BATCHED && mode != MYNAH_PREFILL_STEPS)) {
+        mynah_set_error("prefill mode %d", mode);
+        return -1;
+    }
+    s->prefill_mode = mode;
+    return 0;
+}
+
+/* src/generate.c:13-86 with the prompt's cache-filling tokens prefilled in
+ * batches (bit-identical to filling them one decode step at a time), then
+ * the greedy steps from the last prompt token. */
+static int prompt_batched(mynah_qwen3 *s, mynah_device *d, const uint32_t *prompt,
+                          uint32_t n_prompt, uint32_t n_steps, uint32_t *tokens_out,
+                          float *prefill_ms, float *decode_ms) {
+    const uint32_t cap = prefill_chunk_cap();
+    if (prefill_alloc(s, n_prompt - 1u < cap ? n_prompt - 1u : cap) != 0) return -1;
+    ensure_graph(s, d, n_steps >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
+    if (n_steps % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
+    hipEvent_t ev[4] = {NULL, NULL, NULL, NULL};
+    for (int i = 0; i < 4; i++)
+        if (hipEventCreate(&ev[i]) != hipSuccess) {
+            mynah_set_error("hipEventCreate failed");
+            for (int j = 0; j < i; j++) (void)hipEventDestroy(ev[j]);
+            return -1;
+        }
+    const uint32_t start = s->n_past;
+    (void)hipEventRecord(ev[0], d->stream);
+    int rc = mynah_hip_qwen3_prefill(s, prompt, n_prompt - 1u);
+    (void)hipEventRecord(ev[1], d->stream);
+    if (rc == 0) rc = set_counters(s, d, prompt[n_prompt - 1u], 0, 0);
+    (void)hipEventRecord(ev[2], d->stream);
+    if (rc == 0) rc = embed_current(s, d);
+    if (rc == 0) rc = run_steps(s, d, STEP_FULL, n_steps);
+    (void)hipEventRecord(ev[3], d->stream);
+    if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("decode failed");
+        rc = -1;
+    }
+    if (rc == 0 && prefill_ms) (void)hipEventElapsedTime(prefill_ms, ev[0], ev[1]);
+    if (rc == 0 && decode_ms) (void)hipEventElapsedTime(decode_ms, ev[2], ev[3]);
+    for (int i = 0; i < 4; i++) (void)hipEventDestroy(ev[i]);
+    if (rc != 0) return -1;
+    s->n_past = start + (n_prompt - 1u) + n_steps;
+    if (hipMemcpy(tokens_out, s->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        mynah_set_error("token download failed");
+        return -1;
+    }
+    return 0;
+}
+
 int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_prompt,
                            uint32_t n_steps, uint32_t *tokens_out, float *prefill_ms,
                            float *decode_ms) {
@@ -529,6 +782,8 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
             mynah_set_error("token %u out of range", prompt[i]);
             return -1;
         }
+    if (n_prompt > 1 && s->prefill_mode == MYNAH_PREFILL_BATCHED)
+        return prompt_batched(s, d, prompt, n_prompt, n_steps, tokens_out, prefill_ms, decode_ms);
     if (n_prompt > 1 &&
         hipMemcpy(s->forced, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice) != hipSuccess) {
         mynah_set_error("prompt upload failed");
@@ -597,6 +852,27 @@ int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint3
         }
     }
     s->n_past = n_pos;
+    return 0;
+}
+
+int mynah_hip_qwen3_get_kv(const mynah_qwen3 *s, float *k, float *v, uint32_t n_pos) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || k == NULL || v == NULL || n_pos > s->n_ctx) {
+        mynah_set_error("bad KV download");
+        return -1;
+    }
+    if (hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("stream failed");
+        return -1;
+    }
+    const size_t row = (size_t)n_pos * s->kv_dim, per_layer = (size_t)s->n_ctx * s->kv_dim;
+    for (uint32_t l = 0; l < s->c.n_layers; l++) {
+        if (hipMemcpy(k + l * row, s->k_cache + l * per_layer, row * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(v + l * row, s->v_cache + l * per_layer, row * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+            mynah_set_error("KV download failed");
+            return -1;
+        }
+    }
     return 0;
 }
 

@@ -76,46 +76,54 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
 // key from LDS). Scores rows are `sstride` floats apart. Grid (n_kv_heads,
 // ceil(n_ctx / SC_POS)), block 256; group <= 8, hd == 128.
 #define SC_POS 16
-extern "C" __global__ void __launch_bounds__(256)
-mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
-                  const float *__restrict__ q_norm, const float *__restrict__ k_norm,
-                  const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
-                  const uint32_t *__restrict__ pos_ptr, float *__restrict__ scores,
-                  uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group, float eps,
-                  float scale) {
+// ROT: normalise and rotate the query heads and the new key here (the
+// decode step); otherwise q already holds the rotated queries and the
+// cache every rotated key up to pos (the batched prefill).
+template <bool ROT>
+MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__ k_layer,
+                                const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+                                const float *__restrict__ rope_cos,
+                                const float *__restrict__ rope_sin, uint32_t pos,
+                                float *__restrict__ scores, uint32_t sstride, uint32_t kv_dim,
+                                uint32_t group, float eps, float scale) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float qn[8][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
     __shared__ float tmp[9][128];
-    const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
+    const uint32_t n_kv = pos + 1u;
     const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * SC_POS;
     if (t0 >= n_kv) return;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t t = t0 + 4u * wave + r;
-    const bool live = t < pos;                      // the new key is rotated below
+    const bool live = ROT ? t < pos : t < n_kv;     // the new key is rotated below
     const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
     float kv[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) kv[j] = krow[16 * j];
-    const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
-    const bool has_pos = pos < t0 + SC_POS;
-    const uint32_t ntask = group + (has_pos ? 1u : 0u);
-    for (uint32_t task = wave; task < ntask; task += 4u) {
-        if (task < group) {
-            head_norm_rope(q + (size_t)(kvh * group + task) * 128u, qn[task], q_norm, cs, sn, 128u,
-                           eps, tmp[task]);
-        } else {
-            float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
-            head_norm_rope(kpos, kn, k_norm, cs, sn, 128u, eps, tmp[8]);
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
+    if (ROT) {
+        const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
+        const bool has_pos = pos < t0 + SC_POS;
+        const uint32_t ntask = group + (has_pos ? 1u : 0u);
+        for (uint32_t task = wave; task < ntask; task += 4u) {
+            if (task < group) {
+                head_norm_rope(q + (size_t)(kvh * group + task) * 128u, qn[task], q_norm, cs, sn,
+                               128u, eps, tmp[task]);
+            } else {
+                float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
+                head_norm_rope(kpos, kn, k_norm, cs, sn, 128u, eps, tmp[8]);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
+            }
         }
+    } else {
+        for (uint32_t i = threadIdx.x; i < group * 128u; i += blockDim.x)
+            qn[i >> 7][i & 127u] = q[(size_t)kvh * group * 128u + i];
     }
     __syncthreads();
     if (t < n_kv) {
-        if (!live) {
+        if (ROT && !live) {
 #pragma unroll
             for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
         }
@@ -127,6 +135,18 @@ mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
             if (l == 0) scores[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
         }
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
+                  const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+                  const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
+                  const uint32_t *__restrict__ pos_ptr, float *__restrict__ scores,
+                  uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group, float eps,
+                  float scale) {
+    (void)n_ctx;
+    attn_scores_body<true>(q, k_layer, q_norm, k_norm, rope_cos, rope_sin, pos_ptr[0], scores,
+                           sstride, kv_dim, group, eps, scale);
 }
 
 // Softmax and weighted sum of V for one key head and AO_DV = 8 output
@@ -172,14 +192,13 @@ MYNAH_DEV float ao_fma4(float4 v, float4 p, float o) {
     return __builtin_fmaf(v.w, p.w, o);
 }
 
-extern "C" __global__ void __launch_bounds__(512)
-mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scores,
-               const uint32_t *__restrict__ pos_ptr, float *__restrict__ out, uint32_t sstride,
-               uint32_t kv_dim, uint32_t group) {
+MYNAH_DEV void attn_out_body(const float *__restrict__ v_layer, const float *__restrict__ scores,
+                             uint32_t pos, float *__restrict__ out, uint32_t sstride,
+                             uint32_t kv_dim, uint32_t group) {
 #pragma clang fp contract(off)
     extern __shared__ __attribute__((aligned(16))) float p_all[];
     __shared__ __attribute__((aligned(16))) float vt[AO_DV][AO_CH + 4];
-    const uint32_t n_kv = pos_ptr[0] + 1u;
+    const uint32_t n_kv = pos + 1u;
     const uint32_t kvh = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t nthr = blockDim.x;
     const float *vcol = v_layer + (size_t)kvh * 128u + AO_DV * blockIdx.y;
@@ -274,6 +293,13 @@ mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scor
         __syncthreads();
     }
     if (chain) out[(size_t)(kvh * group + wave) * 128u + AO_DV * blockIdx.y + lane] = o;
+}
+
+extern "C" __global__ void __launch_bounds__(512)
+mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scores,
+               const uint32_t *__restrict__ pos_ptr, float *__restrict__ out, uint32_t sstride,
+               uint32_t kv_dim, uint32_t group) {
+    attn_out_body(v_layer, scores, pos_ptr[0], out, sstride, kv_dim, group);
 }
 
 // ── attention with the positions split across workgroups ───────────────────
@@ -618,4 +644,108 @@ mynah_embed_row(const uint8_t *__restrict__ table, const uint32_t *__restrict__ 
     const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;   // 32-value group
     if (c >= d / 32u) return;
     embed_group(table, token_ptr[0], x, c, type, row_bytes);
+}
+
+// ── batched prompt prefill ─────────────────────────────────────────────────
+// The prompt's tokens fill the cache T at a time (positions p0 .. p0 + T - 1)
+// with the same operations, in the same order, as T decode steps: every
+// value a kernel here writes is bit-identical to the one the decode step
+// writes for that token (same device functions, same reduction orders).
+// Rows are tokens: X[t][d], Q[t][q_dim], scores[t][head][sstride].
+
+// Input RMSNorm of row t (src/kernels.c:118-128), reduced exactly as the
+// fused norm of a grouped GEMV launch with blockDim.x threads (stage_x):
+// thread i accumulates the float4s i, i + blockDim.x, ... in order, then
+// block_sum_d. Grid: rows; the caller passes the decode launch's block size.
+extern "C" __global__ void __launch_bounds__(1024)
+mynah_rmsnorm_rows(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ out,
+                   uint32_t cols, float eps) {
+#pragma clang fp contract(off)
+    __shared__ double shd[16];
+    const float4 *x4 = (const float4 *)(x + (size_t)blockIdx.x * cols);
+    const float4 *w4 = (const float4 *)w;
+    float4 *o4 = (float4 *)(out + (size_t)blockIdx.x * cols);
+    const uint32_t n4 = cols / 4u;
+    double acc = 0.0;
+#pragma unroll 4
+    for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
+        const float4 v = x4[q];
+        acc = __builtin_fma((double)v.x, (double)v.x, acc);
+        acc = __builtin_fma((double)v.y, (double)v.y, acc);
+        acc = __builtin_fma((double)v.z, (double)v.z, acc);
+        acc = __builtin_fma((double)v.w, (double)v.w, acc);
+    }
+    const double sum = block_sum_d(acc, shd);
+    const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)eps));
+    for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
+        float4 v = x4[q];
+        const float4 wv = w4[q];
+        v.x = v.x * sc * wv.x; v.y = v.y * sc * wv.y; v.z = v.z * sc * wv.z; v.w = v.w * sc * wv.w;
+        o4[q] = v;
+    }
+}
+
+// act = (g * sigmoid(g)) * u elementwise (src/kernels.c:193-205, the
+// grouped GEMV's gate/up epilogue); act may alias g.
+extern "C" __global__ void __launch_bounds__(256)
+mynah_swiglu_rows(const float *g, const float *__restrict__ u, float *act, uint32_t n) {
+#pragma clang fp contract(off)
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    act[i] = gv * sigmoid_ref(gv) * u[i];
+}
+
+// Embedding rows of T tokens: grid (ceil(d / 32 / 256), T), one thread per
+// 32 values (src/arch_qwen3.c:160-176).
+extern "C" __global__ void __launch_bounds__(DEC_WG)
+mynah_embed_rows(const uint8_t *__restrict__ table, const uint32_t *__restrict__ tokens,
+                 float *__restrict__ x, uint32_t d, uint32_t type, uint32_t row_bytes) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= d / 32u) return;
+    embed_group(table, tokens[blockIdx.y], x + (size_t)blockIdx.y * d, c, type, row_bytes);
+}
+
+// Per-head RMSNorm + RoPE of the T new tokens (src/arch_qwen3.c:209-218):
+// grid (T, n_heads + n_kv_heads), one wave; head h < n_heads rotates query
+// head h of row t in q, the others key head h - n_heads of position p0 + t in
+// the layer's cache, both in place.
+extern "C" __global__ void __launch_bounds__(64)
+mynah_prefill_rope(float *__restrict__ q, float *__restrict__ k_layer,
+                   const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+                   const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
+                   uint32_t p0, uint32_t n_heads, uint32_t kv_dim, float eps) {
+    __shared__ float tmp[128];
+    const uint32_t t = blockIdx.x, h = blockIdx.y, pos = p0 + t;
+    const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
+    if (h < n_heads) {
+        float *qh = q + ((size_t)t * n_heads + h) * 128u;
+        head_norm_rope(qh, qh, q_norm, cs, sn, 128u, eps, tmp);
+    } else {
+        float *kh = k_layer + (size_t)pos * kv_dim + (size_t)(h - n_heads) * 128u;
+        head_norm_rope(kh, kh, k_norm, cs, sn, 128u, eps, tmp);
+    }
+}
+
+// Scores of query row t = blockIdx.z at position p0 + t against positions
+// 0 .. p0 + t: grid (n_kv_heads, ceil((p0 + T) / SC_POS), T), block 256.
+extern "C" __global__ void __launch_bounds__(256)
+mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_layer,
+                     float *__restrict__ scores, uint32_t p0, uint32_t sstride, uint32_t kv_dim,
+                     uint32_t group, float scale) {
+    const uint32_t t = blockIdx.z, q_dim = gridDim.x * group * 128u;
+    attn_scores_body<false>(qn + (size_t)t * q_dim, (float *)k_layer, nullptr, nullptr, nullptr,
+                            nullptr, p0 + t, scores + (size_t)t * (q_dim / 128u) * sstride, sstride,
+                            kv_dim, group, 0.0f, scale);
+}
+
+// Softmax and weighted V of query row t = blockIdx.z: grid (n_kv_heads,
+// hd / AO_DV, T), block 64 * group, dynamic LDS group * sstride floats.
+extern "C" __global__ void __launch_bounds__(512)
+mynah_prefill_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scores,
+                       float *__restrict__ out, uint32_t p0, uint32_t sstride, uint32_t kv_dim,
+                       uint32_t group) {
+    const uint32_t t = blockIdx.z, n_heads = gridDim.x * group;
+    attn_out_body(v_layer, scores + (size_t)t * n_heads * sstride, p0 + t,
+                  out + (size_t)t * n_heads * 128u, sstride, kv_dim, group);
 }

@@ -11,6 +11,15 @@
 // rounding (one fma gives it), each product and each sum is its own rounding
 // (no contraction), so every output is bit-identical to the reference.
 //
+// The same kernel in the matvec order (ORD = 1) is the prefill GEMM of the
+// resident decoder: every (row, token) output is then the one the
+// reference's matvec (kernels.c:94-115, 319-337; 2525-2551) gives for that
+// token — Q4_K interleaves the low- and high-nibble weights of each byte of
+// a group, Q8_0 folds its sum into the row every 32 values, Q6_K is the same
+// in both orders — so a prompt filled in batches leaves the bits a
+// token-by-token fill would. With `res` set the output is res + W x (the
+// reference's residual add, src/arch_qwen3.c:224, 234; res may alias y).
+//
 // Tiling: a workgroup of 256 threads owns 64 rows x 64 tokens; thread
 // (tr, tc) = (tid / 16, tid % 16) owns rows tr + 16 k and tokens tc + 16 j,
 // k, j < 4: 16 independent chains. Each super-block is processed in two
@@ -146,10 +155,11 @@ MYNAH_DEV void gm_fetch_x(gm_f4 (&xr)[8], const float *__restrict__ x, uint32_t 
     }
 }
 
-template <class Raw, uint32_t UB>
+// ORD: 0 the batched order, 1 the matvec order; FMT the block type.
+template <class Raw, uint32_t UB, int ORD = 0, int FMT = 0>
 MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict__ x,
                           float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens,
-                          uint32_t row_bytes) {
+                          uint32_t row_bytes, const float *res = nullptr) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float wl[GM_ROWS][GM_LD];
     __shared__ __attribute__((aligned(16))) float xl[GM_TOK][GM_LD];
@@ -195,21 +205,63 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
                 raw.load(wrow + UB * nu, 4u * nh + dp);
                 gm_fetch_x(xr, x, tid, tok0, tokens, cols, nu, nh);
             }
-            for (uint32_t i = 0; i < GM_HALF; i += 4) {
-                float4 wv[4], xv[4];
+            if (ORD == 1 && FMT == 12) {
+                // Q4_K matvec order: per group of 64, value j then 32 + j.
+                for (uint32_t g = 0; g < GM_HALF; g += 64)
+                    for (uint32_t j = 0; j < 32; j += 4) {
+                        float4 wl4[4], wh4[4], xl4[4], xh4[4];
 #pragma unroll
-                for (int a = 0; a < 4; a++) wv[a] = *(const float4 *)&wl[tr + 16u * a][i];
+                        for (int a = 0; a < 4; a++) {
+                            wl4[a] = *(const float4 *)&wl[tr + 16u * a][g + j];
+                            wh4[a] = *(const float4 *)&wl[tr + 16u * a][g + 32u + j];
+                        }
 #pragma unroll
-                for (int b = 0; b < 4; b++) xv[b] = *(const float4 *)&xl[tc + 16u * b][i];
+                        for (int b = 0; b < 4; b++) {
+                            xl4[b] = *(const float4 *)&xl[tc + 16u * b][g + j];
+                            xh4[b] = *(const float4 *)&xl[tc + 16u * b][g + 32u + j];
+                        }
 #pragma unroll
-                for (int a = 0; a < 4; a++)
+                        for (int a = 0; a < 4; a++)
 #pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        s[a][b] = s[a][b] + wv[a].x * xv[b].x;
-                        s[a][b] = s[a][b] + wv[a].y * xv[b].y;
-                        s[a][b] = s[a][b] + wv[a].z * xv[b].z;
-                        s[a][b] = s[a][b] + wv[a].w * xv[b].w;
+                            for (int b = 0; b < 4; b++) {
+                                s[a][b] = s[a][b] + wl4[a].x * xl4[b].x;
+                                s[a][b] = s[a][b] + wh4[a].x * xh4[b].x;
+                                s[a][b] = s[a][b] + wl4[a].y * xl4[b].y;
+                                s[a][b] = s[a][b] + wh4[a].y * xh4[b].y;
+                                s[a][b] = s[a][b] + wl4[a].z * xl4[b].z;
+                                s[a][b] = s[a][b] + wh4[a].z * xh4[b].z;
+                                s[a][b] = s[a][b] + wl4[a].w * xl4[b].w;
+                                s[a][b] = s[a][b] + wh4[a].w * xh4[b].w;
+                            }
                     }
+            } else {
+                for (uint32_t i = 0; i < GM_HALF; i += 4) {
+                    float4 wv[4], xv[4];
+#pragma unroll
+                    for (int a = 0; a < 4; a++) wv[a] = *(const float4 *)&wl[tr + 16u * a][i];
+#pragma unroll
+                    for (int b = 0; b < 4; b++) xv[b] = *(const float4 *)&xl[tc + 16u * b][i];
+#pragma unroll
+                    for (int a = 0; a < 4; a++)
+#pragma unroll
+                        for (int b = 0; b < 4; b++) {
+                            s[a][b] = s[a][b] + wv[a].x * xv[b].x;
+                            s[a][b] = s[a][b] + wv[a].y * xv[b].y;
+                            s[a][b] = s[a][b] + wv[a].z * xv[b].z;
+                            s[a][b] = s[a][b] + wv[a].w * xv[b].w;
+                        }
+                    if (ORD == 1 && FMT == 8 && (i & 31u) == 28u) {
+                        // Q8_0 matvec order: each 32-value block's sum joins
+                        // the row total on its own.
+#pragma unroll
+                        for (int a = 0; a < 4; a++)
+#pragma unroll
+                            for (int b = 0; b < 4; b++) {
+                                acc[a][b] = acc[a][b] + s[a][b];
+                                s[a][b] = 0.0f;
+                            }
+                    }
+                }
             }
             __syncthreads();
         }
@@ -224,7 +276,10 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             const uint32_t t = tok0 + tc + 16u * b;
-            if (r < rows && t < tokens) y[(size_t)t * rows + r] = acc[a][b];
+            if (r < rows && t < tokens) {
+                const size_t o = (size_t)t * rows + r;
+                y[o] = res ? res[o] + acc[a][b] : acc[a][b];
+            }
         }
     }
 }
@@ -241,3 +296,16 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
 GEMM_EXACT_ENTRY(mynah_q4k_gemm_exact, GmQ4K, 144u)
 GEMM_EXACT_ENTRY(mynah_q6k_gemm_exact, GmQ6K, 210u)
 GEMM_EXACT_ENTRY(mynah_q80_gemm_exact, GmQ80, 272u)
+
+// The matvec order, with the residual epilogue (res may be NULL or alias y).
+#define GEMM_MV_ENTRY(name, RAW, UB, FMT)                                                      \
+    extern "C" __global__ void __launch_bounds__(256)                                          \
+        name(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,             \
+             uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,                \
+             const float *res) {                                                               \
+        gemm_exact<RAW, UB, 1, FMT>(w, x, y, rows, cols, tokens, row_bytes, res);              \
+    }
+
+GEMM_MV_ENTRY(mynah_q4k_gemm_mv, GmQ4K, 144u, 12)
+GEMM_MV_ENTRY(mynah_q6k_gemm_mv, GmQ6K, 210u, 14)
+GEMM_MV_ENTRY(mynah_q80_gemm_mv, GmQ80, 272u, 8)

@@ -45,3 +45,26 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
     return mynah_launch(d, k, (unsigned)((rows + 63) / 64), (unsigned)((tokens + 63) / 64), 256, 0,
                         stream, args);
 }
+
+int mynah_matmat_mv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                           const float *x, float *y, size_t tokens, const float *res,
+                           hipStream_t stream) {
+    size_t rb;
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if (cols % 256 != 0 || tokens == 0 || tokens > 0xffffffffu || rb > 0xffffffffu) {
+        mynah_set_error("matvec-order GEMM needs cols %% 256 == 0 and 1 <= tokens < 2^32");
+        return -1;
+    }
+    if (((uintptr_t)x & 15u) != 0 || (type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) ||
+        ((uintptr_t)w & 1u) != 0) {
+        mynah_set_error("misaligned operand for the matvec-order GEMM");
+        return -1;
+    }
+    const int k = type == MYNAH_Q4_K   ? MYNAH_K_Q4K_GEMM_MV
+                  : type == MYNAH_Q6_K ? MYNAH_K_Q6K_GEMM_MV
+                                       : MYNAH_K_Q80_GEMM_MV;
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, t32 = (uint32_t)tokens, rb32 = (uint32_t)rb;
+    void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32, &res};
+    return mynah_launch(d, k, (unsigned)((rows + 63) / 64), (unsigned)((tokens + 63) / 64), 256, 0,
+                        stream, args);
+}

@@ -120,6 +120,17 @@ int mynah_launch(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned
     return 0;
 }
 
+int mynah_launch3(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned gz,
+                  unsigned block, size_t shmem, hipStream_t stream, void **args) {
+    hipError_t e = hipModuleLaunchKernel(d->fn[kernel], gx, gy, gz, block, 1, 1,
+                                         (unsigned)shmem, stream, args, NULL);
+    if (e != hipSuccess) {
+        mynah_set_error("launch of %s: %s", kernel_names[kernel], hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
 /* ── geometry ────────────────────────────────────────────────────────────── */
 
 int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes) {
@@ -289,15 +300,23 @@ static long env_long(const char *name, long dflt) {
     return (e != NULL && e[0] != '\0') ? strtol(e, NULL, 10) : dflt;
 }
 
+/* How a grouped GEMV runs: which kernel, its grid, block, LDS and shape
+ * word (and, for the streaming kernel, its descriptor). */
+typedef struct {
+    int kernel;
+    uint32_t grid, threads, shape;
+    size_t lds;
+    mynah_stream_desc sd;
+} gemv_plan;
+
 /* The streaming exact GEMV (gemv_stream.hip) for one large Q4_K / Q6_K
  * matrix with long rows and no epilogue beyond the input RMSNorm and argmax
  * keys: a persistent launch of four 4-wave workgroups per CU, each owning a
  * balanced range of rows. Returns 1 when the launch does not qualify (the
- * caller uses the grouped kernel), 0 launched, -1 error. Tuning switches:
+ * grouped kernel runs instead), 0 planned. Tuning switches:
  * MYNAH_GEMV_STREAM=0 off, MYNAH_GEMV_MIX=1 the v_fma_mix_f32 form,
  * MYNAH_STREAM_WGS, MYNAH_STREAM_MIN_UNITS, MYNAH_STREAM_MIN_ROW_UNITS. */
-static int gemv_stream_try(mynah_device *d, const mynah_gemv_group *grp, hipStream_t stream,
-                           uint32_t *tiles_out) {
+static int gemv_stream_plan(const mynah_device *d, const mynah_gemv_group *grp, gemv_plan *p) {
     if (grp->n != 1 || env_long("MYNAH_GEMV_STREAM", 1) == 0) return 1;
     const mynah_gemv_desc *g = &grp->d[0];
     if (g->w2 != NULL || g->res != NULL || g->ypos != NULL ||
@@ -319,18 +338,21 @@ static int gemv_stream_try(mynah_device *d, const mynah_gemv_group *grp, hipStre
     if (lds > 64u * 1024u) return 1;
     mynah_stream_desc sd = {g->w, g->x, g->y, g->norm_w, g->keys, g->rows, g->units,
                             g->row_bytes, g->type, g->cols, g->eps};
-    if (tiles_out) *tiles_out = (uint32_t)wgs;
-    void *args[] = {&sd};
-    const int k = env_long("MYNAH_GEMV_MIX", 0) ? MYNAH_K_GEMV_STREAM : MYNAH_K_GEMV_STREAM_CVT;
-    return mynah_launch(d, k, (unsigned)wgs, 1, 256, lds, stream, args);
+    p->sd = sd;
+    p->kernel = env_long("MYNAH_GEMV_MIX", 0) ? MYNAH_K_GEMV_STREAM : MYNAH_K_GEMV_STREAM_CVT;
+    p->grid = (uint32_t)wgs;
+    p->threads = 256;
+    p->lds = lds;
+    p->shape = 0;
+    return 0;
 }
 
-/* The grouped GEMV in the current order: exact (lane = row x unit slot,
- * unit sums folded in order) or reordered (8-lane row blocks, KS waves
- * splitting the super-blocks of a tile). A single large matrix in the
- * exact order takes the streaming kernel. */
-int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
-                            uint32_t *tiles_out, int order) {
+/* Plan a grouped GEMV in the given order (-1: the library's current one):
+ * exact (lane = row x unit slot, unit sums folded in order; a single large
+ * matrix with long rows takes the streaming kernel) or reordered (8-lane row
+ * blocks, KS waves splitting the super-blocks of a tile). Sets each
+ * descriptor's tile0. */
+static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int order, gemv_plan *p) {
     if (grp->n == 0 || grp->n > MYNAH_GROUP_MAX) {
         mynah_set_error("group of %u matrices", grp->n);
         return -1;
@@ -352,10 +374,7 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
             return -1;
         }
     }
-    if (exact) {
-        const int rc = gemv_stream_try(d, grp, stream, tiles_out);
-        if (rc != 1) return rc;
-    }
+    if (exact && gemv_stream_plan(d, grp, p) == 0) return 0;
     /* Split super-blocks across quads when the launch is small enough that
      * four times the waves still fit the 1,024 SIMDs about twice. */
     if (all_units > 32768u) split = 0;
@@ -402,14 +421,40 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
         mynah_set_error("input of this GEMV exceeds the LDS budget (%zu B)", lds);
         return -1;
     }
-    if (tiles_out) *tiles_out = tiles;
-    void *args[] = {grp};
+    p->grid = tiles;
+    p->lds = lds;
     if (!exact) {
-        grp->shape = ks;
-        return mynah_launch(d, MYNAH_K_GEMV_FAST_GROUP, tiles, 1, 256, lds, stream, args);
+        p->kernel = MYNAH_K_GEMV_FAST_GROUP;
+        p->threads = 256;
+        p->shape = ks;
+    } else {
+        p->kernel = MYNAH_K_GEMV_GROUP;
+        p->threads = 64u * ws * wr;
+        p->shape = lk | (ws << 8) | (wr << 16) | ((uint32_t)(exact && split) << 24);
     }
-    grp->shape = lk | (ws << 8) | (wr << 16) | ((uint32_t)(exact && split) << 24);
-    return mynah_launch(d, MYNAH_K_GEMV_GROUP, tiles, 1, 64u * ws * wr, lds, stream, args);
+    return 0;
+}
+
+int mynah_gemv_group_threads(mynah_gemv_group *grp, int order, uint32_t *threads) {
+    mynah_device *d = mynah_dev();
+    gemv_plan p;
+    if (d == NULL || gemv_group_plan(d, grp, order, &p) != 0) return -1;
+    *threads = p.threads;
+    return 0;
+}
+
+int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
+                            uint32_t *tiles_out, int order) {
+    gemv_plan p;
+    if (gemv_group_plan(d, grp, order, &p) != 0) return -1;
+    if (tiles_out) *tiles_out = p.grid;
+    if (p.kernel == MYNAH_K_GEMV_STREAM || p.kernel == MYNAH_K_GEMV_STREAM_CVT) {
+        void *args[] = {&p.sd};
+        return mynah_launch(d, p.kernel, p.grid, 1, p.threads, p.lds, stream, args);
+    }
+    grp->shape = p.shape;
+    void *args[] = {grp};
+    return mynah_launch(d, p.kernel, p.grid, 1, p.threads, p.lds, stream, args);
 }
 
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -688,6 +733,18 @@ int mynah_hip_matvec_dev(int type, const void *w, size_t rows, size_t cols, cons
         return -1;
     }
     return mynah_gemv_launch(d, type, w, rows, cols, x, y, mynah_stream_or_default(d, stream));
+}
+
+int mynah_hip_matmat_mv_dev(int type, const void *w, size_t rows, size_t cols, const float *x,
+                            float *y, size_t tokens, const float *res, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w == NULL || x == NULL || y == NULL || tokens == 0) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    return mynah_matmat_mv_launch(d, type, w, rows, cols, x, y, tokens, res,
+                                  mynah_stream_or_default(d, stream));
 }
 
 int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols, const float *x,

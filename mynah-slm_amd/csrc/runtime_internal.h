@@ -19,6 +19,9 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_Q4K_GEMM, "mynah_q4k_gemm_exact")        \
     X(MYNAH_K_Q6K_GEMM, "mynah_q6k_gemm_exact")        \
     X(MYNAH_K_Q80_GEMM, "mynah_q80_gemm_exact")        \
+    X(MYNAH_K_Q4K_GEMM_MV, "mynah_q4k_gemm_mv")        \
+    X(MYNAH_K_Q6K_GEMM_MV, "mynah_q6k_gemm_mv")        \
+    X(MYNAH_K_Q80_GEMM_MV, "mynah_q80_gemm_mv")        \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
     X(MYNAH_K_GEMV_STREAM, "mynah_gemv_stream")        \
     X(MYNAH_K_GEMV_STREAM_CVT, "mynah_gemv_stream_cvt") \
@@ -30,6 +33,12 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
     X(MYNAH_K_EMBED, "mynah_embed_row")                \
+    X(MYNAH_K_RMSNORM_ROWS, "mynah_rmsnorm_rows")      \
+    X(MYNAH_K_SWIGLU_ROWS, "mynah_swiglu_rows")        \
+    X(MYNAH_K_EMBED_ROWS, "mynah_embed_rows")          \
+    X(MYNAH_K_PREFILL_ROPE, "mynah_prefill_rope")      \
+    X(MYNAH_K_PREFILL_SCORES, "mynah_prefill_scores")  \
+    X(MYNAH_K_PREFILL_ATTN_OUT, "mynah_prefill_attn_out") \
     X(MYNAH_K_COPY16, "mynah_copy16")                  \
     X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
     X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \
@@ -63,6 +72,8 @@ mynah_device *mynah_dev(void);
 hipStream_t mynah_stream_or_default(mynah_device *d, void *stream);
 int mynah_launch(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned block,
                  size_t shmem, hipStream_t stream, void **args);
+int mynah_launch3(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned gz,
+                  unsigned block, size_t shmem, hipStream_t stream, void **args);
 int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes);
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
@@ -133,5 +144,15 @@ int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t row
  * current order. */
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
                             uint32_t *tiles, int order);
+/* The block size the launch above would use (its input RMSNorm reduces in
+ * an order that depends on it). */
+int mynah_gemv_group_threads(mynah_gemv_group *grp, int order, uint32_t *threads);
+
+/* Y[tokens][rows] = (res +) X[tokens][cols] · W^T in the matvec summation
+ * order (every output bit-identical to the matvec of its token);
+ * cols % 256 == 0; res may be NULL or alias y. */
+int mynah_matmat_mv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                           const float *x, float *y, size_t tokens, const float *res,
+                           hipStream_t stream);
 
 #endif

@@ -59,6 +59,7 @@ def _load() -> C.CDLL:
         "mynah_hip_matvec_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _P]),
         "mynah_hip_matmat_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _P]),
         "mynah_hip_dequant_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "mynah_hip_matmat_mv_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _P, _P]),
         "mynah_hip_alloc": (_P, [_SZ]),
         "mynah_hip_free": (C.c_int, [_P]),
         "mynah_hip_h2d": (C.c_int, [_P, _P, _SZ]),
@@ -94,6 +95,9 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_generate": (C.c_int, [_P, C.c_uint32, C.c_uint32, _P,
                                                C.POINTER(C.c_float)]),
         "mynah_hip_qwen3_set_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
+        "mynah_hip_qwen3_get_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
+        "mynah_hip_qwen3_prefill": (C.c_int, [_P, _P, C.c_uint32]),
+        "mynah_hip_qwen3_set_prefill": (C.c_int, [_P, C.c_int]),
         "mynah_hip_qwen3_n_past": (C.c_uint32, [_P]),
         "mynah_hip_qwen3_uses_graph": (C.c_int, [_P]),
         "mynah_hip_qwen3_set_attention": (C.c_int, [_P, C.c_int]),
@@ -241,6 +245,22 @@ def q4k_int8_dev(w: int, rows: int, cols: int, xq: int, xs: int, xsum: int, y: i
           "q4k_int8")
 
 
+def matmat_mv(qtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, tokens: int,
+              res: np.ndarray = None) -> np.ndarray:
+    """Y[tokens][rows] in the matvec summation order (+ res), via the GPU."""
+    wd, xd = DeviceBuffer.from_array(w), DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+    yd = DeviceBuffer.from_array(np.ascontiguousarray(res, np.float32)) if res is not None \
+        else DeviceBuffer(4 * rows * tokens)
+    try:
+        check(lib.mynah_hip_matmat_mv_dev(qtype, wd.ptr, rows, cols, xd.ptr, yd.ptr, tokens,
+                                          yd.ptr if res is not None else None, None), "matmat_mv")
+        sync()
+        return yd.download(np.float32, rows * tokens)
+    finally:
+        for b in (wd, xd, yd):
+            b.free()
+
+
 def dequant(qtype: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
     y = np.empty(rows * cols, dtype=np.float32)
     check(lib.ingot_dequant_matrix(qtype, ptr(w), rows, cols, ptr(y)), "ingot_dequant_matrix")
@@ -341,6 +361,7 @@ class SynthQwen3:
 
 
 ATTN_EXACT, ATTN_SPLIT = 0, 1
+PREFILL_BATCHED, PREFILL_STEPS = 0, 1
 
 
 class Qwen3Decoder:
@@ -358,6 +379,25 @@ class Qwen3Decoder:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         check(lib.mynah_hip_qwen3_set_kv(self.h, ptr(k), ptr(v), n_pos), "set_kv")
+
+    def get_kv(self, n_pos: int):
+        """Positions [0, n_pos) of the cache as (k, v), [layer][n_pos][kv_dim]."""
+        sh = self.model.shape
+        kv_dim = sh.n_kv_heads * sh.head_dim
+        k = np.empty((sh.n_layers, n_pos, kv_dim), np.float32)
+        v = np.empty_like(k)
+        check(lib.mynah_hip_qwen3_get_kv(self.h, ptr(k), ptr(v), n_pos), "get_kv")
+        return k, v
+
+    def prefill(self, tokens) -> None:
+        """Fill the cache with `tokens` at the next positions, no logits
+        (bit-identical to one forward(token, want_logits=False) per token)."""
+        p = np.ascontiguousarray(tokens, dtype=np.uint32)
+        check(lib.mynah_hip_qwen3_prefill(self.h, ptr(p), p.size), "prefill")
+
+    def set_prefill(self, mode: int) -> None:
+        """PREFILL_BATCHED (default) or PREFILL_STEPS for prompt()."""
+        check(lib.mynah_hip_qwen3_set_prefill(self.h, mode), "set_prefill")
 
     def forward(self, token: int, want_logits: bool = True):
         logits = np.empty(self.model.shape.vocab, np.float32) if want_logits else None

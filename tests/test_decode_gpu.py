@@ -192,7 +192,7 @@ def test_qwen3_06b_split_attention_same_tokens(M):
 
 
 def test_prompt_prefill_equals_stepwise(M):
-    """Prompt prefill (cache-filling steps without the head) then greedy
+    """Prompt prefill by decode steps (cache-filling steps without the head) then greedy
     steps gives the same ids as feeding the prompt through forward() and
     generating from its last token, and the oracle's greedy run."""
     shape, steps = CF.QWEN3_TINY, 12
@@ -202,6 +202,7 @@ def test_prompt_prefill_equals_stepwise(M):
     for attn in (M.ATTN_EXACT, M.ATTN_SPLIT):
         dec = M.Qwen3Decoder(model, n_ctx)
         dec.set_attention(attn)
+        dec.set_prefill(M.PREFILL_STEPS)
         got, pre_ms, dec_ms = dec.prompt(prompt, steps)
         assert dec.n_past == len(prompt) - 1 + steps
         dec.reset()
