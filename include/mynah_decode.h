@@ -71,7 +71,7 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
  * advance n_past by n, without logits — the same bits n calls of
  * mynah_hip_qwen3_forward(s, token, NULL) leave in the exact GEMV order and
  * the exact attention (no reference counterpart: the reference prefills
- * token by token, src/arch_qwen3.c:3-7). Tokens run in chunks of up to 512
+ * token by token, src/arch_qwen3.c:3-7). Tokens run in chunks of up to 2048
  * (MYNAH_PREFILL_CHUNK) through matvec-order GEMMs, per-row RMSNorm and
  * SwiGLU, and per-query attention; the chunk buffers are allocated on first
  * use. 0, or -1 when the tokens do not fit the context. */

@@ -520,11 +520,12 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
 
 /* ── batched prompt prefill ──────────────────────────────────────────────── */
 
-/* Tokens per prefill chunk: the GEMMs work in 64-token tiles, the scores
+/* Tokens per prefill chunk: the GEMMs work in 64-token tiles (a chunk of
+ * 2048 gives even the 1024-row projections 512 workgroups), the scores
  * buffer holds chunk x n_heads x sstride floats. */
 static uint32_t prefill_chunk_cap(void) {
     const char *e = getenv("MYNAH_PREFILL_CHUNK");
-    long v = e ? strtol(e, NULL, 10) : 512;
+    long v = e ? strtol(e, NULL, 10) : 2048;
     if (v < 1) v = 1;
     if (v > 4096) v = 4096;
     return (uint32_t)v;
@@ -634,11 +635,14 @@ static int enqueue_prefill_chunk(mynah_qwen3 *s, mynah_device *d, hipStream_t st
             rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 15) / 16, T,
                                256, 0, st, args);
             if (rc) break;
-            const float *vc = vl, *scc = s->pf_s;
+            void *args2[] = {&sc, &p0, &sstride};
+            rc = mynah_launch(d, MYNAH_K_PREFILL_SOFTMAX, T, c->n_heads, 64, 0, st, args2);
+            if (rc) break;
+            const float *vc = vl, *pr = s->pf_s;
             float *out = s->pf_att;
-            void *args2[] = {&vc, &scc, &out, &p0, &sstride, &kvd, &grp};
-            rc = mynah_launch3(d, MYNAH_K_PREFILL_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, T,
-                               64 * group, (size_t)group * s->sstride * 4, st, args2);
+            uint32_t tt = T;
+            void *args3[] = {&vc, &pr, &out, &p0, &tt, &sstride, &kvd, &grp};
+            rc = mynah_launch(d, MYNAH_K_PREFILL_PV, c->n_kv_heads, (T + 7) / 8, 512, 0, st, args3);
         }
         if (rc) break;
         /* src/arch_qwen3.c:223-224: x += Wo attn */

@@ -192,6 +192,67 @@ MYNAH_DEV float ao_fma4(float4 v, float4 p, float o) {
     return __builtin_fmaf(v.w, p.w, o);
 }
 
+// Softmax of one scores row over positions 0 .. n_kv - 1 by one wave
+// (src/kernels.c:207-220): the scores are loaded into registers (lane l
+// holds positions 4 l + 256 k .. + 3, n_kv <= 4096), then the f32 max, expf,
+// the double sum and the product with the f32 reciprocal of the sum; p gets
+// the probabilities of the float4s that hold positions < n_kv (positions
+// past n_kv in the last float4 get 0). p may equal sc_row (every score is
+// read before any probability is written).
+MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
+    const float4 *sc = (const float4 *)sc_row;
+    const uint32_t n4 = (n_kv + 3u) / 4u, kmax = (n4 + 63u) / 64u;
+    const float ninf = -__builtin_inff();
+    float4 sv[AO_SK];
+#pragma unroll
+    for (int k = 0; k < AO_SK; k++) {
+        if ((uint32_t)k < kmax) {
+            const uint32_t i = lane + 64u * (uint32_t)k, t = 4u * i;
+            float4 v = i < n4 ? sc[i] : make_float4(ninf, ninf, ninf, ninf);
+            if (t + 1u >= n_kv) v.y = ninf;
+            if (t + 2u >= n_kv) v.z = ninf;
+            if (t + 3u >= n_kv) v.w = ninf;
+            sv[k] = v;
+        }
+    }
+    float m = ninf;
+#pragma unroll
+    for (int k = 0; k < AO_SK; k++)
+        if ((uint32_t)k < kmax)
+            m = fmaxf(fmaxf(fmaxf(m, sv[k].x), fmaxf(sv[k].y, sv[k].z)), sv[k].w);
+    m = wave_max_f(m);
+    double acc = 0.0;
+#pragma unroll
+    for (int k = 0; k < AO_SK; k++) {
+        if ((uint32_t)k < kmax) {
+            float4 e;
+            e.x = expf(sv[k].x - m);
+            e.y = expf(sv[k].y - m);
+            e.z = expf(sv[k].z - m);
+            e.w = expf(sv[k].w - m);
+            acc += (double)e.x;
+            acc += (double)e.y;
+            acc += (double)e.z;
+            acc += (double)e.w;
+            sv[k] = e;
+        }
+    }
+    const double sum = wave_sum_d(acc);
+    const float inv = (float)(1.0 / sum);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < AO_SK; k++) {
+        if ((uint32_t)k < kmax) {
+            const uint32_t i = lane + 64u * (uint32_t)k;
+            const float4 e = sv[k];
+            if (i < n4)
+                *(float4 *)(p + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+        }
+    }
+}
+
 MYNAH_DEV void attn_out_body(const float *__restrict__ v_layer, const float *__restrict__ scores,
                              uint32_t pos, float *__restrict__ out, uint32_t sstride,
                              uint32_t kv_dim, uint32_t group) {
@@ -206,59 +267,9 @@ MYNAH_DEV void attn_out_body(const float *__restrict__ v_layer, const float *__r
     float4 vr[AO_VR];
     ao_fetch(vr, vcol, 0, n_kv, kv_dim, nthr);
 
-    // Softmax of head g = wave, in registers; positions >= n_kv read as -inf
-    // (they leave the max alone and their exponential is 0).
+    // Softmax of head g = wave into LDS.
     float *p = p_all + (size_t)wave * sstride;
-    {
-        const float4 *sc = (const float4 *)(scores + (size_t)(kvh * group + wave) * sstride);
-        const uint32_t n4 = (n_kv + 3u) / 4u, kmax = (n4 + 63u) / 64u;
-        const float ninf = -__builtin_inff();
-        float4 sv[AO_SK];
-#pragma unroll
-        for (int k = 0; k < AO_SK; k++) {
-            if ((uint32_t)k < kmax) {
-                const uint32_t i = lane + 64u * (uint32_t)k, t = 4u * i;
-                float4 v = i < n4 ? sc[i] : make_float4(ninf, ninf, ninf, ninf);
-                if (t + 1u >= n_kv) v.y = ninf;
-                if (t + 2u >= n_kv) v.z = ninf;
-                if (t + 3u >= n_kv) v.w = ninf;
-                sv[k] = v;
-            }
-        }
-        float m = ninf;
-#pragma unroll
-        for (int k = 0; k < AO_SK; k++)
-            if ((uint32_t)k < kmax)
-                m = fmaxf(fmaxf(fmaxf(m, sv[k].x), fmaxf(sv[k].y, sv[k].z)), sv[k].w);
-        m = wave_max_f(m);
-        double acc = 0.0;
-#pragma unroll
-        for (int k = 0; k < AO_SK; k++) {
-            if ((uint32_t)k < kmax) {
-                float4 e;
-                e.x = expf(sv[k].x - m);
-                e.y = expf(sv[k].y - m);
-                e.z = expf(sv[k].z - m);
-                e.w = expf(sv[k].w - m);
-                acc += (double)e.x;
-                acc += (double)e.y;
-                acc += (double)e.z;
-                acc += (double)e.w;
-                sv[k] = e;
-            }
-        }
-        const double sum = wave_sum_d(acc);
-        const float inv = (float)(1.0 / sum);
-#pragma unroll
-        for (int k = 0; k < AO_SK; k++) {
-            if ((uint32_t)k < kmax) {
-                const uint32_t i = lane + 64u * (uint32_t)k;
-                const float4 e = sv[k];
-                if (i < n4)
-                    *(float4 *)(p + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
-            }
-        }
-    }
+    softmax_row(scores + (size_t)(kvh * group + wave) * sstride, n_kv, p);
 
     const bool chain = lane < AO_DV;
     float o = 0.0f;
@@ -739,13 +750,85 @@ mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_l
                             kv_dim, group, 0.0f, scale);
 }
 
-// Softmax and weighted V of query row t = blockIdx.z: grid (n_kv_heads,
-// hd / AO_DV, T), block 64 * group, dynamic LDS group * sstride floats.
+// Softmax of query row t = blockIdx.x, head blockIdx.y (positions 0 ..
+// p0 + t), written back over its scores: grid (T, n_heads), one wave.
+extern "C" __global__ void __launch_bounds__(64)
+mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride) {
+    float *row = scores + ((size_t)blockIdx.x * gridDim.y + blockIdx.y) * sstride;
+    softmax_row(row, p0 + blockIdx.x + 1u, row);
+}
+
+// Weighted V sums of PV_Q consecutive query rows for one key head
+// (src/kernels.c:244-249): out[t][h][d] = fma(v_j[d], p_t,h[j], o) for
+// j = 0 .. p0 + t in order, each chain one thread's register. Thread
+// (d = tid % 128, c = tid / 128) owns the chains (query, head) = pairs
+// c, c + 4, ... of the tile. Per chunk of PV_CH positions the probabilities
+// (0 past each query's own last position, which leaves its chain unchanged:
+// fma(v, 0, o) = o for finite v and o != -0, and o never becomes -0 from
+// +0) and the V rows are staged in LDS; the next chunk's V rows are fetched
+// into registers while this one is summed. Grid (n_kv_heads,
+// ceil(T / PV_Q)), block 512.
+#define PV_Q 8
+#define PV_CH 64
 extern "C" __global__ void __launch_bounds__(512)
-mynah_prefill_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scores,
-                       float *__restrict__ out, uint32_t p0, uint32_t sstride, uint32_t kv_dim,
-                       uint32_t group) {
-    const uint32_t t = blockIdx.z, n_heads = gridDim.x * group;
-    attn_out_body(v_layer, scores + (size_t)t * n_heads * sstride, p0 + t,
-                  out + (size_t)t * n_heads * 128u, sstride, kv_dim, group);
+mynah_prefill_pv(const float *__restrict__ v_layer, const float *__restrict__ probs,
+                 float *__restrict__ out, uint32_t p0, uint32_t T, uint32_t sstride,
+                 uint32_t kv_dim, uint32_t group) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float pl[PV_Q * 8][PV_CH];
+    __shared__ __attribute__((aligned(16))) float vl[PV_CH][128];
+    const uint32_t kvh = blockIdx.x, q0 = blockIdx.y * PV_Q;
+    const uint32_t nq = T - q0 < PV_Q ? T - q0 : PV_Q;
+    const uint32_t npair = nq * group, n_heads = gridDim.x * group;
+    const uint32_t tid = threadIdx.x, d = tid & 127u, c = tid >> 7;
+    const uint32_t n_end = p0 + q0 + nq;            // positions of the last query
+    const float *vbase = v_layer + (size_t)kvh * 128u;
+    // V fetch role: float4 f = tid + 512 k of the chunk: row f / 32, column
+    // 4 (f % 32); rows past n_end read row 0 (never used).
+    float4 vr[4];
+    auto fetch = [&](uint32_t t0) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t f = tid + 512u * (uint32_t)k, r = t0 + (f >> 5);
+            vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
+        }
+    };
+    float o[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) o[k] = 0.0f;
+    fetch(0);
+    for (uint32_t t0 = 0; t0 < n_end; t0 += PV_CH) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t f = tid + 512u * (uint32_t)k;
+            *(float4 *)&vl[f >> 5][4u * (f & 31u)] = vr[k];
+        }
+        for (uint32_t i = tid; i < npair * PV_CH; i += blockDim.x) {
+            const uint32_t pr = i / PV_CH, j = i % PV_CH, t = t0 + j;
+            const uint32_t qi = pr / group, h = pr % group;
+            const uint32_t n_kv = p0 + q0 + qi + 1u;
+            pl[pr][j] = t < n_kv ? probs[((size_t)(q0 + qi) * n_heads + kvh * group + h) * sstride + t]
+                                 : 0.0f;
+        }
+        __syncthreads();
+        if (t0 + PV_CH < n_end) fetch(t0 + PV_CH);
+        const uint32_t tn = n_end - t0 < PV_CH ? n_end - t0 : PV_CH;
+        for (uint32_t j = 0; j < tn; j++) {
+            const float vv = vl[j][d];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t pr = c + 4u * (uint32_t)k;
+                if (pr < npair) o[k] = __builtin_fmaf(vv, pl[pr][j], o[k]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const uint32_t pr = c + 4u * (uint32_t)k;
+        if (pr < npair) {
+            const uint32_t qi = pr / group, h = pr % group;
+            out[((size_t)(q0 + qi) * n_heads + kvh * group + h) * 128u + d] = o[k];
+        }
+    }
 }

@@ -38,7 +38,8 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_EMBED_ROWS, "mynah_embed_rows")          \
     X(MYNAH_K_PREFILL_ROPE, "mynah_prefill_rope")      \
     X(MYNAH_K_PREFILL_SCORES, "mynah_prefill_scores")  \
-    X(MYNAH_K_PREFILL_ATTN_OUT, "mynah_prefill_attn_out") \
+    X(MYNAH_K_PREFILL_SOFTMAX, "mynah_prefill_softmax") \
+    X(MYNAH_K_PREFILL_PV, "mynah_prefill_pv")          \
     X(MYNAH_K_COPY16, "mynah_copy16")                  \
     X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
     X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \
