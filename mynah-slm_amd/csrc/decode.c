@@ -631,16 +631,16 @@ static int enqueue_prefill_chunk(mynah_qwen3 *s, mynah_device *d, hipStream_t st
             const float *kc = kl;
             float *sc = s->pf_s, scale = s->scale;
             uint32_t sstride = s->sstride, kvd = s->kv_dim, grp = group;
-            void *args[] = {&qn, &kc, &sc, &p0, &sstride, &kvd, &grp, &scale};
-            rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 15) / 16, T,
-                               256, 0, st, args);
+            uint32_t tt = T;
+            void *args[] = {&qn, &kc, &sc, &p0, &tt, &sstride, &kvd, &grp, &scale};
+            rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 63) / 64,
+                               (T + 7) / 8, 256, 0, st, args);
             if (rc) break;
             void *args2[] = {&sc, &p0, &sstride};
             rc = mynah_launch(d, MYNAH_K_PREFILL_SOFTMAX, T, c->n_heads, 64, 0, st, args2);
             if (rc) break;
             const float *vc = vl, *pr = s->pf_s;
             float *out = s->pf_att;
-            uint32_t tt = T;
             void *args3[] = {&vc, &pr, &out, &p0, &tt, &sstride, &kvd, &grp};
             rc = mynah_launch(d, MYNAH_K_PREFILL_PV, c->n_kv_heads, (T + 7) / 8, 512, 0, st, args3);
         }

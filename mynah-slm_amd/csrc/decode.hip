@@ -76,10 +76,6 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
 // key from LDS). Scores rows are `sstride` floats apart. Grid (n_kv_heads,
 // ceil(n_ctx / SC_POS)), block 256; group <= 8, hd == 128.
 #define SC_POS 16
-// ROT: normalise and rotate the query heads and the new key here (the
-// decode step); otherwise q already holds the rotated queries and the
-// cache every rotated key up to pos (the batched prefill).
-template <bool ROT>
 MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__ k_layer,
                                 const float *__restrict__ q_norm, const float *__restrict__ k_norm,
                                 const float *__restrict__ rope_cos,
@@ -96,12 +92,12 @@ MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t t = t0 + 4u * wave + r;
-    const bool live = ROT ? t < pos : t < n_kv;     // the new key is rotated below
+    const bool live = t < pos;                      // the new key is rotated below
     const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
     float kv[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) kv[j] = krow[16 * j];
-    if (ROT) {
+    {
         const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
         const bool has_pos = pos < t0 + SC_POS;
         const uint32_t ntask = group + (has_pos ? 1u : 0u);
@@ -117,13 +113,10 @@ MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__
                 for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
             }
         }
-    } else {
-        for (uint32_t i = threadIdx.x; i < group * 128u; i += blockDim.x)
-            qn[i >> 7][i & 127u] = q[(size_t)kvh * group * 128u + i];
     }
     __syncthreads();
     if (t < n_kv) {
-        if (ROT && !live) {
+        if (!live) {
 #pragma unroll
             for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
         }
@@ -145,7 +138,7 @@ mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
                   uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group, float eps,
                   float scale) {
     (void)n_ctx;
-    attn_scores_body<true>(q, k_layer, q_norm, k_norm, rope_cos, rope_sin, pos_ptr[0], scores,
+    attn_scores_body(q, k_layer, q_norm, k_norm, rope_cos, rope_sin, pos_ptr[0], scores,
                            sstride, kv_dim, group, eps, scale);
 }
 
@@ -738,16 +731,66 @@ mynah_prefill_rope(float *__restrict__ q, float *__restrict__ k_layer,
     }
 }
 
-// Scores of query row t = blockIdx.z at position p0 + t against positions
-// 0 .. p0 + t: grid (n_kv_heads, ceil((p0 + T) / SC_POS), T), block 256.
+// Scores of PS_Q consecutive query rows q0 .. q0 + PS_Q - 1 (positions
+// p0 + q0 + i) against a chunk of PS_POS positions, with the dot of the
+// decode kernel (attn_scores_body): lane (r, l) of wave w holds
+// k_t[16 j + l] of positions t = t0 + 16 w + 4 i + r (i < 4), accumulates
+// fma(q[16 j + l], k_t[16 j + l]) over j and the 16 lanes combine in the
+// reference's AVX2 order (row16_dot). The K rows are loaded once for the
+// tile; a query scores only positions up to its own. Grid (n_kv_heads,
+// ceil((p0 + T) / PS_POS), ceil(T / PS_Q)), block 256; group <= 8.
+#define PS_Q 8
+#define PS_POS 64
 extern "C" __global__ void __launch_bounds__(256)
 mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_layer,
-                     float *__restrict__ scores, uint32_t p0, uint32_t sstride, uint32_t kv_dim,
-                     uint32_t group, float scale) {
-    const uint32_t t = blockIdx.z, q_dim = gridDim.x * group * 128u;
-    attn_scores_body<false>(qn + (size_t)t * q_dim, (float *)k_layer, nullptr, nullptr, nullptr,
-                            nullptr, p0 + t, scores + (size_t)t * (q_dim / 128u) * sstride, sstride,
-                            kv_dim, group, 0.0f, scale);
+                     float *__restrict__ scores, uint32_t p0, uint32_t T, uint32_t sstride,
+                     uint32_t kv_dim, uint32_t group, float scale) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float ql[PS_Q][8][128];
+    const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * PS_POS, q0 = blockIdx.z * PS_Q;
+    const uint32_t nq = T - q0 < PS_Q ? T - q0 : PS_Q;
+    const uint32_t last = p0 + q0 + nq - 1u;          // position of the tile's last query
+    if (t0 > last) return;
+    const uint32_t n_heads = gridDim.x * group, q_dim = n_heads * 128u;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t r = lane >> 4, l = lane & 15u;
+    uint32_t tp[4];
+    float kv[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        tp[i] = t0 + 16u * wave + 4u * (uint32_t)i + r;
+        const float *krow =
+            k_layer + (size_t)(tp[i] <= last ? tp[i] : 0u) * kv_dim + (size_t)kvh * 128u + l;
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[i][j] = krow[16 * j];
+    }
+    // Query values stored lane-major: ql[qi][h][8 l + j] = q[16 j + l], so a
+    // lane's eight values are two float4.
+    for (uint32_t i = threadIdx.x; i < nq * group * 128u; i += blockDim.x) {
+        const uint32_t qi = i / (group * 128u), rem = i % (group * 128u), e = rem & 127u;
+        ql[qi][rem >> 7][8u * (e & 15u) + (e >> 4)] =
+            qn[(size_t)(q0 + qi) * q_dim + (size_t)kvh * group * 128u + rem];
+    }
+    __syncthreads();
+    for (uint32_t qi = 0; qi < nq; qi++) {
+        const uint32_t pos = p0 + q0 + qi;
+        if (t0 + 16u * wave > pos) continue;            // wave-uniform
+        float *srow = scores + (size_t)(q0 + qi) * n_heads * sstride;
+        for (uint32_t h = 0; h < group; h++) {
+            const float4 qa = *(const float4 *)&ql[qi][h][8u * l];
+            const float4 qb = *(const float4 *)&ql[qi][h][8u * l + 4u];
+            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            float* hrow = srow + (size_t)(kvh * group + h) * sstride;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qv[j], kv[i][j], acc);
+                const float dot = row16_dot(acc);
+                if (l == 0 && tp[i] <= pos) hrow[tp[i]] = dot * scale;
+            }
+        }
+    }
 }
 
 // Softmax of query row t = blockIdx.x, head blockIdx.y (positions 0 ..
@@ -765,8 +808,9 @@ mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride) {
 // c, c + 4, ... of the tile. Per chunk of PV_CH positions the probabilities
 // (0 past each query's own last position, which leaves its chain unchanged:
 // fma(v, 0, o) = o for finite v and o != -0, and o never becomes -0 from
-// +0) and the V rows are staged in LDS; the next chunk's V rows are fetched
-// into registers while this one is summed. Grid (n_kv_heads,
+// +0) and the V rows (rows past the tile's last position hold row 0, finite)
+// are staged in LDS; the next chunk's V rows are fetched into registers
+// while this one is summed. Grid (n_kv_heads,
 // ceil(T / PV_Q)), block 512.
 #define PV_Q 8
 #define PV_CH 64
@@ -813,13 +857,21 @@ mynah_prefill_pv(const float *__restrict__ v_layer, const float *__restrict__ pr
         }
         __syncthreads();
         if (t0 + PV_CH < n_end) fetch(t0 + PV_CH);
+        // Four positions per step (rounded up: the padding has p = 0).
         const uint32_t tn = n_end - t0 < PV_CH ? n_end - t0 : PV_CH;
-        for (uint32_t j = 0; j < tn; j++) {
-            const float vv = vl[j][d];
+        for (uint32_t j = 0; j < tn; j += 4) {
+            const float v0 = vl[j][d], v1 = vl[j + 1][d], v2 = vl[j + 2][d], v3 = vl[j + 3][d];
 #pragma unroll
             for (int k = 0; k < 16; k++) {
                 const uint32_t pr = c + 4u * (uint32_t)k;
-                if (pr < npair) o[k] = __builtin_fmaf(vv, pl[pr][j], o[k]);
+                if (pr < npair) {
+                    const float4 pp = *(const float4 *)&pl[pr][j];
+                    float acc = o[k];
+                    acc = __builtin_fmaf(v0, pp.x, acc);
+                    acc = __builtin_fmaf(v1, pp.y, acc);
+                    acc = __builtin_fmaf(v2, pp.z, acc);
+                    o[k] = __builtin_fmaf(v3, pp.w, acc);
+                }
             }
         }
     }
