@@ -1,0 +1,85 @@
+/* mynah_gguf.h — real checkpoints: a GGUF file's Qwen3 config and tensor
+ * table, and the resident decoder built from them.
+ *
+ * The reference opens a checkpoint with ingot's GGUF reader and binds its
+ * tensors in src/model.c:71-228 (mynah_slm_load): the config comes from the
+ * "<arch>.*" metadata keys, the tensors by their GGUF names, the head is tied
+ * to token_embd when output.weight is absent, and the vocabulary is the
+ * embedding's row count. This header is that path for the GPU decoder: the
+ * file is memory-mapped, parsed (GGUF v2 / v3, bounds-checked), and its data
+ * section is handed unchanged to mynah_hip_qwen3_new, which uploads it to HBM
+ * once — the tensors are read in place, never repacked.
+ *
+ * SPDX-License-Identifier: MIT */
+#ifndef MYNAH_GGUF_H
+#define MYNAH_GGUF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mynah_decode.h"
+#include "mynah_synth.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mynah_gguf mynah_gguf;
+
+/* Map and parse `path` (third_party/ingot/src/gguf.c's reader, v2 / v3):
+ * header, metadata (every value type, arrays of scalars and strings; strings
+ * up to 16 MiB, counts up to 2^28), tensor infos (up to 8 non-zero
+ * dimensions, quantized rows made of whole blocks, offsets aligned to
+ * general.alignment, default 32, data inside the file). One file: the
+ * reference's split checkpoints (<prefix>-0000k-of-0000n.gguf) are not read.
+ * NULL on any malformed input, with the reason in err. */
+mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz);
+void mynah_gguf_close(mynah_gguf *g);
+
+/* GGUF version, the numbers of metadata entries and tensors, and the data
+ * alignment in force (gguf.h ingot_gguf_version / _kv_count / _count /
+ * _alignment). */
+uint32_t mynah_gguf_version(const mynah_gguf *g);
+uint64_t mynah_gguf_alignment(const mynah_gguf *g);
+uint64_t mynah_gguf_n_kv(const mynah_gguf *g);
+uint64_t mynah_gguf_n_tensors(const mynah_gguf *g);
+
+/* Scalar metadata by key (src/model.c:39-69 kv_u32 / kv_f32): any integer,
+ * float or bool scalar converts (saturating); 0, or -1 when the key is
+ * absent or not a scalar. mynah_gguf_kv_str: a string value (not
+ * NUL-terminated) and its length. mynah_gguf_kv_arr_len: an array's length. */
+int mynah_gguf_kv_u64(const mynah_gguf *g, const char *key, uint64_t *out);
+int mynah_gguf_kv_f64(const mynah_gguf *g, const char *key, double *out);
+int mynah_gguf_kv_str(const mynah_gguf *g, const char *key, const char **out, size_t *len);
+int mynah_gguf_kv_arr_len(const mynah_gguf *g, const char *key, uint64_t *out);
+
+/* The architecture config the way mynah-slm reads it (src/model.c:71-130):
+ * general.architecture gives the key prefix; block_count, embedding_length,
+ * feed_forward_length, attention.head_count, attention.head_count_kv,
+ * attention.key_length, context_length, attention.layer_norm_rms_epsilon and
+ * rope.freq_base are required; attention.value_length, when present, must
+ * equal key_length; the vocabulary is token_embd's row count. *n_ctx_train
+ * (optional) gets context_length. 0, or -1 with the missing key in err. */
+int mynah_gguf_qwen3_shape(const mynah_gguf *g, mynah_qwen3_shape *out, uint32_t *n_ctx_train,
+                           char *err, size_t errsz);
+
+/* Tensor descriptors (name, ggml type, rank, cols = ne[0], rows = the
+ * product of ne[1..] (1 for rank 1), offset within the data section, bytes):
+ * up to `cap` written, *count gets the number of tensors whose names fit the
+ * descriptor (< 48 bytes, the others are skipped). */
+int mynah_gguf_tensor_table(const mynah_gguf *g, mynah_synth_tensor *table, size_t cap,
+                            size_t *count);
+
+/* The data section: base address in the mapping and its size. */
+const void *mynah_gguf_data(const mynah_gguf *g, uint64_t *bytes);
+
+/* mynah_slm_load + mynah_slm_state_init (src/model.c:177-228,
+ * src/arch_qwen3.c:89-131) for the GPU: open `path`, read the config and
+ * tensors, build the resident decoder for n_ctx positions (0: the file's
+ * context_length, capped at 4096), unmap. NULL with the reason in err. */
+mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *err, size_t errsz);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

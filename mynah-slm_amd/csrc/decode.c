@@ -110,6 +110,8 @@ static int bind(dtensor *out, const mynah_synth_tensor *table, size_t count,
         return fail(err, errsz, "tensor has the wrong shape or type", name);
     if (t->offset > blob_bytes || t->nbytes > blob_bytes - t->offset)
         return fail(err, errsz, "tensor outside the blob", name);
+    /* The kernels read weights and norm vectors in 16-byte pieces. */
+    if ((t->offset & 15u) != 0) return fail(err, errsz, "tensor offset not 16-byte aligned", name);
     size_t rb = cols * 4;
     if (t->type != 0 && mynah_geometry(t->type, rows, cols, &rb) != 0)
         return fail(err, errsz, "tensor type has no kernel", name);

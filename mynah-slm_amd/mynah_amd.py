@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import types
 
 import numpy as np
 
@@ -103,6 +104,21 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_set_attention": (C.c_int, [_P, C.c_int]),
         "mynah_hip_qwen3_prompt": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, _P,
                                              C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+        "mynah_gguf_open": (_P, [C.c_char_p, C.c_char_p, _SZ]),
+        "mynah_gguf_close": (None, [_P]),
+        "mynah_gguf_version": (C.c_uint32, [_P]),
+        "mynah_gguf_alignment": (C.c_uint64, [_P]),
+        "mynah_gguf_n_kv": (C.c_uint64, [_P]),
+        "mynah_gguf_n_tensors": (C.c_uint64, [_P]),
+        "mynah_gguf_kv_u64": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "mynah_gguf_kv_f64": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_double)]),
+        "mynah_gguf_kv_str": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(_SZ)]),
+        "mynah_gguf_kv_arr_len": (C.c_int, [_P, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "mynah_gguf_qwen3_shape": (C.c_int, [_P, C.POINTER(Qwen3Shape), C.POINTER(C.c_uint32),
+                                             C.c_char_p, _SZ]),
+        "mynah_gguf_tensor_table": (C.c_int, [_P, C.POINTER(SynthTensor), _SZ, C.POINTER(_SZ)]),
+        "mynah_gguf_data": (_P, [_P, C.POINTER(C.c_uint64)]),
+        "mynah_hip_qwen3_from_gguf": (_P, [C.c_char_p, C.c_uint32, C.c_char_p, _SZ]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -360,6 +376,106 @@ class SynthQwen3:
         return int(sum(self.table[i].nbytes for i in range(self.count)))
 
 
+class GgufShape:
+    """A Qwen3 config read from a GGUF file (the fields of Qwen3Shape)."""
+
+    def __init__(self, c: Qwen3Shape):
+        for name, _ in Qwen3Shape._fields_:
+            setattr(self, name, getattr(c, name))
+
+
+class GgufFile:
+    """A memory-mapped GGUF v2 / v3 file (include/mynah_gguf.h)."""
+
+    def __init__(self, path: str):
+        err = C.create_string_buffer(512)
+        self.h = lib.mynah_gguf_open(os.fsencode(path), err, 512)
+        if not self.h:
+            raise HipError(f"gguf_open: {err.value.decode(errors='replace')}")
+
+    @property
+    def version(self) -> int:
+        return int(lib.mynah_gguf_version(self.h))
+
+    @property
+    def alignment(self) -> int:
+        return int(lib.mynah_gguf_alignment(self.h))
+
+    @property
+    def n_kv(self) -> int:
+        return int(lib.mynah_gguf_n_kv(self.h))
+
+    @property
+    def n_tensors(self) -> int:
+        return int(lib.mynah_gguf_n_tensors(self.h))
+
+    def get_int(self, key: str):
+        v = C.c_uint64(0)
+        return int(v.value) if lib.mynah_gguf_kv_u64(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def get_float(self, key: str):
+        v = C.c_double(0.0)
+        return float(v.value) if lib.mynah_gguf_kv_f64(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def get_str(self, key: str):
+        p, n = C.c_void_p(), _SZ(0)
+        if lib.mynah_gguf_kv_str(self.h, key.encode(), C.byref(p), C.byref(n)) != 0:
+            return None
+        return C.string_at(p.value, n.value).decode("utf-8", errors="replace") if n.value else ""
+
+    def array_len(self, key: str):
+        v = C.c_uint64(0)
+        return int(v.value) if lib.mynah_gguf_kv_arr_len(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def qwen3_shape(self):
+        """(GgufShape, context_length) the way the reference's loader reads them."""
+        c, n_ctx, err = Qwen3Shape(), C.c_uint32(0), C.create_string_buffer(512)
+        if lib.mynah_gguf_qwen3_shape(self.h, C.byref(c), C.byref(n_ctx), err, 512) != 0:
+            raise HipError(f"gguf config: {err.value.decode(errors='replace')}")
+        return GgufShape(c), int(n_ctx.value)
+
+    def tensors(self):
+        """[(name, ggml type, rank, rows, cols, offset, nbytes)] in file order."""
+        n = _SZ(0)
+        check(lib.mynah_gguf_tensor_table(self.h, None, 0, C.byref(n)), "gguf tensors")
+        table = (SynthTensor * max(n.value, 1))()
+        check(lib.mynah_gguf_tensor_table(self.h, table, n.value, C.byref(n)), "gguf tensors")
+        return [(t.name.decode(errors="replace"), t.type, t.rank, t.rows, t.cols, t.offset,
+                 t.nbytes)
+                for t in table[:n.value]]
+
+    def data_bytes(self) -> int:
+        """Bytes from the start of the data section to the end of the file."""
+        n = C.c_uint64(0)
+        lib.mynah_gguf_data(self.h, C.byref(n))
+        return int(n.value)
+
+    def tensor_data(self, offset: int, nbytes: int) -> bytes:
+        """A copy of `nbytes` of the data section from `offset`."""
+        n = C.c_uint64(0)
+        base = lib.mynah_gguf_data(self.h, C.byref(n))
+        if offset < 0 or nbytes < 0 or offset + nbytes > n.value:
+            raise ValueError("range outside the data section")
+        return C.string_at(base + offset, nbytes)
+
+    def close(self) -> None:
+        if self.h:
+            lib.mynah_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 ATTN_EXACT, ATTN_SPLIT = 0, 1
 PREFILL_BATCHED, PREFILL_STEPS = 0, 1
 
@@ -374,6 +490,20 @@ class Qwen3Decoder:
                                          ptr(model.blob), model.blob.nbytes, n_ctx, err, 512)
         if not self.h:
             raise HipError(f"qwen3_new: {err.value.decode()}")
+
+    @classmethod
+    def from_gguf(cls, path: str, n_ctx: int = 0) -> "Qwen3Decoder":
+        """The decoder over a GGUF checkpoint (mynah_slm_load, src/model.c:177):
+        n_ctx 0 takes the file's context_length, capped at 4096."""
+        with GgufFile(path) as g:
+            shape, _ = g.qwen3_shape()
+        self = cls.__new__(cls)
+        self.model = types.SimpleNamespace(shape=shape, path=path)
+        err = C.create_string_buffer(512)
+        self.h = lib.mynah_hip_qwen3_from_gguf(os.fsencode(path), n_ctx, err, 512)
+        if not self.h:
+            raise HipError(f"qwen3_from_gguf: {err.value.decode(errors='replace')}")
+        return self
 
     def set_kv(self, k: np.ndarray, v: np.ndarray, n_pos: int) -> None:
         k = np.ascontiguousarray(k, np.float32)

@@ -47,6 +47,22 @@ class SynthTensor(C.Structure):
                 ("nbytes", C.c_uint64)]
 
 
+class RefTensor(C.Structure):
+    """ingot_tensor (third_party/ingot/include/ingot/gguf.h:41-50)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("rank", C.c_uint32),
+                ("ne", C.c_uint64 * 8), ("nelem", C.c_uint64), ("nbytes", C.c_uint64),
+                ("offset", C.c_uint64), ("shard", C.c_uint32)]
+
+
+class RefConfig(C.Structure):
+    """mynah_slm_config (src/model.h:25-48)."""
+    _fields_ = [("arch", C.c_char * 32)] + \
+               [(n, C.c_uint32) for n in ("n_layers", "d_model", "d_ff", "n_heads", "n_kv_heads",
+                                          "head_dim", "n_ctx", "vocab_size")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float), ("eos", C.c_uint32 * 8),
+                ("n_eos", _SZ), ("q_dim", C.c_uint32), ("kv_dim", C.c_uint32)]
+
+
 def _load_oracle() -> C.CDLL:
     if not os.path.exists(ORACLE_SO):
         raise ImportError(f"{ORACLE_SO} missing: run `make -C oracle`")
@@ -111,6 +127,24 @@ def load_ref():
                                        C.c_uint32, C.c_int, _P, _P, C.c_char_p, _SZ]),
         "ref_qwen3_prompt_greedy": (C.c_int, [C.c_char_p, _P, C.c_uint32, C.c_uint32, C.c_uint32,
                                               C.c_int, _P, _P, C.c_char_p, _SZ]),
+        # ingot's GGUF reader (third_party/ingot/include/ingot/gguf.h:60-130)
+        "ingot_gguf_open": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
+        "ingot_gguf_close": (None, [_P]),
+        "ingot_gguf_version": (C.c_uint32, [_P]),
+        "ingot_gguf_alignment": (C.c_uint64, [_P]),
+        "ingot_gguf_data_base": (C.c_uint64, [_P, C.c_uint32]),
+        "ingot_gguf_count": (_SZ, [_P]),
+        "ingot_gguf_at": (C.POINTER(RefTensor), [_P, _SZ]),
+        "ingot_gguf_kv_count": (_SZ, [_P]),
+        "ingot_gguf_kv_find": (_P, [_P, C.c_char_p]),
+        "ingot_kv_u64": (C.c_int, [_P, C.POINTER(C.c_uint64)]),
+        "ingot_kv_f64": (C.c_int, [_P, C.POINTER(C.c_double)]),
+        "ingot_kv_str": (C.c_int, [_P, C.POINTER(C.c_char_p)]),
+        "ingot_kv_arr_len": (C.c_int, [_P, C.POINTER(C.c_uint64)]),
+        # the loader (src/model.h:60-90)
+        "mynah_slm_load": (_P, [C.c_char_p, C.c_char_p, _SZ]),
+        "mynah_slm_model_config": (C.POINTER(RefConfig), [_P]),
+        "mynah_slm_free": (None, [_P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -349,3 +383,53 @@ def ref_greedy(ref, model: SynthModel, k, v, n_prefill, first, steps, n_ctx, thr
                                   ptr(tokens), ptr(logits), err, 512)
         assert rc == 0, err.value
     return [int(t) for t in tokens], logits
+
+
+def ref_gguf_read(ref, path: str, keys=()):
+    """What the reference's reader makes of the file at `path`: None when
+    ingot_gguf_open refuses it, else its header, tensor table and, for each of
+    `keys`, the u64 / f64 / string / array-length reads (None where refused)."""
+    g = _P()
+    err = C.create_string_buffer(512)
+    if ref.ingot_gguf_open(C.byref(g), os.fsencode(path), err, 512) != 0:
+        assert g.value is None and err.value
+        return None
+    try:
+        out = {"version": int(ref.ingot_gguf_version(g)), "n_kv": int(ref.ingot_gguf_kv_count(g)),
+               "alignment": int(ref.ingot_gguf_alignment(g)),
+               "data_base": int(ref.ingot_gguf_data_base(g, 0)), "tensors": [], "kv": {}}
+        for i in range(ref.ingot_gguf_count(g)):
+            t = ref.ingot_gguf_at(g, i).contents
+            out["tensors"].append([t.name.decode(), t.type, t.rank, list(t.ne[:t.rank]),
+                                   int(t.offset), int(t.nbytes)])
+        for key in keys:
+            kv = ref.ingot_gguf_kv_find(g, key.encode())
+            if not kv:
+                out["kv"][key] = None
+                continue
+            u, f, sp, n = C.c_uint64(), C.c_double(), C.c_char_p(), C.c_uint64()
+            out["kv"][key] = {
+                "u64": int(u.value) if ref.ingot_kv_u64(kv, C.byref(u)) == 0 else None,
+                "f64": float(f.value) if ref.ingot_kv_f64(kv, C.byref(f)) == 0 else None,
+                "str": sp.value.decode() if ref.ingot_kv_str(kv, C.byref(sp)) == 0 else None,
+                "arr_len": int(n.value) if ref.ingot_kv_arr_len(kv, C.byref(n)) == 0 else None}
+        return out
+    finally:
+        ref.ingot_gguf_close(g)
+
+
+def ref_qwen3_config(ref, path: str):
+    """mynah_slm_load's config for the file, or None when it refuses it."""
+    err = C.create_string_buffer(512)
+    m = ref.mynah_slm_load(os.fsencode(path), err, 512)
+    if not m:
+        assert err.value
+        return None
+    try:
+        c = ref.mynah_slm_model_config(m).contents
+        return {"n_layers": c.n_layers, "d_model": c.d_model, "d_ff": c.d_ff,
+                "n_heads": c.n_heads, "n_kv_heads": c.n_kv_heads, "head_dim": c.head_dim,
+                "n_ctx": c.n_ctx, "vocab": c.vocab_size, "rms_eps": float(c.rms_eps),
+                "rope_theta": float(c.rope_theta)}
+    finally:
+        ref.mynah_slm_free(m)
