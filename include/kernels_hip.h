@@ -15,8 +15,8 @@
  * other weights are staged to the device for the call. x and y cross PCIe on
  * every call, so a decoder that wants device speed uses part 2.
  *
- * Type ids are ggml's on-disk ids: Q8_0 = 8, Q4_K = 12, Q6_K = 14
- * (third_party/ingot/include/ingot/dtype.h:24-59).
+ * Type ids are ggml's on-disk ids: Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13,
+ * Q6_K = 14 (third_party/ingot/include/ingot/dtype.h:24-59).
  *
  * Part 2 is new API with no reference counterpart: device-pointer twins with a
  * stream argument (the stream is a hipStream_t passed as void *, NULL = the
@@ -47,13 +47,14 @@ extern "C" {
 int ingot_matvec(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output);
 /* quant.h:157-158. Exact f32 for every width unless the int8 lane is on
- * (mynah_hip_set_int8 below), which then takes Q4_K from two tokens up. */
+ * (mynah_hip_set_int8 below), which then takes Q4_K from two tokens up
+ * (the reference's AVX2 build would also take Q5_K; here Q5_K stays exact). */
 int ingot_matmat(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output, size_t tokens);
 /* quant.h:159-160 — bit-identical to the reference decoders. */
 int ingot_dequant_matrix(int type, const void *weights, size_t rows, size_t cols,
                          float *output);
-/* quant.h:161 — 1 for Q4_K, Q6_K, Q8_0. */
+/* quant.h:161 — 1 for Q4_K, Q5_K, Q6_K, Q8_0, Q4_0. */
 int ingot_has_kernel(int type);
 /* quant.h:149 (kernels.c:1714-1721): 1 when `tokens` takes the exact path —
  * always for tokens <= 1, otherwise unless the int8 lane is on. */
@@ -75,12 +76,32 @@ int ingot_q4_k_matmat_exact(const void *weights, size_t rows, size_t cols,
  * epilogue; bit-identical to an AVX2 + FMA build of ingot. */
 int ingot_q4_k_matvec_int8(const void *weights, size_t rows, size_t cols,
                            const float *input, float *output);
+/* quant.h:80-86. Q5_K: the matvec in the order of the scalar lane the
+ * reference builds without -march (kernels.c:1785-1853), so the _scalar
+ * entry point gives the same bits; matmat from two tokens up in its batched
+ * core's order (kernels.c:2573-2606). */
+int ingot_q5_k_matvec(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output);
+int ingot_q5_k_matvec_scalar(const void *weights, size_t rows, size_t cols,
+                             const float *input, float *output);
+int ingot_q5_k_dequant(const void *weights, size_t rows, size_t cols, float *output);
+int ingot_q5_k_matmat(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output, size_t tokens);
+/* quant.h:152-153: the exact batched order whatever the int8 lane's mode. */
+int ingot_q5_k_matmat_exact(const void *weights, size_t rows, size_t cols,
+                            const float *input, float *output, size_t tokens);
 /* quant.h:83-88 */
 int ingot_q6_k_matvec(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output);
 int ingot_q6_k_dequant(const void *weights, size_t rows, size_t cols, float *output);
 int ingot_q6_k_matmat(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output, size_t tokens);
+/* quant.h:108-110. Q4_0: one running sum over each whole row
+ * (kernels.c:2467-2484); ingot_matmat(Q4_0, ...) runs that chain per token,
+ * as the reference's generic path does (generic.c:76-93). cols % 32 == 0. */
+int ingot_q4_0_matvec(const void *weights, size_t rows, size_t cols,
+                      const float *input, float *output);
+int ingot_q4_0_dequant(const void *weights, size_t rows, size_t cols, float *output);
 /* quant.h:107-112 */
 int ingot_q8_0_matvec(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output);
@@ -109,9 +130,9 @@ int mynah_hip_unregister(const void *host);
 /* Device address of a registered host pointer, or NULL. */
 void *mynah_hip_device_ptr(const void *host);
 
-/* Device-pointer twins. Weights 16-byte aligned for Q4_K and 2-byte aligned
- * for Q6_K / Q8_0 (GGUF data and whole-row offsets satisfy both); x 16-byte
- * aligned. Asynchronous on `stream`. */
+/* Device-pointer twins. Weights 16-byte aligned for Q4_K / Q5_K and 2-byte
+ * aligned for Q6_K / Q8_0 / Q4_0 (GGUF data and whole-row offsets satisfy
+ * both); x 16-byte aligned. Asynchronous on `stream`. */
 int mynah_hip_matvec_dev(int type, const void *w, size_t rows, size_t cols,
                          const float *x, float *y, void *stream);
 int mynah_hip_matmat_dev(int type, const void *w, size_t rows, size_t cols,

@@ -20,6 +20,9 @@
  *   Q6_K (210 B): 128 ql bytes; 64 qh bytes; 16 scales int8 in [-64, 63];
  *                 d = f16(|N|*0.005) at byte 208.
  *   Q8_0 (34 B):  d = f16(|N|*0.01); 32 int8 in [-127, 127].
+ *   Q5_K (176 B): d, dmin = f16(|N|*0.01); 12 scale bytes, 32 qh bytes and
+ *                 128 quant bytes, all uniform.
+ *   Q4_0 (18 B):  d = f16(|N|*0.01); 16 quant bytes uniform.
  *
  * SPDX-License-Identifier: MIT */
 #ifndef MYNAH_SYNTH_H
@@ -40,8 +43,9 @@ uint64_t mynah_synth_substream(uint64_t seed, uint64_t k);
 uint16_t mynah_synth_f32_to_f16(float value);
 
 /* Fill `rows` rows of `cols` weights in block format `type` (12 = Q4_K,
- * 14 = Q6_K, 8 = Q8_0) into `out`, rows [row0, row0 + rows) of a tensor whose
- * seed is `seed`. Returns 0, or -1 for an unsupported type or a partial block.
+ * 13 = Q5_K, 14 = Q6_K, 8 = Q8_0, 2 = Q4_0) into `out`, rows
+ * [row0, row0 + rows) of a tensor whose seed is `seed`. Returns 0, or -1 for
+ * an unsupported type or a partial block.
  * Uses up to `threads` threads (<= 0: all online cores). */
 int mynah_synth_blocks(int type, uint64_t seed, size_t row0, size_t rows,
                        size_t cols, void *out, int threads);

@@ -15,8 +15,16 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-TYPE_NAME = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+TYPE_NAME = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+
+# The adjacent block types (Q5_K, Q4_0): shapes of their parity cases —
+# (type, rows, cols, token counts of the batched product). Ragged rows,
+# Q4_0 rows that are not whole 256-value units, and token counts around the
+# kernels' tiles (8 tokens per Q4_0 lane group, 64 per GEMM tile).
+ADJACENT = ((Q5_K, 37, 512, (3, 9)), (Q5_K, 5, 2048, (2, 65)), (Q5_K, 130, 1024, (64,)),
+            (Q4_0, 37, 96, (3, 9)), (Q4_0, 8, 4096, (2, 17)), (Q4_0, 3, 32, (8,)),
+            (Q4_0, 70, 2080, (5, 64)))
 
 
 @dataclass(frozen=True)

@@ -113,8 +113,10 @@ static int bind(dtensor *out, const mynah_synth_tensor *table, size_t count,
     /* The kernels read weights and norm vectors in 16-byte pieces. */
     if ((t->offset & 15u) != 0) return fail(err, errsz, "tensor offset not 16-byte aligned", name);
     size_t rb = cols * 4;
-    if (t->type != 0 && mynah_geometry(t->type, rows, cols, &rb) != 0)
-        return fail(err, errsz, "tensor type has no kernel", name);
+    /* The step's kernels take F32, Q4_K, Q5_K, Q6_K and Q8_0 tensors (Q4_0's
+     * serial row sum has no fused grouped kernel). */
+    if (t->type == MYNAH_Q4_0 || (t->type != 0 && mynah_geometry(t->type, rows, cols, &rb) != 0))
+        return fail(err, errsz, "tensor type has no kernel in the decode step", name);
     out->type = t->type;
     out->rows = rows;
     out->cols = cols;

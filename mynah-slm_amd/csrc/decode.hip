@@ -582,6 +582,24 @@ MYNAH_DEV void embed_group(const uint8_t *__restrict__ table, uint32_t token, fl
             const uint32_t q = (j & 1u) ? (blk[16 + 32 * g + i] >> 4) : (blk[16 + 32 * g + i] & 15u);
             dst[i] = a * (float)q - o;
         }
+    } else if (type == 13u) {
+        // Q5_K: Q4_K's scales, quants at 48, fifth bits in qh[i] bit j.
+        const uint8_t *blk = row + (c / 8u) * 176u;
+        const uint32_t j = c % 8u, g = j >> 1;
+        const float dd = f16_to_f32(blk[0] | (blk[1] << 8)), dmin = f16_to_f32(blk[2] | (blk[3] << 8));
+        const uint8_t *s = blk + 4;
+        uint32_t sc, m;
+        if (j < 4) { sc = s[j] & 63u; m = s[j + 4] & 63u; }
+        else {
+            sc = (s[j + 4] & 15u) | ((s[j - 4] >> 6) << 4);
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float a = dd * (float)sc, o = dmin * (float)m;
+        for (int i = 0; i < 32; i++) {
+            const uint32_t b = blk[48 + 32 * g + i];
+            const uint32_t q = ((j & 1u) ? (b >> 4) : (b & 15u)) + (((blk[16 + i] >> j) & 1u) << 4);
+            dst[i] = a * (float)q - o;
+        }
     } else if (type == 14u) {
         const uint8_t *blk = row + (c / 8u) * 210u;
         const uint32_t qq = c % 8u, h = qq >> 2, k = qq & 3u;

@@ -5,8 +5,9 @@
 
 // ── bit-exact dequantisation ────────────────────────────────────────────────
 // Same operation order as the reference decoders, so every value is the
-// identical f32 (kernels.c:117-136 Q4_K, 2176-2199 Q6_K, 2518-2523 Q8_0).
-// One thread per 32 output values; `units` = rows * cols / 32.
+// identical f32 (kernels.c:117-136 Q4_K, 1812-1833 Q5_K, 2176-2199 Q6_K,
+// 2518-2523 Q8_0, 2353-2360 Q4_0). One thread per 32 output values; `units`
+// = rows * cols / 32.
 
 extern "C" __global__ void __launch_bounds__(256)
 mynah_dequant(const uint8_t *__restrict__ w, float *__restrict__ y, uint32_t type,
@@ -33,6 +34,31 @@ mynah_dequant(const uint8_t *__restrict__ w, float *__restrict__ y, uint32_t typ
         for (int i = 0; i < 32; i++) {
             const uint32_t q = (j & 1u) ? (qs[i] >> 4) : (qs[i] & 15u);
             out[i] = dd * (float)q - mm;
+        }
+    } else if (type == 13u) {
+        const uint8_t *blk = w + row * (cols / 256u) * 176u + (c / 8u) * 176u;
+        const uint32_t j = (uint32_t)(c % 8u), g = j >> 1;
+        const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+        const float dmin = f16_to_f32(blk[2] | (blk[3] << 8));
+        const uint8_t *s = blk + 4;
+        uint32_t sc, m;
+        if (j < 4) { sc = s[j] & 63u; m = s[j + 4] & 63u; }
+        else {
+            sc = (s[j + 4] & 15u) | ((s[j - 4] >> 6) << 4);
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float dd = d * (float)sc, mm = dmin * (float)m;
+        const uint8_t *qh = blk + 16, *qs = blk + 48 + 32u * g;
+        for (int i = 0; i < 32; i++) {
+            const uint32_t q = ((j & 1u) ? (qs[i] >> 4) : (qs[i] & 15u)) + (((qh[i] >> j) & 1u) << 4);
+            out[i] = dd * (float)q - mm;
+        }
+    } else if (type == 2u) {
+        const uint8_t *blk = w + row * (cols / 32u) * 18u + c * 18u;
+        const float d = f16_to_f32(blk[0] | (blk[1] << 8));
+        for (int i = 0; i < 16; i++) {
+            out[i] = d * (float)((int)(blk[2 + i] & 15u) - 8);
+            out[16 + i] = d * (float)((int)(blk[2 + i] >> 4) - 8);
         }
     } else if (type == 14u) {
         const uint8_t *blk = w + row * (cols / 256u) * 210u + (c / 8u) * 210u;

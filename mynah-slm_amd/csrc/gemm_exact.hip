@@ -14,7 +14,7 @@
 // The same kernel in the matvec order (ORD = 1) is the prefill GEMM of the
 // resident decoder: every (row, token) output is then the one the
 // reference's matvec (kernels.c:94-115, 319-337; 2525-2551) gives for that
-// token — Q4_K interleaves the low- and high-nibble weights of each byte of
+// token — Q4_K (and Q5_K) interleaves the low- and high-nibble weights of each byte of
 // a group (the decoded weights and x are stored in LDS in that order, so
 // the inner loop stays a sequential walk), Q8_0 folds its sum into the row
 // every 32 values, Q6_K is the same in both orders — so a prompt filled in
@@ -133,6 +133,68 @@ struct GmQ4KMv {
     }
 };
 
+// Q5_K (kernels.c:1812-1833 q5_dequant_block, the decoder of its batched
+// core, 2573-2595): Q4_K's pieces, with the fifth bit of each weight from
+// qh: bytes 16 (p & 1) .. + 15 of qh, bit p / 2 (the sub-block).
+struct GmQ5K {
+    uint4 hdr, q, h;
+    __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
+        hdr = *(const uint4 *)blk;
+        h = *(const uint4 *)(blk + 16u + 16u * (p & 1u));
+        q = *(const uint4 *)(blk + 48u + 32u * (p >> 2) + 16u * (p & 1u));
+    }
+    __device__ __forceinline__ void decode(uint32_t p, float *dst) const {
+#pragma clang fp contract(off)
+        float d1, m1;
+        gm_q4k_sm(hdr, p >> 1, f16_to_f32(hdr.x), f16_to_f32(hdr.x >> 16), d1, m1);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w}, hb[4] = {h.x, h.y, h.z, h.w};
+        const uint32_t shift = ((p >> 1) & 1u) ? 4u : 0u, bit = p >> 1;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t n = ((w[k] >> shift) & 0x0f0f0f0fu) | (((hb[k] >> bit) & 0x01010101u) << 4);
+            dst[4 * k] = __builtin_fmaf(d1, ubyte_f<0>(n), -m1);
+            dst[4 * k + 1] = __builtin_fmaf(d1, ubyte_f<1>(n), -m1);
+            dst[4 * k + 2] = __builtin_fmaf(d1, ubyte_f<2>(n), -m1);
+            dst[4 * k + 3] = __builtin_fmaf(d1, ubyte_f<3>(n), -m1);
+        }
+    }
+};
+
+// Q5_K in the matvec order (kernels.c:1785-1810): Q4_KMv's pieces and LDS
+// order; qh bytes 8 (p & 3) .. + 7, bits 2 g (low) and 2 g + 1 (high).
+struct GmQ5KMv {
+    uint4 hdr;
+    uint2 q, h;
+    __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
+        hdr = *(const uint4 *)blk;
+        h = *(const uint2 *)(blk + 16u + 8u * (p & 3u));
+        q = *(const uint2 *)(blk + 48u + 32u * (p >> 2) + 8u * (p & 3u));
+    }
+    __device__ __forceinline__ void decode(uint32_t p, float *dst) const {
+#pragma clang fp contract(off)
+        const uint32_t g = p >> 2;
+        const float d = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+        float dl, ml, dh, mh;
+        gm_q4k_sm(hdr, 2u * g, d, dmin, dl, ml);
+        gm_q4k_sm(hdr, 2u * g + 1u, d, dmin, dh, mh);
+        const uint32_t w[2] = {q.x, q.y}, hb[2] = {h.x, h.y};
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t lo = (w[k] & 0x0f0f0f0fu) | (((hb[k] >> (2u * g)) & 0x01010101u) << 4);
+            const uint32_t hi =
+                ((w[k] >> 4) & 0x0f0f0f0fu) | (((hb[k] >> (2u * g + 1u)) & 0x01010101u) << 4);
+            dst[8 * k + 0] = __builtin_fmaf(dl, ubyte_f<0>(lo), -ml);
+            dst[8 * k + 1] = __builtin_fmaf(dh, ubyte_f<0>(hi), -mh);
+            dst[8 * k + 2] = __builtin_fmaf(dl, ubyte_f<1>(lo), -ml);
+            dst[8 * k + 3] = __builtin_fmaf(dh, ubyte_f<1>(hi), -mh);
+            dst[8 * k + 4] = __builtin_fmaf(dl, ubyte_f<2>(lo), -ml);
+            dst[8 * k + 5] = __builtin_fmaf(dh, ubyte_f<2>(hi), -mh);
+            dst[8 * k + 6] = __builtin_fmaf(dl, ubyte_f<3>(lo), -ml);
+            dst[8 * k + 7] = __builtin_fmaf(dh, ubyte_f<3>(hi), -mh);
+        }
+    }
+};
+
 // Q6_K: piece p = values 16 p .. + 15 = weight 128 h + 32 k + l for
 // h = p / 8, k = (p / 2) & 3, l = 16 (p & 1) .. + 15; scale byte p.
 struct GmQ6K {
@@ -235,7 +297,7 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
             for (int k = 0; k < 4; k++)
                 *(float4 *)&wl[dr][16u * dp + 4 * k] =
                     make_float4(vals[4 * k], vals[4 * k + 1], vals[4 * k + 2], vals[4 * k + 3]);
-            if (ORD == 1 && FMT == 12) {
+            if (ORD == 1 && (FMT == 12 || FMT == 13)) {
                 // x in the matvec order of the stage's group: position 2 j + h
                 // holds x[32 h + j].
 #pragma unroll
@@ -309,7 +371,8 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
 }
 
 // Grid (ceil(rows / 64), ceil(tokens / 64)), block 256; cols % 256 == 0;
-// x 16-byte aligned. Q4_K rows 16-byte aligned, Q6_K / Q8_0 2-byte aligned.
+// x 16-byte aligned. Q4_K / Q5_K rows 16-byte aligned, Q6_K / Q8_0 2-byte
+// aligned.
 #define GEMM_EXACT_ENTRY(name, RAW, UB)                                                        \
     extern "C" __global__ void __launch_bounds__(256)                                          \
         name(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, \
@@ -318,6 +381,7 @@ MYNAH_DEV void gemm_exact(const uint8_t *__restrict__ w, const float *__restrict
     }
 
 GEMM_EXACT_ENTRY(mynah_q4k_gemm_exact, GmQ4K, 144u)
+GEMM_EXACT_ENTRY(mynah_q5k_gemm_exact, GmQ5K, 176u)
 GEMM_EXACT_ENTRY(mynah_q6k_gemm_exact, GmQ6K, 210u)
 GEMM_EXACT_ENTRY(mynah_q80_gemm_exact, GmQ80, 272u)
 
@@ -331,5 +395,6 @@ GEMM_EXACT_ENTRY(mynah_q80_gemm_exact, GmQ80, 272u)
     }
 
 GEMM_MV_ENTRY(mynah_q4k_gemm_mv, GmQ4KMv, 144u, 12)
+GEMM_MV_ENTRY(mynah_q5k_gemm_mv, GmQ5KMv, 176u, 13)
 GEMM_MV_ENTRY(mynah_q6k_gemm_mv, GmQ6K, 210u, 14)
 GEMM_MV_ENTRY(mynah_q80_gemm_mv, GmQ80, 272u, 8)

@@ -8,12 +8,16 @@
 //         super-block one running sum, the low-nibble weight 64g+i then the
 //         high-nibble weight 64g+32+i for i = 0..31, g = 0..3; weight value
 //         (d*sc)*q - dmin*m (one rounding); row sum of block sums in order.
+//   Q5_K  kernels.c:1785-1810 and 1835-1853: Q4_K's order and weight form,
+//         with 16 added to the quant when its bit of qh[i] is set (bit 2g for
+//         the low nibble, 2g+1 for the high one).
 //   Q6_K  kernels.c:2096-2124 + 2176-2199 + 2037-2041: decode the 256 values
 //         (d*sc)*(q-32), sequential dot from weight 0, row sum in order.
 //   Q8_0  kernels.c:2518-2546: values q*d, sequential dot per 32-block, row
 //         sum in order.
 // Every weight value is exact in f32 before its final rounding, so a single
-// fused multiply-add produces the identical value: (d*sc)*q - dmin*m as
+// fused multiply-add produces the identical value: (d*sc)*q - dmin*m (q up
+// to 31 for Q5_K: 11 + 6 + 5 significant bits) as
 // fma(d*sc, q, -dmin*m); (d*sc)*(q-32) as fma(d*sc, q6, -32*d*sc) with q6 the
 // raw 6-bit code; q*d as fma(d, q + 128, -128*d) with q + 128 = q ^ 0x80. The
 // product with x and the sum stay separate roundings, as in the reference.
@@ -146,6 +150,68 @@ MYNAH_DEV float q4k_unit(const uint8_t *__restrict__ blk, const float *__restric
     uint32_t v[36];
     q4k_load(blk, v);
     return q4k_sum<SEQ>(v, x);
+}
+
+// ── Q5_K: 176-byte block, 16-byte aligned ──────────────────────────────────
+// d, dmin @0, scales[12] @4 (Q4_K's packing), qh[32] @16, qs[128] @48. In
+// registers: v[0] = d | dmin << 16, v[1..3] scales, v[4..11] qh, v[12..43] qs.
+
+// The 5-bit quants of qs word m of group G: byte i of qh word m holds the
+// fifth bits of weights 4m + i, bit 2G (low nibble) and 2G + 1 (high).
+template <int G>
+MYNAH_DEV void q5k_quants(uint32_t v, uint32_t hb, uint32_t &lo, uint32_t &hi) {
+    lo = (v & 0x0f0f0f0fu) | (((hb >> (2 * G)) & 0x01010101u) << 4);
+    hi = ((v >> 4) & 0x0f0f0f0fu) | (((hb >> (2 * G + 1)) & 0x01010101u) << 4);
+}
+
+template <int G>
+MYNAH_DEV float q5k_group(const uint32_t *q, const uint32_t *qh, float d, float dmin,
+                          uint32_t s0, uint32_t s1, uint32_t s2, const float *__restrict__ x,
+                          float acc) {
+#pragma clang fp contract(off)
+    float sa, ma, sb, mb;
+    q4k_sm<2 * G>(s0, s1, s2, sa, ma);
+    q4k_sm<2 * G + 1>(s0, s1, s2, sb, mb);
+    const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
+#pragma unroll
+    for (int m = 0; m < 8; m++) {
+        uint32_t lo, hi;
+        q5k_quants<G>(q[8 * G + m], qh[m], lo, hi);
+        const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
+        const float qu[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
+        const float4 xa4 = *(const float4 *)(x + 64 * G + 4 * m);
+        const float4 xb4 = *(const float4 *)(x + 64 * G + 32 + 4 * m);
+        const float xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w}, xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float wa = __builtin_fmaf(da, ql[t], -oa);
+            acc = acc + wa * xa[t];
+            const float wb = __builtin_fmaf(db, qu[t], -ob);
+            acc = acc + wb * xb[t];
+        }
+    }
+    return acc;
+}
+
+MYNAH_DEV float q5k_sum(const uint32_t *v, const float *__restrict__ x) {
+    const float d = f16_to_f32(v[0]), dmin = f16_to_f32(v[0] >> 16);
+    const uint32_t s0 = v[1], s1 = v[2], s2 = v[3];
+    const uint32_t *qh = v + 4, *q = v + 12;
+    float acc = 0.0f;
+    acc = q5k_group<0>(q, qh, d, dmin, s0, s1, s2, x, acc);
+    acc = q5k_group<1>(q, qh, d, dmin, s0, s1, s2, x, acc);
+    acc = q5k_group<2>(q, qh, d, dmin, s0, s1, s2, x, acc);
+    acc = q5k_group<3>(q, qh, d, dmin, s0, s1, s2, x, acc);
+    return acc;
+}
+
+MYNAH_DEV void q5k_load(const uint8_t *__restrict__ blk, uint32_t *v) {
+    const uint4 *p = (const uint4 *)blk;
+#pragma unroll
+    for (int k = 0; k < 11; k++) {
+        const uint4 c = p[k];
+        v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
+    }
 }
 
 // ── Q6_K: 210-byte block, 2-byte aligned ───────────────────────────────────
@@ -312,7 +378,7 @@ GEMV_SEQ_ENTRY(mynah_q80_gemv_exact_seq, 8)
 //
 // grp.shape = log2(K) | WS << 8 | WR << 16 | SPLIT << 24, with (64 / K) * WR
 // (SPLIT: (16 / K) * WR) rows per workgroup and 64 * WS * WR threads; SPLIT
-// (Q4_K and Q6_K only) shares each super-block among the four lanes of a
+// (super-block types only) shares each super-block among the four lanes of a
 // quad. Dynamic LDS (floats): the padded x,
 // (units | 1) unit sums per row of the workgroup, and with norm_w a copy of
 // the norm weights (cols).
@@ -397,6 +463,12 @@ template <> struct Raw<12> {
     __device__ __forceinline__ void load(const uint8_t *b) { q4k_load(b, v); }
     __device__ __forceinline__ float sum(const float *x) const { return q4k_sum<false>(v, x); }
 };
+template <> struct Raw<13> {
+    static constexpr uint32_t BYTES = 176;
+    uint32_t v[44];
+    __device__ __forceinline__ void load(const uint8_t *b) { q5k_load(b, v); }
+    __device__ __forceinline__ float sum(const float *x) const { return q5k_sum(v, x); }
+};
 template <> struct Raw<14> {
     static constexpr uint32_t BYTES = 210;
     uint32_t raw[53], s;
@@ -463,6 +535,45 @@ template <> struct RawSeg<12> {
         }
     }
 };
+// Q5_K segment g = group g: the header, all of qh and the 32 quant bytes of
+// the group.
+template <> struct RawSeg<13> {
+    uint4 hdr, h0, h1, q0, q1;
+    __device__ __forceinline__ void load(const uint8_t *b, uint32_t g) {
+        const uint4 *p = (const uint4 *)b;
+        hdr = p[0];
+        h0 = p[1];
+        h1 = p[2];
+        q0 = p[3 + 2u * g];
+        q1 = p[4 + 2u * g];
+    }
+    __device__ __forceinline__ void products(const float *x, uint32_t g, float *p) const {
+#pragma clang fp contract(off)
+        const float d = f16_to_f32(hdr.x), dmin = f16_to_f32(hdr.x >> 16);
+        float sa, ma, sb, mb;
+        q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g, sa, ma);
+        q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g + 1u, sb, mb);
+        const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int m = 0; m < 8; m++) {
+            const uint32_t lo = (q[m] & 0x0f0f0f0fu) | (((qh[m] >> (2u * g)) & 0x01010101u) << 4);
+            const uint32_t hi =
+                ((q[m] >> 4) & 0x0f0f0f0fu) | (((qh[m] >> (2u * g + 1u)) & 0x01010101u) << 4);
+            const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
+            const float qu[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
+            const float4 xa4 = *(const float4 *)(x + 4 * m);
+            const float4 xb4 = *(const float4 *)(x + 32 + 4 * m);
+            const float xa[4] = {xa4.x, xa4.y, xa4.z, xa4.w}, xb[4] = {xb4.x, xb4.y, xb4.z, xb4.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                p[8 * m + 2 * t] = __builtin_fmaf(da, ql[t], -oa) * xa[t];
+                p[8 * m + 2 * t + 1] = __builtin_fmaf(db, qu[t], -ob) * xb[t];
+            }
+        }
+    }
+};
 // Q6_K segment s = (h, half) = (s >> 1, s & 1): weights 128 h + 32 k + 4 m + t
 // for k = 2 half, 2 half + 1; realigned words 16 h .. 16 h + 15 (ql),
 // 32 + 8 h .. + 7 (qh), 48 + 2 h + half (four scales) and d.
@@ -508,7 +619,7 @@ template <> struct RawSeg<14> {
             }
     }
 };
-template <> struct RawSeg<8> {   // never launched: split mode is Q4_K / Q6_K only
+template <> struct RawSeg<8> {   // never launched: split mode is for super-block types only
     __device__ __forceinline__ void load(const uint8_t *, uint32_t) {}
     __device__ __forceinline__ void products(const float *, uint32_t, float *p) const {
 #pragma unroll
@@ -627,9 +738,12 @@ mynah_gemv_group(const GemvGroup grp) {
     const GemvDesc &g = grp.d[i];
     if (grp.shape & (1u << 24)) {
         if (g.type == 12u) group_split<12, true>(g, t, grp.shape, lds, shd);
+        else if (g.type == 13u) group_split<13, true>(g, t, grp.shape, lds, shd);
         else group_split<14, true>(g, t, grp.shape, lds, shd);
     } else if (g.type == 12u) {
         group_split<12, false>(g, t, grp.shape, lds, shd);
+    } else if (g.type == 13u) {
+        group_split<13, false>(g, t, grp.shape, lds, shd);
     } else if (g.type == 14u) {
         group_split<14, false>(g, t, grp.shape, lds, shd);
     } else {

@@ -5,6 +5,7 @@
 #include "dequant.hip"
 #include "gemv_exact.hip"
 #include "gemv_stream.hip"
+#include "gemv_q40.hip"
 #include "gemv_fast.hip"
 #include "gemm_exact.hip"
 #include "decode.hip"

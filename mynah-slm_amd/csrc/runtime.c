@@ -137,8 +137,10 @@ int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes) {
     size_t elems, bytes;
     switch (type) {
     case MYNAH_Q4_K: elems = 256; bytes = 144; break;
+    case MYNAH_Q5_K: elems = 256; bytes = 176; break;
     case MYNAH_Q6_K: elems = 256; bytes = 210; break;
     case MYNAH_Q8_0: elems = 32;  bytes = 34;  break;
+    case MYNAH_Q4_0: elems = 32;  bytes = 18;  break;
     default:
         mynah_set_error("type %d has no kernel", type);
         return -1;
@@ -199,6 +201,7 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
      * (third_party/ingot/src/kernels.c:819-834). */
     if (type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
         return mynah_int8_product(d, w, rows, cols, x, y, 1, stream);
+    if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, 1, stream);
     if (type != MYNAH_Q8_0 && cols % 256 != 0) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
@@ -207,7 +210,7 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
         mynah_set_error("x must be 16-byte aligned");
         return -1;
     }
-    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0) {
+    if (mynah_w_misaligned(type, w)) {
         mynah_set_error("weights misaligned for type %d", type);
         return -1;
     }
@@ -226,15 +229,35 @@ int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows,
                           const float *x, float *y, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
-    if (cols % 256 != 0 || rb > 0xffffffffu) {
-        mynah_set_error("batched order needs cols to be a multiple of 256");
+    if (cols % 256 != 0 || rb > 0xffffffffu ||
+        (type != MYNAH_Q4_K && type != MYNAH_Q6_K && type != MYNAH_Q8_0)) {
+        mynah_set_error("batched order needs Q4_K / Q6_K / Q8_0 and cols %% 256 == 0");
         return -1;
     }
-    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0) {
+    if (mynah_w_misaligned(type, w)) {
         mynah_set_error("weights misaligned for type %d", type);
         return -1;
     }
     return gemv_seq_launch(d, type, w, rows, cols, rb, x, y, stream);
+}
+
+int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
+                     float *y, size_t tokens, hipStream_t stream) {
+    size_t rb;
+    if (mynah_geometry(MYNAH_Q4_0, rows, cols, &rb) != 0) return -1;
+    const size_t groups = tokens == 1 ? 1 : (tokens + 7) / 8;
+    if (tokens == 0 || groups > 65535u || rb > 0xffffffffu) {
+        mynah_set_error("bad token count for the Q4_0 product");
+        return -1;
+    }
+    if (((uintptr_t)w & 1u) != 0 || ((uintptr_t)x & 15u) != 0) {
+        mynah_set_error("misaligned operand for the Q4_0 product");
+        return -1;
+    }
+    uint32_t r32 = (uint32_t)rows, c32 = (uint32_t)cols, t32 = (uint32_t)tokens, rb32 = (uint32_t)rb;
+    void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32};
+    return mynah_launch(d, tokens == 1 ? MYNAH_K_Q40_CHAIN1 : MYNAH_K_Q40_CHAIN8,
+                        (unsigned)((rows + 63) / 64), (unsigned)groups, 64, 0, stream, args);
 }
 
 int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,
@@ -242,12 +265,15 @@ int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t row
     size_t rb;
     memset(g, 0, sizeof *g);
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    if (type == MYNAH_Q4_0) {
+        mynah_set_error("Q4_0 has no grouped GEMV (its row is one serial sum)");
+        return -1;
+    }
     if ((type != MYNAH_Q8_0 && cols % 256 != 0) || rb > 0xffffffffu) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
     }
-    if ((type == MYNAH_Q4_K && ((uintptr_t)w & 15u) != 0) || ((uintptr_t)w & 1u) != 0 ||
-        ((uintptr_t)x & 3u) != 0) {
+    if (mynah_w_misaligned(type, w) || ((uintptr_t)x & 3u) != 0) {
         mynah_set_error("misaligned operand for type %d", type);
         return -1;
     }
@@ -357,12 +383,19 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         mynah_set_error("group of %u matrices", grp->n);
         return -1;
     }
-    const int exact = (order < 0 ? gemv_order : order) == MYNAH_GEMV_EXACT;
+    int exact = (order < 0 ? gemv_order : order) == MYNAH_GEMV_EXACT;
     uint32_t all_rows = 0, max_units = 1;
     uint64_t all_units = 0;
     int split = 1;
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
+        if (g->type != MYNAH_Q4_K && g->type != MYNAH_Q5_K && g->type != MYNAH_Q6_K &&
+            g->type != MYNAH_Q8_0) {
+            mynah_set_error("type %u has no grouped GEMV", g->type);
+            return -1;
+        }
+        /* Q5_K has only the exact kernel; its order is the reference's anyway. */
+        if (g->type == MYNAH_Q5_K) exact = 1;
         all_rows += g->rows;
         const uint32_t u = g->w2 ? 2u * g->units : g->units;
         if (u > max_units) max_units = u;
@@ -462,8 +495,9 @@ int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, 
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
     /* Like the reference (kernels.c:2096-2101, 2563-2567): matrix dequant
-     * works in 256-value units for every type, ragged Q8_0 rows included. */
-    if (cols % 256 != 0) {
+     * works in 256-value units for every type, ragged Q8_0 rows included,
+     * except Q4_0, whose dequant takes any multiple of 32 (kernels.c:2500-2514). */
+    if (type != MYNAH_Q4_0 && cols % 256 != 0) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
     }
@@ -658,7 +692,8 @@ int ingot_dequant_matrix(int type, const void *weights, size_t rows, size_t cols
 }
 
 int ingot_has_kernel(int type) {
-    return type == MYNAH_Q4_K || type == MYNAH_Q6_K || type == MYNAH_Q8_0;
+    return type == MYNAH_Q4_K || type == MYNAH_Q5_K || type == MYNAH_Q6_K ||
+           type == MYNAH_Q8_0 || type == MYNAH_Q4_0;
 }
 
 int ingot_matmat_is_exact(size_t tokens) {
@@ -679,9 +714,30 @@ int ingot_matmat_is_exact(size_t tokens) {
         return ingot_matmat(id, w, rows, cols, x, y, tokens);                              \
     }
 PER_TYPE(q4_k, MYNAH_Q4_K)
+PER_TYPE(q5_k, MYNAH_Q5_K)
 PER_TYPE(q6_k, MYNAH_Q6_K)
 PER_TYPE(q8_0, MYNAH_Q8_0)
 #undef PER_TYPE
+
+/* The as-built Q5_K matvec is its scalar lane (kernels.c:1924-1939 without
+ * -march), so the scalar entry point gives the same bits. */
+int ingot_q5_k_matvec_scalar(const void *w, size_t rows, size_t cols, const float *x, float *y) {
+    return ingot_matvec(MYNAH_Q5_K, w, rows, cols, x, y);
+}
+
+int ingot_q5_k_matmat_exact(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                            size_t tokens) {
+    return host_call(tokens == 1 ? OP_MATVEC : OP_MATMAT_EXACT, MYNAH_Q5_K, w, rows, cols, x, y,
+                     tokens);
+}
+
+int ingot_q4_0_matvec(const void *w, size_t rows, size_t cols, const float *x, float *y) {
+    return ingot_matvec(MYNAH_Q4_0, w, rows, cols, x, y);
+}
+
+int ingot_q4_0_dequant(const void *w, size_t rows, size_t cols, float *y) {
+    return ingot_dequant_matrix(MYNAH_Q4_0, w, rows, cols, y);
+}
 
 int ingot_q4_k_matmat_exact(const void *w, size_t rows, size_t cols, const float *x, float *y,
                             size_t tokens) {

@@ -8,7 +8,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
+enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q6_K = 14 };
 
 /* Every kernel of the embedded code object: id and symbol name. */
 #define MYNAH_KERNEL_LIST(X)                          \
@@ -17,6 +17,10 @@ enum { MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q6_K = 14 };
     X(MYNAH_K_Q6K_EXACT_SEQ, "mynah_q6k_gemv_exact_seq") \
     X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq") \
     X(MYNAH_K_Q4K_GEMM, "mynah_q4k_gemm_exact")        \
+    X(MYNAH_K_Q5K_GEMM, "mynah_q5k_gemm_exact")        \
+    X(MYNAH_K_Q5K_GEMM_MV, "mynah_q5k_gemm_mv")        \
+    X(MYNAH_K_Q40_CHAIN1, "mynah_q40_chain1")          \
+    X(MYNAH_K_Q40_CHAIN8, "mynah_q40_chain8")          \
     X(MYNAH_K_Q6K_GEMM, "mynah_q6k_gemm_exact")        \
     X(MYNAH_K_Q80_GEMM, "mynah_q80_gemm_exact")        \
     X(MYNAH_K_Q4K_GEMM_MV, "mynah_q4k_gemm_mv")        \
@@ -76,6 +80,16 @@ int mynah_launch(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned
 int mynah_launch3(mynah_device *d, int kernel, unsigned gx, unsigned gy, unsigned gz,
                   unsigned block, size_t shmem, hipStream_t stream, void **args);
 int mynah_geometry(int type, size_t rows, size_t cols, size_t *row_bytes);
+/* Alignment the kernels need of a weight pointer of `type`: 16 bytes for the
+ * super-blocks read as uint4 (Q4_K, Q5_K), 2 bytes otherwise. */
+static inline int mynah_w_misaligned(int type, const void *w) {
+    const uintptr_t m = (type == MYNAH_Q4_K || type == MYNAH_Q5_K) ? 15u : 1u;
+    return ((uintptr_t)w & m) != 0;
+}
+/* Q4_0 products (gemv_q40.hip): y[t][r] for tokens >= 1, the reference's
+ * single running sum per (row, token). */
+int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
+                     float *y, size_t tokens, hipStream_t stream);
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                       const float *x, float *y, hipStream_t stream);

@@ -113,6 +113,23 @@ static void gen_q4_k_row(stream *s, unsigned char *row, size_t blocks) {
     }
 }
 
+static void gen_q5_k_row(stream *s, unsigned char *row, size_t blocks) {
+    for (size_t b = 0; b < blocks; b++) {
+        unsigned char *blk = row + b * 176;
+        put_f16(blk, fabs(next_normal(s)) * 0.01);
+        put_f16(blk + 2, fabs(next_normal(s)) * 0.01);
+        for (int i = 0; i < 172; i++) blk[4 + i] = (unsigned char)next_byte(s);
+    }
+}
+
+static void gen_q4_0_row(stream *s, unsigned char *row, size_t blocks) {
+    for (size_t b = 0; b < blocks; b++) {
+        unsigned char *blk = row + b * 18;
+        put_f16(blk, fabs(next_normal(s)) * 0.01);
+        for (int i = 0; i < 16; i++) blk[2 + i] = (unsigned char)next_byte(s);
+    }
+}
+
 static void gen_q6_k_row(stream *s, unsigned char *row, size_t blocks) {
     for (size_t b = 0; b < blocks; b++) {
         unsigned char *blk = row + b * 210;
@@ -150,7 +167,9 @@ static void run_blocks(synth_job *j) {
         stream_init(&s, mynah_synth_substream(j->seed, j->row0 + r));
         unsigned char *row = j->out + r * j->row_bytes;
         if (j->type == 12) gen_q4_k_row(&s, row, j->blocks);
+        else if (j->type == 13) gen_q5_k_row(&s, row, j->blocks);
         else if (j->type == 14) gen_q6_k_row(&s, row, j->blocks);
+        else if (j->type == 2) gen_q4_0_row(&s, row, j->blocks);
         else gen_q8_0_row(&s, row, j->blocks);
     }
 }
@@ -211,8 +230,10 @@ int mynah_synth_blocks(int type, uint64_t seed, size_t row0, size_t rows,
     size_t elems, bytes;
     switch (type) {
     case 12: elems = 256; bytes = 144; break;
+    case 13: elems = 256; bytes = 176; break;
     case 14: elems = 256; bytes = 210; break;
     case 8:  elems = 32;  bytes = 34;  break;
+    case 2:  elems = 32;  bytes = 18;  break;
     default: return -1;
     }
     if (out == NULL || rows == 0 || cols == 0 || cols % elems != 0) return -1;

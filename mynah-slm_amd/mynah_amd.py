@@ -16,8 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 # MYNAH_HIP_LIB names another build of the library (e.g. a tuning variant).
 LIB_PATH = os.environ.get("MYNAH_HIP_LIB") or os.path.join(HERE, "libmynah_hip.so")
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18)}
 
 _P = C.c_void_p
 _SZ = C.c_size_t
@@ -48,6 +48,8 @@ def _load() -> C.CDLL:
         "ingot_matmat_is_exact": (C.c_int, [_SZ]),
         "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_q4_k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_q5_k_matvec_scalar": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_q5_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "mynah_hip_set_int8": (C.c_int, [C.c_int]),
         "mynah_hip_int8": (C.c_int, []),
         "mynah_hip_q8_quantize_dev": (C.c_int, [_P, _SZ, _SZ, _P, _P, _P, _P]),
@@ -120,6 +122,13 @@ def _load() -> C.CDLL:
         "mynah_gguf_data": (_P, [_P, C.POINTER(C.c_uint64)]),
         "mynah_hip_qwen3_from_gguf": (_P, [C.c_char_p, C.c_uint32, C.c_char_p, _SZ]),
     }
+    # The per-type kernels of quant.h: matvec(w, rows, cols, x, y),
+    # dequant(w, rows, cols, y), matmat(w, rows, cols, x, y, tokens).
+    for prefix in ("q4_k", "q5_k", "q6_k", "q8_0", "q4_0"):
+        sig[f"ingot_{prefix}_matvec"] = (C.c_int, [_P, _SZ, _SZ, _P, _P])
+        sig[f"ingot_{prefix}_dequant"] = (C.c_int, [_P, _SZ, _SZ, _P])
+        if prefix != "q4_0":
+            sig[f"ingot_{prefix}_matmat"] = (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ])
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
         fn.restype = res

@@ -54,12 +54,14 @@ void orc_scale_min(const unsigned char *s, int j, unsigned char *sc, unsigned ch
     *m = (unsigned char)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
 }
 
-/* third_party/ingot/src/dtype.c:37-… for the three formats on the path. */
+/* third_party/ingot/src/dtype.c:37-83 for the five formats restated here. */
 int orc_type_geometry(int type, uint64_t *block_elems, uint64_t *block_bytes) {
     switch (type) {
     case ORC_Q4_K: *block_elems = 256; *block_bytes = 144; return 0;
+    case ORC_Q5_K: *block_elems = 256; *block_bytes = 176; return 0;
     case ORC_Q6_K: *block_elems = 256; *block_bytes = 210; return 0;
     case ORC_Q8_0: *block_elems = 32;  *block_bytes = 34;  return 0;
+    case ORC_Q4_0: *block_elems = 32;  *block_bytes = 18;  return 0;
     default: return -1;
     }
 }
@@ -115,6 +117,72 @@ static void q4_k_block_decode(const unsigned char *blk, float *w) {
             w[64 * g + i] = da * (float)(q & 15u) - oa;
             w[64 * g + 32 + i] = db * (float)(q >> 4) - ob;
         }
+    }
+}
+
+/* ── Q5_K ─────────────────────────────────────────────────────────────────
+ * Block: d f16 @0, dmin f16 @2, scales[12] @4 (Q4_K's packing), qh[32] @16,
+ * qs[128] @48. Group g = 0..3 reads qs[32g .. 32g+31]: low nibble plus 16 when
+ * bit 2g of qh[i] is set -> weight 64g+i (sub-block 2g); high nibble plus 16
+ * when bit 2g+1 of qh[i] is set -> weight 64g+32+i (sub-block 2g+1). */
+
+/* third_party/ingot/src/kernels.c:1785-1810 (q5_dot_block, the lane of a
+ * build without -march): one running f32 sum per super-block, the low term
+ * then the high term for each i; weight (d*sc)*q - dmin*m. */
+static float q5_k_block_dot(const unsigned char *blk, const float *x) {
+    const float d = orc_f16_to_f32(le16(blk));
+    const float dmin = orc_f16_to_f32(le16(blk + 2));
+    const unsigned char *qh = blk + 16, *qs = blk + 48;
+    float acc = 0.0f;
+    for (int g = 0; g < 4; g++) {
+        unsigned char sa, ma, sb, mb;
+        orc_scale_min(blk + 4, 2 * g, &sa, &ma);
+        orc_scale_min(blk + 4, 2 * g + 1, &sb, &mb);
+        const float da = d * (float)sa, db = d * (float)sb;
+        const float oa = dmin * (float)ma, ob = dmin * (float)mb;
+        const float *xa = x + 64 * g, *xb = xa + 32;
+        for (int i = 0; i < 32; i++) {
+            const unsigned q = qs[32 * g + i], h = qh[i];
+            const unsigned lo = (q & 15u) + (((h >> (2 * g)) & 1u) << 4);
+            const unsigned hi = (q >> 4) + (((h >> (2 * g + 1)) & 1u) << 4);
+            const float wa = da * (float)lo - oa;
+            acc = acc + wa * xa[i];
+            const float wb = db * (float)hi - ob;
+            acc = acc + wb * xb[i];
+        }
+    }
+    return acc;
+}
+
+/* third_party/ingot/src/kernels.c:1812-1833 (q5_dequant_block). */
+static void q5_k_block_decode(const unsigned char *blk, float *w) {
+    const float d = orc_f16_to_f32(le16(blk));
+    const float dmin = orc_f16_to_f32(le16(blk + 2));
+    const unsigned char *qh = blk + 16, *qs = blk + 48;
+    for (int g = 0; g < 4; g++) {
+        unsigned char sa, ma, sb, mb;
+        orc_scale_min(blk + 4, 2 * g, &sa, &ma);
+        orc_scale_min(blk + 4, 2 * g + 1, &sb, &mb);
+        const float da = d * (float)sa, db = d * (float)sb;
+        const float oa = dmin * (float)ma, ob = dmin * (float)mb;
+        for (int i = 0; i < 32; i++) {
+            const unsigned q = qs[32 * g + i], h = qh[i];
+            w[64 * g + i] = da * (float)((q & 15u) + (((h >> (2 * g)) & 1u) << 4)) - oa;
+            w[64 * g + 32 + i] = db * (float)((q >> 4) + (((h >> (2 * g + 1)) & 1u) << 4)) - ob;
+        }
+    }
+}
+
+/* ── Q4_0 ─────────────────────────────────────────────────────────────────
+ * third_party/ingot/src/kernels.c:2353-2360 (q4_0_dequant_block) and
+ * dequant.c:73-83 (dq_q4_0, the same values): d f16 @0, qs[16] @2; weight i
+ * (i < 16) is d*((qs[i] & 15) - 8), weight 16+i is d*((qs[i] >> 4) - 8). */
+static void q4_0_block_decode(const unsigned char *blk, float *w) {
+    const float d = orc_f16_to_f32(le16(blk));
+    const unsigned char *q = blk + 2;
+    for (int i = 0; i < 16; i++) {
+        w[i] = d * (float)((int)(q[i] & 15u) - 8);
+        w[16 + i] = d * (float)((int)(q[i] >> 4) - 8);
     }
 }
 
@@ -176,18 +244,24 @@ static int row_bytes_of(int type, size_t rows, size_t cols, size_t *rb) {
 }
 
 /* The reference's matrix dequant goes through kquant_apply in 256-wide units
- * for all three types (kernels.c:2096-2101, 2563-2567), so a Q8_0 row that is
- * not a whole number of 256-value units is refused (-1). */
+ * for Q4_K, Q6_K and Q8_0 (kernels.c:2096-2101, 2563-2567), so a Q8_0 row
+ * that is not a whole number of 256-value units is refused (-1); Q5_K
+ * (kernels.c:1941-1959) is whole super-blocks anyway, and Q4_0
+ * (kernels.c:2500-2514) takes any multiple of 32. */
 int orc_dequant_matrix(int type, const void *w, size_t rows, size_t cols, float *y) {
     size_t rb;
     if (w == NULL || y == NULL || row_bytes_of(type, rows, cols, &rb) != 0) return -1;
-    if (cols % QK != 0) return -1;
+    if (type != ORC_Q4_0 && cols % QK != 0) return -1;
     const unsigned char *base = (const unsigned char *)w;
     for (size_t r = 0; r < rows; r++) {
         const unsigned char *row = base + r * rb;
         float *out = y + r * cols;
         if (type == ORC_Q4_K)
             for (size_t b = 0; b < cols / QK; b++) q4_k_block_decode(row + 144 * b, out + QK * b);
+        else if (type == ORC_Q5_K)
+            for (size_t b = 0; b < cols / QK; b++) q5_k_block_decode(row + 176 * b, out + QK * b);
+        else if (type == ORC_Q4_0)
+            for (size_t b = 0; b < cols / 32; b++) q4_0_block_decode(row + 18 * b, out + 32 * b);
         else if (type == ORC_Q6_K)
             for (size_t b = 0; b < cols / QK; b++) q6_k_block_decode(row + 210 * b, out + QK * b);
         else
@@ -198,9 +272,12 @@ int orc_dequant_matrix(int type, const void *w, size_t rows, size_t cols, float 
 
 /* matvec lanes of the as-built reference:
  *   Q4_K kernels.c:319-337: y[r] = sum over blocks (in order) of dot_block;
+ *   Q5_K kernels.c:1835-1853: the same with q5_dot_block;
  *   Q6_K kernels.c:2096-2124 with 2305-2318: per block decode 256 values,
  *        then a sequential dot, added to the row sum;
- *   Q8_0 kernels.c:2525-2546: the same per 32-value block. */
+ *   Q8_0 kernels.c:2525-2546: the same per 32-value block;
+ *   Q4_0 kernels.c:2467-2484: ONE running sum over the whole row, no
+ *        per-block partials. */
 int orc_matvec(int type, const void *w, size_t rows, size_t cols,
                const float *x, float *y) {
     size_t rb;
@@ -214,6 +291,14 @@ int orc_matvec(int type, const void *w, size_t rows, size_t cols,
         if (type == ORC_Q4_K) {
             for (size_t b = 0; b < cols / QK; b++)
                 sum = sum + q4_k_block_dot(row + 144 * b, x + QK * b);
+        } else if (type == ORC_Q5_K) {
+            for (size_t b = 0; b < cols / QK; b++)
+                sum = sum + q5_k_block_dot(row + 176 * b, x + QK * b);
+        } else if (type == ORC_Q4_0) {
+            for (size_t b = 0; b < cols / 32; b++) {
+                q4_0_block_decode(row + 18 * b, tmp);
+                for (int i = 0; i < 32; i++) sum = sum + tmp[i] * x[32 * b + i];
+            }
         } else if (type == ORC_Q6_K) {
             for (size_t b = 0; b < cols / QK; b++) {
                 q6_k_block_decode(row + 210 * b, tmp);
@@ -235,16 +320,36 @@ int orc_matvec(int type, const void *w, size_t rows, size_t cols,
  * zero and adds, per 256-wide super-block in order, the sequential dot of the
  * decoded 256 values with the token's slice. Token tiles and row strips only
  * change which (row, token) pairs are in flight, never this order.
- * tokens == 1 is the matvec (kernels.c:1726-1727, 2627-2648). */
+ * tokens == 1 is the matvec (kernels.c:1726-1727, 2627-2648). Q5_K takes the
+ * same core with its own decoder (kernels.c:2573-2595).
+ *
+ * Q4_0 has no batched kernel: ingot_matmat runs its generic path
+ * (third_party/ingot/src/generic.c:76-93): each row decoded whole, then per
+ * token one running sum over all cols in order — the matvec's chain. */
 static void matmat_rows(int type, const unsigned char *base, size_t rb, size_t r0,
                         size_t r1, size_t rows, size_t cols, const float *x,
                         float *y, size_t tokens) {
     float dec[QK];
+    if (type == ORC_Q4_0) {
+        for (size_t r = r0; r < r1; r++) {
+            const unsigned char *row = base + r * rb;
+            for (size_t t = 0; t < tokens; t++) {
+                float sum = 0.0f;
+                for (size_t b = 0; b < cols / 32; b++) {
+                    q4_0_block_decode(row + 18 * b, dec);
+                    for (int i = 0; i < 32; i++) sum = sum + dec[i] * x[t * cols + 32 * b + i];
+                }
+                y[t * rows + r] = sum;
+            }
+        }
+        return;
+    }
     for (size_t r = r0; r < r1; r++) {
         const unsigned char *row = base + r * rb;
         for (size_t t = 0; t < tokens; t++) y[t * rows + r] = 0.0f;
         for (size_t b = 0; b < cols / QK; b++) {
             if (type == ORC_Q4_K) q4_k_block_decode(row + 144 * b, dec);
+            else if (type == ORC_Q5_K) q5_k_block_decode(row + 176 * b, dec);
             else if (type == ORC_Q6_K) q6_k_block_decode(row + 210 * b, dec);
             else q8_0_super_decode(row + 272 * b, dec);
             for (size_t t = 0; t < tokens; t++)
@@ -257,7 +362,8 @@ static int matmat_check(int type, const void *w, size_t rows, size_t cols,
                         const float *x, const float *y, size_t tokens, size_t *rb) {
     if (w == NULL || x == NULL || y == NULL || tokens == 0) return -1;
     if (row_bytes_of(type, rows, cols, rb) != 0) return -1;
-    if (cols % QK != 0) return -1;   /* the batched core works in 256-wide units */
+    /* the batched core works in 256-wide units; Q4_0's generic path does not */
+    if (type != ORC_Q4_0 && cols % QK != 0) return -1;
     if (tokens > SIZE_MAX / rows) return -1;
     return 0;
 }

@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 /* ggml type ids (third_party/ingot/include/ingot/dtype.h:24-59). */
-enum { ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14 };
+enum { ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14 };
 
 /* ── formats (third_party/ingot/src/kernels.c:57-136, 2176-2199, 2518-2523) ─ */
 float orc_f16_to_f32(uint16_t h);

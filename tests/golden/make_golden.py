@@ -21,6 +21,9 @@ records a SHA-256 of the input bytes so generator drift is detected):
   qwen3_4b_prompt.npz  configs[4]'s model (Qwen3-4B): the first 8 prompt ids,
                      prefill + 8 greedy steps, the first step's logits' top 64
                      (`--only c5` writes just this file)
+  adjacent.npz       Q5_K and Q4_0 (configs.ADJACENT): matvec, batched
+                     products and dequant of every shape (`--only adjacent`
+                     writes just this file and those types' fixtures)
   int8.npz           the int8 activation lane of an AVX2 + FMA build of ingot
                      (oracle/_ref/libref_int8.so, INGOT_SDOT=1): Q4_K matvec
                      and batched outputs, incl. round-half-even ties, an
@@ -80,6 +83,26 @@ def golden_c5(ref) -> None:
                         tokens=np.array(toks, np.uint32), top_ids=top.astype(np.uint32),
                         top_vals=lg[top], logits0_sha=np.array(sha(lg)),
                         blob_sha=np.array(sha(model.blob)))
+
+
+def golden_adjacent(ref) -> None:
+    fx = os.path.join(HERE, "ingot_fixtures")
+    for name in ("Q5_K", "Q4_0"):
+        for ext in ("bin", "ref"):
+            shutil.copyfile(os.path.join(REF_FIXTURES, f"{name}.{ext}"),
+                            os.path.join(fx, f"{name}.{ext}"))
+    out = {}
+    for t, rows, cols, token_counts in CF.ADJACENT:
+        key = f"{CF.TYPE_NAME[t]}_{rows}x{cols}"
+        w = O.blocks(t, 1000 + t + rows, rows, cols)
+        x = O.normal(2000 + t + rows, max(token_counts) * cols)
+        out[f"{key}_w_sha"] = np.array(sha(w))
+        out[f"{key}_x_sha"] = np.array(sha(x))
+        out[f"{key}_matvec"] = ref_matvec(ref, t, w, rows, cols, x)
+        out[f"{key}_dequant"] = ref_dequant(ref, t, w, rows, cols)
+        for n in token_counts:
+            out[f"{key}_matmat{n}"] = ref_matmat(ref, t, w, rows, cols, x, n)
+    np.savez_compressed(os.path.join(HERE, "adjacent.npz"), **out)
 
 
 INT8_MATVEC = ((37, 512), (64, 3072))
@@ -215,6 +238,7 @@ def main() -> int:
                         first=np.array(first), logits0_sha=np.array(sha(lg)),
                         top_ids=top.astype(np.uint32), top_vals=lg[top],
                         blob_sha=np.array(sha(model.blob)))
+    golden_adjacent(ref)
     r8 = O.load_ref_int8()
     if r8 is not None:
         golden_int8(r8)
@@ -227,6 +251,11 @@ if __name__ == "__main__":
         r8 = O.load_ref_int8()
         assert r8 is not None, "oracle/_ref/libref_int8.so is missing: run make -C oracle"
         golden_int8(r8)
+        sys.exit(0)
+    if sys.argv[1:] == ["--only", "adjacent"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_adjacent(r)
         sys.exit(0)
     if sys.argv[1:] == ["--only", "c5"]:
         r = O.load_ref()

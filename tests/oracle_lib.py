@@ -205,7 +205,7 @@ def q4k_int8_dots(w: np.ndarray, rows: int, cols: int, q: np.ndarray) -> np.ndar
     return prod.reshape(rows, q.shape[0], nb, 8, 32).sum(axis=-1).reshape(rows, q.shape[0], -1)
 
 
-BLOCK = {12: (256, 144), 14: (256, 210), 8: (32, 34)}
+BLOCK = {12: (256, 144), 13: (256, 176), 14: (256, 210), 8: (32, 34), 2: (32, 18)}
 
 
 def ptr(a: np.ndarray) -> int:

@@ -24,7 +24,7 @@ def declared_functions(header: str):
 
 
 def test_every_declared_symbol_is_exported():
-    for header in ("kernels_hip.h", "mynah_synth.h"):
+    for header in sorted(f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h")):
         names = declared_functions(header)
         assert len(names) > 5, header
         for n in names:
@@ -32,7 +32,10 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_has_kernel_and_exactness():
-    assert [M.lib.ingot_has_kernel(t) for t in (8, 12, 14, 2, 13)] == [1, 1, 1, 0, 0]
+    # The reference's specialised kernels (generic.c:24-37) for the five
+    # types built here; Q4_1 has none there either.
+    assert [M.lib.ingot_has_kernel(t) for t in (8, 12, 14, 2, 13)] == [1, 1, 1, 1, 1]
+    assert [M.lib.ingot_has_kernel(t) for t in (3, 99)] == [0, 0]
     assert M.lib.ingot_matmat_is_exact(1) == 1 and M.lib.ingot_matmat_is_exact(512) == 1
 
 
