@@ -240,6 +240,24 @@ def gpu_qwen3_4b(M, CF):
     return out
 
 
+def gpu_decode_4b(M, CF, steps: int):
+    """configs[4]'s decode alone in the headline mode (exact GEMV + split
+    attention): the 2048-token prompt prefilled in batches, then `steps`
+    greedy steps; one warm-up prompt first (graph captures)."""
+    shape = CF.QWEN3_4B
+    model = M.SynthQwen3(shape, 0)
+    prompt = CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)
+    dec = M.Qwen3Decoder(model, int(prompt.size) + steps + 1)
+    dec.set_attention(M.ATTN_SPLIT)
+    dec.prompt(prompt[:4], 4)
+    dec.reset()
+    toks, pre_ms, dec_ms = dec.prompt(prompt, steps)
+    dec.close()
+    return {"model": "Qwen3-4B random-init Q4_K_M mix", "mode": "exact_gemv_split_attention",
+            "prompt": int(prompt.size), "steps": steps, "decode_ms": round(dec_ms, 2),
+            "decode_tok_s": round(steps / (dec_ms * 1e-3), 1), "first_tokens": toks[:4]}
+
+
 def gpu_prefill_4b(M, CF, reps: int = 3):
     """configs[4]'s prompt prefill alone: the 2047 cache-filling tokens of
     the 2048-token prompt through mynah_hip_qwen3_prefill (batched), best of
@@ -339,6 +357,9 @@ def main() -> int:
                     help="only the configs[2] decode section, printed as one JSON line")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configs[4] batched prompt prefill, printed as one JSON line")
+    ap.add_argument("--decode-4b-only", action="store_true",
+                    help="only configs[4]'s decode (2048-token prompt, then --steps greedy "
+                         "steps, exact GEMV + split attention), printed as one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only the head GEMV + calibration copies, for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -359,6 +380,9 @@ def main() -> int:
         return 0
     if args.decode_only:
         print(json.dumps({"decode": gpu_decode(M, CF)}), flush=True)
+        return 0
+    if args.decode_4b_only:
+        print(json.dumps({"decode_4b": gpu_decode_4b(M, CF, args.steps)}), flush=True)
         return 0
 
     log("[bench] configs[1] sweep")
