@@ -297,15 +297,10 @@ static uint32_t fast_ks(uint32_t all_rows) {
  * workgroup. Small launches spread one unit per lane over as many
  * workgroups as possible (they are latency-bound); large ones keep every
  * lane busy (K divides the units) and group rows to share the staged x. */
-static long env_long(const char *name, long dflt);
-
 static void exact_shape(uint32_t all_rows, uint32_t units, uint32_t *lk, uint32_t *ws,
                         uint32_t *wr) {
     uint32_t k = 1;
-    const long fk = env_long("MYNAH_EXACT_K", 0);
-    if (fk == 1 || fk == 2 || fk == 4 || fk == 8 || fk == 16) {
-        k = (uint32_t)fk;
-    } else if (all_rows >= 16384u) {
+    if (all_rows >= 16384u) {
         while (k < 16u && units % (2u * k) == 0) k *= 2u;
     } else {
         while (k < 16u && k < units) k *= 2u;
@@ -414,9 +409,8 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
     }
     if (exact && gemv_stream_plan(d, grp, p) == 0) return 0;
     /* Split super-blocks across quads when the launch is small enough that
-     * four times the waves still fit the 1,024 SIMDs about twice
-     * (MYNAH_SPLIT_MAX_UNITS tunes the limit). */
-    if (all_units > (uint64_t)env_long("MYNAH_SPLIT_MAX_UNITS", 32768)) split = 0;
+     * four times the waves still fit the 1,024 SIMDs about twice. */
+    if (all_units > 32768u) split = 0;
     const char *env = getenv("MYNAH_GEMV_SPLIT");
     if (env != NULL) split = split && env[0] != '0';
     uint32_t lk = 0, ws = 1, wr = 1, ks = 1, tile_rows;
