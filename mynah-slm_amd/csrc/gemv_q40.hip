@@ -11,7 +11,9 @@
 // every output is one serial chain of cols adds that cannot be split or
 // reordered without changing its bits.
 //
-// Layout: lane = row (64 rows per one-wave workgroup), T tokens per lane as T
+// Layout (batched, and the matvec with MYNAH_Q40_PC=0; the matvec's default
+// kernel is mynah_q40_chain_pc below): lane = row (64 rows per one-wave
+// workgroup), T tokens per lane as T
 // independent chains interleaved (T = 1 for the matvec, 8 batched), grid.y
 // over token groups. The row is streamed in chunks of 8 blocks (256 values,
 // 144 bytes): a chunk's words are loaded one chunk ahead of their use, and
@@ -122,6 +124,109 @@ MYNAH_DEV void q40_chain(const uint8_t *__restrict__ w, const float *__restrict_
         for (int t = 0; t < T; t++)
             if (t0 + (uint32_t)t < tokens) y[(size_t)(t0 + (uint32_t)t) * rows + row] = acc[t];
     }
+}
+
+// ── the matvec with the products computed beside the chain ────────────────
+// One token: the chain is the whole cost, and a wave that decodes, converts
+// and multiplies every weight before adding it issues ~5 instructions per
+// weight of its chain. Here wave 0 of a 256-thread workgroup only adds: for
+// its 64 rows (lane = row) it reads the products w_i * x_i, four at a time,
+// from LDS and extends each row's running sum in the reference's order.
+// Waves 1..3 produce them: at step s wave p decodes block 3 s + p - 1 of its
+// lane's row and writes its 32 products (the reference's f32 roundings) into
+// one of two LDS buffers; one barrier per step hands a buffer over. Each
+// producer keeps its next four blocks in flight (a ring of four register
+// sets, indexed statically by unrolling the steps by four).
+#define QP_AHEAD 4
+
+struct Q40Blk {
+    uint32_t raw[5], s;
+};
+
+MYNAH_DEV void q40_fetch(Q40Blk &bk, const uint8_t *row, uint32_t b, uint32_t nb) {
+    if (b < nb) {
+        const uint8_t *p = row + 18u * b;
+        bk.s = (uint32_t)(uintptr_t)p & 3u;
+        const uint32_t *a = (const uint32_t *)(p - bk.s);
+        // 18 block bytes at skew 0 or 2 lie in dwords 0..4 (at skew 0 dword 4
+        // holds the last two quant bytes and two bytes past the block).
+#pragma unroll
+        for (int k = 0; k < 5; k++) bk.raw[k] = a[k];
+    }
+}
+
+// The 32 products of a block (kernels.c:2353-2360 values times x, one
+// rounding each) into quads 8 p .. 8 p + 7 of buffer `dst`.
+MYNAH_DEV void q40_products(const Q40Blk &bk, const float *__restrict__ xb, float4 (*dst)[64],
+                            uint32_t p, uint32_t lane) {
+#pragma clang fp contract(off)
+    const float d = f16_to_f32(bk.s ? (bk.raw[0] >> 16) : bk.raw[0]);
+    uint32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) q[j] = bk.s ? bk.raw[j + 1] : align_bytes(bk.raw[j + 1], bk.raw[j], 2u);
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t nib = hf ? ((q[j] >> 4) & 0x0f0f0f0fu) : (q[j] & 0x0f0f0f0fu);
+            const float4 x4 = *(const float4 *)(xb + 16 * hf + 4 * j);
+            float4 pr;
+            pr.x = (d * (ubyte_f<0>(nib) - 8.0f)) * x4.x;
+            pr.y = (d * (ubyte_f<1>(nib) - 8.0f)) * x4.y;
+            pr.z = (d * (ubyte_f<2>(nib) - 8.0f)) * x4.z;
+            pr.w = (d * (ubyte_f<3>(nib) - 8.0f)) * x4.w;
+            dst[8u * p + 4u * (uint32_t)hf + (uint32_t)j][lane] = pr;
+        }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+mynah_q40_chain_pc(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                   float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t row_bytes) {
+#pragma clang fp contract(off)
+    __shared__ float4 pr[2][24][64];          // [buffer][quad of the step][row]
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t row = blockIdx.x * 64u + lane;
+    const uint8_t *wr = w + (size_t)(row < rows ? row : rows - 1u) * row_bytes;
+    const uint32_t nb = cols / 32u, nsteps = (nb + 2u) / 3u;
+    const uint32_t p = wave - 1u;             // producer index (waves 1..3)
+    Q40Blk ring[QP_AHEAD];
+    if (wave != 0u) {
+#pragma unroll
+        for (int k = 0; k < QP_AHEAD; k++) q40_fetch(ring[k], wr, 3u * (uint32_t)k + p, nb);
+        if (p < nb) q40_products(ring[0], x + 32u * p, pr[0], p, lane);
+        q40_fetch(ring[0], wr, 3u * QP_AHEAD + p, nb);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    // Step s: the consumer adds buffer s & 1 while the producers fill buffer
+    // (s + 1) & 1 with step s + 1, whose block sits in ring[(s + 1) % 4].
+    for (uint32_t s0 = 0; s0 < nsteps; s0 += QP_AHEAD) {
+#pragma unroll
+        for (int j = 0; j < QP_AHEAD; j++) {
+            const uint32_t st = s0 + (uint32_t)j;
+            if (st >= nsteps) break;
+            if (wave == 0u) {
+                const uint32_t nq = 8u * (nb - 3u * st < 3u ? nb - 3u * st : 3u);
+#pragma unroll
+                for (uint32_t q = 0; q < 24u; q++) {
+                    if (q >= nq) break;
+                    const float4 v = pr[st & 1u][q][lane];
+                    acc = acc + v.x;
+                    acc = acc + v.y;
+                    acc = acc + v.z;
+                    acc = acc + v.w;
+                }
+            } else if (st + 1u < nsteps) {
+                const uint32_t b = 3u * (st + 1u) + p;
+                const int slot = (j + 1) % QP_AHEAD;   // static once unrolled
+                if (b < nb) q40_products(ring[slot], x + 32u * b, pr[(st + 1u) & 1u], p, lane);
+                q40_fetch(ring[slot], wr, b + 3u * QP_AHEAD, nb);
+            }
+            __syncthreads();
+        }
+    }
+    if (wave == 0u && row < rows) y[row] = acc;
 }
 
 extern "C" __global__ void __launch_bounds__(64)

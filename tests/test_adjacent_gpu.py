@@ -59,7 +59,9 @@ def test_golden(M, case):
 
 
 @pytest.mark.parametrize("qtype,rows,cols", [(13, 4096, 4096), (13, 40000, 1024), (13, 64, 9728),
-                                             (2, 4096, 4096), (2, 1000, 2080), (2, 65, 32)])
+                                             (2, 4096, 4096), (2, 1000, 2080), (2, 65, 32),
+                                             (2, 130, 96), (2, 64, 288), (2, 3, 4160),
+                                             (2, 33000, 96)])
 def test_matvec_against_oracle(M, qtype, rows, cols):
     """Small and large launches (split quads vs one lane per super-block for
     Q5_K; long and short chains for Q4_0)."""
@@ -67,6 +69,16 @@ def test_matvec_against_oracle(M, qtype, rows, cols):
     w, x = M.synth_blocks(qtype, 7, rows, cols), M.synth_normal(8, cols)
     got, ref = M.matvec(qtype, w, rows, cols, x), O.project(qtype, w, rows, cols, x)
     assert np.array_equal(bits(got), bits(ref)) and rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("cols", [32, 96, 2080, 4096])
+def test_q40_one_wave_matvec_against_oracle(M, monkeypatch, cols):
+    """The matvec's other kernel (MYNAH_Q40_PC=0: one wave decodes and adds)."""
+    monkeypatch.setenv("MYNAH_Q40_PC", "0")
+    rows = 200
+    print(f"[case] Q4_0 one-wave matvec {rows}x{cols}", flush=True)
+    w, x = M.synth_blocks(2, 20, rows, cols), M.synth_normal(21, cols)
+    assert np.array_equal(bits(M.matvec(2, w, rows, cols, x)), bits(O.matvec(2, w, rows, cols, x)))
 
 
 @pytest.mark.parametrize("qtype,rows,cols,tokens", [(13, 1024, 2048, 130), (13, 70, 512, 2),
