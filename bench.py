@@ -440,8 +440,9 @@ def main() -> int:
             "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": ("mynah_gemv_group" if order == 0 else "mynah_gemv_fast_group")
-                      + " (Q6_K 151936x1024 head)",
+            "kernel": ("mynah_gemv_fast_group" if order != 0 else
+                       "mynah_gemv_group" if os.environ.get("MYNAH_GEMV_TYPED") == "0" else
+                       "mynah_gemv_group_q6k") + " (Q6_K 151936x1024 head)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,

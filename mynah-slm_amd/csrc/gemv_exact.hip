@@ -265,6 +265,43 @@ MYNAH_DEV float q6k_sum(const uint32_t *raw, uint32_t s, const float *__restrict
     return acc;
 }
 
+// The same sum with each block word realigned where it is used (no second
+// copy of the block): fewer live registers, so the Q6_K-only entry below
+// fits five waves per SIMD. Same operations in the same order.
+MYNAH_DEV float q6k_sum_lean(const uint32_t *raw, uint32_t s, const float *__restrict__ x) {
+#pragma clang fp contract(off)
+    const float d = f16_to_f32(raw[52] >> (8u * s));
+    float acc = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            // scales 8h + 2k and 8h + 2k + 1: bytes 2 (k & 1), + 1 of word 48 + 2h + k / 2
+            const uint32_t scw = align_bytes(raw[48 + 2 * h + k / 2 + 1], raw[48 + 2 * h + k / 2], s);
+            const float ds0 = d * (float)(int)(int8_t)(scw >> (16 * (k & 1)));
+            const float ds1 = d * (float)(int)(int8_t)(scw >> (16 * (k & 1) + 8));
+            const float n0 = -32.0f * ds0, n1 = -32.0f * ds1;
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const int iq = 16 * h + 8 * (k & 1) + m, ih = 32 + 8 * h + m;
+                const uint32_t ql = align_bytes(raw[iq + 1], raw[iq], s);
+                const uint32_t qh = align_bytes(raw[ih + 1], raw[ih], s);
+                const uint32_t nib = (k < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                const uint32_t q6 = nib | (((qh >> (2 * k)) & 0x03030303u) << 4);
+                const float dsc = m >= 4 ? ds1 : ds0, n32 = m >= 4 ? n1 : n0;
+                const float qf[4] = {ubyte_f<0>(q6), ubyte_f<1>(q6), ubyte_f<2>(q6), ubyte_f<3>(q6)};
+                const float4 x4 = *(const float4 *)(x + 128 * h + 32 * k + 4 * m);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const float w = __builtin_fmaf(dsc, qf[t], n32);
+                    acc = acc + w * xv[t];
+                }
+            }
+        }
+    return acc;
+}
+
 MYNAH_DEV float q6k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
     uint32_t raw[53], s;
     q6k_load(blk, raw, s);
@@ -474,6 +511,12 @@ template <> struct Raw<14> {
     uint32_t raw[53], s;
     __device__ __forceinline__ void load(const uint8_t *b) { q6k_load(b, raw, s); }
     __device__ __forceinline__ float sum(const float *x) const { return q6k_sum(raw, s, x); }
+};
+struct RawQ6Lean {
+    static constexpr uint32_t BYTES = 210;
+    uint32_t raw[53], s;
+    __device__ __forceinline__ void load(const uint8_t *b) { q6k_load(b, raw, s); }
+    __device__ __forceinline__ float sum(const float *x) const { return q6k_sum_lean(raw, s, x); }
 };
 template <> struct Raw<8> {
     static constexpr uint32_t BYTES = 34;
@@ -749,4 +792,30 @@ mynah_gemv_group(const GemvGroup grp) {
     } else {
         group_split<8, false>(g, t, grp.shape, lds, shd);
     }
+}
+
+// Launches whose every matrix is Q4_K, in the one-lane-per-super-block
+// layout and at most 256 threads per workgroup (the Qwen3-4B projections):
+// six waves per SIMD (80 VGPRs, no spills) instead of the general entry's four.
+extern "C" __global__ void __launch_bounds__(256, 6)
+mynah_gemv_group_q4k(const GemvGroup grp) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ double shd[16];
+    const uint32_t t = blockIdx.x;
+    uint32_t i = 0;
+    while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
+    group_split<12, false>(grp.d[i], t, grp.shape, lds, shd);
+}
+
+// Launches whose every matrix is Q6_K, in the one-lane-per-super-block
+// layout and at most 256 threads per workgroup (the 0.6B head among them):
+// the lean sum at five waves per SIMD instead of four.
+extern "C" __global__ void __launch_bounds__(256, 5)
+mynah_gemv_group_q6k(const GemvGroup grp) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ double shd[16];
+    const uint32_t t = blockIdx.x;
+    uint32_t i = 0;
+    while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
+    group_split<14, false, RawQ6Lean>(grp.d[i], t, grp.shape, lds, shd);
 }

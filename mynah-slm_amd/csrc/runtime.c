@@ -476,6 +476,19 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         p->kernel = MYNAH_K_GEMV_GROUP;
         p->threads = 64u * ws * wr;
         p->shape = lk | (ws << 8) | (wr << 16) | ((uint32_t)(exact && split) << 24);
+        /* Single-type launches in the one-lane layout, at most 256 threads:
+         * entries compiled for that type alone hold more waves per SIMD
+         * (Q6_K five, Q4_K six, against four). MYNAH_GEMV_TYPED=0 keeps the
+         * general entry. */
+        int all_q6k = !split && p->threads <= 256u, all_q4k = all_q6k;
+        for (uint32_t i = 0; i < grp->n; i++) {
+            all_q6k = all_q6k && grp->d[i].type == MYNAH_Q6_K;
+            all_q4k = all_q4k && grp->d[i].type == MYNAH_Q4_K;
+        }
+        if (env_long("MYNAH_GEMV_TYPED", 1) != 0) {
+            if (all_q6k) p->kernel = MYNAH_K_GEMV_GROUP_Q6K;
+            else if (all_q4k) p->kernel = MYNAH_K_GEMV_GROUP_Q4K;
+        }
     }
     return 0;
 }
