@@ -21,7 +21,9 @@ reference's), `prefill_gemm` (configs[3], the exact batched GEMM at 512
 tokens), `prefill_gemm_int8` (the same with Q4_K on the int8 activation
 lane, the batched default of the reference's AVX2 build),
 `qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
-greedy steps on Qwen3-4B) and `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class).
+greedy steps on Qwen3-4B), `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class) and
+`qwen3_4b_copy_ceiling_gbs` (a plain copy moving the same HBM bytes per launch:
+what any kernel launched back to back reaches at that size).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -87,9 +89,36 @@ def gpu_sweep(M, CF, steps: int, warmup: int):
     return step_bytes, copies, total_ms, head_ms, algorithmic_bytes(mats[head]), per
 
 
+def copy_ceiling(M, traffic: int, launches: int = 64) -> float:
+    """GB/s of HBM traffic a plain device copy (mynah_copy16) reaches when
+    each launch moves `traffic` bytes (reads traffic/2, writes traffic/2),
+    launched back to back from rotating sources like the GEMVs: the
+    practical per-launch ceiling at that size."""
+    half = max(256, traffic // 2 // 256 * 256)
+    copies = max(2, -(-2 * MALL_BYTES // half))
+    src = [M.DeviceBuffer(half) for _ in range(copies)]
+    dst = M.DeviceBuffer(half)
+    for b in src:
+        M.check(M.lib.mynah_hip_memset(b.ptr, 1, half), "memset")
+    n = max(launches, 4 * copies)
+    for i in range(copies):
+        M.copy_dev(dst.ptr, src[i].ptr, half)
+    a, e = M.Event(), M.Event()
+    a.record()
+    for i in range(n):
+        M.copy_dev(dst.ptr, src[i % copies].ptr, half)
+    e.record()
+    M.sync()
+    ms = a.elapsed_ms(e) / n
+    for b in src + [dst]:
+        b.free()
+    return 2 * half / (ms * 1e-3) / 1e9
+
+
 def gpu_4b_classes(M, CF, launches: int = 64):
-    """GB/s of each Qwen3-4B GEMV class, rotating copies totalling > 2x MALL."""
-    out = {}
+    """GB/s of each Qwen3-4B GEMV class, rotating copies totalling > 2x MALL,
+    and beside it the copy ceiling for the same traffic per launch."""
+    out, ceiling = {}, {}
     for i, m in enumerate(CF.QWEN3_4B_GEMV):
         wseed, xseed = CF.matrix_seeds(M.substream, 4, i)
         nbytes = algorithmic_bytes(m)
@@ -104,7 +133,8 @@ def gpu_4b_classes(M, CF, launches: int = 64):
         out[m.name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         for b in w + [x, y]:
             b.free()
-    return out
+        ceiling[m.name] = round(copy_ceiling(M, nbytes, launches), 1)
+    return out, ceiling
 
 
 def gpu_decode(M, CF):
@@ -409,10 +439,10 @@ def main() -> int:
         log("[bench] configs[4] Qwen3-4B end to end")
         e2e_4b = gpu_qwen3_4b(M, CF)
 
-    extra_4b = None
+    extra_4b = ceiling_4b = None
     if not args.no_4b:
         log("[bench] Qwen3-4B GEMV classes")
-        extra_4b = gpu_4b_classes(M, CF)
+        extra_4b, ceiling_4b = gpu_4b_classes(M, CF)
 
     cpu = None
     if not args.no_cpu:
@@ -459,6 +489,7 @@ def main() -> int:
         "qwen3_4b_end_to_end": e2e_4b,
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
+        "qwen3_4b_copy_ceiling_gbs": ceiling_4b,
     }
     print(json.dumps(line), flush=True)
     return 0
