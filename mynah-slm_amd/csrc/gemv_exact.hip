@@ -83,56 +83,17 @@ MYNAH_DEV float q4k_group(const uint32_t *q, float d, float dmin, uint32_t s0, u
     return acc;
 }
 
-// The batched reference (kernels.c:1017-1039: dequant_block, then a plain
-// sequential dot) walks the same weights in natural order: the 32 low-nibble
-// weights of sub-block 2g, then the 32 high-nibble weights of 2g+1.
-template <int G>
-MYNAH_DEV float q4k_group_seq(const uint32_t *q, float d, float dmin, uint32_t s0, uint32_t s1,
-                              uint32_t s2, const float *__restrict__ x, float acc) {
-#pragma clang fp contract(off)
-    float sa, ma, sb, mb;
-    q4k_sm<2 * G>(s0, s1, s2, sa, ma);
-    q4k_sm<2 * G + 1>(s0, s1, s2, sb, mb);
-    const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
-#pragma unroll
-    for (int half = 0; half < 2; half++) {
-        const float dd = half ? db : da, oo = half ? ob : oa;
-#pragma unroll
-        for (int m = 0; m < 8; m++) {
-            const uint32_t v = q[8 * G + m];
-            const uint32_t n = half ? ((v >> 4) & 0x0f0f0f0fu) : (v & 0x0f0f0f0fu);
-            const float qf[4] = {ubyte_f<0>(n), ubyte_f<1>(n), ubyte_f<2>(n), ubyte_f<3>(n)};
-            const float4 x4 = *(const float4 *)(x + 64 * G + 32 * half + 4 * m);
-            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const float w = __builtin_fmaf(dd, qf[t], -oo);
-                acc = acc + w * xv[t];
-            }
-        }
-    }
-    return acc;
-}
-
 // Raw block words in registers, loaded apart from the arithmetic so the
 // grouped kernel can issue a block's loads before it stages x.
-template <bool SEQ>
 MYNAH_DEV float q4k_sum(const uint32_t *v, const float *__restrict__ x) {
     const float d = f16_to_f32(v[0]), dmin = f16_to_f32(v[0] >> 16);
     const uint32_t s0 = v[1], s1 = v[2], s2 = v[3];
     const uint32_t *q = v + 4;
     float acc = 0.0f;
-    if (SEQ) {
-        acc = q4k_group_seq<0>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group_seq<1>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group_seq<2>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group_seq<3>(q, d, dmin, s0, s1, s2, x, acc);
-    } else {
-        acc = q4k_group<0>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group<1>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group<2>(q, d, dmin, s0, s1, s2, x, acc);
-        acc = q4k_group<3>(q, d, dmin, s0, s1, s2, x, acc);
-    }
+    acc = q4k_group<0>(q, d, dmin, s0, s1, s2, x, acc);
+    acc = q4k_group<1>(q, d, dmin, s0, s1, s2, x, acc);
+    acc = q4k_group<2>(q, d, dmin, s0, s1, s2, x, acc);
+    acc = q4k_group<3>(q, d, dmin, s0, s1, s2, x, acc);
     return acc;
 }
 
@@ -143,13 +104,6 @@ MYNAH_DEV void q4k_load(const uint8_t *__restrict__ blk, uint32_t *v) {
         const uint4 c = p[k];
         v[4 * k] = c.x; v[4 * k + 1] = c.y; v[4 * k + 2] = c.z; v[4 * k + 3] = c.w;
     }
-}
-
-template <bool SEQ>
-MYNAH_DEV float q4k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
-    uint32_t v[36];
-    q4k_load(blk, v);
-    return q4k_sum<SEQ>(v, x);
 }
 
 // ── Q5_K: 176-byte block, 16-byte aligned ──────────────────────────────────
@@ -302,12 +256,6 @@ MYNAH_DEV float q6k_sum_lean(const uint32_t *raw, uint32_t s, const float *__res
     return acc;
 }
 
-MYNAH_DEV float q6k_unit(const uint8_t *__restrict__ blk, const float *__restrict__ x) {
-    uint32_t raw[53], s;
-    q6k_load(blk, raw, s);
-    return q6k_sum(raw, s, x);
-}
-
 // ── Q8_0: 34-byte block, 2-byte aligned ────────────────────────────────────
 
 MYNAH_DEV void q80_load(const uint8_t *__restrict__ blk, uint32_t *raw, uint32_t &s) {
@@ -335,67 +283,6 @@ MYNAH_DEV float q80_sum(const uint32_t *raw, uint32_t s, const float *__restrict
     }
     return acc;
 }
-
-MYNAH_DEV float q80_block(const uint8_t *__restrict__ blk, const float *__restrict__ x,
-                          float acc) {
-    uint32_t raw[9], s;
-    q80_load(blk, raw, s);
-    return q80_sum(raw, s, x, acc);
-}
-
-// ── batched-order driver ───────────────────────────────────────────────────
-// One token of the exact matmat (kernels.c:1053-1104): natural weight order
-// within a Q4_K block, Q8_0 summed in 256-value units of eight blocks
-// (kernels.c:2635-2648); Q6_K is the same as the matvec. Lane = row (64 rows
-// per workgroup), wave w of W sums units w, w + W, ...; x by scalar loads;
-// wave 0 folds each phase's unit sums in unit order.
-
-template <int FMT>
-MYNAH_DEV float seq_unit(const uint8_t *__restrict__ row, uint32_t u, const float *__restrict__ x) {
-    if (FMT == 12) return q4k_unit<true>(row + 144u * u, x + 256u * u);
-    if (FMT == 14) return q6k_unit(row + 210u * u, x + 256u * u);
-    float acc = 0.0f;
-#pragma unroll
-    for (int b = 0; b < 8; b++) acc = q80_block(row + 272u * u + 34u * b, x + 256u * u + 32u * b, acc);
-    return acc;
-}
-
-template <int FMT>
-MYNAH_DEV void gemv_seq(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                        float *__restrict__ y, uint32_t rows, uint32_t units, uint32_t row_bytes) {
-#pragma clang fp contract(off)
-    __shared__ float part[EX_MAX_WAVES][EX_ROWS];
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
-    const uint32_t row = blockIdx.x * EX_ROWS + lane;
-    const uint8_t *wr = w + (size_t)(row < rows ? row : rows - 1u) * row_bytes;
-    float total = 0.0f;
-    for (uint32_t p = 0; p < units; p += nw) {
-        const uint32_t u = p + wave;
-        float s = 0.0f;
-        if (u < units) s = seq_unit<FMT>(wr, u, x);
-        part[wave][lane] = s;
-        __syncthreads();
-        if (wave == 0) {
-            const uint32_t n = units - p < nw ? units - p : nw;
-            for (uint32_t k = 0; k < n; k++) total = total + part[k][lane];
-        }
-        __syncthreads();
-    }
-    if (wave == 0 && row < rows) y[row] = total;
-}
-
-#define GEMV_SEQ_ENTRY(name, FMT)                                                          \
-    extern "C" __global__ void __launch_bounds__(EX_ROWS * EX_MAX_WAVES)                  \
-        name(const uint8_t *__restrict__ w, const float *__restrict__ x,                  \
-             float *__restrict__ y, uint32_t rows, uint32_t units, uint32_t row_bytes) {  \
-        gemv_seq<FMT>(w, x, y, rows, units, row_bytes);                                    \
-    }
-
-GEMV_SEQ_ENTRY(mynah_q4k_gemv_exact_seq, 12)
-GEMV_SEQ_ENTRY(mynah_q6k_gemv_exact_seq, 14)
-GEMV_SEQ_ENTRY(mynah_q80_gemv_exact_seq, 8)
 
 
 // ── grouped matvec with fused epilogues (every matvec, decode included) ────
@@ -498,7 +385,7 @@ template <> struct Raw<12> {
     static constexpr uint32_t BYTES = 144;
     uint32_t v[36];
     __device__ __forceinline__ void load(const uint8_t *b) { q4k_load(b, v); }
-    __device__ __forceinline__ float sum(const float *x) const { return q4k_sum<false>(v, x); }
+    __device__ __forceinline__ float sum(const float *x) const { return q4k_sum(v, x); }
 };
 template <> struct Raw<13> {
     static constexpr uint32_t BYTES = 176;

@@ -176,23 +176,6 @@ int mynah_hip_set_gemv_order(int order) {
 
 int mynah_hip_gemv_order(void) { return gemv_order; }
 
-/* Exact kernels: 64 rows per workgroup, W waves splitting the units of a
- * row (W <= 16, balanced so every wave gets the same count). */
-/* One token of the exact matmat: the batched reference's summation order. */
-static int gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                           size_t rb, const float *x, float *y, hipStream_t stream) {
-    const size_t units = cols / 256;
-    const size_t per_wave = (units + 15) / 16;
-    const size_t waves = (units + per_wave - 1) / per_wave;
-    const unsigned grid = (unsigned)((rows + 63) / 64);
-    const int k = type == MYNAH_Q4_K   ? MYNAH_K_Q4K_EXACT_SEQ
-                  : type == MYNAH_Q6_K ? MYNAH_K_Q6K_EXACT_SEQ
-                                       : MYNAH_K_Q80_EXACT_SEQ;
-    uint32_t rows32 = (uint32_t)rows, units32 = (uint32_t)units, rb32 = (uint32_t)rb;
-    void *args[] = {&w, &x, &y, &rows32, &units32, &rb32};
-    return mynah_launch(d, k, grid, 1, (unsigned)(64 * waves), 0, stream, args);
-}
-
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                       const float *x, float *y, hipStream_t stream) {
     size_t rb;
@@ -223,22 +206,6 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     g.n = 1;
     if (mynah_gemv_desc_init(&g.d[0], type, w, rows, cols, x, y) != 0) return -1;
     return mynah_gemv_group_launch(d, &g, stream, NULL, -1);
-}
-
-int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                          const float *x, float *y, hipStream_t stream) {
-    size_t rb;
-    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
-    if (cols % 256 != 0 || rb > 0xffffffffu ||
-        (type != MYNAH_Q4_K && type != MYNAH_Q6_K && type != MYNAH_Q8_0)) {
-        mynah_set_error("batched order needs Q4_K / Q6_K / Q8_0 and cols %% 256 == 0");
-        return -1;
-    }
-    if (mynah_w_misaligned(type, w)) {
-        mynah_set_error("weights misaligned for type %d", type);
-        return -1;
-    }
-    return gemv_seq_launch(d, type, w, rows, cols, rb, x, y, stream);
 }
 
 static long env_long(const char *name, long dflt);

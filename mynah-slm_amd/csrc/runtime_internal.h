@@ -13,9 +13,6 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
 /* Every kernel of the embedded code object: id and symbol name. */
 #define MYNAH_KERNEL_LIST(X)                          \
     X(MYNAH_K_DEQUANT, "mynah_dequant")                 \
-    X(MYNAH_K_Q4K_EXACT_SEQ, "mynah_q4k_gemv_exact_seq") \
-    X(MYNAH_K_Q6K_EXACT_SEQ, "mynah_q6k_gemv_exact_seq") \
-    X(MYNAH_K_Q80_EXACT_SEQ, "mynah_q80_gemv_exact_seq") \
     X(MYNAH_K_Q4K_GEMM, "mynah_q4k_gemm_exact")        \
     X(MYNAH_K_Q5K_GEMM, "mynah_q5k_gemm_exact")        \
     X(MYNAH_K_Q5K_GEMM_MV, "mynah_q5k_gemm_mv")        \
@@ -96,10 +93,6 @@ int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, c
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                       const float *x, float *y, hipStream_t stream);
-/* The exact GEMV in the batched reference's summation order (one token of
- * the exact matmat). cols must be a multiple of 256. */
-int mynah_gemv_seq_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                          const float *x, float *y, hipStream_t stream);
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                          float *y, hipStream_t stream);
 /* exact != 0 keeps the exact batched order whatever the int8 lane's mode
