@@ -14,7 +14,8 @@
 // Layout (batched, and the matvec with MYNAH_Q40_PC=0; the matvec's default
 // kernel is mynah_q40_chain_pc below): lane = row (64 rows per one-wave
 // workgroup), T tokens per lane as T
-// independent chains interleaved (T = 1 for the matvec, 8 batched), grid.y
+// independent chains interleaved (T = 1 for the matvec; 2, 4 or 8 batched,
+// the most that still leaves enough waves to fill the chip), grid.y
 // over token groups. The row is streamed in chunks of 8 blocks (256 values,
 // 144 bytes): a chunk's words are loaded one chunk ahead of their use, and
 // the matching 256 x values of each token are staged in LDS and read as
@@ -233,6 +234,18 @@ extern "C" __global__ void __launch_bounds__(64)
 mynah_q40_chain1(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
                  uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
     q40_chain<1>(w, x, y, rows, cols, tokens, row_bytes);
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+mynah_q40_chain2(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
+    q40_chain<2>(w, x, y, rows, cols, tokens, row_bytes);
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+mynah_q40_chain4(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
+    q40_chain<4>(w, x, y, rows, cols, tokens, row_bytes);
 }
 
 extern "C" __global__ void __launch_bounds__(64)

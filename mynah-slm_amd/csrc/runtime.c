@@ -214,7 +214,13 @@ int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, c
                      float *y, size_t tokens, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(MYNAH_Q4_0, rows, cols, &rb) != 0) return -1;
-    const size_t groups = tokens == 1 ? 1 : (tokens + 7) / 8;
+    /* Batched: T token chains per lane, the largest of 8, 4, 2 that still
+     * gives >= 2048 one-wave workgroups (two per SIMD), since each chain is
+     * serial and a lane's T chains are its only overlap. */
+    const size_t row_groups = (rows + 63) / 64;
+    size_t per = tokens == 1 ? 1 : 8;
+    while (per > 2 && row_groups * ((tokens + per - 1) / per) < 2048) per /= 2;
+    const size_t groups = (tokens + per - 1) / per;
     if (tokens == 0 || groups > 65535u || rb > 0xffffffffu) {
         mynah_set_error("bad token count for the Q4_0 product");
         return -1;
@@ -235,8 +241,9 @@ int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, c
         return mynah_launch(d, MYNAH_K_Q40_CHAIN_PC, grid, 1, 256, 0, stream, args);
     }
     void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32};
-    return mynah_launch(d, tokens == 1 ? MYNAH_K_Q40_CHAIN1 : MYNAH_K_Q40_CHAIN8, grid,
-                        (unsigned)groups, 64, 0, stream, args);
+    const int k = per == 1 ? MYNAH_K_Q40_CHAIN1 : per == 2 ? MYNAH_K_Q40_CHAIN2
+                : per == 4 ? MYNAH_K_Q40_CHAIN4 : MYNAH_K_Q40_CHAIN8;
+    return mynah_launch(d, k, grid, (unsigned)groups, 64, 0, stream, args);
 }
 
 int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t rows, size_t cols,

@@ -17,6 +17,8 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_Q5K_GEMM, "mynah_q5k_gemm_exact")        \
     X(MYNAH_K_Q5K_GEMM_MV, "mynah_q5k_gemm_mv")        \
     X(MYNAH_K_Q40_CHAIN1, "mynah_q40_chain1")          \
+    X(MYNAH_K_Q40_CHAIN2, "mynah_q40_chain2")          \
+    X(MYNAH_K_Q40_CHAIN4, "mynah_q40_chain4")          \
     X(MYNAH_K_Q40_CHAIN8, "mynah_q40_chain8")          \
     X(MYNAH_K_Q40_CHAIN_PC, "mynah_q40_chain_pc")      \
     X(MYNAH_K_Q6K_GEMM, "mynah_q6k_gemm_exact")        \

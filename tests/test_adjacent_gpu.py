@@ -82,7 +82,10 @@ def test_q40_one_wave_matvec_against_oracle(M, monkeypatch, cols):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,tokens", [(13, 1024, 2048, 130), (13, 70, 512, 2),
-                                                    (2, 512, 2080, 64), (2, 33, 4096, 9)])
+                                                    (2, 512, 2080, 64), (2, 33, 4096, 9),
+                                                    # Q4_0 token chains per lane: 8, 4 (ragged), 4
+                                                    (2, 4096, 64, 256), (2, 4100, 64, 130),
+                                                    (2, 4096, 96, 128)])
 def test_matmat_against_oracle(M, qtype, rows, cols, tokens):
     print(f"[case] matmat type={qtype} {rows}x{cols} tokens={tokens}", flush=True)
     w, x = M.synth_blocks(qtype, 9, rows, cols), M.synth_normal(10, tokens * cols)
