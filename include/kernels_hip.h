@@ -47,8 +47,8 @@ extern "C" {
 int ingot_matvec(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output);
 /* quant.h:157-158. Exact f32 for every width unless the int8 lane is on
- * (mynah_hip_set_int8 below), which then takes Q4_K from two tokens up
- * (the reference's AVX2 build would also take Q5_K; here Q5_K stays exact). */
+ * (mynah_hip_set_int8 below), which then takes Q4_K and Q5_K from two tokens
+ * up, as the reference's AVX2 build does (kernels.c:1714-1751, 2573-2595). */
 int ingot_matmat(int type, const void *weights, size_t rows, size_t cols,
                  const float *input, float *output, size_t tokens);
 /* quant.h:159-160 — bit-identical to the reference decoders. */

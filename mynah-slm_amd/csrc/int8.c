@@ -1,10 +1,12 @@
-/* int8.c — host side of the int8 activation lane of Q4_K products
- * (int8.hip): the lane switch, the launches and the per-call workspace.
+/* int8.c — host side of the int8 activation lane of Q4_K products and of
+ * batched Q5_K products (int8.hip): the lane switch, the launches and the
+ * per-call workspace.
  *
  * The reference has this lane only in an AVX2 + FMA (or Arm dotprod) build of
  * ingot. There, INGOT_SDOT selects it (third_party/ingot/src/kernels.c:
  * 812-838 for the matvec, 1704-1721 for the batched form):
- *   - the batched Q4_K matmat (tokens >= 2) is int8 unless INGOT_SDOT=0;
+ *   - the batched Q4_K and Q5_K matmat (tokens >= 2) is int8 unless
+ *     INGOT_SDOT=0 (kernels.c:1742-1751, 2573-2595);
  *   - the Q4_K matvec is int8 only with INGOT_SDOT=1;
  *   - ingot_matmat_is_exact(tokens) says which path a width takes.
  * The as-built reference (ingot's -O2, no -march) has no int8 lane, and this
@@ -58,16 +60,24 @@ static uint32_t token_tile(size_t cols) {
     return (uint32_t)tile;
 }
 
-static int check_q4k(const void *w, size_t rows, size_t cols, size_t tokens) {
+static int check_kq(int type, const void *w, size_t rows, size_t cols, size_t tokens) {
     size_t rb;
-    if (mynah_geometry(MYNAH_Q4_K, rows, cols, &rb) != 0) return -1;
+    if (type != MYNAH_Q4_K && type != MYNAH_Q5_K) {
+        mynah_set_error("the int8 lane takes Q4_K and Q5_K only");
+        return -1;
+    }
+    if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
     if (tokens == 0 || tokens > 0xffffffffu || rows > 0xffffffffu ||
         tokens > SIZE_MAX / cols || cols / 256 > 0xffffffffu / tokens) {
         mynah_set_error("bad token count");
         return -1;
     }
     if (((uintptr_t)w & 15u) != 0) {
-        mynah_set_error("Q4_K weights must be 16-byte aligned");
+        mynah_set_error("Q4_K / Q5_K weights must be 16-byte aligned");
+        return -1;
+    }
+    if (type == MYNAH_Q5_K && tokens < 2) {
+        mynah_set_error("Q5_K has no int8 matvec (the reference's lane is batched only)");
         return -1;
     }
     return 0;
@@ -95,14 +105,14 @@ int mynah_q8_quantize_launch(mynah_device *d, const float *x, size_t tokens, siz
     return mynah_launch(d, MYNAH_K_Q8_QUANTIZE, (units + 3u) / 4u, 1, 256, 0, stream, args);
 }
 
-int mynah_q4k_int8_launch(mynah_device *d, const void *w, size_t rows, size_t cols,
+int mynah_q4k_int8_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                           const int8_t *xq, const float *xs, const int32_t *xsum, float *y,
                           size_t tokens, hipStream_t stream) {
     if (w == NULL || xq == NULL || xs == NULL || xsum == NULL || y == NULL) {
         mynah_set_error("null argument");
         return -1;
     }
-    if (check_q4k(w, rows, cols, tokens) != 0) return -1;
+    if (check_kq(type, w, rows, cols, tokens) != 0) return -1;
     if (((uintptr_t)xq & 15u) != 0 || ((uintptr_t)xsum & 15u) != 0 || ((uintptr_t)xs & 3u) != 0) {
         mynah_set_error("int8 operands must be 16-byte aligned");
         return -1;
@@ -128,8 +138,10 @@ int mynah_q4k_int8_launch(mynah_device *d, const void *w, size_t rows, size_t co
         tr = env[0] - '0';
         tt = env[1] - '0';
     }
-    const int k = tr == 1 ? (tt == 1 ? MYNAH_K_Q4K_GEMM_INT8_11 : MYNAH_K_Q4K_GEMM_INT8_12)
-                          : (tt == 1 ? MYNAH_K_Q4K_GEMM_INT8_21 : MYNAH_K_Q4K_GEMM_INT8_22);
+    if (type == MYNAH_Q5_K) tr = tt = 2;      /* the one Q5_K tile */
+    const int k = type == MYNAH_Q5_K ? MYNAH_K_Q5K_GEMM_INT8_22
+                  : tr == 1 ? (tt == 1 ? MYNAH_K_Q4K_GEMM_INT8_11 : MYNAH_K_Q4K_GEMM_INT8_12)
+                            : (tt == 1 ? MYNAH_K_Q4K_GEMM_INT8_21 : MYNAH_K_Q4K_GEMM_INT8_22);
     const size_t wr = (size_t)32 * tr, wt = (size_t)32 * tt;
     return mynah_launch(d, k, (unsigned)((rows + wr - 1) / wr), (unsigned)((tokens + wt - 1) / wt),
                         256, 0, stream, args);
@@ -146,9 +158,9 @@ static size_t ws_bytes(size_t tokens, size_t cols, size_t *o_xs, size_t *o_sum) 
     return off;
 }
 
-int mynah_int8_product(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
-                       float *y, size_t tokens, hipStream_t stream) {
-    if (check_q4k(w, rows, cols, tokens) != 0) return -1;
+int mynah_int8_product(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                       const float *x, float *y, size_t tokens, hipStream_t stream) {
+    if (check_kq(type, w, rows, cols, tokens) != 0) return -1;
     if (tokens > (SIZE_MAX / 2) / cols) {
         mynah_set_error("size overflow");
         return -1;
@@ -167,7 +179,7 @@ int mynah_int8_product(mynah_device *d, const void *w, size_t rows, size_t cols,
     int rc = mynah_q8_quantize_launch(d, x, tokens, cols, (int8_t *)ws, (float *)(ws + o_xs),
                                       (int32_t *)(ws + o_sum), stream);
     if (rc == 0)
-        rc = mynah_q4k_int8_launch(d, w, rows, cols, (const int8_t *)ws,
+        rc = mynah_q4k_int8_launch(d, type, w, rows, cols, (const int8_t *)ws,
                                    (const float *)(ws + o_xs), (const int32_t *)(ws + o_sum), y,
                                    tokens, stream);
     e = hipFreeAsync(ws, stream);
@@ -193,6 +205,6 @@ int mynah_hip_q4k_int8_dev(const void *w, size_t rows, size_t cols, const int8_t
                            void *stream) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;
-    return mynah_q4k_int8_launch(d, w, rows, cols, xq, xs, xsum, y, tokens,
+    return mynah_q4k_int8_launch(d, MYNAH_Q4_K, w, rows, cols, xq, xs, xsum, y, tokens,
                                  mynah_stream_or_default(d, stream));
 }

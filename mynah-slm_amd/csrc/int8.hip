@@ -164,24 +164,34 @@ extern "C" __global__ __launch_bounds__(256) void mynah_q4k_gemv_int8(
 // super-block into LDS (double buffered: one barrier per super-block), and
 // the next super-block's operands are fetched while the current one is
 // summed. The dots of sub-block j + 1 are issued before the epilogue of j.
+// Q5_K (FMT 13, kernels.c:1155-1185 q5_k_quants): the same tiles, the quant
+// bytes at block offset 48 instead of 16, and each lane also holds the 8 qh
+// bytes of its 8 positions: bit j of qh[i] is the fifth bit (+16) of weight
+// i of sub-block j.
 template <int GI_TR, int GI_TT>
 struct GiOps {
     unsigned long long a[GI_TR][4];   // quant bytes of group g of each row tile
+    unsigned long long h[GI_TR];      // Q5_K: the qh bytes of this lane's positions
     unsigned long long q[GI_TT][8];   // activations of sub-block j of each token tile
     int4 s[GI_TT][2];                 // the 8 sub-block sums of each token tile
     float xs[GI_TT];                  // activation scale of each token tile
     uint4 hdr;                        // the header this thread stages
 };
 
-template <int GI_TR, int GI_TT>
+template <int FMT, int GI_TR, int GI_TT>
 MYNAH_DEV void gi_load(GiOps<GI_TR, GI_TT> &o, const uint8_t *const *arow, const int8_t *const *btok,
                        const float *const *xsp, const int32_t *const *xsump,
                        const uint8_t *hrow, uint32_t b) {
+    constexpr uint32_t UB = FMT == 13 ? 176u : 144u;
 #pragma unroll
-    for (int i = 0; i < GI_TR; i++)
+    for (int i = 0; i < GI_TR; i++) {
 #pragma unroll
         for (int g = 0; g < 4; g++)
-            o.a[i][g] = *(const unsigned long long *)(arow[i] + (size_t)b * 144u + 32u * g);
+            o.a[i][g] = *(const unsigned long long *)(arow[i] + (size_t)b * UB + 32u * g);
+        // arow points at the lane's quant bytes (block + 48 + 8 lk); its qh
+        // bytes sit 32 bytes before them.
+        if (FMT == 13) o.h[i] = *(const unsigned long long *)(arow[i] + (size_t)b * UB - 32u);
+    }
 #pragma unroll
     for (int k = 0; k < GI_TT; k++) {
 #pragma unroll
@@ -191,7 +201,7 @@ MYNAH_DEV void gi_load(GiOps<GI_TR, GI_TT> &o, const uint8_t *const *arow, const
         o.s[k][1] = ((const int4 *)(xsump[k] + 8u * b))[1];
         o.xs[k] = xsp[k][b];
     }
-    o.hdr = *(const uint4 *)(hrow + (size_t)b * 144u);
+    o.hdr = *(const uint4 *)(hrow + (size_t)b * UB);
 }
 
 // Scale and offset of sub-blocks hj, hj + 1 of the staged row, into LDS.
@@ -208,12 +218,13 @@ MYNAH_DEV void gi_stage(float *buf, const uint4 hdr, uint32_t hj, uint32_t row) 
     buf[(9u + hj) * GI_ROWS + row] = dmin * (float)m1;
 }
 
-template <int GI_TR, int GI_TT>
+template <int FMT, int GI_TR, int GI_TT>
 MYNAH_DEV void gi_dots(i32x4 (&dt)[GI_TR][GI_TT], const GiOps<GI_TR, GI_TT> &o, int j) {
 #pragma unroll
     for (int i = 0; i < GI_TR; i++) {
-        const unsigned long long q =
+        unsigned long long q =
             ((j & 1) ? (o.a[i][j >> 1] >> 4) : o.a[i][j >> 1]) & 0x0f0f0f0f0f0f0f0full;
+        if (FMT == 13) q |= ((o.h[i] >> j) & 0x0101010101010101ull) << 4;
 #pragma unroll
         for (int k = 0; k < GI_TT; k++) {
             const i32x4 zero = {0, 0, 0, 0};
@@ -225,7 +236,7 @@ MYNAH_DEV void gi_dots(i32x4 (&dt)[GI_TR][GI_TT], const GiOps<GI_TR, GI_TT> &o, 
 
 // One super-block's epilogue: tot[i][k][e] over j = 0..7. MIXED: some lane
 // has a token outside the groups of four, which takes the plain form.
-template <bool MIXED, int GI_TR, int GI_TT>
+template <int FMT, bool MIXED, int GI_TR, int GI_TT>
 MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT> &o,
                         const float4 *sbuf,
                         uint32_t wr, uint32_t lk, const bool (&fma_path)[GI_TT]) {
@@ -247,10 +258,10 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT>
 #pragma unroll
             for (int e = 0; e < 4; e++) tot[i][k][e] = 0.0f;
     i32x4 cur[GI_TR][GI_TT], nxt[GI_TR][GI_TT];
-    gi_dots(cur, o, 0);
+    gi_dots<FMT>(cur, o, 0);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        if (j < 7) gi_dots(nxt, o, j + 1);
+        if (j < 7) gi_dots<FMT>(nxt, o, j + 1);
 #pragma unroll
         for (int i = 0; i < GI_TR; i++) {
             const uint32_t slot = (16u * (GI_TR * wr + i)) / 4u + lk;
@@ -289,7 +300,7 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT>
             for (int e = 0; e < 4; e++) acc[i][k][e] = acc[i][k][e] + tot[i][k][e] * o.xs[k];
 }
 
-template <int GI_TR, int GI_TT>
+template <int FMT, int GI_TR, int GI_TT>
 MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,
                          const float *__restrict__ xs, const int32_t *__restrict__ xsum,
                          float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens,
@@ -299,7 +310,7 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wr = wave & 1u, wt = wave >> 1;
     const uint32_t R0 = blockIdx.x * GI_ROWS, T0 = blockIdx.y * GI_TOK;
-    const size_t rb = (size_t)nb * 144u;
+    const size_t rb = (size_t)nb * (FMT == 13 ? 176u : 144u);
     const uint32_t lm = lane & 15u, lk = lane >> 4;
 
     // Operand rows and tokens of this lane (clamped for loads; stores check).
@@ -314,7 +325,7 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
     for (int i = 0; i < GI_TR; i++) {
         uint32_t r = R0 + 16u * (GI_TR * wr + i) + lm;
         r = r < rows ? r : rows - 1u;
-        arow[i] = w + (size_t)r * rb + 16u + 8u * lk;
+        arow[i] = w + (size_t)r * rb + (FMT == 13 ? 48u : 16u) + 8u * lk;
     }
 #pragma unroll
     for (int k = 0; k < GI_TT; k++) {
@@ -347,14 +358,14 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
             for (int e = 0; e < 4; e++) acc[i][k][e] = 0.0f;
 
     GiOps<GI_TR, GI_TT> cur, nxt;
-    gi_load(cur, arow, btok, xsp, xsump, hrow, 0);
+    gi_load<FMT>(cur, arow, btok, xsp, xsump, hrow, 0);
     if (stager) gi_stage<GI_ROWS>((float *)so[0], cur.hdr, hj, srow);
     __syncthreads();
     for (uint32_t b = 0; b < nb; b++) {
         const bool more = b + 1u < nb;
-        if (more) gi_load(nxt, arow, btok, xsp, xsump, hrow, b + 1u);
-        if (mixed) gi_block<true>(acc, cur, so[b & 1u], wr, lk, fma_path);
-        else gi_block<false>(acc, cur, so[b & 1u], wr, lk, fma_path);
+        if (more) gi_load<FMT>(nxt, arow, btok, xsp, xsump, hrow, b + 1u);
+        if (mixed) gi_block<FMT, true>(acc, cur, so[b & 1u], wr, lk, fma_path);
+        else gi_block<FMT, false>(acc, cur, so[b & 1u], wr, lk, fma_path);
         if (more && stager) gi_stage<GI_ROWS>((float *)so[(b + 1u) & 1u], nxt.hdr, hj, srow);
         __syncthreads();
         if (more) cur = nxt;
@@ -374,15 +385,16 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
         }
 }
 
-#define GEMM_INT8(TR, TT)                                                                    \
-    extern "C" __global__ __launch_bounds__(256) void mynah_q4k_gemm_int8_##TR##TT(          \
+#define GEMM_INT8(NAME, FMT, TR, TT)                                                         \
+    extern "C" __global__ __launch_bounds__(256) void NAME##_##TR##TT(                       \
         const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,                        \
         const float *__restrict__ xs, const int32_t *__restrict__ xsum,                      \
         float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t nb,   \
         uint32_t tile) {                                                                     \
-        gemm_int8<TR, TT>(w, xq, xs, xsum, y, rows, cols, tokens, nb, tile);                 \
+        gemm_int8<FMT, TR, TT>(w, xq, xs, xsum, y, rows, cols, tokens, nb, tile);            \
     }
-GEMM_INT8(1, 1)
-GEMM_INT8(1, 2)
-GEMM_INT8(2, 1)
-GEMM_INT8(2, 2)
+GEMM_INT8(mynah_q4k_gemm_int8, 12, 1, 1)
+GEMM_INT8(mynah_q4k_gemm_int8, 12, 1, 2)
+GEMM_INT8(mynah_q4k_gemm_int8, 12, 2, 1)
+GEMM_INT8(mynah_q4k_gemm_int8, 12, 2, 2)
+GEMM_INT8(mynah_q5k_gemm_int8, 13, 2, 2)

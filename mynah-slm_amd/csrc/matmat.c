@@ -17,11 +17,12 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
                         const float *x, float *y, size_t tokens, int exact, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
-    /* The batched Q4_K product takes the int8 lane when it is on, exactly
-     * where the reference's does (kernels.c:1723-1751; only Q4_K of the
-     * types here, tokens >= 2). */
-    if (!exact && type == MYNAH_Q4_K && tokens >= 2 && mynah_int8_mode() != MYNAH_INT8_OFF)
-        return mynah_int8_product(d, w, rows, cols, x, y, tokens, stream);
+    /* The batched Q4_K and Q5_K products take the int8 lane when it is on,
+     * exactly where the reference's do (kernels.c:1723-1751, 2573-2595;
+     * tokens >= 2). */
+    if (!exact && (type == MYNAH_Q4_K || type == MYNAH_Q5_K) && tokens >= 2 &&
+        mynah_int8_mode() != MYNAH_INT8_OFF)
+        return mynah_int8_product(d, type, w, rows, cols, x, y, tokens, stream);
     /* Q4_0 has no batched kernel in the reference: its generic path runs the
      * matvec's chain per token (generic.c:76-93), and so does this one. */
     if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, tokens, stream);

@@ -183,7 +183,7 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     /* INGOT_SDOT=1 semantics: the Q4_K matvec quantises its input
      * (third_party/ingot/src/kernels.c:819-834). */
     if (type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
-        return mynah_int8_product(d, w, rows, cols, x, y, 1, stream);
+        return mynah_int8_product(d, MYNAH_Q4_K, w, rows, cols, x, y, 1, stream);
     if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, 1, stream);
     if (type != MYNAH_Q8_0 && cols % 256 != 0) {
         mynah_set_error("cols must be a multiple of 256");
@@ -654,7 +654,7 @@ static int host_call(host_op op, int type, const void *w, size_t rows, size_t co
     }
     if (op == OP_MATVEC) rc = mynah_gemv_launch(d, type, wd, rows, cols, (const float *)stage_x,
                                                 (float *)stage_y, s);
-    else if (op == OP_MATVEC_INT8) rc = mynah_int8_product(d, wd, rows, cols,
+    else if (op == OP_MATVEC_INT8) rc = mynah_int8_product(d, MYNAH_Q4_K, wd, rows, cols,
                                                            (const float *)stage_x,
                                                            (float *)stage_y, 1, s);
     else if (op == OP_MATMAT || op == OP_MATMAT_EXACT)

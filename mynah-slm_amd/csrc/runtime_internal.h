@@ -52,7 +52,8 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_Q4K_GEMM_INT8_11, "mynah_q4k_gemm_int8_11") \
     X(MYNAH_K_Q4K_GEMM_INT8_12, "mynah_q4k_gemm_int8_12") \
     X(MYNAH_K_Q4K_GEMM_INT8_21, "mynah_q4k_gemm_int8_21") \
-    X(MYNAH_K_Q4K_GEMM_INT8_22, "mynah_q4k_gemm_int8_22")
+    X(MYNAH_K_Q4K_GEMM_INT8_22, "mynah_q4k_gemm_int8_22") \
+    X(MYNAH_K_Q5K_GEMM_INT8_22, "mynah_q5k_gemm_int8_22")
 
 enum {
 #define X(id, name) id,
@@ -109,11 +110,12 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
 int mynah_int8_mode(void);
 int mynah_q8_quantize_launch(mynah_device *d, const float *x, size_t tokens, size_t cols,
                              int8_t *xq, float *xs, int32_t *xsum, hipStream_t stream);
-int mynah_q4k_int8_launch(mynah_device *d, const void *w, size_t rows, size_t cols,
+int mynah_q4k_int8_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                           const int8_t *xq, const float *xs, const int32_t *xsum, float *y,
                           size_t tokens, hipStream_t stream);
-int mynah_int8_product(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
-                       float *y, size_t tokens, hipStream_t stream);
+/* type: Q4_K (any token count) or Q5_K (tokens >= 2, the batched lane only). */
+int mynah_int8_product(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                       const float *x, float *y, size_t tokens, hipStream_t stream);
 
 /* Host mirror of the grouped exact GEMV launch (gemv_exact.hip GemvGroup). */
 #define MYNAH_GROUP_MAX 8

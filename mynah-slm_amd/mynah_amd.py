@@ -241,8 +241,8 @@ INT8_OFF, INT8_BATCHED, INT8_ALL = 0, 1, 2
 
 
 def set_int8(mode: int) -> None:
-    """The int8 activation lane of Q4_K products (INT8_OFF, INT8_BATCHED,
-    INT8_ALL)."""
+    """The int8 activation lane (INT8_OFF, INT8_BATCHED, INT8_ALL): batched
+    Q4_K and Q5_K products, and with INT8_ALL also the Q4_K matvec."""
     check(lib.mynah_hip_set_int8(mode), "set_int8")
 
 

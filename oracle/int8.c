@@ -68,6 +68,24 @@ int32_t orc_q4k_int8_dot(const unsigned char *blk, const int8_t *xq, int j) {
     return d;
 }
 
+/* q5_k_quants (kernels.c:1155-1185): sub-block j's 32 quants are the nibbles
+ * of bytes 48 + 32 * (j / 2) .. (low for j even, high for j odd) plus 16
+ * when bit j of qh[i] (bytes 16 ..) is set. */
+int32_t orc_q5k_int8_dot(const unsigned char *blk, const int8_t *xq, int j) {
+    int32_t d = 0;
+    for (int i = 0; i < 32; i++) {
+        const unsigned char b = blk[48 + 32 * (j / 2) + i];
+        const uint32_t q = ((j & 1) ? (uint32_t)(b >> 4) : (uint32_t)(b & 15u)) +
+                           ((uint32_t)((blk[16 + i] >> j) & 1u) << 4);
+        d += (int32_t)q * (int32_t)xq[32 * j + i];
+    }
+    return d;
+}
+
+static int32_t kq_int8_dot(int type, const unsigned char *blk, const int8_t *xq, int j) {
+    return type == ORC_Q5_K ? orc_q5k_int8_dot(blk, xq, j) : orc_q4k_int8_dot(blk, xq, j);
+}
+
 /* kernels.c:712-739 (q4_k_dot_block_x86): per group, the low then the high
  * sub-block: total += (d * sc) * dot - (dmin * m) * sum; times the
  * activation scale. */
@@ -129,13 +147,13 @@ static size_t token_tile(size_t cols) {
  * super-block's total times the activation scale is added to the output.
  * tokens == 1 is the matvec (kernels.c:1726), which with INGOT_SDOT=1 is the
  * int8 matvec above (kernels.c:819-834). */
-int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
-                        size_t tokens) {
-    if (tokens == 1) return orc_q4k_matvec_int8(w, rows, cols, x, y);
+static int kq_matmat_int8(int type, const void *w, size_t rows, size_t cols, const float *x,
+                          float *y, size_t tokens) {
     if (w == NULL || x == NULL || y == NULL || rows == 0 || cols == 0 || tokens == 0 ||
         cols % QK != 0)
         return -1;
-    const size_t nb = cols / QK, rb = nb * 144;
+    const size_t ub = type == ORC_Q5_K ? 176 : 144;
+    const size_t nb = cols / QK, rb = nb * ub;
     int8_t *q = malloc(tokens * cols);
     float *xs = malloc(nb * tokens * sizeof *xs);
     float *xsum = malloc(nb * 8 * tokens * sizeof *xsum);
@@ -157,7 +175,7 @@ int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x,
             const size_t cnt = tokens - t0 < tile ? tokens - t0 : tile;
             for (size_t t = 0; t < cnt; t++) acc[t] = 0.0f;
             for (size_t b = 0; b < nb; b++) {
-                const unsigned char *blk = base + r * rb + b * 144;
+                const unsigned char *blk = base + r * rb + b * ub;
                 const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
                 const float dmin = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
                 float scale[8], offset[8];
@@ -173,7 +191,7 @@ int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x,
                         const size_t tt = t0 + t + k;
                         float total = 0.0f;
                         for (int j = 0; j < 8; j++) {
-                            const float dot = (float)orc_q4k_int8_dot(blk, q + tt * cols + b * QK, j);
+                            const float dot = (float)kq_int8_dot(type, blk, q + tt * cols + b * QK, j);
                             total = fmaf(dot, scale[j], total);
                             total = fmaf(-xsum[(b * 8 + (size_t)j) * tokens + tt], offset[j], total);
                         }
@@ -183,7 +201,7 @@ int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x,
                     const size_t tt = t0 + t;
                     float total = 0.0f;
                     for (int j = 0; j < 8; j++) {
-                        const float dot = (float)orc_q4k_int8_dot(blk, q + tt * cols + b * QK, j);
+                        const float dot = (float)kq_int8_dot(type, blk, q + tt * cols + b * QK, j);
                         total += scale[j] * dot - offset[j] * xsum[(b * 8 + (size_t)j) * tokens + tt];
                     }
                     acc[t] += total * xs[b * tokens + tt];
@@ -194,4 +212,18 @@ int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x,
     }
     free(q); free(xs); free(xsum); free(acc);
     return 0;
+}
+
+int orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                        size_t tokens) {
+    if (tokens == 1) return orc_q4k_matvec_int8(w, rows, cols, x, y);
+    return kq_matmat_int8(ORC_Q4_K, w, rows, cols, x, y, tokens);
+}
+
+/* Q5_K through the same batched lane (kernels.c:2573-2595); its matvec has no
+ * int8 form (tokens == 1 is the exact matvec, kernels.c:2576-2577). */
+int orc_q5k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                        size_t tokens) {
+    if (tokens == 1) return orc_matvec(ORC_Q5_K, w, rows, cols, x, y);
+    return kq_matmat_int8(ORC_Q5_K, w, rows, cols, x, y, tokens);
 }

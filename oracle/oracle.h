@@ -58,8 +58,11 @@ int  orc_matmat_mt(int type, const void *w, size_t rows, size_t cols,
 float   orc_q8_quantize_block(const float *x, int8_t *q, int32_t sums[8]);
 /* Integer dot of sub-block j (0..7) of one Q4_K block with the quants. */
 int32_t orc_q4k_int8_dot(const unsigned char *blk, const int8_t *xq, int j);
+int32_t orc_q5k_int8_dot(const unsigned char *blk, const int8_t *xq, int j);
 int     orc_q4k_matvec_int8(const void *w, size_t rows, size_t cols, const float *x, float *y);
 int     orc_q4k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
+                            size_t tokens);
+int     orc_q5k_matmat_int8(const void *w, size_t rows, size_t cols, const float *x, float *y,
                             size_t tokens);
 
 /* ── Qwen3 decoder restatement (src/arch_qwen3.c:178-252) ───────────────── */

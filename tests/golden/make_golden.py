@@ -27,7 +27,8 @@ records a SHA-256 of the input bytes so generator drift is detected):
   int8.npz           the int8 activation lane of an AVX2 + FMA build of ingot
                      (oracle/_ref/libref_int8.so, INGOT_SDOT=1): Q4_K matvec
                      and batched outputs, incl. round-half-even ties, an
-                     all-zero block and token counts around the token tile
+                     all-zero block and token counts around the token tile,
+                     and Q5_K batched outputs
                      (`--only int8` writes just this file)
 """
 from __future__ import annotations
@@ -106,6 +107,9 @@ def golden_adjacent(ref) -> None:
 
 
 INT8_MATVEC = ((37, 512), (64, 3072))
+# Q5_K on the int8 lane (batched only): token counts across the tile and the
+# groups of four, ragged rows.
+INT8_Q5K_MATMAT = ((40, 2048, 70), (9, 512, 130), (24, 1024, 5), (3, 256, 2))
 INT8_MATMAT = ((16, 2048, 16), (24, 2048, 70), (9, 512, 130), (8, 6144, 5), (4, 9728, 110),
                (5, 512, 2), (3, 256, 3), (6, 1024, 1))
 
@@ -142,6 +146,14 @@ def golden_int8(ref8) -> None:
         w, x = O.blocks(CF.Q4_K, 800 + rows, rows, cols), O.normal(900 + tokens, tokens * cols)
         y = np.empty(rows * tokens, np.float32)
         assert ref8.ingot_q4_k_matmat(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+        out[f"{key}_y"] = y
+        out[f"{key}_w_sha"] = np.array(sha(w))
+        out[f"{key}_x_sha"] = np.array(sha(x))
+    for rows, cols, tokens in INT8_Q5K_MATMAT:
+        key = f"q5k_mm_{rows}x{cols}_t{tokens}"
+        w, x = O.blocks(CF.Q5_K, 1100 + rows, rows, cols), O.normal(1200 + tokens, tokens * cols)
+        y = np.empty(rows * tokens, np.float32)
+        assert ref8.ingot_q5_k_matmat(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
         out[f"{key}_y"] = y
         out[f"{key}_w_sha"] = np.array(sha(w))
         out[f"{key}_x_sha"] = np.array(sha(x))

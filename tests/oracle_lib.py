@@ -87,8 +87,10 @@ def _load_oracle() -> C.CDLL:
         "orc_argmax": (C.c_uint32, [_P, _SZ]),
         "orc_q8_quantize_block": (C.c_float, [_P, _P, _P]),
         "orc_q4k_int8_dot": (C.c_int32, [_P, _P, C.c_int]),
+        "orc_q5k_int8_dot": (C.c_int32, [_P, _P, C.c_int]),
         "orc_q4k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
         "orc_q4k_matmat_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "orc_q5k_matmat_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
         "mynah_synth_normal": (C.c_int, [C.c_uint64, _SZ, C.c_float, C.c_float, _P, C.c_int]),
         "mynah_synth_uniform_u32": (C.c_int, [C.c_uint64, _SZ, C.c_uint32, _P]),
@@ -165,6 +167,7 @@ def load_ref_int8():
         "ingot_q4_k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
         "ingot_q4_k_matmat": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
+        "ingot_q5_k_matmat": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_matmat_is_exact": (C.c_int, [_SZ]),
     }
     for name, (res, args) in sig.items():

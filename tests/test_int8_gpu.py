@@ -1,4 +1,4 @@
-"""GPU parity of the int8 activation lane of Q4_K products (int8.hip).
+"""GPU parity of the int8 activation lane of Q4_K and Q5_K products (int8.hip).
 
 Bar: BIT-IDENTICAL outputs to the oracle's int8 restatement, which is itself
 bit-identical to an AVX2 + FMA build of the reference's own sources
@@ -46,6 +46,12 @@ def say(*a):
 def orc_matmat_int8(w, rows, cols, x, tokens):
     y = np.empty(rows * tokens, np.float32)
     assert O.orc.orc_q4k_matmat_int8(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+    return y
+
+
+def orc_q5k_matmat_int8(w, rows, cols, x, tokens):
+    y = np.empty(rows * tokens, np.float32)
+    assert O.orc.orc_q5k_matmat_int8(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
     return y
 
 
@@ -144,6 +150,20 @@ def test_matmat_int8_golden(M, gold, rows, cols, tokens):
     np.testing.assert_array_equal(bits(got), bits(gold[f"mm_{rows}x{cols}_t{tokens}_y"]))
 
 
+@pytest.mark.parametrize("rows,cols,tokens", [(40, 2048, 70), (9, 512, 130), (24, 1024, 5),
+                                              (3, 256, 2)])
+def test_q5k_matmat_int8_golden(M, gold, rows, cols, tokens):
+    say("golden q5k matmat", rows, cols, tokens)
+    w = M.synth_blocks(CF.Q5_K, 1100 + rows, rows, cols)
+    x = M.synth_normal(1200 + tokens, tokens * cols)
+    M.set_int8(M.INT8_BATCHED)
+    try:
+        got = M.matmat(CF.Q5_K, w, rows, cols, x, tokens)
+    finally:
+        M.set_int8(M.INT8_OFF)
+    np.testing.assert_array_equal(bits(got), bits(gold[f"q5k_mm_{rows}x{cols}_t{tokens}_y"]))
+
+
 # ── larger shapes against the oracle ───────────────────────────────────────
 
 @pytest.mark.parametrize("rows,cols", [(1024, 3072), (333, 1024), (2560, 9728), (9728, 2560)])
@@ -165,6 +185,46 @@ def test_matmat_int8_against_oracle(M, rows, cols, tokens):
     finally:
         M.set_int8(M.INT8_OFF)
     np.testing.assert_array_equal(bits(got), bits(orc_matmat_int8(w, rows, cols, x, tokens)))
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(100, 2048, 70), (2048, 2048, 512), (77, 9728, 213),
+                                              (1027, 4096, 33)])
+def test_q5k_matmat_int8_against_oracle(M, rows, cols, tokens):
+    say("q5k matmat int8", rows, cols, tokens)
+    w, x = M.synth_blocks(CF.Q5_K, 77, rows, cols), M.synth_normal(78, tokens * cols)
+    M.set_int8(M.INT8_BATCHED)
+    try:
+        got = M.matmat(CF.Q5_K, w, rows, cols, x, tokens)
+    finally:
+        M.set_int8(M.INT8_OFF)
+    np.testing.assert_array_equal(bits(got), bits(orc_q5k_matmat_int8(w, rows, cols, x, tokens)))
+
+
+def test_q5k_lane_modes(M):
+    """Q5_K: the batched product follows the lane; the matvec, the one-token
+    product and the explicit exact entry stay exact in every mode."""
+    rows, cols, tokens = 48, 1024, 9
+    say("q5k modes", rows, cols, tokens)
+    w, x = M.synth_blocks(CF.Q5_K, 85, rows, cols), M.synth_normal(86, tokens * cols)
+    exact = np.empty(rows * tokens, np.float32)
+    assert O.orc.orc_matmat(CF.Q5_K, O.ptr(w), rows, cols, O.ptr(x), O.ptr(exact), tokens) == 0
+    exact_mv = np.empty(rows, np.float32)
+    assert O.orc.orc_matvec(CF.Q5_K, O.ptr(w), rows, cols, O.ptr(x), O.ptr(exact_mv)) == 0
+    int8 = orc_q5k_matmat_int8(w, rows, cols, x, tokens)
+    assert not np.array_equal(bits(int8), bits(exact))
+    y = np.empty(rows * tokens, np.float32)
+    try:
+        for mode in (M.INT8_OFF, M.INT8_BATCHED, M.INT8_ALL):
+            M.set_int8(mode)
+            want = exact if mode == M.INT8_OFF else int8
+            assert np.array_equal(bits(M.matmat(CF.Q5_K, w, rows, cols, x, tokens)), bits(want))
+            assert np.array_equal(bits(M.matvec(CF.Q5_K, w, rows, cols, x)), bits(exact_mv))
+            assert np.array_equal(bits(M.matmat(CF.Q5_K, w, rows, cols, x, 1)), bits(exact_mv))
+            M.check(M.lib.ingot_q5_k_matmat_exact(M.ptr(w), rows, cols, M.ptr(x), M.ptr(y),
+                                                  tokens), "q5_k_matmat_exact")
+            assert np.array_equal(bits(y), bits(exact))
+    finally:
+        M.set_int8(M.INT8_OFF)
 
 
 def test_device_twin_int8(M):

@@ -1,8 +1,8 @@
 """CPU tests of the oracle's int8 activation lane (oracle/int8.c).
 
 The reference's int8 lane (third_party/ingot/src/kernels.c:636-788 for the
-matvec, 1120-1751 for the batched form) exists only in an AVX2 + FMA build of
-ingot. The restatement is pinned by:
+Q4_K matvec, 1120-1751 for the batched form, which Q5_K also takes through
+kernels.c:2573-2595) exists only in an AVX2 + FMA build of ingot. The restatement is pinned by:
   * golden vectors written by such a build of the reference's own sources
     (tests/golden/int8.npz, tests/golden/make_golden.py --only int8), matched
     bit for bit, including round-half-even ties, an all-zero block and token
@@ -53,6 +53,12 @@ def orc_matmat_int8(w, rows, cols, x, tokens):
     return y
 
 
+def orc_q5k_matmat_int8(w, rows, cols, x, tokens):
+    y = np.empty(rows * tokens, np.float32)
+    assert O.orc.orc_q5k_matmat_int8(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+    return y
+
+
 # ── golden vectors of the AVX2 reference build ─────────────────────────────
 
 @pytest.mark.parametrize("rows,cols", [(37, 512), (64, 3072)])
@@ -80,6 +86,20 @@ def test_matmat_int8_golden(gold, rows, cols, tokens):
     assert sha(x) == str(gold[f"{key}_x_sha"])
     np.testing.assert_array_equal(bits(orc_matmat_int8(w, rows, cols, x, tokens)),
                                   bits(gold[f"{key}_y"]))
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(40, 2048, 70), (9, 512, 130), (24, 1024, 5),
+                                              (3, 256, 2)])
+def test_q5k_matmat_int8_golden(gold, rows, cols, tokens):
+    key = f"q5k_mm_{rows}x{cols}_t{tokens}"
+    w, x = O.blocks(CF.Q5_K, 1100 + rows, rows, cols), O.normal(1200 + tokens, tokens * cols)
+    assert sha(w) == str(gold[f"{key}_w_sha"])
+    assert sha(x) == str(gold[f"{key}_x_sha"])
+    got = orc_q5k_matmat_int8(w, rows, cols, x, tokens)
+    np.testing.assert_array_equal(bits(got), bits(gold[f"{key}_y"]))
+    # The lane is not the exact product: a restatement that fell back to the
+    # exact order would still match nothing above but must not pass here.
+    assert not np.array_equal(bits(got), bits(O.matmat(CF.Q5_K, w, rows, cols, x, tokens)))
 
 
 # ── the quantiser ──────────────────────────────────────────────────────────
@@ -166,6 +186,35 @@ def test_matmat_int8_columns_equal_f64_epilogue():
         assert (np.abs(y[t] - want) / np.maximum(1.0, np.abs(want))).max() < 2e-5
 
 
+def _q5k_sub_quants(w, rows, cols):
+    """Q5_K quants 0..31 by an independent numpy unpacking: sub-block j of a
+    super-block takes nibble (j & 1) of qs bytes 32*(j//2) .. +32 and bit j of
+    the 32 qh bytes as its fifth bit."""
+    wb = w.view(np.uint8).reshape(rows, cols // 256, 176)
+    qh, qs = wb[:, :, 16:48], wb[:, :, 48:176]
+    out = np.empty((rows, cols // 256, 8, 32), np.int64)
+    for j in range(8):
+        nib = qs[:, :, 32 * (j // 2):32 * (j // 2) + 32]
+        nib = (nib >> 4) if j & 1 else (nib & 15)
+        out[:, :, j] = nib.astype(np.int64) + (((qh >> j) & 1).astype(np.int64) << 4)
+    return out
+
+
+def test_q5k_int8_dots_against_numpy_unpacking():
+    rows, cols = 4, 768
+    w, x = O.blocks(CF.Q5_K, 33, rows, cols), O.normal(34, cols)
+    q, _, _ = O.q8_quantize(x.reshape(1, -1))
+    quants = _q5k_sub_quants(w, rows, cols)
+    wb = w.view(np.uint8).reshape(rows, cols // 256, 176)
+    for r in range(rows):
+        for b in range(cols // 256):
+            for j in range(8):
+                want = int((quants[r, b, j] * q[0, 256 * b + 32 * j:256 * b + 32 * j + 32]
+                            .astype(np.int64)).sum())
+                assert O.orc.orc_q5k_int8_dot(wb[r, b].ctypes.data,
+                                              q[0, 256 * b:].ctypes.data, j) == want
+
+
 def test_int8_near_exact_matvec():
     """Quantising the activations costs ~1e-3 relative, not more."""
     rows, cols = 64, 2048
@@ -183,6 +232,7 @@ def test_int8_guards():
     assert O.orc.orc_q4k_matvec_int8(O.ptr(w), 2, 255, O.ptr(x), O.ptr(y)) == -1
     assert O.orc.orc_q4k_matvec_int8(O.ptr(w), 0, 256, O.ptr(x), O.ptr(y)) == -1
     assert O.orc.orc_q4k_matmat_int8(O.ptr(w), 2, 256, O.ptr(x), O.ptr(y), 0) == -1
+    assert O.orc.orc_q5k_matmat_int8(O.ptr(w), 2, 255, O.ptr(x), O.ptr(y), 2) == -1
 
 
 # ── the compiled AVX2 reference, where it was built ────────────────────────
@@ -197,3 +247,14 @@ def test_int8_against_compiled_reference(rows, cols, tokens):
     y = np.empty(rows * tokens, np.float32)
     assert ref8.ingot_q4_k_matmat(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
     np.testing.assert_array_equal(bits(orc_matmat_int8(w, rows, cols, x, tokens)), bits(y))
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(5, 1536, 4), (11, 768, 37), (2, 4096, 66)])
+def test_q5k_int8_against_compiled_reference(rows, cols, tokens):
+    ref8 = O.load_ref_int8()
+    if ref8 is None:
+        pytest.skip("oracle/_ref/libref_int8.so not built (needs /root/reference)")
+    w, x = O.blocks(CF.Q5_K, 53, rows, cols), O.normal(54, tokens * cols)
+    y = np.empty(rows * tokens, np.float32)
+    assert ref8.ingot_q5_k_matmat(O.ptr(w), rows, cols, O.ptr(x), O.ptr(y), tokens) == 0
+    np.testing.assert_array_equal(bits(orc_q5k_matmat_int8(w, rows, cols, x, tokens)), bits(y))
