@@ -600,6 +600,15 @@ MYNAH_DEV void embed_group(const uint8_t *__restrict__ table, uint32_t token, fl
             const uint32_t q = ((j & 1u) ? (b >> 4) : (b & 15u)) + (((blk[16 + i] >> j) & 1u) << 4);
             dst[i] = a * (float)q - o;
         }
+    } else if (type == 2u) {
+        // Q4_0 (kernels.c:2353-2360): d f16 @0, qs[16] @2; weight i is the low
+        // nibble of qs[i] minus 8, weight i + 16 the high nibble minus 8.
+        const uint8_t *blk = row + c * 18u;
+        const float dd = f16_to_f32(blk[0] | (blk[1] << 8));
+        for (int i = 0; i < 16; i++) {
+            dst[i] = dd * ((float)(blk[2 + i] & 15u) - 8.0f);
+            dst[i + 16] = dd * ((float)(blk[2 + i] >> 4) - 8.0f);
+        }
     } else if (type == 14u) {
         const uint8_t *blk = row + (c / 8u) * 210u;
         const uint32_t qq = c % 8u, h = qq >> 2, k = qq & 3u;

@@ -284,6 +284,41 @@ MYNAH_DEV float q80_sum(const uint32_t *raw, uint32_t s, const float *__restrict
     return acc;
 }
 
+// ── Q4_0: 18-byte block, 2-byte aligned; one running sum per row ───────────
+// kernels.c:2353-2360 values (d * (q - 8)) times x, each product rounded,
+// added to the row's single running sum (kernels.c:2467-2484): the low
+// nibbles (weights 0..15), then the high nibbles (16..31). `acc` carries the
+// sum in from the previous block.
+struct RawQ40 {
+    uint32_t raw[5], s;
+    __device__ __forceinline__ void load(const uint8_t *b) {
+        s = (uint32_t)(uintptr_t)b & 3u;
+        const uint32_t *a = (const uint32_t *)(b - s);
+        // At skew 0 dword 4 holds the last two quant bytes and two bytes past
+        // the block, inside the same aligned dword.
+#pragma unroll
+        for (int k = 0; k < 5; k++) raw[k] = a[k];
+    }
+    __device__ __forceinline__ float chain(const float *__restrict__ x, float acc) const {
+#pragma clang fp contract(off)
+        const float d = f16_to_f32(s ? (raw[0] >> 16) : raw[0]);
+        uint32_t q[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) q[j] = s ? raw[j + 1] : align_bytes(raw[j + 1], raw[j], 2u);
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t nib = hf ? ((q[j] >> 4) & 0x0f0f0f0fu) : (q[j] & 0x0f0f0f0fu);
+                const float4 x4 = *(const float4 *)(x + 16 * hf + 4 * j);
+                acc = acc + (d * (ubyte_f<0>(nib) - 8.0f)) * x4.x;
+                acc = acc + (d * (ubyte_f<1>(nib) - 8.0f)) * x4.y;
+                acc = acc + (d * (ubyte_f<2>(nib) - 8.0f)) * x4.z;
+                acc = acc + (d * (ubyte_f<3>(nib) - 8.0f)) * x4.w;
+            }
+        return acc;
+    }
+};
 
 // ── grouped matvec with fused epilogues (every matvec, decode included) ────
 // One launch covers up to EX_GROUP_MAX matrices; workgroup t serves the
@@ -658,6 +693,50 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     }
 }
 
+// Q4_0 rows of a grouped launch. The planner gives a launch holding a Q4_0
+// matrix the shape K = 1, WS = 1, WR = 1 (one wave, 64 rows): lane = row,
+// whose single running sum goes through every block in order (a gate/up
+// pair: one sum per matrix), then the same epilogues as group_split. x is
+// staged as for the other types; no unit partials are kept.
+MYNAH_DEV void group_chain_q40(const GemvDesc &g, uint32_t t, float *lds, double *shd) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x;
+    const uint32_t row = (t - g.tile0) * 64u + lane;
+    const bool live = row < g.rows;
+    const size_t roff = (size_t)(live ? row : g.rows - 1u) * g.row_bytes;
+    const uint32_t U = g.units;
+    RawQ40 cur;
+    cur.load(g.w + roff);
+    const float resv = (live && g.res) ? g.res[row] : 0.0f;
+    const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
+    stage_x(g.x, g.norm_w, g.cols, g.eps, lds, lds + xpad_floats(g.cols), shd);
+    __syncthreads();
+    float t1 = 0.0f, t2 = 0.0f;
+    const uint32_t n_mat = g.w2 ? 2u : 1u;
+    for (uint32_t m = 0; m < n_mat; m++) {
+        const uint8_t *r = (m ? g.w2 : g.w) + roff;
+        float acc = 0.0f;
+        for (uint32_t u = 0; u < U; u++) {
+            // Prefetch the next block (or the pair's first) before this one's sum.
+            RawQ40 nxt = cur;
+            if (u + 1u < U) nxt.load(r + 18u * (u + 1u));
+            else if (m + 1u < n_mat) nxt.load(g.w2 + roff);
+            acc = cur.chain(unit_x<8>(lds, u), acc);
+            cur = nxt;
+        }
+        if (m) t2 = acc;
+        else t1 = acc;
+    }
+    float v = t1;
+    if (g.w2) v = t1 * sigmoid_ref(t1) * t2;
+    else if (g.res) v = resv + t1;
+    if (live) g.y[yoff + row] = v;
+    if (g.keys) {
+        const unsigned long long key = wave_max_u64(live ? argmax_key(v, row) : 0ull);
+        if (lane == 0) g.keys[t - g.tile0] = key;
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(1024)
 mynah_gemv_group(const GemvGroup grp) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -676,6 +755,8 @@ mynah_gemv_group(const GemvGroup grp) {
         group_split<13, false>(g, t, grp.shape, lds, shd);
     } else if (g.type == 14u) {
         group_split<14, false>(g, t, grp.shape, lds, shd);
+    } else if (g.type == 2u) {
+        group_chain_q40(g, t, lds, shd);
     } else {
         group_split<8, false>(g, t, grp.shape, lds, shd);
     }

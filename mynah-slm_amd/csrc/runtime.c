@@ -251,11 +251,7 @@ int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t row
     size_t rb;
     memset(g, 0, sizeof *g);
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
-    if (type == MYNAH_Q4_0) {
-        mynah_set_error("Q4_0 has no grouped GEMV (its row is one serial sum)");
-        return -1;
-    }
-    if ((type != MYNAH_Q8_0 && cols % 256 != 0) || rb > 0xffffffffu) {
+    if ((type != MYNAH_Q8_0 && type != MYNAH_Q4_0 && cols % 256 != 0) || rb > 0xffffffffu) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
     }
@@ -268,7 +264,7 @@ int mynah_gemv_desc_init(mynah_gemv_desc *g, int type, const void *w, size_t row
     g->y = y;
     g->rows = (uint32_t)rows;
     g->cols = (uint32_t)cols;
-    g->units = (uint32_t)(type == MYNAH_Q8_0 ? cols / 32 : cols / 256);
+    g->units = (uint32_t)(type == MYNAH_Q8_0 || type == MYNAH_Q4_0 ? cols / 32 : cols / 256);
     g->row_bytes = (uint32_t)rb;
     g->type = (uint32_t)type;
     return 0;
@@ -372,16 +368,18 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
     int exact = (order < 0 ? gemv_order : order) == MYNAH_GEMV_EXACT;
     uint32_t all_rows = 0, max_units = 1;
     uint64_t all_units = 0;
-    int split = 1;
+    int split = 1, chain = 0;
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
         if (g->type != MYNAH_Q4_K && g->type != MYNAH_Q5_K && g->type != MYNAH_Q6_K &&
-            g->type != MYNAH_Q8_0) {
+            g->type != MYNAH_Q8_0 && g->type != MYNAH_Q4_0) {
             mynah_set_error("type %u has no grouped GEMV", g->type);
             return -1;
         }
-        /* Q5_K has only the exact kernel; its order is the reference's anyway. */
+        /* Q5_K and Q4_0 have only the exact kernel; their order is the
+         * reference's anyway. */
         if (g->type == MYNAH_Q5_K) exact = 1;
+        if (g->type == MYNAH_Q4_0) exact = 1, chain = 1;
         all_rows += g->rows;
         const uint32_t u = g->w2 ? 2u * g->units : g->units;
         if (u > max_units) max_units = u;
@@ -393,7 +391,10 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
             return -1;
         }
     }
-    if (exact && gemv_stream_plan(d, grp, p) == 0) return 0;
+    if (exact && !chain && gemv_stream_plan(d, grp, p) == 0) return 0;
+    /* A Q4_0 row is one running sum: with a Q4_0 matrix in the launch every
+     * lane owns a whole row (K = 1, one wave of 64 rows per workgroup). */
+    if (chain) split = 0;
     /* Split super-blocks across quads when the launch is small enough that
      * four times the waves still fit the 1,024 SIMDs about twice. */
     if (all_units > 32768u) split = 0;
@@ -413,6 +414,8 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
             if (grp->d[i].w2 != NULL) wr = 8u;
         while (wr > 1u && ws * wr > 16u) wr /= 2u;
         tile_rows = (16u >> lk) * wr;
+    } else if (exact && chain) {
+        tile_rows = 64u;
     } else if (exact) {
         exact_shape(all_rows, max_units, &lk, &ws, &wr);
         tile_rows = (64u >> lk) * wr;
@@ -427,8 +430,9 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
     for (uint32_t i = 0; i < grp->n; i++) {
         mynah_gemv_desc *g = &grp->d[i];
         const uint32_t ut = g->w2 ? 2u * g->units : g->units;
-        const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
-                                     (size_t)tile_rows * (ut | 1u) +
+        /* Q4_0 keeps no unit partials in LDS. */
+        const size_t parts = g->type == MYNAH_Q4_0 ? 0u : (size_t)tile_rows * (ut | 1u);
+        const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) + parts +
                                      (g->norm_w ? (size_t)g->cols : 0u)) * 4u
                                   : ((size_t)g->cols + g->cols / 16 + g->cols / 8 +
                                      (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
