@@ -474,7 +474,8 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
 
 // Grid n_heads, block 64: one wave combines the chunks of one query head,
 // lane l holding dimensions l and l + 64. M = max m_c and the double sum
-// L = sum_c expf(m_c - M) l_c are wave reductions (lane c holds chunk c);
+// L = sum_c expf(m_c - M) l_c are wave reductions (lane c holds chunks c
+// and c + 64, in that order);
 // then o = fma(expf(m_c - M) * inv, o_c, o) in chunk order, inv =
 // (float)(1 / L).
 #define AC_MAXC 128                                 // chunks (n_ctx <= 4096)
@@ -484,38 +485,54 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
                    float *__restrict__ out, uint32_t nch_max, uint32_t group) {
 #pragma clang fp contract(off)
     __shared__ float wsc[AC_MAXC];
-    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
     const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
     const uint32_t lane = threadIdx.x;
     const size_t base = (size_t)kvh * nch_max * group + h;    // slot of chunk c: base + c * group
     const float *pob = po + base * 128u + lane;
     const size_t cstride = (size_t)group * 128u;
-    // The first weighted partials are in flight while M and L are reduced.
-    float pv[16][2];
+    // Every slot below nch_max is in bounds, so the partials are loaded
+    // before the position arrives and masked by the live chunk count after:
+    // lane c holds chunks c and c + 64 (nch_max <= AC_MAXC = 128), and the
+    // first 32 weighted partials of each dimension are in flight meanwhile.
+    const float pm0 = lane < nch_max ? pm[base + (size_t)lane * group] : 0.0f;
+    const float pm1 = lane + 64u < nch_max ? pm[base + (size_t)(lane + 64u) * group] : 0.0f;
+    const double pl0 = lane < nch_max ? pl[base + (size_t)lane * group] : 0.0;
+    const double pl1 = lane + 64u < nch_max ? pl[base + (size_t)(lane + 64u) * group] : 0.0;
+    float pv[32][2];
 #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        pv[u][0] = (uint32_t)u < nch ? pob[(size_t)u * cstride] : 0.0f;
-        pv[u][1] = (uint32_t)u < nch ? pob[(size_t)u * cstride + 64u] : 0.0f;
+    for (int u = 0; u < 32; u++) {
+        pv[u][0] = (uint32_t)u < nch_max ? pob[(size_t)u * cstride] : 0.0f;
+        pv[u][1] = (uint32_t)u < nch_max ? pob[(size_t)u * cstride + 64u] : 0.0f;
     }
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
     float M = -__builtin_inff();
-    for (uint32_t c = lane; c < nch; c += 64u) M = fmaxf(M, pm[base + (size_t)c * group]);
+    if (lane < nch) M = fmaxf(M, pm0);
+    if (lane + 64u < nch) M = fmaxf(M, pm1);
     M = wave_max_f(M);
     double L = 0.0;
-    for (uint32_t c = lane; c < nch; c += 64u) {
-        const float w = expf(pm[base + (size_t)c * group] - M);
-        wsc[c] = w;
-        L += (double)w * pl[base + (size_t)c * group];
+    if (lane < nch) {
+        const float w = expf(pm0 - M);
+        wsc[lane] = w;
+        L += (double)w * pl0;
+    }
+    if (lane + 64u < nch) {
+        const float w = expf(pm1 - M);
+        wsc[lane + 64u] = w;
+        L += (double)w * pl1;
     }
     L = wave_sum_d(L);
     const float inv = (float)(1.0 / L);
     __syncthreads();
     float o0 = 0.0f, o1 = 0.0f;
-    uint32_t c = 0;
-    for (; c < 16u && c < nch; c++) {
-        const float sc = wsc[c] * inv;
-        o0 = __builtin_fmaf(sc, pv[c][0], o0);
-        o1 = __builtin_fmaf(sc, pv[c][1], o1);
+#pragma unroll
+    for (int u = 0; u < 32; u++) {          // static indices keep pv in registers
+        if ((uint32_t)u < nch) {
+            const float sc = wsc[u] * inv;
+            o0 = __builtin_fmaf(sc, pv[u][0], o0);
+            o1 = __builtin_fmaf(sc, pv[u][1], o1);
+        }
     }
+    uint32_t c = nch < 32u ? nch : 32u;
     for (; c + 8u <= nch; c += 8u) {
         float a[8], b[8];
 #pragma unroll
