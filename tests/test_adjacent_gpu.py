@@ -269,14 +269,16 @@ def test_decoder_batched_prefill_is_bit_identical(M, qtype):
     assert np.array_equal(bits(a.forward(3)), bits(b.forward(3)))
 
 
+ALL_PROJECTIONS = tuple(["token_embd.weight", "output.weight"] + [
+    f"blk.{l}.{n}.weight" for l in range(CF.QWEN3_TINY.n_layers)
+    for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")])
+
+
 def test_decoder_all_q40_projections(M):
     """Every projection and the embedding/head Q4_0 (a Q4_0 checkpoint's
     layout): greedy ids equal the oracle's."""
     print("[case] tiny decoder, all projections Q4_0, 10 steps", flush=True)
-    names = ["token_embd.weight", "output.weight"] + [
-        f"blk.{l}.{n}.weight" for l in range(CF.QWEN3_TINY.n_layers)
-        for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
-    model = Variant(M, tuple(names), qtype=2)
+    model = Variant(M, ALL_PROJECTIONS, qtype=2)
     shape, npre, steps = CF.QWEN3_TINY, 8, 10
     k, v = O.kv_prefill(O.substream, shape, 0, npre)
     first = O.first_token(0, shape.vocab)
@@ -290,3 +292,29 @@ def test_decoder_all_q40_projections(M):
         assert rel_err(a, b) <= TOL
         tok = int(np.argmax(b))
         assert int(np.argmax(a)) == tok
+
+
+@pytest.mark.parametrize("qtype", DECODER_TYPES)
+def test_checkpoint_from_gguf(M, qtype, tmp_path):
+    """The all-`qtype` model written as a GGUF file: mynah_hip_qwen3_from_gguf
+    gives the table-built decoder's bits, and greedy ids equal the oracle's."""
+    import gguf_writer as GW
+    print(f"[case] all-type-{qtype} GGUF -> from_gguf vs table vs oracle, 6 steps", flush=True)
+    model = Variant(M, ALL_PROJECTIONS, qtype=qtype)
+    shape, npre, n_ctx = CF.QWEN3_TINY, 8, 24
+    path = tmp_path / f"t{qtype}.gguf"
+    path.write_bytes(GW.qwen3_writer(model.shape, model.table, model.count, model.blob,
+                                     n_ctx).to_bytes())
+    a, b = M.Qwen3Decoder.from_gguf(str(path), n_ctx), M.Qwen3Decoder(model, n_ctx)
+    ref = O.OracleQwen3(model, n_ctx)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    for dec in (a, b):
+        dec.set_kv(k, v, npre)
+    ref.prefill_kv(k, v, npre)
+    tok = O.first_token(0, shape.vocab)
+    for _ in range(6):
+        la, lb, lr = a.forward(tok), b.forward(tok), ref.forward(tok)
+        assert np.array_equal(bits(la), bits(lb))
+        assert rel_err(la, lr) <= TOL
+        tok = int(np.argmax(lr))
+        assert int(np.argmax(la)) == tok
