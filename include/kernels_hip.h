@@ -159,17 +159,18 @@ enum { MYNAH_GEMV_EXACT = 0, MYNAH_GEMV_REORDERED = 1 };
 int mynah_hip_set_gemv_order(int order);
 int mynah_hip_gemv_order(void);
 
-/* The int8 activation lane of Q4_K products (the reference's lane of an
- * AVX2 + FMA build of ingot, third_party/ingot/src/kernels.c:636-788,
- * 1120-1751), bit-identical to that build:
+/* The int8 activation lane of Q4_K and Q5_K products (the reference's lane
+ * of an AVX2 + FMA build of ingot, third_party/ingot/src/kernels.c:636-788,
+ * 1120-1751, 2573-2595), bit-identical to that build:
  *   MYNAH_INT8_OFF (default, like the as-built reference, which has no int8
  *     lane): exact f32 everywhere;
- *   MYNAH_INT8_BATCHED: Q4_K matmat with tokens >= 2 quantises its input
- *     (that build's batched default);
- *   MYNAH_INT8_ALL: the Q4_K matvec too (that build with INGOT_SDOT=1).
+ *   MYNAH_INT8_BATCHED: Q4_K and Q5_K matmat with tokens >= 2 quantise
+ *     their input (that build's batched default);
+ *   MYNAH_INT8_ALL: the Q4_K matvec too (that build with INGOT_SDOT=1; Q5_K
+ *     has no int8 matvec there).
  * INGOT_SDOT=1 in the environment, read at the first call that needs the
- * mode, starts the library in MYNAH_INT8_ALL. Q6_K and Q8_0 stay exact, and
- * the resident decode step (mynah_decode.h) always runs exact. */
+ * mode, starts the library in MYNAH_INT8_ALL. Q6_K, Q8_0 and Q4_0 stay
+ * exact, and the resident decode step (mynah_decode.h) always runs exact. */
 enum { MYNAH_INT8_OFF = 0, MYNAH_INT8_BATCHED = 1, MYNAH_INT8_ALL = 2 };
 int mynah_hip_set_int8(int mode);
 int mynah_hip_int8(void);
