@@ -705,24 +705,38 @@ MYNAH_DEV void group_chain_q40(const GemvDesc &g, uint32_t t, float *lds, double
     const bool live = row < g.rows;
     const size_t roff = (size_t)(live ? row : g.rows - 1u) * g.row_bytes;
     const uint32_t U = g.units;
-    RawQ40 cur;
-    cur.load(g.w + roff);
     const float resv = (live && g.res) ? g.res[row] : 0.0f;
     const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
+    // Blocks go through a register ring of 4-block chunks, each chunk's loads
+    // issued a chunk ahead of its sums (one block ahead leaves every block's
+    // memory latency exposed; 8-block chunks spill in this entry).
+    constexpr uint32_t CH = 4;
+    RawQ40 cur[CH];
+#pragma unroll
+    for (uint32_t k = 0; k < CH; k++)
+        if (k < U) cur[k].load(g.w + roff + 18u * k);
     stage_x(g.x, g.norm_w, g.cols, g.eps, lds, lds + xpad_floats(g.cols), shd);
     __syncthreads();
     float t1 = 0.0f, t2 = 0.0f;
     const uint32_t n_mat = g.w2 ? 2u : 1u;
     for (uint32_t m = 0; m < n_mat; m++) {
         const uint8_t *r = (m ? g.w2 : g.w) + roff;
+        if (m) {
+#pragma unroll
+            for (uint32_t k = 0; k < CH; k++)
+                if (k < U) cur[k].load(r + 18u * k);
+        }
         float acc = 0.0f;
-        for (uint32_t u = 0; u < U; u++) {
-            // Prefetch the next block (or the pair's first) before this one's sum.
-            RawQ40 nxt = cur;
-            if (u + 1u < U) nxt.load(r + 18u * (u + 1u));
-            else if (m + 1u < n_mat) nxt.load(g.w2 + roff);
-            acc = cur.chain(unit_x<8>(lds, u), acc);
-            cur = nxt;
+        for (uint32_t c0 = 0; c0 < U; c0 += CH) {
+            RawQ40 nxt[CH];
+#pragma unroll
+            for (uint32_t k = 0; k < CH; k++)
+                if (c0 + CH + k < U) nxt[k].load(r + 18u * (c0 + CH + k));
+#pragma unroll
+            for (uint32_t k = 0; k < CH; k++)
+                if (c0 + k < U) acc = cur[k].chain(unit_x<8>(lds, c0 + k), acc);
+#pragma unroll
+            for (uint32_t k = 0; k < CH; k++) cur[k] = nxt[k];
         }
         if (m) t2 = acc;
         else t1 = acc;
