@@ -70,6 +70,11 @@ int ingot_q4_k_matmat(const void *weights, size_t rows, size_t cols,
  * (tokens == 1 is the matvec, kernels.c:1723-1726). */
 int ingot_q4_k_matmat_exact(const void *weights, size_t rows, size_t cols,
                             const float *input, float *output, size_t tokens);
+/* quant.h:74-75 (kernels.c:319-337): the scalar lane — the exact order —
+ * whatever the int8 lane's mode. The as-built ingot_q4_k_matvec is that lane
+ * too, so both give the same bits unless the int8 lane is on. */
+int ingot_q4_k_matvec_scalar(const void *weights, size_t rows, size_t cols,
+                             const float *input, float *output);
 /* kernels.c:799-810 (exported by ingot's kernels, not declared in quant.h):
  * the int8 matvec whatever the mode — activations quantised per 256 values
  * (amax / 127, round half to even), integer dots per 32, the reference's f32
@@ -109,12 +114,17 @@ int ingot_q8_0_dequant(const void *weights, size_t rows, size_t cols, float *out
 int ingot_q8_0_matmat(const void *weights, size_t rows, size_t cols,
                       const float *input, float *output, size_t tokens);
 
-/* quant.h:175-176 (ingot_gguf_matvec). `g` and `t` are the reference's
- * ingot_gguf / ingot_tensor (third_party/ingot/include/ingot/gguf.h:41-50);
- * the tensor's bytes are located through the host process's
- * ingot_gguf_data(), so this entry point needs ingot's GGUF reader linked in
- * (it returns -1 otherwise). rows = ne[1] (1 for rank 1), cols = ne[0]. */
+/* quant.h:179-183 (ingot_gguf_matvec / _matmat / _dequant_matrix,
+ * generic.c:148-173). `g` and `t` are the reference's ingot_gguf /
+ * ingot_tensor (third_party/ingot/include/ingot/gguf.h:41-50); the tensor's
+ * bytes are located through the host process's ingot_gguf_data(), so these
+ * entry points need ingot's GGUF reader linked in (they return -1
+ * otherwise). rows = ne[1] (1 for rank 1), cols = ne[0]; rank 0, rank > 2
+ * and zero dimensions return -1. */
 int ingot_gguf_matvec(const void *g, const void *t, const float *input, float *output);
+int ingot_gguf_matmat(const void *g, const void *t, const float *input, float *output,
+                      size_t tokens);
+int ingot_gguf_dequant_matrix(const void *g, const void *t, float *output);
 
 /* ── part 2: device-resident API (no reference counterpart) ────────────── */
 

@@ -46,6 +46,15 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits);
 int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
                              uint32_t *tokens_out, float *ms);
 
+/* Teacher forcing (no reference counterpart: the reference's loop always
+ * feeds back its own choice, src/generate.c:47-77): n steps whose inputs are
+ * inputs[0 .. n) at positions n_past .. n_past + n - 1, replayed through the
+ * same captured step graphs as generate(). greedy_out[i] receives the greedy
+ * choice of step i's logits (src/sampler.c:122-129); last_logits (optional,
+ * host, vocab floats) the logits of the last step. n_past advances by n. */
+int mynah_hip_qwen3_forced(mynah_qwen3 *s, const uint32_t *inputs, uint32_t n,
+                           uint32_t *greedy_out, float *last_logits);
+
 /* Fill positions [0, n_pos) of the KV cache from host arrays laid out
  * [layer][n_pos][kv_dim] and set n_past = n_pos (the configs prefill the
  * cache with synthetic values instead of running a prompt). */

@@ -10,6 +10,7 @@ Seed scheme (all derived from a config seed s, 0 for every configuration):
   * Qwen3 first decode token:    uniform over the vocabulary from substream(s, 1 << 21)
                                  (configs[4]'s prompt: the first 2048 values of that stream)
   * prefill activations (C4):    X from substream(s, 1 << 22 + i) for matrix i
+  * teacher-forced decode inputs: uniform over the vocabulary from substream(s, 1 << 23)
 """
 from __future__ import annotations
 
@@ -95,6 +96,18 @@ MATRIX_SEED_STRIDE = 2
 KV_SEED_INDEX = 1 << 20
 TOKEN_SEED_INDEX = 1 << 21
 PREFILL_X_INDEX = 1 << 22
+FORCED_SEED_INDEX = 1 << 23
+
+# Teacher-forced decode parity (configs[2]'s model and KV prefill): the input
+# of every step is drawn uniformly instead of being the previous step's
+# greedy id, so each step's logits (and greedy id) differ; the compiled
+# reference's logits of every step are the golden vectors.
+C3_FORCED_STEPS = 64
+FORCED_SAMPLE_STRIDE = 293   # every 293rd logit of each step kept in full
+
+# configs[4] end to end against the compiled reference: the greedy ids of
+# all 256 steps and the top-64 logits of the steps listed here.
+C5_SNAPSHOT_STEPS = (0, 1, 31, 63, 127, 191, 255)
 
 
 def matrix_seeds(substream, config_seed: int, i: int) -> tuple[int, int]:
@@ -121,3 +134,9 @@ def c5_prompt(uniform, substream, vocab: int, n: int = C5_PROMPT, config_seed: i
     first value is the decode configs' first token); `uniform(seed, n, bound)`
     is the shared generator's uniform vector."""
     return uniform(substream(config_seed, TOKEN_SEED_INDEX), n, vocab)
+
+
+def forced_inputs(uniform, substream, vocab: int, n: int, config_seed: int = 0):
+    """The inputs of a teacher-forced decode run: n ids uniform over the
+    vocabulary."""
+    return uniform(substream(config_seed, FORCED_SEED_INDEX), n, vocab)

@@ -101,7 +101,12 @@ MYNAH_DEV unsigned long long wave_max_u64(unsigned long long v) {
 // Key ordering logits like the reference's greedy choice (src/sampler.c:
 // 124-129): a larger value wins, and among equal values the smaller index
 // (hence ~index in the low word). -0 is folded onto +0 so they compare equal.
+// The reference starts from logits[0] and moves on a strict `>`, so a NaN
+// is never picked past index 0, and a NaN at index 0 is never left (no
+// comparison with it holds): NaN keys are 0 (below every number's key, all
+// of which are > 0) except at index 0, whose NaN key is the largest key.
 MYNAH_DEV unsigned long long argmax_key(float v, uint32_t index) {
+    if (v != v) return index == 0u ? ~0ull : 0ull;
     uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)b << 32) | (unsigned long long)(~index);

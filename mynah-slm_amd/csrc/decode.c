@@ -26,12 +26,14 @@
 #define _GNU_SOURCE
 #include "kernels_hip.h"
 #include "mynah_decode.h"
+#include "mynah_generate.h"
 #include "runtime_internal.h"
 
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 typedef struct {
     int type;
@@ -77,6 +79,7 @@ struct mynah_qwen3 {
     uint32_t pf_cap;
     float *pf_x, *pf_xn, *pf_q, *pf_att, *pf_g, *pf_u, *pf_s;
     uint32_t *pf_tok;
+    float *host_logits;             /* pinned: logits for a host-side sampler */
 };
 
 #define TOKEN(s) ((s)->counters + 0)
@@ -117,6 +120,10 @@ static int bind(dtensor *out, const mynah_synth_tensor *table, size_t count,
     /* The step's kernels take F32, Q4_0, Q4_K, Q5_K, Q6_K and Q8_0 tensors. */
     if (t->type != 0 && mynah_geometry(t->type, rows, cols, &rb) != 0)
         return fail(err, errsz, "tensor type has no kernel in the decode step", name);
+    /* The kernels read rows * row_bytes from the tensor's offset: the table's
+     * byte count must cover them (it lies inside the blob, checked above). */
+    if (rows > UINT64_MAX / rb || t->nbytes < rows * rb)
+        return fail(err, errsz, "tensor byte count shorter than its rows", name);
     out->type = t->type;
     out->rows = rows;
     out->cols = cols;
@@ -134,6 +141,21 @@ static void *dalloc(size_t bytes, int *ok) {
     return p;
 }
 
+/* The head launch of a full step: final RMSNorm fused in front
+ * (src/arch_qwen3.c:239), one argmax key per workgroup behind it
+ * (src/sampler.c:124-129). */
+static int head_group(const mynah_qwen3 *s, mynah_gemv_group *g) {
+    memset(g, 0, sizeof *g);
+    g->n = 1;
+    if (mynah_gemv_desc_init(&g->d[0], s->head.type, s->head.dev, s->head.rows, s->head.cols,
+                             s->x, s->logits) != 0)
+        return -1;
+    g->d[0].norm_w = (const float *)s->out_norm.dev;
+    g->d[0].eps = s->c.rms_eps;
+    g->d[0].keys = s->keys;
+    return 0;
+}
+
 void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
     for (int v = 0; v < 4; v++) {
@@ -146,6 +168,7 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
                     s->pf_tok};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
+    if (s->host_logits) (void)hipHostFree(s->host_logits);
     free(s->layers);
     free(s);
 }
@@ -256,7 +279,22 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
         s->pl = (double *)dalloc(parts * 8, &ok);
         s->po = (float *)dalloc(parts * 128 * 4, &ok);
     }
+    /* One argmax key per head workgroup: sized from the head launch as it
+     * is planned now (x and logits exist, so the plan sees its real
+     * operands); enqueue_step re-plans and refuses a launch that would
+     * outgrow the buffer before anything is enqueued. */
     s->n_keys = c->vocab / 8 + 64;
+    if (ok) {
+        mynah_gemv_group hg;
+        uint32_t grid = 0;
+        if (head_group(s, &hg) != 0 ||
+            mynah_gemv_group_geometry(&hg, MYNAH_GEMV_EXACT, NULL, &grid) != 0) {
+            fail(err, errsz, "the output head has no GEMV launch", mynah_hip_last_error());
+            mynah_hip_qwen3_free(s);
+            return NULL;
+        }
+        if (grid > s->n_keys) s->n_keys = grid;
+    }
     s->keys = (unsigned long long *)dalloc((size_t)s->n_keys * 8, &ok);
     s->tokens = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
     if (!ok) {
@@ -386,20 +424,18 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
     if (rc == 0 && variant == STEP_FULL) {
         /* The final norm (src/arch_qwen3.c:239) runs inside the head GEMV. */
         mynah_gemv_group g;
-        memset(&g, 0, sizeof g);
-        g.n = 1;
-        rc = gemv_desc(&g.d[0], &s->head, s->x, s->logits);
-        g.d[0].norm_w = (const float *)s->out_norm.dev;
-        g.d[0].eps = c->rms_eps;
-        g.d[0].keys = s->keys;                               /* src/sampler.c:124-129 */
         /* The exact kernel is also the faster one for the head (its fused
          * norm costs the reordered kernel more), so the head always runs in
-         * the reference's order. */
-        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles, MYNAH_GEMV_EXACT);
+         * the reference's order. Its workgroups each write one key: the
+         * launch is planned and checked against the key buffer before it is
+         * enqueued. */
+        rc = head_group(s, &g);
+        rc = rc ? rc : mynah_gemv_group_geometry(&g, MYNAH_GEMV_EXACT, NULL, &head_tiles);
         if (rc == 0 && head_tiles > s->n_keys) {
             mynah_set_error("head launch of %u workgroups exceeds the key buffer", head_tiles);
             rc = -1;
         }
+        rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles, MYNAH_GEMV_EXACT);
     }
     if (rc == 0) {
         const unsigned long long *keys = s->keys;
@@ -857,6 +893,183 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
 int mynah_hip_qwen3_generate(mynah_qwen3 *s, uint32_t first_token, uint32_t n_steps,
                              uint32_t *tokens_out, float *ms) {
     return mynah_hip_qwen3_prompt(s, &first_token, 1, n_steps, tokens_out, NULL, ms);
+}
+
+/* Teacher forcing through the same captured steps the greedy loop replays:
+ * the forced-token list makes the argmax kernel embed inputs[i + 1] after
+ * step i instead of its choice, and still record the choice. */
+int mynah_hip_qwen3_forced(mynah_qwen3 *s, const uint32_t *inputs, uint32_t n,
+                           uint32_t *greedy_out, float *last_logits) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || inputs == NULL || greedy_out == NULL || n == 0) {
+        mynah_set_error("bad teacher-forcing arguments");
+        return -1;
+    }
+    if (n > s->n_ctx - s->n_past) {
+        mynah_set_error("%u forced steps do not fit the context (%u of %u used)", n, s->n_past,
+                        s->n_ctx);
+        return -1;
+    }
+    for (uint32_t i = 0; i < n; i++)
+        if (inputs[i] >= s->c.vocab) {
+            mynah_set_error("token %u out of range", inputs[i]);
+            return -1;
+        }
+    if (hipMemcpy(s->forced, inputs, (size_t)n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        mynah_set_error("forced-token upload failed");
+        return -1;
+    }
+    if (set_counters(s, d, inputs[0], 0, n) != 0) return -1;
+    ensure_graph(s, d, n >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
+    if (n % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
+    if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, n) != 0) return -1;
+    if (hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("forced decode failed");
+        return -1;
+    }
+    s->n_past += n;
+    if (hipMemcpy(greedy_out, s->tokens, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        (last_logits && hipMemcpy(last_logits, s->logits, (size_t)s->c.vocab * 4,
+                                  hipMemcpyDeviceToHost) != hipSuccess)) {
+        mynah_set_error("forced decode download failed");
+        return -1;
+    }
+    return 0;
+}
+
+/* ── the generation loop (src/generate.c:13-86) ──────────────────────────── */
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+static int is_eos(const mynah_hip_gen_params *p, uint32_t id) {
+    for (size_t i = 0; i < p->n_eos; i++)
+        if (p->eos[i] == id) return 1;
+    return 0;
+}
+
+/* src/timing.c:48-55: the first generated token stamps TTFT (prefill plus
+ * the decode time so far), every token counts. */
+static void timing_token(mynah_hip_timing *t, double t0) {
+    if (!t->ttft_done) {
+        t->ttft_s = t->prefill_s + (now_s() - t0);
+        t->ttft_done = 1;
+    }
+    t->n_gen++;
+}
+
+/* What the loop does with one sampled id (src/generate.c:50-77): 1 to go on,
+ * 0 to stop after it. The id counts as produced either way. */
+static int take_token(const mynah_hip_gen_params *p, mynah_hip_timing *t, double t0,
+                      uint32_t id, long *produced) {
+    if (p->accept) p->accept(p->sampler, id);
+    (*produced)++;
+    timing_token(t, t0);
+    if (is_eos(p, id)) return 0;
+    if (p->on_token && p->on_token(p->token_ctx, id) != 0) return 0;
+    return 1;
+}
+
+long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params *p,
+                                     mynah_hip_timing *t) {
+    mynah_device *d = mynah_dev();
+    mynah_hip_timing scratch_t;
+    if (t == NULL) t = &scratch_t;
+    memset(t, 0, sizeof *t);
+    if (d == NULL || s == NULL || p == NULL || p->prompt == NULL || p->n_prompt == 0 ||
+        (p->n_eos > 0 && p->eos == NULL) || p->n_prompt > 0xffffffffu) {
+        mynah_set_error("bad generation arguments");
+        return -1;
+    }
+    for (size_t i = 0; i < p->n_prompt; i++)
+        if (p->prompt[i] >= s->c.vocab) {
+            mynah_set_error("token %u out of range", p->prompt[i]);
+            return -1;
+        }
+    const uint32_t n_prompt = (uint32_t)p->n_prompt;
+    double t0 = now_s();
+    /* src/generate.c:26-33: every prompt token but the last only fills the
+     * cache (batched here; the same bits as one step per token). */
+    if (n_prompt > 1) {
+        if (s->prefill_mode == MYNAH_PREFILL_BATCHED) {
+            if (mynah_hip_qwen3_prefill(s, p->prompt, n_prompt - 1u) != 0) return -1;
+        } else {
+            for (uint32_t i = 0; i + 1 < n_prompt; i++)
+                if (mynah_hip_qwen3_forward(s, p->prompt[i], NULL) != 0) return -1;
+        }
+    }
+    if (p->accept)
+        for (uint32_t i = 0; i + 1 < n_prompt; i++) p->accept(p->sampler, p->prompt[i]);
+    {   /* src/timing.c:30-35 */
+        const double now = now_s();
+        t->prefill_s = now - t0;
+        t->n_prompt = n_prompt;
+        t0 = now;
+    }
+    uint32_t next = p->prompt[n_prompt - 1u];
+    if (p->accept) p->accept(p->sampler, next);
+    long produced = 0;
+    if (p->sample != NULL) {
+        /* Host sampling: every step's logits come back to the host and the
+         * caller's sampler (the reference's mynah_slm_sample, say) picks. */
+        if (s->host_logits == NULL &&
+            hipHostMalloc((void **)&s->host_logits, (size_t)s->c.vocab * 4, 0) != hipSuccess) {
+            s->host_logits = NULL;
+            mynah_set_error("cannot allocate the host logits buffer");
+            return -1;
+        }
+        for (uint32_t step = 0; step < p->max_new; step++) {
+            /* src/generate.c:48: a full context ends the loop, not the call. */
+            if (s->n_past >= s->n_ctx) break;
+            if (mynah_hip_qwen3_forward(s, next, s->host_logits) != 0) return -1;
+            const uint32_t id = p->sample(p->sampler, s->host_logits);
+            if (!take_token(p, t, t0, id, &produced)) break;
+            next = id;
+        }
+    } else {
+        /* Greedy on the device: up to `chunk` steps replay as graphs per
+         * host round trip (the first step alone, so TTFT is one step), then
+         * the ids come back and run through the loop's checks in order. A
+         * stop inside a chunk rewinds the position to just after the
+         * stopping step: the cache slots past it are rewritten before any
+         * later step reads them. */
+        const uint32_t chunk = p->chunk ? p->chunk : STEP_BATCH;
+        uint32_t done = 0;
+        int go = 1;
+        while (go && done < p->max_new && s->n_past < s->n_ctx) {
+            uint32_t c = done == 0 ? 1u : chunk;
+            if (c > p->max_new - done) c = p->max_new - done;
+            if (c > s->n_ctx - s->n_past) c = s->n_ctx - s->n_past;
+            if (set_counters(s, d, next, 0, 0) != 0) return -1;
+            ensure_graph(s, d, c >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
+            if (c % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
+            if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, c) != 0) return -1;
+            uint32_t ids[64];
+            uint32_t *buf = c <= 64u ? ids : (uint32_t *)malloc((size_t)c * 4);
+            if (buf == NULL ||
+                hipMemcpyAsync(buf, s->tokens, (size_t)c * 4, hipMemcpyDeviceToHost, d->stream) !=
+                    hipSuccess ||
+                hipStreamSynchronize(d->stream) != hipSuccess) {
+                if (buf != ids) free(buf);
+                mynah_set_error("greedy decode failed");
+                return -1;
+            }
+            uint32_t used = 0;
+            while (used < c && go) {
+                const uint32_t id = buf[used++];
+                go = take_token(p, t, t0, id, &produced);
+                next = id;
+            }
+            if (buf != ids) free(buf);
+            s->n_past += used;
+            done += used;
+        }
+    }
+    t->decode_s = now_s() - t0;        /* src/timing.c:57-59 */
+    return produced;
 }
 
 int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint32_t n_pos) {

@@ -89,27 +89,27 @@ static uint64_t ld_u64(const unsigned char *p) {
     return (uint64_t)ld_u32(p) | (uint64_t)ld_u32(p + 4) << 32;
 }
 
-static int cur_take(gg_cur *c, uint64_t n, const unsigned char **out) {
+static int rd_bytes(gg_cur *c, uint64_t n, const unsigned char **out) {
     if ((uint64_t)(c->end - c->p) < n) return -1;
     *out = c->p;
     c->p += n;
     return 0;
 }
-static int cur_u32(gg_cur *c, uint32_t *v) {
+static int rd_le32(gg_cur *c, uint32_t *v) {
     const unsigned char *p;
-    if (cur_take(c, 4, &p)) return -1;
+    if (rd_bytes(c, 4, &p)) return -1;
     *v = ld_u32(p);
     return 0;
 }
-static int cur_u64(gg_cur *c, uint64_t *v) {
+static int rd_le64(gg_cur *c, uint64_t *v) {
     const unsigned char *p;
-    if (cur_take(c, 8, &p)) return -1;
+    if (rd_bytes(c, 8, &p)) return -1;
     *v = ld_u64(p);
     return 0;
 }
-static int cur_str(gg_cur *c, const char **s, uint64_t *len) {
+static int rd_string(gg_cur *c, const char **s, uint64_t *len) {
     const unsigned char *p;
-    if (cur_u64(c, len) || *len > GG_MAX_STRING || cur_take(c, *len, &p)) return -1;
+    if (rd_le64(c, len) || *len > GG_MAX_STRING || rd_bytes(c, *len, &p)) return -1;
     *s = (const char *)p;
     return 0;
 }
@@ -160,9 +160,9 @@ static int type_geometry(uint32_t type, uint64_t *elems, uint64_t *bytes) {
 
 /* ── parsing ────────────────────────────────────────────────────────────── */
 
-static int parse_kv(gg_cur *c, gg_kv *kv, uint64_t index, char *err, size_t errsz) {
-    if (cur_str(c, &kv->key, &kv->klen) || cur_u32(c, &kv->type)) {
-        gg_err(err, errsz, "GGUF metadata truncated at entry %llu", (unsigned long long)index);
+static int read_entry(gg_cur *c, gg_kv *kv, uint64_t index, char *err, size_t errsz) {
+    if (rd_string(c, &kv->key, &kv->klen) || rd_le32(c, &kv->type)) {
+        gg_err(err, errsz, "metadata entry %llu is cut short by the end of the file", (unsigned long long)index);
         return -1;
     }
     const int kl = (int)(kv->klen < 200 ? kv->klen : 200);
@@ -171,28 +171,28 @@ static int parse_kv(gg_cur *c, gg_kv *kv, uint64_t index, char *err, size_t errs
         const char *s;
         uint64_t len;
         kv->val = c->p;
-        if (cur_str(c, &s, &len)) {
-            gg_err(err, errsz, "GGUF string value of '%.*s' truncated", kl, kv->key);
+        if (rd_string(c, &s, &len)) {
+            gg_err(err, errsz, "string of key '%.*s' is cut short", kl, kv->key);
             return -1;
         }
         return 0;
     }
     if (kv->type == KV_ARRAY) {
-        if (cur_u32(c, &kv->arr_type) || cur_u64(c, &kv->arr_len) || kv->arr_len > GG_MAX_COUNT) {
-            gg_err(err, errsz, "GGUF array header of '%.*s' invalid", kl, kv->key);
+        if (rd_le32(c, &kv->arr_type) || rd_le64(c, &kv->arr_len) || kv->arr_len > GG_MAX_COUNT) {
+            gg_err(err, errsz, "key '%.*s': bad array element type or length", kl, kv->key);
             return -1;
         }
         kv->val = c->p;
         if (kv->arr_type == KV_ARRAY) {
-            gg_err(err, errsz, "GGUF nested arrays are not allowed ('%.*s')", kl, kv->key);
+            gg_err(err, errsz, "key '%.*s' holds an array of arrays, which GGUF readers refuse", kl, kv->key);
             return -1;
         }
         if (kv->arr_type == KV_STRING) {
             for (uint64_t i = 0; i < kv->arr_len; i++) {
                 const char *s;
                 uint64_t len;
-                if (cur_str(c, &s, &len)) {
-                    gg_err(err, errsz, "GGUF string array '%.*s' truncated at %llu", kl, kv->key,
+                if (rd_string(c, &s, &len)) {
+                    gg_err(err, errsz, "key '%.*s': string element %llu is cut short", kl, kv->key,
                            (unsigned long long)i);
                     return -1;
                 }
@@ -201,21 +201,21 @@ static int parse_kv(gg_cur *c, gg_kv *kv, uint64_t index, char *err, size_t errs
         }
         const unsigned char *p;
         if (scalar_bytes(kv->arr_type, &n)) {
-            gg_err(err, errsz, "GGUF array '%.*s' has element type %u", kl, kv->key, kv->arr_type);
+            gg_err(err, errsz, "key '%.*s': array element type %u is unknown", kl, kv->key, kv->arr_type);
             return -1;
         }
-        if (cur_take(c, n * kv->arr_len, &p)) {
-            gg_err(err, errsz, "GGUF array '%.*s' runs past the file", kl, kv->key);
+        if (rd_bytes(c, n * kv->arr_len, &p)) {
+            gg_err(err, errsz, "key '%.*s': array data ends past the file", kl, kv->key);
             return -1;
         }
         return 0;
     }
     if (scalar_bytes(kv->type, &n)) {
-        gg_err(err, errsz, "GGUF metadata '%.*s' has type %u", kl, kv->key, kv->type);
+        gg_err(err, errsz, "key '%.*s': value type %u is unknown", kl, kv->key, kv->type);
         return -1;
     }
-    if (cur_take(c, n, &kv->val)) {
-        gg_err(err, errsz, "GGUF metadata '%.*s' truncated", kl, kv->key);
+    if (rd_bytes(c, n, &kv->val)) {
+        gg_err(err, errsz, "key '%.*s': value is cut short", kl, kv->key);
         return -1;
     }
     return 0;
@@ -298,7 +298,7 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
     struct stat st;
     if (fstat(fd, &st) != 0 || st.st_size < 24) {
         close(fd);
-        gg_err(err, errsz, "'%s' is not a GGUF file (too small)", path);
+        gg_err(err, errsz, "'%s' is shorter than a GGUF header", path);
         return NULL;
     }
     mynah_gguf *g = (mynah_gguf *)calloc(1, sizeof *g);
@@ -318,19 +318,19 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
     g->map = (unsigned char *)m;
     gg_cur c = {g->map, g->map + g->size};
     uint32_t magic;
-    if (cur_u32(&c, &magic) || magic != GG_MAGIC) {
-        gg_err(err, errsz, "'%s' is not a GGUF file (bad magic)", path);
+    if (rd_le32(&c, &magic) || magic != GG_MAGIC) {
+        gg_err(err, errsz, "'%s' does not start with the GGUF magic", path);
         goto fail;
     }
-    if (cur_u32(&c, &g->version) || g->version < 2 || g->version > 3) {
-        gg_err(err, errsz, "unsupported GGUF version %u in '%s' (need 2 or 3)", g->version, path);
+    if (rd_le32(&c, &g->version) || g->version < 2 || g->version > 3) {
+        gg_err(err, errsz, "'%s': GGUF version %u (this reader takes 2 and 3)", path, g->version);
         goto fail;
     }
     /* A metadata entry takes at least 13 bytes and a tensor info 24, so the
      * counts are bounded by the file before anything is allocated for them. */
-    if (cur_u64(&c, &g->n_tensors) || cur_u64(&c, &g->n_kv) || g->n_tensors > GG_MAX_COUNT ||
+    if (rd_le64(&c, &g->n_tensors) || rd_le64(&c, &g->n_kv) || g->n_tensors > GG_MAX_COUNT ||
         g->n_kv > GG_MAX_COUNT || g->n_kv * 13 + g->n_tensors * 24 > g->size - 24) {
-        gg_err(err, errsz, "GGUF header of '%s' declares more entries than the file holds", path);
+        gg_err(err, errsz, "'%s': the header counts more entries than the file can hold", path);
         goto fail;
     }
     g->kv = (gg_kv *)calloc(g->n_kv ? g->n_kv : 1, sizeof *g->kv);
@@ -340,7 +340,7 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
         goto fail;
     }
     for (uint64_t i = 0; i < g->n_kv; i++)
-        if (parse_kv(&c, &g->kv[i], i, err, errsz)) goto fail;
+        if (read_entry(&c, &g->kv[i], i, err, errsz)) goto fail;
     /* The last general.alignment that reads as a number sets the alignment
      * (ingot's header scan); it must be a power of two up to 1 MiB. */
     g->alignment = 32;
@@ -352,38 +352,38 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
             g->alignment = v;
     }
     if (g->alignment == 0 || g->alignment > (1u << 20) || (g->alignment & (g->alignment - 1))) {
-        gg_err(err, errsz, "GGUF alignment %llu is invalid in '%s'",
-               (unsigned long long)g->alignment, path);
+        gg_err(err, errsz, "'%s': general.alignment %llu is not a power of two up to 1 MiB",
+               path, (unsigned long long)g->alignment);
         goto fail;
     }
     for (uint64_t i = 0; i < g->n_tensors; i++) {
         gg_tensor *t = &g->t[i];
-        if (cur_str(&c, &t->name, &t->nlen) || cur_u32(&c, &t->rank)) {
-            gg_err(err, errsz, "GGUF tensor info %llu truncated", (unsigned long long)i);
+        if (rd_string(&c, &t->name, &t->nlen) || rd_le32(&c, &t->rank)) {
+            gg_err(err, errsz, "tensor entry %llu is cut short by the end of the file", (unsigned long long)i);
             goto fail;
         }
         const int nl = (int)(t->nlen < 200 ? t->nlen : 200);
         if (t->rank > GG_MAX_DIMS) {
-            gg_err(err, errsz, "tensor '%.*s' has rank %u (max %d)", nl, t->name, t->rank,
+            gg_err(err, errsz, "tensor '%.*s': rank %u is above %d", nl, t->name, t->rank,
                    GG_MAX_DIMS);
             goto fail;
         }
         uint64_t nelem = 1;
         for (uint32_t d = 0; d < t->rank; d++) {
-            if (cur_u64(&c, &t->ne[d]) || t->ne[d] == 0 || nelem > UINT64_MAX / t->ne[d]) {
-                gg_err(err, errsz, "tensor '%.*s' has an invalid shape", nl, t->name);
+            if (rd_le64(&c, &t->ne[d]) || t->ne[d] == 0 || nelem > UINT64_MAX / t->ne[d]) {
+                gg_err(err, errsz, "tensor '%.*s': a zero or overflowing dimension", nl, t->name);
                 goto fail;
             }
             nelem *= t->ne[d];
         }
         for (uint32_t d = t->rank; d < GG_MAX_DIMS; d++) t->ne[d] = 1;
-        if (cur_u32(&c, &t->type) || cur_u64(&c, &t->offset)) {
-            gg_err(err, errsz, "GGUF tensor info '%.*s' truncated", nl, t->name);
+        if (rd_le32(&c, &t->type) || rd_le64(&c, &t->offset)) {
+            gg_err(err, errsz, "tensor '%.*s': its entry is cut short", nl, t->name);
             goto fail;
         }
         uint64_t be, bb;
         if (type_geometry(t->type, &be, &bb)) {
-            gg_err(err, errsz, "tensor '%.*s' has unknown ggml type %u", nl, t->name, t->type);
+            gg_err(err, errsz, "tensor '%.*s': ggml type %u is unknown", nl, t->name, t->type);
             goto fail;
         }
         /* Quantized blocks lie along ne[0] and may not straddle rows. */
@@ -394,7 +394,7 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
         }
         t->nbytes = nelem / be * bb;
         if (t->offset % g->alignment != 0) {
-            gg_err(err, errsz, "tensor '%.*s' offset %llu is not aligned to %llu", nl, t->name,
+            gg_err(err, errsz, "tensor '%.*s': data offset %llu is off the %llu-byte alignment", nl, t->name,
                    (unsigned long long)t->offset, (unsigned long long)g->alignment);
             goto fail;
         }
@@ -403,7 +403,7 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
         const uint64_t head = (uint64_t)(c.p - g->map);
         const uint64_t data_off = (head + g->alignment - 1) & ~(g->alignment - 1);
         if (data_off > g->size) {
-            gg_err(err, errsz, "'%s' ends before its data section", path);
+            gg_err(err, errsz, "'%s': the data section starts past the end of the file", path);
             goto fail;
         }
         g->data = g->map + data_off;
@@ -411,7 +411,7 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
         for (uint64_t i = 0; i < g->n_tensors; i++) {
             const gg_tensor *t = &g->t[i];
             if (t->offset > g->data_bytes || t->nbytes > g->data_bytes - t->offset) {
-                gg_err(err, errsz, "tensor '%.*s' runs past the end of '%s'",
+                gg_err(err, errsz, "tensor '%.*s': data ends past the end of '%s'",
                        (int)(t->nlen < 200 ? t->nlen : 200), t->name, path);
                 goto fail;
             }
@@ -467,7 +467,7 @@ static int req_u32(const mynah_gguf *g, const char *arch, size_t alen, const cha
         return -1;
     }
     if (mynah_gguf_kv_u64(g, key, &v)) {
-        gg_err(err, errsz, "%s is not an integer", key);
+        gg_err(err, errsz, "key %s does not hold an integer", key);
         return -1;
     }
     *out = (uint32_t)v;                  /* truncated, as src/model.c:50 does */
@@ -484,7 +484,7 @@ static int req_f32(const mynah_gguf *g, const char *arch, size_t alen, const cha
         return -1;
     }
     if (mynah_gguf_kv_f64(g, key, &v)) {
-        gg_err(err, errsz, "%s is not a float", key);
+        gg_err(err, errsz, "key %s does not hold a number", key);
         return -1;
     }
     *out = (float)v;
@@ -500,11 +500,11 @@ int mynah_gguf_qwen3_shape(const mynah_gguf *g, mynah_qwen3_shape *out, uint32_t
     const char *arch;
     size_t alen;
     if (mynah_gguf_kv_str(g, "general.architecture", &arch, &alen) || alen == 0) {
-        gg_err(err, errsz, "no general.architecture in this file");
+        gg_err(err, errsz, "general.architecture is missing or not a string");
         return -1;
     }
     if (alen >= 32) {                    /* mynah_slm_config.arch[32] */
-        gg_err(err, errsz, "architecture name too long: %.*s", (int)(alen < 200 ? alen : 200),
+        gg_err(err, errsz, "architecture name longer than 31 bytes: %.*s", (int)(alen < 200 ? alen : 200),
                arch);
         return -1;
     }
@@ -522,7 +522,7 @@ int mynah_gguf_qwen3_shape(const mynah_gguf *g, mynah_qwen3_shape *out, uint32_t
         req_f32(g, arch, alen, "rope.freq_base", &s.rope_theta, err, errsz))
         return -1;
     if (s.n_heads == 0 || s.n_kv_heads == 0) {
-        gg_err(err, errsz, "head counts must be non-zero");
+        gg_err(err, errsz, "a head count is zero");
         return -1;
     }
     if (s.n_heads % s.n_kv_heads != 0) {

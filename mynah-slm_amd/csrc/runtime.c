@@ -176,13 +176,15 @@ int mynah_hip_set_gemv_order(int order) {
 
 int mynah_hip_gemv_order(void) { return gemv_order; }
 
-int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
-                      const float *x, float *y, hipStream_t stream) {
+/* allow_int8 == 0 keeps the exact order whatever the int8 lane's mode (the
+ * reference's ingot_q4_k_matvec_scalar). */
+static int gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                       const float *x, float *y, hipStream_t stream, int allow_int8) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
     /* INGOT_SDOT=1 semantics: the Q4_K matvec quantises its input
      * (third_party/ingot/src/kernels.c:819-834). */
-    if (type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
+    if (allow_int8 && type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
         return mynah_int8_product(d, MYNAH_Q4_K, w, rows, cols, x, y, 1, stream);
     if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, 1, stream);
     if (type != MYNAH_Q8_0 && cols % 256 != 0) {
@@ -206,6 +208,11 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
     g.n = 1;
     if (mynah_gemv_desc_init(&g.d[0], type, w, rows, cols, x, y) != 0) return -1;
     return mynah_gemv_group_launch(d, &g, stream, NULL, -1);
+}
+
+int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
+                      const float *x, float *y, hipStream_t stream) {
+    return gemv_launch(d, type, w, rows, cols, x, y, stream, 1);
 }
 
 static long env_long(const char *name, long dflt);
@@ -472,10 +479,16 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
 }
 
 int mynah_gemv_group_threads(mynah_gemv_group *grp, int order, uint32_t *threads) {
+    return mynah_gemv_group_geometry(grp, order, threads, NULL);
+}
+
+int mynah_gemv_group_geometry(mynah_gemv_group *grp, int order, uint32_t *threads,
+                              uint32_t *grid) {
     mynah_device *d = mynah_dev();
     gemv_plan p;
     if (d == NULL || gemv_group_plan(d, grp, order, &p) != 0) return -1;
-    *threads = p.threads;
+    if (threads) *threads = p.threads;
+    if (grid) *grid = p.grid;
     return 0;
 }
 
@@ -617,7 +630,9 @@ static int grow(unsigned char **buf, size_t *cap, size_t need) {
     return 0;
 }
 
-typedef enum { OP_MATVEC, OP_MATVEC_INT8, OP_MATMAT, OP_MATMAT_EXACT, OP_DEQUANT } host_op;
+typedef enum {
+    OP_MATVEC, OP_MATVEC_EXACT, OP_MATVEC_INT8, OP_MATMAT, OP_MATMAT_EXACT, OP_DEQUANT
+} host_op;
 
 static int host_call(host_op op, int type, const void *w, size_t rows, size_t cols,
                      const float *x, float *y, size_t tokens) {
@@ -656,8 +671,9 @@ static int host_call(host_op op, int type, const void *w, size_t rows, size_t co
             goto out;
         }
     }
-    if (op == OP_MATVEC) rc = mynah_gemv_launch(d, type, wd, rows, cols, (const float *)stage_x,
-                                                (float *)stage_y, s);
+    if (op == OP_MATVEC || op == OP_MATVEC_EXACT)
+        rc = gemv_launch(d, type, wd, rows, cols, (const float *)stage_x, (float *)stage_y, s,
+                         op == OP_MATVEC);
     else if (op == OP_MATVEC_INT8) rc = mynah_int8_product(d, MYNAH_Q4_K, wd, rows, cols,
                                                            (const float *)stage_x,
                                                            (float *)stage_y, 1, s);
@@ -752,6 +768,13 @@ int ingot_q4_k_matvec_int8(const void *w, size_t rows, size_t cols, const float 
     return host_call(OP_MATVEC_INT8, MYNAH_Q4_K, w, rows, cols, x, y, 1);
 }
 
+/* kernels.c:319-337: the scalar lane whatever the build or INGOT_SDOT; the
+ * exact order is that lane's, so this is the exact matvec with the int8
+ * lane bypassed. */
+int ingot_q4_k_matvec_scalar(const void *w, size_t rows, size_t cols, const float *x, float *y) {
+    return host_call(OP_MATVEC_EXACT, MYNAH_Q4_K, w, rows, cols, x, y, 1);
+}
+
 /* The reference's tensor descriptor (third_party/ingot/include/ingot/gguf.h:41-50)
  * and data accessor (gguf.h:74-76), resolved from the host process. */
 typedef struct {
@@ -764,21 +787,52 @@ typedef struct {
 } ingot_tensor_view;
 extern const void *ingot_gguf_data(const void *g, const void *t) __attribute__((weak));
 
-int ingot_gguf_matvec(const void *g, const void *t, const float *input, float *output) {
-    if (g == NULL || t == NULL) {
-        mynah_set_error("null argument");
-        return -1;
-    }
+/* generic.c:148-155: ggml's ne[0] is the input width, so rows = ne[1] and
+ * cols = ne[0]; rank 1 is one row; rank 0, rank > 2 and zero dimensions are
+ * refused. The data pointer is looked up first, as there (generic.c:161). */
+static const void *gguf_tensor(const void *g, const void *t, size_t *rows, size_t *cols) {
     if (ingot_gguf_data == NULL) {
         mynah_set_error("ingot_gguf_data is not linked into this process");
-        return -1;
+        return NULL;
+    }
+    const void *w = ingot_gguf_data(g, t);
+    if (w == NULL) {
+        mynah_set_error("tensor data not found");
+        return NULL;
     }
     const ingot_tensor_view *tv = (const ingot_tensor_view *)t;
-    const void *data = ingot_gguf_data(g, t);
-    if (data == NULL) return -1;
-    const size_t cols = (size_t)tv->ne[0];
-    const size_t rows = tv->rank >= 2 ? (size_t)tv->ne[1] : 1;
-    return ingot_matvec(tv->type, data, rows, cols, input, output);
+    if (tv->rank == 0 || tv->rank > 2) {
+        mynah_set_error("tensor rank %u is not 1 or 2", tv->rank);
+        return NULL;
+    }
+    *cols = (size_t)tv->ne[0];
+    *rows = tv->rank == 2 ? (size_t)tv->ne[1] : 1;
+    if (*rows == 0 || *cols == 0) {
+        mynah_set_error("tensor has a zero dimension");
+        return NULL;
+    }
+    return w;
+}
+
+/* quant.h:179-183 (generic.c:157-173) */
+int ingot_gguf_matmat(const void *g, const void *t, const float *input, float *output,
+                      size_t tokens) {
+    size_t rows, cols;
+    const void *w = gguf_tensor(g, t, &rows, &cols);
+    if (w == NULL) return -1;
+    return ingot_matmat(((const ingot_tensor_view *)t)->type, w, rows, cols, input, output,
+                        tokens);
+}
+
+int ingot_gguf_matvec(const void *g, const void *t, const float *input, float *output) {
+    return ingot_gguf_matmat(g, t, input, output, 1);
+}
+
+int ingot_gguf_dequant_matrix(const void *g, const void *t, float *output) {
+    size_t rows, cols;
+    const void *w = gguf_tensor(g, t, &rows, &cols);
+    if (w == NULL) return -1;
+    return ingot_dequant_matrix(((const ingot_tensor_view *)t)->type, w, rows, cols, output);
 }
 
 /* ── device-resident API ─────────────────────────────────────────────────── */

@@ -162,6 +162,11 @@ int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t 
 /* The block size the launch above would use (its input RMSNorm reduces in
  * an order that depends on it). */
 int mynah_gemv_group_threads(mynah_gemv_group *grp, int order, uint32_t *threads);
+/* Block size and workgroup count of that launch, without launching (either
+ * pointer may be NULL). The workgroup count is the length of the argmax key
+ * array a one-member group with `keys` writes. */
+int mynah_gemv_group_geometry(mynah_gemv_group *grp, int order, uint32_t *threads,
+                              uint32_t *grid);
 
 /* Y[tokens][rows] = (res +) X[tokens][cols] · W^T in the matvec summation
  * order (every output bit-identical to the matvec of its token);

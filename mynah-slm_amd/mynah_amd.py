@@ -35,6 +35,24 @@ class SynthTensor(C.Structure):
                 ("nbytes", C.c_uint64)]
 
 
+class GenParams(C.Structure):
+    """mynah_hip_gen_params (include/mynah_generate.h); the callbacks are
+    plain function addresses."""
+    _fields_ = [("prompt", C.c_void_p), ("n_prompt", C.c_size_t), ("max_new", C.c_uint32),
+                ("eos", C.c_void_p), ("n_eos", C.c_size_t), ("on_token", C.c_void_p),
+                ("token_ctx", C.c_void_p), ("sample", C.c_void_p), ("accept", C.c_void_p),
+                ("sampler", C.c_void_p), ("chunk", C.c_uint32)]
+
+
+class GenTiming(C.Structure):
+    """mynah_hip_timing (include/mynah_generate.h)."""
+    _fields_ = [("prefill_s", C.c_double), ("decode_s", C.c_double), ("ttft_s", C.c_double),
+                ("n_prompt", C.c_uint32), ("n_gen", C.c_uint32), ("ttft_done", C.c_int)]
+
+
+TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32)
+
+
 def _load() -> C.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(
@@ -48,6 +66,10 @@ def _load() -> C.CDLL:
         "ingot_matmat_is_exact": (C.c_int, [_SZ]),
         "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_q4_k_matvec_int8": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_q4_k_matvec_scalar": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+        "ingot_gguf_matvec": (C.c_int, [_P, _P, _P, _P]),
+        "ingot_gguf_matmat": (C.c_int, [_P, _P, _P, _P, _SZ]),
+        "ingot_gguf_dequant_matrix": (C.c_int, [_P, _P, _P]),
         "ingot_q5_k_matvec_scalar": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
         "ingot_q5_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "mynah_hip_set_int8": (C.c_int, [C.c_int]),
@@ -97,6 +119,9 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
         "mynah_hip_qwen3_generate": (C.c_int, [_P, C.c_uint32, C.c_uint32, _P,
                                                C.POINTER(C.c_float)]),
+        "mynah_hip_qwen3_forced": (C.c_int, [_P, _P, C.c_uint32, _P, _P]),
+        "mynah_hip_qwen3_generate_tokens": (C.c_long, [_P, C.POINTER(GenParams),
+                                                       C.POINTER(GenTiming)]),
         "mynah_hip_qwen3_set_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
         "mynah_hip_qwen3_get_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
         "mynah_hip_qwen3_prefill": (C.c_int, [_P, _P, C.c_uint32]),
@@ -133,10 +158,13 @@ def _load() -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    return lib
+    return lib, frozenset(sig)
 
 
-lib = _load()
+# SIGNATURES: every entry point given restype / argtypes above. ctypes passes
+# an undeclared pointer argument as a C int (the upper 32 bits lost), so
+# nothing may call the library through a name outside this set.
+lib, SIGNATURES = _load()
 
 
 class HipError(RuntimeError):
@@ -550,6 +578,46 @@ class Qwen3Decoder:
         check(lib.mynah_hip_qwen3_generate(self.h, first, steps, ptr(out), C.byref(ms)),
               "generate")
         return [int(t) for t in out], float(ms.value)
+
+    def forced(self, inputs):
+        """Teacher forcing through the replayed step graphs: step i runs
+        inputs[i]; returns (greedy id of every step, last step's logits)."""
+        p = np.ascontiguousarray(inputs, dtype=np.uint32)
+        out = np.empty(p.size, np.uint32)
+        logits = np.empty(self.model.shape.vocab, np.float32)
+        check(lib.mynah_hip_qwen3_forced(self.h, ptr(p), p.size, ptr(out), ptr(logits)),
+              "forced")
+        return [int(t) for t in out], logits
+
+    def generate_tokens(self, prompt, max_new: int, eos=(), sampler=None, chunk: int = 0,
+                        stop_after=None):
+        """The generation loop (include/mynah_generate.h). `sampler`: None for
+        greedy on the device, else an object with a C handle `h` and
+        `fn_addresses()` -> (sample, accept). The token callback stops after
+        `stop_after` ids. Returns (ids the callback saw, count the loop
+        returned, timing)."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        e = np.ascontiguousarray(list(eos) or [0], dtype=np.uint32)
+        seen = []
+
+        def on_token(_ctx, tok):
+            seen.append(int(tok))
+            return 1 if stop_after is not None and len(seen) >= stop_after else 0
+
+        cb = TOKEN_FN(on_token)
+        gp = GenParams()
+        gp.prompt, gp.n_prompt, gp.max_new = ptr(p), p.size, max_new
+        gp.eos, gp.n_eos = ptr(e), len(eos)
+        gp.on_token = C.cast(cb, C.c_void_p).value
+        gp.chunk = chunk
+        if sampler is not None:
+            gp.sample, gp.accept = sampler.fn_addresses()
+            gp.sampler = sampler.h
+        t = GenTiming()
+        n = lib.mynah_hip_qwen3_generate_tokens(self.h, C.byref(gp), C.byref(t))
+        if n < 0:
+            raise HipError(f"generate_tokens: {lib.mynah_hip_last_error().decode()}")
+        return seen, int(n), t
 
     @property
     def n_past(self) -> int:

@@ -95,6 +95,21 @@ void  orc_qwen3_set_n_past(orc_qwen3 *s, uint32_t n_past);
 uint32_t orc_qwen3_n_past(const orc_qwen3 *s);
 /* mynah_slm_forward: 0, or -1 when the context is full. */
 int   orc_qwen3_forward(orc_qwen3 *s, uint32_t token, float *logits);
+
+/* The token sampler (src/sampler.h:16-43, src/sampler.c). */
+typedef struct {
+    float temp;
+    uint32_t top_k;
+    float top_p, min_p;
+    float repeat_penalty, freq_penalty, presence_penalty;
+    uint32_t penalty_window;
+    uint64_t seed;
+} orc_sampler_params;
+typedef struct orc_sampler orc_sampler;
+orc_sampler *orc_sampler_new(const orc_sampler_params *p, uint32_t vocab);
+void     orc_sampler_free(orc_sampler *s);
+void     orc_sampler_accept(orc_sampler *s, uint32_t token);
+uint32_t orc_sampler_sample(orc_sampler *s, float *logits);
 /* Greedy choice of src/sampler.c:122-129: first index of the maximum. */
 uint32_t orc_argmax(const float *logits, size_t n);
 

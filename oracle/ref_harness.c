@@ -181,3 +181,59 @@ int ref_qwen3_prompt_greedy(const char *path, const uint32_t *prompt, uint32_t n
     mynah_slm_free(m);
     return rc;
 }
+
+/* One run of the reference decoder on the model at `path`, for golden
+ * vectors: optional KV prefill (k/v [layer][n_prefill][kv_dim]), optional
+ * prompt (all but its last token fill the cache without logits, as
+ * src/generate.c:33-36 does; the last is step 0's input), then n_steps
+ * steps. Step i's input is inputs[i] when `inputs` is given (teacher
+ * forcing), else step 0's input is `first` (or the prompt's last token) and
+ * step i + 1's the greedy sample of step i (src/sampler.c:122-129).
+ * greedy_out[i] is the greedy sample of step i's logits either way;
+ * logits_out (n_steps x vocab, optional) gets every step's logits. */
+int ref_qwen3_run(const char *path, const float *k_prefill, const float *v_prefill,
+                  uint32_t n_prefill, const uint32_t *prompt, uint32_t n_prompt, uint32_t first,
+                  const uint32_t *inputs, uint32_t n_steps, uint32_t n_ctx, int threads,
+                  uint32_t *greedy_out, float *logits_out, char *err, size_t errsz) {
+    mynah_slm_threads_init(threads);
+    mynah_slm_model_t *m = mynah_slm_load(path, err, errsz);
+    if (m == NULL) return -1;
+    mynah_slm_state st;
+    if (mynah_slm_state_init(&st, m, n_ctx, err, errsz) != 0) {
+        mynah_slm_free(m);
+        return -1;
+    }
+    const mynah_slm_config *c = mynah_slm_model_config(m);
+    if (n_prefill > 0) {
+        const size_t per_layer = (size_t)st.n_ctx * c->kv_dim;
+        const size_t row = (size_t)n_prefill * c->kv_dim;
+        for (uint32_t l = 0; l < c->n_layers; l++) {
+            memcpy(st.k_cache + l * per_layer, k_prefill + l * row, row * sizeof(float));
+            memcpy(st.v_cache + l * per_layer, v_prefill + l * row, row * sizeof(float));
+        }
+        st.n_past = n_prefill;
+    }
+    mynah_slm_sampler_params p;
+    memset(&p, 0, sizeof p);
+    p.temp = 0.0f;
+    p.top_p = 1.0f;
+    p.repeat_penalty = 1.0f;
+    mynah_slm_sampler *sam = mynah_slm_sampler_new(&p, c->vocab_size);
+    int rc = sam ? 0 : -1;
+    for (uint32_t i = 0; i + 1 < n_prompt && rc == 0; i++)
+        if (mynah_slm_forward(&st, prompt[i], NULL) != 0) rc = -1;
+    uint32_t tok = n_prompt > 0 ? prompt[n_prompt - 1] : first;
+    for (uint32_t i = 0; i < n_steps && rc == 0; i++) {
+        if (inputs) tok = inputs[i];
+        if (mynah_slm_forward(&st, tok, st.logits) != 0) { rc = -1; break; }
+        if (logits_out)
+            memcpy(logits_out + (size_t)i * c->vocab_size, st.logits, c->vocab_size * sizeof(float));
+        tok = mynah_slm_sample(sam, st.logits);
+        greedy_out[i] = tok;
+    }
+    if (rc != 0) snprintf(err, errsz, "forward failed");
+    if (sam) mynah_slm_sampler_free(sam);
+    mynah_slm_state_free(&st);
+    mynah_slm_free(m);
+    return rc;
+}

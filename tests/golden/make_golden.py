@@ -18,6 +18,14 @@ records a SHA-256 of the input bytes so generator drift is detected):
   qwen3_tiny.npz     3-layer model: 32 greedy steps, first-step logits
   qwen3_06b.npz      configs[2]: 0.6B, KV prefill 512, 64 greedy steps,
                      first-step logits' top 64 and the SHA-256 of all of them
+  qwen3_06b_forced.npz  configs[2]'s model and KV prefill, 64 teacher-forced
+                     steps (uniform random inputs): every step's greedy id,
+                     top-64 logits, every 293rd logit and SHA-256
+                     (`--only forced` writes just this file)
+  qwen3_4b_c5.npz    configs[4] end to end (2048-token prompt, 256 greedy
+                     steps): every step's greedy id, the top-64 logits of
+                     seven snapshot steps (`--only c5full`; not part of the
+                     default run: about ten minutes of CPU)
   qwen3_4b_prompt.npz  configs[4]'s model (Qwen3-4B): the first 8 prompt ids,
                      prefill + 8 greedy steps, the first step's logits' top 64
                      (`--only c5` writes just this file)
@@ -83,6 +91,53 @@ def golden_c5(ref) -> None:
     np.savez_compressed(os.path.join(HERE, "qwen3_4b_prompt.npz"), prompt=prompt.astype(np.uint32),
                         tokens=np.array(toks, np.uint32), top_ids=top.astype(np.uint32),
                         top_vals=lg[top], logits0_sha=np.array(sha(lg)),
+                        blob_sha=np.array(sha(model.blob)))
+
+
+def step_summary(lg: np.ndarray, stride: int):
+    """Top-64 ids (stable, descending), their values, every `stride`-th
+    logit and the SHA-256 of one step's logits."""
+    top = np.argsort(-lg, kind="stable")[:64]
+    return top.astype(np.uint32), lg[top], lg[::stride].copy(), sha(lg)
+
+
+def golden_forced(ref) -> None:
+    """configs[2]'s model, KV prefill and 64 teacher-forced steps with uniform
+    random inputs: every step's logits summarised, and its greedy id."""
+    shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_FORCED_STEPS
+    model = O.SynthModel(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    inputs = CF.forced_inputs(O.uniform, O.substream, shape.vocab, steps)
+    greedy, lg = O.ref_run(ref, model, npre + steps + 1, steps, k=k, v=v, n_prefill=npre,
+                           inputs=inputs)
+    parts = [step_summary(lg[i], CF.FORCED_SAMPLE_STRIDE) for i in range(steps)]
+    np.savez_compressed(os.path.join(HERE, "qwen3_06b_forced.npz"),
+                        inputs=inputs.astype(np.uint32), greedy=np.array(greedy, np.uint32),
+                        top_ids=np.stack([p[0] for p in parts]),
+                        top_vals=np.stack([p[1] for p in parts]),
+                        sample=np.stack([p[2] for p in parts]),
+                        logits_sha=np.array([p[3] for p in parts]),
+                        blob_sha=np.array(sha(model.blob)))
+
+
+def golden_c5_full(ref) -> None:
+    """configs[4] end to end: the 2048-token prompt and 256 greedy steps on
+    Qwen3-4B, the greedy ids of every step and the top-64 logits (plus every
+    293rd logit) of the snapshot steps."""
+    shape = CF.QWEN3_4B
+    model = O.SynthModel(shape, 0)
+    prompt = CF.c5_prompt(O.uniform, O.substream, shape.vocab, CF.C5_PROMPT)
+    steps = CF.C5_STEPS
+    greedy, lg = O.ref_run(ref, model, CF.C5_PROMPT + steps + 1, steps, prompt=prompt)
+    parts = [step_summary(lg[i], CF.FORCED_SAMPLE_STRIDE) for i in CF.C5_SNAPSHOT_STEPS]
+    np.savez_compressed(os.path.join(HERE, "qwen3_4b_c5.npz"),
+                        prompt_sha=np.array(sha(prompt.astype(np.uint32))),
+                        greedy=np.array(greedy, np.uint32),
+                        snapshot_steps=np.array(CF.C5_SNAPSHOT_STEPS, np.uint32),
+                        top_ids=np.stack([p[0] for p in parts]),
+                        top_vals=np.stack([p[1] for p in parts]),
+                        sample=np.stack([p[2] for p in parts]),
+                        logits_sha=np.array([p[3] for p in parts]),
                         blob_sha=np.array(sha(model.blob)))
 
 
@@ -250,6 +305,7 @@ def main() -> int:
                         first=np.array(first), logits0_sha=np.array(sha(lg)),
                         top_ids=top.astype(np.uint32), top_vals=lg[top],
                         blob_sha=np.array(sha(model.blob)))
+    golden_forced(ref)
     golden_adjacent(ref)
     r8 = O.load_ref_int8()
     if r8 is not None:
@@ -268,6 +324,16 @@ if __name__ == "__main__":
         r = O.load_ref()
         assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
         golden_adjacent(r)
+        sys.exit(0)
+    if sys.argv[1:] == ["--only", "forced"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_forced(r)
+        sys.exit(0)
+    if sys.argv[1:] == ["--only", "c5full"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_c5_full(r)
         sys.exit(0)
     if sys.argv[1:] == ["--only", "c5"]:
         r = O.load_ref()

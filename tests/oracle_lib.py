@@ -54,6 +54,20 @@ class RefTensor(C.Structure):
                 ("offset", C.c_uint64), ("shard", C.c_uint32)]
 
 
+class SamplerParams(C.Structure):
+    """mynah_slm_sampler_params (src/sampler.h:16-30) = orc_sampler_params."""
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("min_p", C.c_float), ("repeat_penalty", C.c_float), ("freq_penalty", C.c_float),
+                ("presence_penalty", C.c_float), ("penalty_window", C.c_uint32),
+                ("seed", C.c_uint64)]
+
+
+def sampler_params(temp=0.0, top_k=0, top_p=1.0, min_p=0.0, repeat_penalty=1.0,
+                   freq_penalty=0.0, presence_penalty=0.0, penalty_window=64, seed=0):
+    return SamplerParams(temp, top_k, top_p, min_p, repeat_penalty, freq_penalty,
+                         presence_penalty, penalty_window, seed)
+
+
 class RefConfig(C.Structure):
     """mynah_slm_config (src/model.h:25-48)."""
     _fields_ = [("arch", C.c_char * 32)] + \
@@ -83,8 +97,13 @@ def _load_oracle() -> C.CDLL:
         "orc_qwen3_k_cache": (C.POINTER(C.c_float), [_P]),
         "orc_qwen3_v_cache": (C.POINTER(C.c_float), [_P]),
         "orc_qwen3_set_n_past": (None, [_P, C.c_uint32]),
+        "orc_qwen3_n_past": (C.c_uint32, [_P]),
         "orc_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
         "orc_argmax": (C.c_uint32, [_P, _SZ]),
+        "orc_sampler_new": (_P, [C.POINTER(SamplerParams), C.c_uint32]),
+        "orc_sampler_free": (None, [_P]),
+        "orc_sampler_accept": (None, [_P, C.c_uint32]),
+        "orc_sampler_sample": (C.c_uint32, [_P, _P]),
         "orc_q8_quantize_block": (C.c_float, [_P, _P, _P]),
         "orc_q4k_int8_dot": (C.c_int32, [_P, _P, C.c_int]),
         "orc_q5k_int8_dot": (C.c_int32, [_P, _P, C.c_int]),
@@ -129,6 +148,9 @@ def load_ref():
                                        C.c_uint32, C.c_int, _P, _P, C.c_char_p, _SZ]),
         "ref_qwen3_prompt_greedy": (C.c_int, [C.c_char_p, _P, C.c_uint32, C.c_uint32, C.c_uint32,
                                               C.c_int, _P, _P, C.c_char_p, _SZ]),
+        "ref_qwen3_run": (C.c_int, [C.c_char_p, _P, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32,
+                                    _P, C.c_uint32, C.c_uint32, C.c_int, _P, _P, C.c_char_p,
+                                    _SZ]),
         # ingot's GGUF reader (third_party/ingot/include/ingot/gguf.h:60-130)
         "ingot_gguf_open": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
         "ingot_gguf_close": (None, [_P]),
@@ -143,6 +165,11 @@ def load_ref():
         "ingot_kv_f64": (C.c_int, [_P, C.POINTER(C.c_double)]),
         "ingot_kv_str": (C.c_int, [_P, C.POINTER(C.c_char_p)]),
         "ingot_kv_arr_len": (C.c_int, [_P, C.POINTER(C.c_uint64)]),
+        # the sampler (src/sampler.h:33-43)
+        "mynah_slm_sampler_new": (_P, [C.POINTER(SamplerParams), C.c_uint32]),
+        "mynah_slm_sampler_free": (None, [_P]),
+        "mynah_slm_sampler_accept": (None, [_P, C.c_uint32]),
+        "mynah_slm_sample": (C.c_uint32, [_P, _P]),
         # the loader (src/model.h:60-90)
         "mynah_slm_load": (_P, [C.c_char_p, C.c_char_p, _SZ]),
         "mynah_slm_model_config": (C.POINTER(RefConfig), [_P]),
@@ -343,6 +370,65 @@ class OracleQwen3:
             self.h = None
 
 
+class OracleSampler:
+    """The restated sampler (oracle/sampler.c); `sample` and `accept` are C
+    function addresses a generation loop can call directly."""
+
+    def __init__(self, vocab: int, **params):
+        self.params = sampler_params(**params)
+        self.h = orc.orc_sampler_new(C.byref(self.params), vocab)
+        assert self.h, "orc_sampler_new failed"
+
+    def sample(self, logits: np.ndarray) -> int:
+        """Picks from `logits` (modified in place, as the reference does)."""
+        return int(orc.orc_sampler_sample(self.h, ptr(logits)))
+
+    def accept(self, token: int) -> None:
+        orc.orc_sampler_accept(self.h, token)
+
+    @staticmethod
+    def fn_addresses():
+        return (C.cast(orc.orc_sampler_sample, C.c_void_p).value,
+                C.cast(orc.orc_sampler_accept, C.c_void_p).value)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            orc.orc_sampler_free(self.h)
+            self.h = None
+
+
+def oracle_generate(orc_model: "OracleQwen3", prompt, max_new: int, eos=(), sampler=None,
+                    stop_after=None):
+    """src/generate.c:13-86 restated over the oracle decoder: the prompt's
+    tokens but the last fill the cache, each step forwards the current
+    token, picks (greedy, or `sampler`), accepts, stops on an EOS id (which
+    counts) or when `stop_after` ids have reached the token callback, and
+    ends early when the context is full. Returns the generated ids."""
+    for t in prompt[:-1]:
+        orc_model.forward(t)
+        if sampler:
+            sampler.accept(t)
+    nxt = prompt[-1]
+    if sampler:
+        sampler.accept(nxt)
+    out, shown = [], 0
+    for _ in range(max_new):
+        if orc.orc_qwen3_n_past(orc_model.h) >= orc_model.n_ctx:
+            break
+        lg = orc_model.forward(nxt)
+        tok = sampler.sample(lg) if sampler else int(orc.orc_argmax(ptr(lg), lg.size))
+        if sampler:
+            sampler.accept(tok)
+        out.append(tok)
+        if tok in eos:
+            break
+        shown += 1
+        if stop_after is not None and shown >= stop_after:
+            break
+        nxt = tok
+    return out
+
+
 def kv_prefill(substream_fn, shape, config_seed: int, n: int):
     """K and V prefill tensors [layer][n][kv_dim] of a config (see configs.py)."""
     import configs
@@ -386,6 +472,29 @@ def ref_greedy(ref, model: SynthModel, k, v, n_prefill, first, steps, n_ctx, thr
                                   ptr(tokens), ptr(logits), err, 512)
         assert rc == 0, err.value
     return [int(t) for t in tokens], logits
+
+
+def ref_run(ref, model: SynthModel, n_ctx, steps, k=None, v=None, n_prefill=0, prompt=None,
+            first=0, inputs=None, want_logits=True, threads=0):
+    """The compiled reference decoder (ref_harness.c ref_qwen3_run): greedy
+    ids of every step and, optionally, every step's logits [steps][vocab]."""
+    greedy = np.zeros(steps, np.uint32)
+    logits = np.zeros((steps, model.shape.vocab), np.float32) if want_logits else None
+    p = np.ascontiguousarray(prompt if prompt is not None else [], np.uint32)
+    f = np.ascontiguousarray(inputs, np.uint32) if inputs is not None else None
+    err = C.create_string_buffer(512)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf").encode()
+        rc = ref.ref_write_qwen3_gguf(path, C.byref(model.c_shape), model.table, model.count,
+                                      ptr(model.blob), n_ctx, err, 512)
+        assert rc == 0, err.value
+        rc = ref.ref_qwen3_run(path, ptr(k) if n_prefill else None,
+                               ptr(v) if n_prefill else None, n_prefill,
+                               ptr(p) if p.size else None, p.size, first,
+                               ptr(f) if f is not None else None, steps, n_ctx, threads,
+                               ptr(greedy), ptr(logits) if want_logits else None, err, 512)
+        assert rc == 0, err.value
+    return [int(t) for t in greedy], logits
 
 
 def ref_gguf_read(ref, path: str, keys=()):

@@ -1,0 +1,195 @@
+"""Multi-step decode parity that a collapsed greedy trajectory cannot hide.
+
+A random-init model's greedy ids settle on one token within a step or two,
+so a token list says little about the later steps. Here every step's input
+is drawn uniformly (teacher forcing), and the compiled reference's logits of
+every step are the golden vectors (tests/golden/qwen3_06b_forced.npz,
+configs[2]'s model and 512-position KV prefill, 64 steps):
+
+  * step by step through forward(): every step's logits at the golden top-64
+    ids and at every 293rd id within |gpu - ref| / max(1, |ref|) <= 1e-4,
+    and every step's greedy id, in both attention modes;
+  * through the replayed multi-step graphs (mynah_hip_qwen3_forced, eight
+    steps per graph launch, the position and step counters advancing on the
+    device): the greedy id of every step and the last step's logits against
+    the golden, and the whole KV cache and last logits bit-identical to the
+    step-by-step run;
+  * greedy generate() (graph-replayed) against forward() fed the same ids:
+    the KV cache and the next step's logits bit-identical.
+
+configs[4] (Qwen3-4B): the batched prefill of a 2048-token prompt in one
+2048-token chunk (the default chunk) against one decode step per token, K/V
+and next logits bit-identical; and, when the golden exists, the whole
+configs[4] run (2048-token prompt, 256 greedy steps) against the compiled
+reference: every greedy id and the logits of seven snapshot steps.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import configs as CF
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-4
+MODES = {"exact": 0, "split": 1}
+
+
+@pytest.fixture(scope="module")
+def M():
+    import mynah_amd
+    mynah_amd.check(mynah_amd.lib.mynah_hip_init(0), "init")
+    mynah_amd.check(mynah_amd.lib.mynah_hip_set_gemv_order(0), "order")
+    return mynah_amd
+
+
+@pytest.fixture(scope="module")
+def g06():
+    return np.load(os.path.join(GOLDEN, "qwen3_06b_forced.npz"), allow_pickle=False)
+
+
+@pytest.fixture(scope="module")
+def m06(M):
+    return M.SynthQwen3(CF.QWEN3_06B, 0)
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float((np.abs(got - ref) / np.maximum(1.0, np.abs(ref))).max())
+
+
+def check_step(lg, g, i, stride=CF.FORCED_SAMPLE_STRIDE):
+    """One step's logits against the golden summary of step i."""
+    e_top = rel_err(lg[g["top_ids"][i]], g["top_vals"][i])
+    e_smp = rel_err(lg[::stride], g["sample"][i])
+    assert e_top <= TOL and e_smp <= TOL, f"step {i}: top {e_top:.2e}, sample {e_smp:.2e}"
+    return max(e_top, e_smp)
+
+
+def decoder_06b(M, model, mode):
+    k, v = O.kv_prefill(O.substream, CF.QWEN3_06B, 0, CF.C3_PREFILL)
+    dec = M.Qwen3Decoder(model, CF.C3_PREFILL + CF.C3_FORCED_STEPS + 1)
+    dec.set_attention(mode)
+    dec.set_kv(k, v, CF.C3_PREFILL)
+    return dec
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_06b_forced_every_step_stepwise(M, m06, g06, mode):
+    print(f"[case] 0.6B teacher-forced stepwise attention={mode}", flush=True)
+    assert hashlib.sha256(m06.blob.tobytes()).hexdigest() == str(g06["blob_sha"])
+    dec = decoder_06b(M, m06, MODES[mode])
+    inputs = [int(t) for t in g06["inputs"]]
+    assert inputs == [int(t) for t in CF.forced_inputs(M.synth_uniform, M.substream,
+                                                       CF.QWEN3_06B.vocab, len(inputs))]
+    worst = 0.0
+    for i, tok in enumerate(inputs):
+        lg = dec.forward(tok)
+        worst = max(worst, check_step(lg, g06, i))
+        assert int(np.argmax(lg)) == int(g06["greedy"][i]), f"step {i}"
+    print(f"0.6B forced ({mode}): worst logit error {worst:.2e} over {len(inputs)} steps")
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_06b_forced_graph_replay(M, m06, g06, mode):
+    print(f"[case] 0.6B teacher-forced graph attention={mode}", flush=True)
+    inputs = [int(t) for t in g06["inputs"]]
+    n = len(inputs)
+    dec = decoder_06b(M, m06, MODES[mode])
+    greedy, last = dec.forced(inputs)
+    assert dec.uses_graph
+    assert greedy == [int(t) for t in g06["greedy"]]
+    check_step(last, g06, n - 1)
+    kg, vg = dec.get_kv(CF.C3_PREFILL + n)
+    ref = decoder_06b(M, m06, MODES[mode])
+    for tok in inputs:
+        lg = ref.forward(tok)
+    ks, vs = ref.get_kv(CF.C3_PREFILL + n)
+    assert np.array_equal(kg.view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(vg.view(np.uint32), vs.view(np.uint32))
+    assert np.array_equal(last.view(np.uint32), lg.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_06b_generate_state_equals_stepwise(M, m06, mode):
+    """24 greedy steps as three 8-step graph launches, then the cache and
+    the next step's logits against forward() fed the same ids."""
+    print(f"[case] 0.6B generate state attention={mode}", flush=True)
+    steps = 24
+    first = O.first_token(0, CF.QWEN3_06B.vocab)
+    dec = decoder_06b(M, m06, MODES[mode])
+    toks, _ = dec.generate(first, steps)
+    ref = decoder_06b(M, m06, MODES[mode])
+    for tok in [first] + toks[:-1]:
+        ref.forward(tok, want_logits=False)
+    n = CF.C3_PREFILL + steps
+    assert dec.n_past == ref.n_past == n
+    kg, vg = dec.get_kv(n)
+    ks, vs = ref.get_kv(n)
+    assert np.array_equal(kg.view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(vg.view(np.uint32), vs.view(np.uint32))
+    a, b = dec.forward(toks[-1]), ref.forward(toks[-1])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_qwen3_4b_prefill_2048_equals_stepwise(M):
+    """configs[4]'s prompt through the batched prefill (one chunk of the
+    default 2048) and through 2047 decode steps: K/V and the last prompt
+    token's logits bit-identical."""
+    print("[case] 4B 2048-token prefill vs steps", flush=True)
+    shape = CF.QWEN3_4B
+    model = M.SynthQwen3(shape, 0)
+    prompt = [int(t) for t in CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)]
+    n = len(prompt)
+    a = M.Qwen3Decoder(model, n + 1)
+    a.prefill(prompt[:-1])
+    la = a.forward(prompt[-1])
+    ka, va = a.get_kv(n)
+    a.close()
+    b = M.Qwen3Decoder(model, n + 1)
+    for tok in prompt[:-1]:
+        b.forward(tok, want_logits=False)
+    lb = b.forward(prompt[-1])
+    kb, vb = b.get_kv(n)
+    b.close()
+    assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32))
+    assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+C5_GOLDEN = os.path.join(GOLDEN, "qwen3_4b_c5.npz")
+
+
+@pytest.mark.skipif(not os.path.exists(C5_GOLDEN), reason="configs[4] golden not written")
+@pytest.mark.parametrize("mode", MODES)
+def test_qwen3_4b_configs4_against_reference(M, mode):
+    """configs[4] end to end: the 2048-token prompt (batched prefill), 256
+    greedy steps graph-replayed, every id against the compiled reference;
+    then the same steps teacher-forced with those ids in segments ending at
+    the snapshot steps, whose logits must match the reference's."""
+    print(f"[case] 4B configs[4] attention={mode}", flush=True)
+    g = np.load(C5_GOLDEN, allow_pickle=False)
+    shape = CF.QWEN3_4B
+    model = M.SynthQwen3(shape, 0)
+    prompt = [int(t) for t in CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)]
+    steps = CF.C5_STEPS
+    dec = M.Qwen3Decoder(model, len(prompt) + steps + 1)
+    dec.set_attention(MODES[mode])
+    got, pre_ms, dec_ms = dec.prompt(prompt, steps)
+    assert got == [int(t) for t in g["greedy"]]
+    print(f"4B configs[4] ({mode}): prefill {pre_ms:.1f} ms, {steps / dec_ms * 1e3:.0f} tok/s")
+    dec.reset()
+    dec.prefill(prompt[:-1])
+    inputs = [prompt[-1]] + got[:-1]
+    done = 0
+    for j, stop in enumerate(int(s) for s in g["snapshot_steps"]):
+        ids, last = dec.forced(inputs[done:stop + 1])
+        assert ids == got[done:stop + 1]
+        check_step(last, g, j)
+        done = stop + 1

@@ -143,10 +143,11 @@ def test_gemm_ragged_tiles(M, qtype, rows, cols, tokens):
     assert same(M.matmat(qtype, w, rows, cols, x, tokens), O.matmat(qtype, w, rows, cols, x, tokens))
 
 
-@pytest.mark.parametrize("name", ["q4k_kv_2048x2048", "q6k_down_2048x6144"])
+@pytest.mark.parametrize("name", [m.name for m in CF.C4])
 def test_gemm_configs3_shapes(M, name):
-    """configs[3] prefill GEMMs (512 tokens) against the oracle's threaded
-    batched path, bit for bit."""
+    """All six configs[3] prefill GEMMs (512 tokens) against the oracle's
+    threaded batched path, bit for bit."""
+    print(f"[case] configs[3] GEMM {name}", flush=True)
     m = next(m for m in CF.C4 if m.name == name)
     i = CF.C4.index(m)
     ws, xs = CF.matrix_seeds(M.substream, 0, i)

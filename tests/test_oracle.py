@@ -267,8 +267,6 @@ def test_argument_guards():
     assert f(99, O.ptr(w), 2, 256, O.ptr(x), O.ptr(y)) == -1
 
 
-@pytest.mark.skipif(not os.environ.get("MYNAH_SLOW_TESTS"),
-                    reason="2.5 GB model on the CPU: set MYNAH_SLOW_TESTS=1")
 def test_qwen3_4b_prompt_golden():
     """The oracle's forward at Qwen3-4B scale (36 layers, 4 query heads per
     key head) against the compiled reference's prompt prefill + greedy run:
