@@ -195,6 +195,22 @@ int mynah_hip_q4k_int8_dev(const void *w, size_t rows, size_t cols, const int8_t
                            const float *xs, const int32_t *xsum, float *y, size_t tokens,
                            void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory — code under HIP graph (stream) capture, serving loops that must
+ * not allocate, harnesses that forbid hipMalloc: the int8 lane's product
+ * (what mynah_hip_matmat_dev computes for Q4_K / Q5_K with the lane on:
+ * activations quantised per 256 values, integer dots, the reference's
+ * epilogue; tokens == 1 the Q4_K matvec epilogue, Q5_K needs tokens >= 2),
+ * whatever the lane's mode, with its quantised activations in a fixed
+ * device workspace of MYNAH_SCRATCH_BYTES (8 MiB, csrc/scratch.h) that each
+ * GPU holds until the process ends. Allocates nothing and calls no
+ * allocating routine. Refuses (-1, nothing launched) a workspace above the
+ * limit: tokens * cols * 1.140625 bytes, about 7.35 M values. Calls that
+ * overlap on one GPU share the workspace and race; serialise them (one
+ * stream, or events). Device pointers; asynchronous on `stream`. */
+int mynah_hip_int8_product_noalloc_dev(int type, const void *w, size_t rows, size_t cols,
+                                       const float *x, float *y, size_t tokens, void *stream);
+
 /* Plain device memory (256-byte aligned) and copies; *_async take a stream. */
 void *mynah_hip_alloc(size_t bytes);
 int   mynah_hip_free(void *p);

@@ -192,6 +192,42 @@ int mynah_int8_product(mynah_device *d, int type, const void *w, size_t rows, si
 
 /* ── public entry points ─────────────────────────────────────────────────── */
 
+/* The int8 product with its workspace in the device's fixed array (the
+ * address the runtime resolved when it loaded the code object): no
+ * allocation of any kind, so it may run under stream capture or in a loop
+ * that must not allocate. Calls that overlap on one device share the array
+ * and race. */
+int mynah_hip_int8_product_noalloc_dev(int type, const void *w, size_t rows, size_t cols,
+                                       const float *x, float *y, size_t tokens, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (w == NULL || x == NULL || y == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    if (check_kq(type, w, rows, cols, tokens) != 0) return -1;
+    if (tokens > (SIZE_MAX / 2) / cols) {
+        mynah_set_error("size overflow");
+        return -1;
+    }
+    size_t o_xs, o_sum;
+    const size_t bytes = ws_bytes(tokens, cols, &o_xs, &o_sum);
+    if (d->scratch == NULL || bytes > d->scratch_bytes) {
+        mynah_set_error("int8 workspace of %zu bytes (%zu tokens x %zu columns) exceeds the "
+                        "fixed %zu-byte scratch", bytes, tokens, cols, d->scratch_bytes);
+        return -1;
+    }
+    hipStream_t s = mynah_stream_or_default(d, stream);
+    unsigned char *ws = d->scratch;
+    int rc = mynah_q8_quantize_launch(d, x, tokens, cols, (int8_t *)ws, (float *)(ws + o_xs),
+                                      (int32_t *)(ws + o_sum), s);
+    if (rc == 0)
+        rc = mynah_q4k_int8_launch(d, type, w, rows, cols, (const int8_t *)ws,
+                                   (const float *)(ws + o_xs), (const int32_t *)(ws + o_sum), y,
+                                   tokens, s);
+    return rc;
+}
+
 int mynah_hip_q8_quantize_dev(const float *x, size_t tokens, size_t cols, int8_t *xq, float *xs,
                               int32_t *xsum, void *stream) {
     mynah_device *d = mynah_dev();

@@ -29,8 +29,22 @@
 //
 // SPDX-License-Identifier: MIT
 #include "common.hip.h"
+#include "scratch.h"
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// The workspace of the allocation-free int8 product: one fixed array per
+// device (each GPU that loads the code object holds its own copy until the
+// process ends). The host resolves its device address by name when it loads
+// the code object and passes that address to the kernels below as their xq /
+// xs / xsum operands; nothing reads it before the quantiser has written it.
+// No kernel names it (they take its address as an argument), so `used`
+// keeps it in the code object's symbol table; the braces make this a
+// definition with C linkage (a bare `extern "C"` would only declare it).
+extern "C" {
+__device__ __attribute__((aligned(256), used, visibility("default")))
+unsigned char mynah_scratch[MYNAH_SCRATCH_BYTES];
+}
 
 // The (scale, min) pair of sub-block j from the 12 scale bytes s0..s2
 // (kernels.c:83-92, scale_min), selects only.

@@ -10,6 +10,7 @@
 #define _GNU_SOURCE
 #include "kernels_hip.h"
 #include "runtime_internal.h"
+#include "scratch.h"
 
 #include <pthread.h>
 #include <stdarg.h>
@@ -65,6 +66,23 @@ static int load_device(int dev) {
                             hipGetErrorString(e));
             return -1;
         }
+    }
+    /* The allocation-free entry point's workspace is a device array of the
+     * code object; its address on this device (each device has its own
+     * copy) is looked up here, once, with the device current. Host code uses
+     * only this address, never the symbol. */
+    {
+        hipDeviceptr_t p = 0;
+        size_t bytes = 0;
+        HIP_OK(hipModuleGetGlobal(&p, &bytes, d->module, "mynah_scratch"),
+               "hipModuleGetGlobal(mynah_scratch)");
+        if (p == 0 || bytes != MYNAH_SCRATCH_BYTES) {
+            mynah_set_error("mynah_scratch: %zu bytes, expected %u", bytes,
+                            (unsigned)MYNAH_SCRATCH_BYTES);
+            return -1;
+        }
+        d->scratch = (unsigned char *)p;
+        d->scratch_bytes = bytes;
     }
     HIP_OK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
     if (hipDeviceGetAttribute(&d->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||

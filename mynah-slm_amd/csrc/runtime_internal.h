@@ -73,6 +73,10 @@ typedef struct {
     hipFunction_t fn[MYNAH_K_COUNT];
     hipStream_t stream;
     int cus;                  /* compute units (sizes the persistent launches) */
+    /* Device address and size of the code object's fixed workspace
+     * (mynah_scratch, int8.hip), resolved once when the module loads. */
+    unsigned char *scratch;
+    size_t scratch_bytes;
 } mynah_device;
 
 void mynah_set_error(const char *fmt, ...);

@@ -76,6 +76,8 @@ def _load() -> C.CDLL:
         "mynah_hip_int8": (C.c_int, []),
         "mynah_hip_q8_quantize_dev": (C.c_int, [_P, _SZ, _SZ, _P, _P, _P, _P]),
         "mynah_hip_q4k_int8_dev": (C.c_int, [_P, _SZ, _SZ, _P, _P, _P, _P, _SZ, _P]),
+        "mynah_hip_int8_product_noalloc_dev": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ,
+                                                         _P]),
         "mynah_hip_init": (C.c_int, [C.c_int]),
         "mynah_hip_last_error": (C.c_char_p, []),
         "mynah_hip_register": (C.c_int, [_P, _SZ]),
