@@ -380,7 +380,8 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             const float *cpm = pm, *cpo = po;
             const double *cpl = pl;
             void *args2[] = {&pos, &cpm, &cpl, &cpo, &out, &nchm, &group};
-            rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_heads, 1, 64, 0, st, args2);
+            rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_heads, 1, 256,
+                              (size_t)s->nch_max * sizeof(float), st, args2);
         } else {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;

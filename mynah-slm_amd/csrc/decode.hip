@@ -322,7 +322,6 @@ mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scor
 // [n_kv][nch_max][group][128].
 #define AS_CH 32                                  // = MYNAH_AS_CH (runtime_internal.h)
 #define AS_PASS ((AS_CH + 15) / 16)                 // K passes of 16 positions (group >= 2)
-#define AS_MAXP 1024                                // group * chunks (n_ctx <= 4096)
 // Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
 // x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
 // head_norm_rope, with the pair (i, i + 64) rotated in registers.
@@ -472,88 +471,97 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     }
 }
 
-// Grid n_heads, block 64: one wave combines the chunks of one query head,
-// lane l holding dimensions l and l + 64. M = max m_c and the double sum
-// L = sum_c expf(m_c - M) l_c are wave reductions (lane c holds chunks c
-// and c + 64, in that order);
-// then o = fma(expf(m_c - M) * inv, o_c, o) in chunk order, inv =
-// (float)(1 / L).
-#define AC_MAXC 128                                 // chunks (n_ctx <= 4096)
-extern "C" __global__ void __launch_bounds__(64)
+// Grid n_heads, block 256: four waves combine the chunks of one query head.
+// Thread c (and c + 256, ...) takes chunk c's max and exp sum: M = max m_c,
+// w_c = expf(m_c - M) (kept in LDS), L = sum_c w_c l_c in double (each
+// wave's share, then the four shares in wave order); inv = (float)(1 / L).
+// Wave w then sums o_w = fma(w_c * inv, o_c, o_w) over its chunks c = w,
+// w + 4, ... in order, lane l holding dimensions l and l + 64, and the four
+// partial vectors are added in wave order. The first AC_PRE chunks of every
+// wave are loaded before the position arrives (every slot below nch_max is
+// in bounds), so nearly all partials are in flight at once. Dynamic LDS:
+// nch_max floats.
+#define AC_WAVES 4
+#define AC_PRE 16
+extern "C" __global__ void __launch_bounds__(256)
 mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                    const double *__restrict__ pl, const float *__restrict__ po,
                    float *__restrict__ out, uint32_t nch_max, uint32_t group) {
 #pragma clang fp contract(off)
-    __shared__ float wsc[AC_MAXC];
+    extern __shared__ float wsc[];
+    __shared__ float smax[AC_WAVES];
+    __shared__ double ssum[AC_WAVES];
+    __shared__ float spart[AC_WAVES - 1][128];
     const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
-    const uint32_t lane = threadIdx.x;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const size_t base = (size_t)kvh * nch_max * group + h;    // slot of chunk c: base + c * group
     const float *pob = po + base * 128u + lane;
     const size_t cstride = (size_t)group * 128u;
-    // Every slot below nch_max is in bounds, so the partials are loaded
-    // before the position arrives and masked by the live chunk count after:
-    // lane c holds chunks c and c + 64 (nch_max <= AC_MAXC = 128), and the
-    // first 32 weighted partials of each dimension are in flight meanwhile.
-    const float pm0 = lane < nch_max ? pm[base + (size_t)lane * group] : 0.0f;
-    const float pm1 = lane + 64u < nch_max ? pm[base + (size_t)(lane + 64u) * group] : 0.0f;
-    const double pl0 = lane < nch_max ? pl[base + (size_t)lane * group] : 0.0;
-    const double pl1 = lane + 64u < nch_max ? pl[base + (size_t)(lane + 64u) * group] : 0.0;
-    float pv[32][2];
+    float pv[AC_PRE][2];
 #pragma unroll
-    for (int u = 0; u < 32; u++) {
-        pv[u][0] = (uint32_t)u < nch_max ? pob[(size_t)u * cstride] : 0.0f;
-        pv[u][1] = (uint32_t)u < nch_max ? pob[(size_t)u * cstride + 64u] : 0.0f;
+    for (uint32_t k = 0; k < AC_PRE; k++) {
+        const uint32_t c = wave + AC_WAVES * k;
+        pv[k][0] = c < nch_max ? pob[(size_t)c * cstride] : 0.0f;
+        pv[k][1] = c < nch_max ? pob[(size_t)c * cstride + 64u] : 0.0f;
     }
     const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
-    float M = -__builtin_inff();
-    if (lane < nch) M = fmaxf(M, pm0);
-    if (lane + 64u < nch) M = fmaxf(M, pm1);
-    M = wave_max_f(M);
-    double L = 0.0;
-    if (lane < nch) {
-        const float w = expf(pm0 - M);
-        wsc[lane] = w;
-        L += (double)w * pl0;
-    }
-    if (lane + 64u < nch) {
-        const float w = expf(pm1 - M);
-        wsc[lane + 64u] = w;
-        L += (double)w * pl1;
-    }
-    L = wave_sum_d(L);
-    const float inv = (float)(1.0 / L);
+    float m = -__builtin_inff();
+    for (uint32_t c = tid; c < nch; c += 256u) m = fmaxf(m, pm[base + (size_t)c * group]);
+    m = wave_max_f(m);
+    if (lane == 0) smax[wave] = m;
     __syncthreads();
+    const float M = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    double l = 0.0;
+    for (uint32_t c = tid; c < nch; c += 256u) {
+        const float w = expf(pm[base + (size_t)c * group] - M);
+        wsc[c] = w;
+        l += (double)w * pl[base + (size_t)c * group];
+    }
+    l = wave_sum_d(l);
+    if (lane == 0) ssum[wave] = l;
+    __syncthreads();
+    const float inv = (float)(1.0 / (((ssum[0] + ssum[1]) + ssum[2]) + ssum[3]));
     float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 32; u++) {          // static indices keep pv in registers
-        if ((uint32_t)u < nch) {
-            const float sc = wsc[u] * inv;
-            o0 = __builtin_fmaf(sc, pv[u][0], o0);
-            o1 = __builtin_fmaf(sc, pv[u][1], o1);
+    for (uint32_t k = 0; k < AC_PRE; k++) {     // static indices keep pv in registers
+        const uint32_t c = wave + AC_WAVES * k;
+        if (c < nch) {
+            const float sc = wsc[c] * inv;
+            o0 = __builtin_fmaf(sc, pv[k][0], o0);
+            o1 = __builtin_fmaf(sc, pv[k][1], o1);
         }
     }
-    uint32_t c = nch < 32u ? nch : 32u;
-    for (; c + 8u <= nch; c += 8u) {
-        float a[8], b[8];
+    uint32_t c = wave + AC_WAVES * AC_PRE;
+    for (; c + AC_WAVES * 3u < nch; c += AC_WAVES * 4u) {
+        float a[4], b[4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            a[u] = pob[(size_t)(c + u) * cstride];
-            b[u] = pob[(size_t)(c + u) * cstride + 64u];
+        for (uint32_t u = 0; u < 4; u++) {
+            a[u] = pob[(size_t)(c + AC_WAVES * u) * cstride];
+            b[u] = pob[(size_t)(c + AC_WAVES * u) * cstride + 64u];
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float sc = wsc[c + u] * inv;
+        for (uint32_t u = 0; u < 4; u++) {
+            const float sc = wsc[c + AC_WAVES * u] * inv;
             o0 = __builtin_fmaf(sc, a[u], o0);
             o1 = __builtin_fmaf(sc, b[u], o1);
         }
     }
-    for (; c < nch; c++) {
+    for (; c < nch; c += AC_WAVES) {
         const float sc = wsc[c] * inv;
         o0 = __builtin_fmaf(sc, pob[(size_t)c * cstride], o0);
         o1 = __builtin_fmaf(sc, pob[(size_t)c * cstride + 64u], o1);
     }
-    out[(size_t)head * 128u + lane] = o0;
-    out[(size_t)head * 128u + 64u + lane] = o1;
+    if (wave > 0) {
+        spart[wave - 1][lane] = o0;
+        spart[wave - 1][lane + 64u] = o1;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        o0 = ((o0 + spart[0][lane]) + spart[1][lane]) + spart[2][lane];
+        o1 = ((o1 + spart[0][lane + 64u]) + spart[1][lane + 64u]) + spart[2][lane + 64u];
+        out[(size_t)head * 128u + lane] = o0;
+        out[(size_t)head * 128u + 64u + lane] = o1;
+    }
 }
 
 

@@ -693,6 +693,71 @@ MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float 
     }
 }
 
+// Flat layout: the workgroup covers R = g.pad whole rows of its descriptor,
+// and thread f (f < R * Ut, stepping by blockDim.x) owns unit u = f % Ut of
+// row f / Ut, the units of a gate/up pair counted gate first. Every thread
+// that has a unit computes it whole, in the reference's order; the unit sums
+// of a row are folded in unit order by one thread (R <= 64: the first wave),
+// followed by the epilogues of group_split. Every lane busy but the last
+// few of the workgroup, and x staged once per R rows.
+template <int FMT, class RawT = Raw<FMT>>
+MYNAH_DEV void group_flat(const GemvDesc &g, uint32_t t, float *lds, double *shd) {
+#pragma clang fp contract(off)
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
+    const uint32_t R = g.pad;
+    const uint32_t U = g.units, Ut = g.w2 ? 2u * U : U, pstride = Ut | 1u;
+    const uint32_t row0 = (t - g.tile0) * R, nf = R * Ut;
+    constexpr uint32_t UB = RawT::BYTES;
+    uint32_t f = tid, rl = f / Ut, u = f - rl * Ut;
+    RawT raw;
+    auto load = [&]() {
+        const uint32_t row = row0 + rl;
+        const size_t roff = (size_t)(row < g.rows ? row : g.rows - 1u) * g.row_bytes;
+        raw.load(u < U ? g.w + roff + UB * u : g.w2 + roff + UB * (u - U));
+    };
+    if (f < nf) load();
+
+    // Prefetch what the epilogue reads (residual row, cache slot).
+    const uint32_t frow = row0 + tid;
+    const bool folds = tid < R && frow < g.rows;
+    float resv = 0.0f;
+    if (folds && g.res) resv = g.res[frow];
+    const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
+
+    const uint32_t cols = g.cols;
+    stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + R * pstride, shd);
+    __syncthreads();
+
+    float *part = lds + xpad_floats(cols);
+    while (f < nf) {
+        part[rl * pstride + u] = raw.sum(unit_x<FMT>(lds, u < U ? u : u - U));
+        f += nthr;
+        if (f < nf) {
+            rl = f / Ut;
+            u = f - rl * Ut;
+            load();
+        }
+    }
+    __syncthreads();
+
+    if (tid < 64u) {
+        float t1 = 0.0f, t2 = 0.0f, v = 0.0f;
+        if (folds) {
+            const float *pr = part + tid * pstride;
+            for (uint32_t q = 0; q < U; q++) t1 = t1 + pr[q];
+            for (uint32_t q = U; q < Ut; q++) t2 = t2 + pr[q];
+            v = t1;
+            if (g.w2) v = t1 * sigmoid_ref(t1) * t2;
+            else if (g.res) v = resv + t1;
+            g.y[yoff + frow] = v;
+        }
+        if (g.keys) {
+            const unsigned long long key = wave_max_u64(folds ? argmax_key(v, frow) : 0ull);
+            if (tid == 0) g.keys[t - g.tile0] = key;
+        }
+    }
+}
+
 // Q4_0 rows of a grouped launch. The planner gives a launch holding a Q4_0
 // matrix the shape K = 1, WS = 1, WR = 1 (one wave, 64 rows): lane = row,
 // whose single running sum goes through every block in order (a gate/up
@@ -759,7 +824,12 @@ mynah_gemv_group(const GemvGroup grp) {
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
     const GemvDesc &g = grp.d[i];
-    if (grp.shape & (1u << 24)) {
+    if (grp.shape & (1u << 25)) {
+        if (g.type == 12u) group_flat<12>(g, t, lds, shd);
+        else if (g.type == 13u) group_flat<13>(g, t, lds, shd);
+        else if (g.type == 14u) group_flat<14>(g, t, lds, shd);
+        else group_flat<8>(g, t, lds, shd);
+    } else if (grp.shape & (1u << 24)) {
         if (g.type == 12u) group_split<12, true>(g, t, grp.shape, lds, shd);
         else if (g.type == 13u) group_split<13, true>(g, t, grp.shape, lds, shd);
         else group_split<14, true>(g, t, grp.shape, lds, shd);
@@ -800,4 +870,26 @@ mynah_gemv_group_q6k(const GemvGroup grp) {
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
     group_split<14, false, RawQ6Lean>(grp.d[i], t, grp.shape, lds, shd);
+}
+
+// The flat layout for launches whose every matrix is Q4_K (up to 512
+// threads, six waves per SIMD) or Q6_K (the lean sum, five).
+extern "C" __global__ void __launch_bounds__(512, 6)
+mynah_gemv_flat_q4k(const GemvGroup grp) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ double shd[16];
+    const uint32_t t = blockIdx.x;
+    uint32_t i = 0;
+    while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
+    group_flat<12>(grp.d[i], t, lds, shd);
+}
+
+extern "C" __global__ void __launch_bounds__(512, 5)
+mynah_gemv_flat_q6k(const GemvGroup grp) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ double shd[16];
+    const uint32_t t = blockIdx.x;
+    uint32_t i = 0;
+    while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
+    group_flat<14, RawQ6Lean>(grp.d[i], t, lds, shd);
 }

@@ -380,6 +380,78 @@ static int gemv_stream_plan(const mynah_device *d, const mynah_gemv_group *grp, 
     return 0;
 }
 
+/* Flat layout: every thread of a T-thread workgroup owns one (row, unit)
+ * pair of R = min(64, T / units) whole rows (units of a gate/up pair
+ * counted twice). T is the multiple of 64 up to 1024 that scores best on
+ * lane use times CU coverage (min(1, workgroups / CUs)); among scores within
+ * 0.02 of the best the largest T wins, since each workgroup stages (and
+ * normalises) the whole input once. MYNAH_FLAT_T forces T. */
+static int gemv_flat_plan(const mynah_device *d, mynah_gemv_group *grp, gemv_plan *p) {
+    const long forced = env_long("MYNAH_FLAT_T", 0);
+    uint32_t max_ut = 1;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        const mynah_gemv_desc *g = &grp->d[i];
+        const uint32_t ut = g->w2 ? 2u * g->units : g->units;
+        if (ut > max_ut) max_ut = ut;
+    }
+    double score[17] = {0};
+    double best = -1.0;
+    for (uint32_t t = 64; t <= 1024; t += 64) {
+        if (t < max_ut || (forced > 0 && (long)t != forced)) continue;
+        uint64_t used = 0, wgs = 0;
+        for (uint32_t i = 0; i < grp->n; i++) {
+            const mynah_gemv_desc *g = &grp->d[i];
+            const uint32_t ut = g->w2 ? 2u * g->units : g->units;
+            uint32_t r = t / ut;
+            if (r > 64u) r = 64u;
+            const uint64_t tiles = (g->rows + r - 1u) / r;
+            wgs += tiles;
+            used += (uint64_t)r * ut * tiles;
+        }
+        const double cover = wgs >= (uint64_t)d->cus ? 1.0 : (double)wgs / (double)d->cus;
+        score[t / 64] = (double)used / ((double)t * (double)wgs) * cover;
+        if (score[t / 64] > best) best = score[t / 64];
+    }
+    if (best < 0.0) {
+        mynah_set_error("no flat layout for %u units per row", max_ut);
+        return -1;
+    }
+    uint32_t T = 64;
+    for (uint32_t t = 64; t <= 1024; t += 64)
+        if (score[t / 64] > 0.0 && score[t / 64] >= best - 0.02) T = t;
+    uint32_t tiles = 0;
+    size_t lds = 0;
+    int all_q4k = T <= 512u, all_q6k = T <= 512u;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        mynah_gemv_desc *g = &grp->d[i];
+        const uint32_t ut = g->w2 ? 2u * g->units : g->units;
+        uint32_t r = T / ut;
+        if (r > 64u) r = 64u;
+        g->pad = r;
+        g->tile0 = tiles;
+        tiles += (g->rows + r - 1u) / r;
+        const size_t need = ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
+                             (size_t)r * (ut | 1u) + (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
+        if (need > lds) lds = need;
+        all_q4k = all_q4k && g->type == MYNAH_Q4_K;
+        all_q6k = all_q6k && g->type == MYNAH_Q6_K;
+    }
+    if (lds > 60u * 1024u) {
+        mynah_set_error("input of this GEMV exceeds the LDS budget (%zu B)", lds);
+        return -1;
+    }
+    p->grid = tiles;
+    p->lds = lds;
+    p->threads = T;
+    p->shape = 1u << 25;
+    p->kernel = MYNAH_K_GEMV_GROUP;
+    if (env_long("MYNAH_GEMV_TYPED", 1) != 0) {
+        if (all_q4k) p->kernel = MYNAH_K_GEMV_FLAT_Q4K;
+        else if (all_q6k) p->kernel = MYNAH_K_GEMV_FLAT_Q6K;
+    }
+    return 0;
+}
+
 /* Plan a grouped GEMV in the given order (-1: the library's current one):
  * exact (lane = row x unit slot, unit sums folded in order; a single large
  * matrix with long rows takes the streaming kernel) or reordered (8-lane row
@@ -425,6 +497,10 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
     if (all_units > 32768u) split = 0;
     const char *env = getenv("MYNAH_GEMV_SPLIT");
     if (env != NULL) split = split && env[0] != '0';
+    /* The flat layout (gemv_exact.hip group_flat) for the one-lane exact
+     * kernels: MYNAH_GEMV_FLAT=0 keeps the slot layout below. */
+    if (exact && !split && !chain && env_long("MYNAH_GEMV_FLAT", 1) != 0)
+        return gemv_flat_plan(d, grp, p);
     uint32_t lk = 0, ws = 1, wr = 1, ks = 1, tile_rows;
     if (exact && split) {
         uint32_t k = 1;

@@ -29,6 +29,8 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
     X(MYNAH_K_GEMV_GROUP_Q6K, "mynah_gemv_group_q6k")  \
     X(MYNAH_K_GEMV_GROUP_Q4K, "mynah_gemv_group_q4k")  \
+    X(MYNAH_K_GEMV_FLAT_Q4K, "mynah_gemv_flat_q4k")    \
+    X(MYNAH_K_GEMV_FLAT_Q6K, "mynah_gemv_flat_q6k")    \
     X(MYNAH_K_GEMV_STREAM, "mynah_gemv_stream")        \
     X(MYNAH_K_GEMV_STREAM_CVT, "mynah_gemv_stream_cvt") \
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
@@ -133,7 +135,7 @@ typedef struct {
     unsigned long long *keys; /* one argmax key per workgroup tile when set */
     uint32_t ystride, rows, units, row_bytes, type, tile0, cols;
     float eps;
-    uint32_t pad;
+    uint32_t pad;            /* flat layout: rows per workgroup (set by the launch) */
 } mynah_gemv_desc;
 
 /* Host mirror of the streaming GEMV's descriptor (gemv_stream.hip
