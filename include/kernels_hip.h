@@ -223,6 +223,12 @@ int   mynah_hip_sync(void *stream);
 int   mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
 void *mynah_hip_stream(void);           /* the library's own stream */
 
+/* y[i] = expf(x[i]) for i < n with the bits of the reference's C library
+ * (glibc's expf, the exponential of the reference's softmax and sigmoid,
+ * src/kernels.c:193-220), which the decode step's softmax and SwiGLU use.
+ * Device pointers; asynchronous. */
+int   mynah_hip_expf_dev(const float *x, float *y, size_t n, void *stream);
+
 /* HIP events on a stream (NULL = the library's stream), for timing kernels
  * exactly where they are launched. Elapsed time in milliseconds. */
 void *mynah_hip_event_create(void);

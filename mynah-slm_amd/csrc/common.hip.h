@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mynah_expf.h"
+
 #define MYNAH_DEV static __device__ __forceinline__
 
 // Exact f16 -> f32 (v_cvt_f32_f16; HIP keeps f16 subnormals by default).

@@ -15,3 +15,12 @@ mynah_copy16(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n1
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
         dst[i] = src[i];
 }
+
+// y[i] = expf(x[i]) with the reference's C library bits (mynah_expf.h), for
+// callers that compute softmaxes beside the library and for its tests.
+extern "C" __global__ void __launch_bounds__(256)
+mynah_expf_map(const float *__restrict__ x, float *__restrict__ y, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        y[i] = mynah_expf(x[i]);
+}

@@ -93,6 +93,13 @@ struct mynah_qwen3 {
 enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_MULTI = 2 };
 #define STEP_BATCH 8u
 
+/* The largest context (positions) a state takes: 2^20, far beyond any Qwen3
+ * (40960), small enough that every offset fits 32 bits. */
+#define MYNAH_MAX_CTX (1u << 20)
+/* Exact attention keeps a key head's score rows (group * sstride floats) in
+ * LDS up to this size; longer contexts take the two-launch form. */
+#define EXACT_LDS_SCORES (48u * 1024u)
+
 static int fail(char *err, size_t errsz, const char *msg, const char *detail) {
     if (err && errsz) snprintf(err, errsz, "%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
     mynah_set_error("%s%s%s", msg, detail ? ": " : "", detail ? detail : "");
@@ -180,10 +187,13 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
         fail(err, errsz, "null argument", NULL);
         return NULL;
     }
+    /* Any context the model and HBM allow (src/arch_qwen3.c:89-131 takes any
+     * n_ctx): exact attention whose score rows fit the LDS keeps them there,
+     * longer ones run its two-launch form. */
     if (c->n_kv_heads == 0 || c->n_heads % c->n_kv_heads != 0 ||
         c->n_heads / c->n_kv_heads > 8 || c->n_heads / c->n_kv_heads < 2 || c->head_dim != 128 ||
         c->d_model % 256 != 0 || c->d_ff % 256 != 0 || c->vocab % 4 != 0 ||
-        n_ctx > 4096 || (size_t)(c->n_heads / c->n_kv_heads) * ((n_ctx + 63) & ~63u) * 4 > 48 * 1024) {
+        n_ctx > MYNAH_MAX_CTX) {
         fail(err, errsz, "unsupported shape", NULL);
         return NULL;
     }
@@ -398,8 +408,16 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             float *out = s->attn;
             const float *scc = s->scores;
             void *args2[] = {&vl, &scc, &pos, &out, &sstride, &kvd, &group};
-            rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, 64 * group,
-                              (size_t)group * sstride * 4, st, args2);
+            if ((size_t)group * sstride * 4 <= EXACT_LDS_SCORES) {
+                rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, 64 * group,
+                                  (size_t)group * sstride * 4, st, args2);
+            } else {
+                void *args1[] = {&sc, &pos, &sstride};
+                rc = mynah_launch(d, MYNAH_K_ATTN_SOFTMAX, c->n_heads, 1, 64, 0, st, args1);
+                rc = rc ? rc : mynah_launch(d, MYNAH_K_ATTN_OUT_LONG, c->n_kv_heads,
+                                            c->head_dim / 8, 64 * group,
+                                            (size_t)group * 1024 * 4, st, args2);
+            }
         }
         if (rc) break;
         memset(&g, 0, sizeof g);
@@ -576,7 +594,17 @@ static uint32_t prefill_chunk_cap(void) {
     return (uint32_t)v;
 }
 
+/* The prefill's score rows ([token][head][sstride] floats) for one chunk
+ * stay within 2 GiB: long contexts take shorter chunks. */
+static uint32_t prefill_cap_for(const mynah_qwen3 *s, uint32_t want) {
+    const size_t per_token = (size_t)s->c.n_heads * s->sstride * 4;
+    const size_t most = ((size_t)2 << 30) / per_token;
+    if (most < 1) return 1;
+    return want < most ? want : (uint32_t)most;
+}
+
 static int prefill_alloc(mynah_qwen3 *s, uint32_t cap) {
+    cap = prefill_cap_for(s, cap);
     if (s->pf_cap >= cap) return 0;
     void *bufs[] = {s->pf_x, s->pf_xn, s->pf_q, s->pf_att, s->pf_g, s->pf_u, s->pf_s, s->pf_tok};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)

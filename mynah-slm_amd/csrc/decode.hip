@@ -221,10 +221,10 @@ MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
     for (int k = 0; k < AO_SK; k++) {
         if ((uint32_t)k < kmax) {
             float4 e;
-            e.x = expf(sv[k].x - m);
-            e.y = expf(sv[k].y - m);
-            e.z = expf(sv[k].z - m);
-            e.w = expf(sv[k].w - m);
+            e.x = mynah_expf(sv[k].x - m);
+            e.y = mynah_expf(sv[k].y - m);
+            e.z = mynah_expf(sv[k].z - m);
+            e.w = mynah_expf(sv[k].w - m);
             acc += (double)e.x;
             acc += (double)e.y;
             acc += (double)e.z;
@@ -246,6 +246,64 @@ MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
     }
 }
 
+// softmax_row for rows of any length, by one wave, through memory instead of
+// registers: the same float4-to-lane assignment (lane l takes float4s l,
+// l + 64, ...), the same masking of the last float4, the same order of each
+// lane's double sum and the same wave reduction, so its results are
+// bit-identical to softmax_row's wherever both apply. Three passes: the
+// maximum; e = expf(s - m) written over p (p may equal sc_row: each float4
+// is read, then written, by the same lane) with the double sum; p = e *
+// inv.
+MYNAH_DEV void softmax_row_long(const float *sc_row, uint32_t n_kv, float *p) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
+    const float4 *sc = (const float4 *)sc_row;
+    float4 *p4 = (float4 *)p;
+    const uint32_t n4 = (n_kv + 3u) / 4u;
+    const float ninf = -__builtin_inff();
+    auto masked = [&](uint32_t i) {
+        float4 v = sc[i];
+        const uint32_t t = 4u * i;
+        if (t + 1u >= n_kv) v.y = ninf;
+        if (t + 2u >= n_kv) v.z = ninf;
+        if (t + 3u >= n_kv) v.w = ninf;
+        return v;
+    };
+    float m = ninf;
+    for (uint32_t i = lane; i < n4; i += 64u) {
+        const float4 v = masked(i);
+        m = fmaxf(fmaxf(fmaxf(m, v.x), fmaxf(v.y, v.z)), v.w);
+    }
+    m = wave_max_f(m);
+    double acc = 0.0;
+    for (uint32_t i = lane; i < n4; i += 64u) {
+        const float4 v = masked(i);
+        float4 e;
+        e.x = mynah_expf(v.x - m);
+        e.y = mynah_expf(v.y - m);
+        e.z = mynah_expf(v.z - m);
+        e.w = mynah_expf(v.w - m);
+        acc += (double)e.x;
+        acc += (double)e.y;
+        acc += (double)e.z;
+        acc += (double)e.w;
+        p4[i] = e;
+    }
+    const double sum = wave_sum_d(acc);
+    const float inv = (float)(1.0 / sum);
+    for (uint32_t i = lane; i < n4; i += 64u) {
+        const float4 e = p4[i];
+        p4[i] = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+    }
+}
+
+// Rows up to 4096 positions in registers, longer ones through memory (the
+// same bits either way).
+MYNAH_DEV void softmax_any(const float *sc_row, uint32_t n_kv, float *p) {
+    if (n_kv <= 64u * 4u * AO_SK) softmax_row(sc_row, n_kv, p);
+    else softmax_row_long(sc_row, n_kv, p);
+}
+
 MYNAH_DEV void attn_out_body(const float *__restrict__ v_layer, const float *__restrict__ scores,
                              uint32_t pos, float *__restrict__ out, uint32_t sstride,
                              uint32_t kv_dim, uint32_t group) {
@@ -262,7 +320,7 @@ MYNAH_DEV void attn_out_body(const float *__restrict__ v_layer, const float *__r
 
     // Softmax of head g = wave into LDS.
     float *p = p_all + (size_t)wave * sstride;
-    softmax_row(scores + (size_t)(kvh * group + wave) * sstride, n_kv, p);
+    softmax_any(scores + (size_t)(kvh * group + wave) * sstride, n_kv, p);
 
     const bool chain = lane < AO_DV;
     float o = 0.0f;
@@ -304,6 +362,71 @@ mynah_attn_out(const float *__restrict__ v_layer, const float *__restrict__ scor
                const uint32_t *__restrict__ pos_ptr, float *__restrict__ out, uint32_t sstride,
                uint32_t kv_dim, uint32_t group) {
     attn_out_body(v_layer, scores, pos_ptr[0], out, sstride, kv_dim, group);
+}
+
+// ── exact attention for contexts whose score rows outgrow the LDS ─────────
+// The same operations as mynah_attn_out in two launches: the softmax of
+// every head's scores in place (one wave per head, softmax_row_long, the
+// bits of softmax_row), then the ordered PV chains of mynah_attn_out with
+// the probabilities staged per chunk of AO_CH positions beside the V slice.
+extern "C" __global__ void __launch_bounds__(64)
+mynah_attn_softmax(float *scores, const uint32_t *__restrict__ pos_ptr, uint32_t sstride) {
+    float *row = scores + (size_t)blockIdx.x * sstride;
+    softmax_row_long(row, pos_ptr[0] + 1u, row);
+}
+
+extern "C" __global__ void __launch_bounds__(512)
+mynah_attn_out_long(const float *__restrict__ v_layer, const float *__restrict__ probs,
+                    const uint32_t *__restrict__ pos_ptr, float *__restrict__ out,
+                    uint32_t sstride, uint32_t kv_dim, uint32_t group) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float vt[AO_DV][AO_CH + 4];
+    extern __shared__ __attribute__((aligned(16))) float pcd[];     // [group][AO_CH]
+    const uint32_t n_kv = pos_ptr[0] + 1u;
+    const uint32_t kvh = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nthr = blockDim.x;
+    const float *vcol = v_layer + (size_t)kvh * 128u + AO_DV * blockIdx.y;
+    const float4 *prow = (const float4 *)(probs + (size_t)(kvh * group + wave) * sstride);
+    const uint32_t nc = (n_kv + AO_CH - 1u) / AO_CH;
+    float4 vr[AO_VR];
+    ao_fetch(vr, vcol, 0, n_kv, kv_dim, nthr);
+    const bool chain = lane < AO_DV;
+    float o = 0.0f;
+    for (uint32_t c = 0; c < nc; c++) {
+        const uint32_t tn = n_kv - c * AO_CH < AO_CH ? n_kv - c * AO_CH : AO_CH;
+        const uint32_t npass = (2u * tn + nthr - 1u) / nthr;
+#pragma unroll
+        for (int k = 0; k < AO_VR; k++) {
+            const uint32_t i = threadIdx.x + nthr * (uint32_t)k;
+            const uint32_t r = i >> 1, d = 4u * (i & 1u);
+            if ((uint32_t)k < npass && r < AO_CH) {
+                vt[d][r] = vr[k].x; vt[d + 1][r] = vr[k].y; vt[d + 2][r] = vr[k].z; vt[d + 3][r] = vr[k].w;
+            }
+        }
+        // This wave's probabilities of the chunk (softmax_row wrote whole
+        // float4s, 0 past n_kv in the last one).
+        for (uint32_t i = lane; i < (tn + 3u) / 4u; i += 64u)
+            *(float4 *)&pcd[wave * AO_CH + 4u * i] = prow[c * (AO_CH / 4u) + i];
+        __syncthreads();
+        if (c + 1 < nc) ao_fetch(vr, vcol, c + 1, n_kv, kv_dim, nthr);
+        if (chain) {
+            const float *pcw = pcd + wave * AO_CH, *vc = vt[lane];
+            uint32_t t = 0;
+            for (; t + 16 <= tn; t += 16) {
+                float4 va[4], pa[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    va[k] = *(const float4 *)(vc + t + 4 * k);
+                    pa[k] = *(const float4 *)(pcw + t + 4 * k);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) o = ao_fma4(va[k], pa[k], o);
+            }
+            for (; t < tn; t++) o = __builtin_fmaf(vc[t], pcw[t], o);
+        }
+        __syncthreads();
+    }
+    if (chain) out[(size_t)(kvh * group + wave) * 128u + AO_DV * blockIdx.y + lane] = o;
 }
 
 // ── attention with the positions split across workgroups ───────────────────
@@ -439,7 +562,7 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
             if ((uint32_t)(4 * k + 2) < tn) m = fmaxf(m, v.z);
             if ((uint32_t)(4 * k + 3) < tn) m = fmaxf(m, v.w);
         }
-        if (d < AS_CH) ee[h][d] = d < tn ? expf(es[h][d] - m) : 0.0f;
+        if (d < AS_CH) ee[h][d] = d < tn ? mynah_expf(es[h][d] - m) : 0.0f;
     }
     __syncthreads();
     // Partial weighted sum (fma chain in t order) and the chunk's exp sum.
@@ -513,7 +636,7 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
     const float M = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
     double l = 0.0;
     for (uint32_t c = tid; c < nch; c += 256u) {
-        const float w = expf(pm[base + (size_t)c * group] - M);
+        const float w = mynah_expf(pm[base + (size_t)c * group] - M);
         wsc[c] = w;
         l += (double)w * pl[base + (size_t)c * group];
     }
@@ -850,7 +973,7 @@ mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_l
 extern "C" __global__ void __launch_bounds__(64)
 mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride) {
     float *row = scores + ((size_t)blockIdx.x * gridDim.y + blockIdx.y) * sstride;
-    softmax_row(row, p0 + blockIdx.x + 1u, row);
+    softmax_any(row, p0 + blockIdx.x + 1u, row);
 }
 
 // Weighted V sums of PV_Q consecutive query rows for one key head

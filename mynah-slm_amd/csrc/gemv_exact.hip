@@ -365,8 +365,8 @@ struct GemvGroup {
 
 MYNAH_DEV float sigmoid_ref(float v) {
 #pragma clang fp contract(off)
-    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
-    const float e = expf(v);
+    if (v >= 0.0f) return 1.0f / (1.0f + mynah_expf(-v));
+    const float e = mynah_expf(v);
     return e / (1.0f + e);
 }
 

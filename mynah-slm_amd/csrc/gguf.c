@@ -601,7 +601,10 @@ mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *e
             gg_err(err, errsz, "out of memory");
         } else {
             mynah_gguf_tensor_table(g, table, count, &count);
-            if (n_ctx == 0) n_ctx = n_train < 4096u ? n_train : 4096u;
+            /* The reference's server asks for the model's own context
+             * (server/main.c:426); a zero context_length means one position
+             * here, which the decoder refuses like any empty context. */
+            if (n_ctx == 0) n_ctx = n_train;
             uint64_t bytes = 0;
             const void *data = mynah_gguf_data(g, &bytes);
             s = mynah_hip_qwen3_new(&shape, table, count, data, bytes, n_ctx, err, errsz);

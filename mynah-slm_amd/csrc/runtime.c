@@ -1030,6 +1030,22 @@ int mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
                         args);
 }
 
+int mynah_hip_expf_dev(const float *x, float *y, size_t n, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (x == NULL || y == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    if (n == 0) return 0;
+    uint64_t n64 = n;
+    const uint64_t want = (n64 + 255) / 256;
+    const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+    void *args[] = {&x, &y, &n64};
+    return mynah_launch(d, MYNAH_K_EXPF, grid, 1, 256, 0, mynah_stream_or_default(d, stream),
+                        args);
+}
+
 int mynah_hip_sync(void *stream) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;

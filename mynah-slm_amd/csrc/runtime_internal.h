@@ -36,6 +36,8 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \
     X(MYNAH_K_ATTN_SCORES, "mynah_attn_scores")        \
     X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
+    X(MYNAH_K_ATTN_SOFTMAX, "mynah_attn_softmax")      \
+    X(MYNAH_K_ATTN_OUT_LONG, "mynah_attn_out_long")    \
     X(MYNAH_K_ATTN_SPLIT, "mynah_attn_split")          \
     X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
@@ -49,6 +51,7 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_PREFILL_SOFTMAX, "mynah_prefill_softmax") \
     X(MYNAH_K_PREFILL_PV, "mynah_prefill_pv")          \
     X(MYNAH_K_COPY16, "mynah_copy16")                  \
+    X(MYNAH_K_EXPF, "mynah_expf_map")                  \
     X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
     X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \
     X(MYNAH_K_Q4K_GEMM_INT8_11, "mynah_q4k_gemm_int8_11") \

@@ -101,6 +101,7 @@ def _load() -> C.CDLL:
         "mynah_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
         "mynah_hip_event_destroy": (C.c_int, [_P]),
         "mynah_hip_copy_dev": (C.c_int, [_P, _P, _SZ, _P]),
+        "mynah_hip_expf_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_time_sweep": (C.c_int, [C.c_int, _P, _P, C.c_int, _P, _P, _P, _P, C.c_int,
                                            C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mynah_hip_time_matvec": (C.c_int, [C.c_int, _P, C.c_int, _SZ, _SZ, _P, _P, C.c_int,
@@ -533,7 +534,7 @@ class Qwen3Decoder:
     @classmethod
     def from_gguf(cls, path: str, n_ctx: int = 0) -> "Qwen3Decoder":
         """The decoder over a GGUF checkpoint (mynah_slm_load, src/model.c:177):
-        n_ctx 0 takes the file's context_length, capped at 4096."""
+        n_ctx 0 takes the file's context_length."""
         with GgufFile(path) as g:
             shape, _ = g.qwen3_shape()
         self = cls.__new__(cls)

@@ -7,8 +7,9 @@ every step are the golden vectors (tests/golden/qwen3_06b_forced.npz,
 configs[2]'s model and 512-position KV prefill, 64 steps):
 
   * step by step through forward(): every step's logits at the golden top-64
-    ids and at every 293rd id within |gpu - ref| / max(1, |ref|) <= 1e-4,
-    and every step's greedy id, in both attention modes;
+    ids and at every 293rd id within |gpu - ref| / max(1, |ref|) <= 1e-4 —
+    and with exact attention bit for bit equal to the reference's — and
+    every step's greedy id, in both attention modes;
   * through the replayed multi-step graphs (mynah_hip_qwen3_forced, eight
     steps per graph launch, the position and step counters advancing on the
     device): the greedy id of every step and the last step's logits against
@@ -64,11 +65,17 @@ def rel_err(got, ref):
     return float((np.abs(got - ref) / np.maximum(1.0, np.abs(ref))).max())
 
 
-def check_step(lg, g, i, stride=CF.FORCED_SAMPLE_STRIDE):
-    """One step's logits against the golden summary of step i."""
-    e_top = rel_err(lg[g["top_ids"][i]], g["top_vals"][i])
-    e_smp = rel_err(lg[::stride], g["sample"][i])
+def check_step(lg, g, i, stride=CF.FORCED_SAMPLE_STRIDE, exact=False):
+    """One step's logits against the golden summary of step i: within 1e-4,
+    and in the exact modes bit for bit (the GEMVs keep the reference's order
+    and the softmax / sigmoid exponential is the C library's)."""
+    top, smp = lg[g["top_ids"][i]], lg[::stride]
+    e_top = rel_err(top, g["top_vals"][i])
+    e_smp = rel_err(smp, g["sample"][i])
     assert e_top <= TOL and e_smp <= TOL, f"step {i}: top {e_top:.2e}, sample {e_smp:.2e}"
+    if exact:
+        assert np.array_equal(top.view(np.uint32), g["top_vals"][i].view(np.uint32)), f"step {i}"
+        assert np.array_equal(smp.view(np.uint32), g["sample"][i].view(np.uint32)), f"step {i}"
     return max(e_top, e_smp)
 
 
@@ -91,7 +98,7 @@ def test_06b_forced_every_step_stepwise(M, m06, g06, mode):
     worst = 0.0
     for i, tok in enumerate(inputs):
         lg = dec.forward(tok)
-        worst = max(worst, check_step(lg, g06, i))
+        worst = max(worst, check_step(lg, g06, i, exact=mode == "exact"))
         assert int(np.argmax(lg)) == int(g06["greedy"][i]), f"step {i}"
     print(f"0.6B forced ({mode}): worst logit error {worst:.2e} over {len(inputs)} steps")
 
@@ -105,7 +112,7 @@ def test_06b_forced_graph_replay(M, m06, g06, mode):
     greedy, last = dec.forced(inputs)
     assert dec.uses_graph
     assert greedy == [int(t) for t in g06["greedy"]]
-    check_step(last, g06, n - 1)
+    check_step(last, g06, n - 1, exact=mode == "exact")
     kg, vg = dec.get_kv(CF.C3_PREFILL + n)
     ref = decoder_06b(M, m06, MODES[mode])
     for tok in inputs:

@@ -131,7 +131,8 @@ def test_refusals(M, tiny, tmp_path):
     w.tensors.insert(0, ("pad.weight", 0, [2], bytes(8)))
     with pytest.raises(M.HipError, match="16-byte aligned"):
         M.Qwen3Decoder.from_gguf(write(tmp_path, "align8", w))
+    # Any context up to 2^20 positions is taken; beyond it the shape is refused.
     with pytest.raises(M.HipError, match="unsupported shape"):
-        M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model)), 8192)
+        M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model)), (1 << 20) + 1)
     with pytest.raises(M.HipError):
         M.Qwen3Decoder.from_gguf(str(tmp_path / "absent.gguf"))
