@@ -89,6 +89,31 @@ def gpu_sweep(M, CF, steps: int, warmup: int):
     return step_bytes, copies, total_ms, head_ms, algorithmic_bytes(mats[head]), per
 
 
+def gpu_c1(M, CF, launches: int = 256):
+    """the single Q4_K 1024 x 3072 matvec, weights rotated over
+    enough device copies (> 2x MALL) that every launch streams from HBM;
+    GB/s of algorithmic bytes over the average launch (HIP events around
+    `launches` back-to-back launches)."""
+    m = CF.C1[0]
+    wseed, xseed = CF.matrix_seeds(M.substream, 0, 0)
+    nbytes = algorithmic_bytes(m)
+    copies = max(2, -(-2 * MALL_BYTES // nbytes))
+    w = upload_copies(M, M.synth_blocks(m.qtype, wseed, m.rows, m.cols), copies)
+    x = M.DeviceBuffer.from_array(M.synth_normal(xseed, m.cols))
+    y = M.DeviceBuffer(4 * m.rows)
+    ptrs = [b.ptr for b in w]
+    n = max(launches, 2 * copies)
+    M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies)
+    ms = M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, n) / n
+    for b in w + [x, y]:
+        b.free()
+    return {"workload": "configs[0]: Q4_K 1024x3072 matvec, seed 0", "kernel":
+            M.gemv_kernel(m.qtype, m.rows, m.cols), "bytes_per_launch": nbytes,
+            "weight_copies": copies, "launches": n, "avg_launch_ms": round(ms, 5),
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "copy_ceiling_gbs": round(copy_ceiling(M, nbytes), 1)}
+
+
 def copy_ceiling(M, traffic: int, launches: int = 64) -> float:
     """GB/s of HBM traffic a plain device copy (mynah_copy16) reaches when
     each launch moves `traffic` bytes (reads traffic/2, writes traffic/2),
@@ -137,16 +162,39 @@ def gpu_4b_classes(M, CF, launches: int = 64):
     return out, ceiling
 
 
+def forced_check(dec, g, k, v, npre):
+    """The teacher-forced golden run of configs[2] (64 uniform-random inputs
+    after the 512-position prefill, logits from the compiled reference)
+    through the replayed step graphs: every step's greedy id, and the last
+    step's logits (whole vector by SHA-256, the golden top-64 and every
+    293rd logit by relative error)."""
+    import hashlib
+    import numpy as np
+    dec.reset()
+    dec.set_kv(k, v, npre)
+    greedy, last = dec.forced([int(t) for t in g["inputs"]])
+    ref = np.concatenate([g["top_vals"][-1], g["sample"][-1]]).astype(np.float64)
+    got = np.concatenate([last[g["top_ids"][-1]], last[::293]]).astype(np.float64)
+    err = float((np.abs(got - ref) / np.maximum(1.0, np.abs(ref))).max())
+    return {"greedy_ids_match": greedy == [int(t) for t in g["greedy"]],
+            "last_logits_bit_identical":
+                hashlib.sha256(last.tobytes()).hexdigest() == str(g["logits_sha"][-1]),
+            "last_logits_max_rel_err": err}
+
+
 def gpu_decode(M, CF):
     """Qwen3-0.6B batch-1 greedy decode, 512 prefilled positions,
-    64 steps, in both GEMV orders; tokens checked against the golden ids the
-    compiled reference produced."""
+    64 steps, in three numerics modes; the generated ids checked against the
+    compiled reference's, and each mode run again teacher-forced over the
+    golden's 64 random inputs (forced_check)."""
     import numpy as np
     shape, npre, steps = CF.QWEN3_06B, CF.C3_PREFILL, CF.C3_STEPS
     model = M.SynthQwen3(shape, 0)
     k, v = CF.kv_prefill(M.substream, M.synth_normal, shape, 0, npre)
     first = M.first_token(0, shape.vocab)
     golden = np.load(os.path.join(ROOT, "tests", "golden", "qwen3_06b.npz"), allow_pickle=False)
+    forced = np.load(os.path.join(ROOT, "tests", "golden", "qwen3_06b_forced.npz"),
+                     allow_pickle=False)
     want = [int(t) for t in golden["tokens"]]
     out = {"model": "Qwen3-0.6B random-init Q4_K_M mix", "prefill": npre, "steps": steps,
            "weight_bytes": model.weight_bytes()}
@@ -164,7 +212,8 @@ def gpu_decode(M, CF):
             dec.set_kv(k, v, npre)
             toks, ms = dec.generate(first, steps)
             out[name] = {"tok_s": round(steps / ms * 1e3, 1), "ms_per_token": round(ms / steps, 4),
-                         "tokens_match_reference": toks == want, "graph": dec.uses_graph}
+                         "tokens_match_reference": toks == want, "graph": dec.uses_graph,
+                         "teacher_forced": forced_check(dec, forced, k, v, npre)}
             dec.close()
     finally:
         M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
@@ -174,7 +223,8 @@ def gpu_decode(M, CF):
                        "tokens_match_reference": head["tokens_match_reference"],
                        "note": "every GEMV bit-identical to the reference kernels; attention "
                                "softmax taken per 32-position chunk and combined (f32 rounding "
-                               "only); 64 greedy ids identical to the compiled reference"}
+                               "only); the 'exact' mode's logits are bit-identical to the "
+                               "compiled reference's (teacher_forced.last_logits_bit_identical)"}
     return out
 
 
@@ -235,6 +285,16 @@ def gpu_prefill_gemm(M, CF, reps: int = 5, int8: bool = False):
     return res
 
 
+def c5_golden_ids():
+    """The 256 greedy ids of configs[4] from the compiled reference
+    (tests/golden/qwen3_4b_c5.npz), or None when that golden is absent."""
+    import numpy as np
+    path = os.path.join(ROOT, "tests", "golden", "qwen3_4b_c5.npz")
+    if not os.path.exists(path):
+        return None
+    return [int(t) for t in np.load(path, allow_pickle=False)["greedy"]]
+
+
 def gpu_qwen3_4b(M, CF):
     """Qwen3-4B random-init Q4_K_M mix, a 2048-token prompt of
     uniform ids, then 256 greedy steps; tok/s as the reference's timing.c
@@ -246,6 +306,7 @@ def gpu_qwen3_4b(M, CF):
     shape = CF.QWEN3_4B
     model = M.SynthQwen3(shape, 0)
     prompt = CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)
+    want = c5_golden_ids()
     out = {"model": "Qwen3-4B random-init Q4_K_M mix", "prompt": int(prompt.size),
            "steps": CF.C5_STEPS, "weight_bytes": model.weight_bytes()}
     old = M.lib.mynah_hip_gemv_order()
@@ -263,7 +324,8 @@ def gpu_qwen3_4b(M, CF):
                          "prefill_tok_s": round(prompt.size / (pre_ms * 1e-3), 1),
                          "decode_tok_s": round(CF.C5_STEPS / (dec_ms * 1e-3), 1),
                          "prefill_ms": round(pre_ms, 2), "decode_ms": round(dec_ms, 2),
-                         "first_tokens": toks[:4]}
+                         "first_tokens": toks[:4],
+                         "tokens_match_reference": None if want is None else toks == want}
             dec.close()
     finally:
         M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
@@ -283,9 +345,12 @@ def gpu_decode_4b(M, CF, steps: int):
     dec.reset()
     toks, pre_ms, dec_ms = dec.prompt(prompt, steps)
     dec.close()
+    want = c5_golden_ids()
     return {"model": "Qwen3-4B random-init Q4_K_M mix", "mode": "exact_gemv_split_attention",
             "prompt": int(prompt.size), "steps": steps, "decode_ms": round(dec_ms, 2),
-            "decode_tok_s": round(steps / (dec_ms * 1e-3), 1), "first_tokens": toks[:4]}
+            "decode_tok_s": round(steps / (dec_ms * 1e-3), 1), "first_tokens": toks[:4],
+            "tokens_match_reference": None if want is None else
+            toks[:len(want)] == want[:len(toks)]}
 
 
 def gpu_prefill_4b(M, CF, reps: int = 3):
@@ -312,34 +377,139 @@ def gpu_prefill_4b(M, CF, reps: int = 3):
                     "token-by-token decode steps; wall time of the call, host sync included"}
 
 
-def cpu_baseline(CF, seconds: float = 10.0):
-    """The CPU oracle on the same sweep, all of this host's cores (<= 16)."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_lib as O
-    threads = min(16, os.cpu_count() or 1)
-    threads = O.orc.orc_threads_init(threads)
-    mats = CF.C2
+def host_cpus() -> dict:
+    """The host cores the CPU leg may use: every core of this process's
+    affinity set (src/threads.c:27-41 starts the pool on all online cores),
+    capped by the CPU share the host grants the job (a cgroup quota, or
+    OMP_NUM_THREADS where the batch system sets it to that share)."""
+    aff = sorted(os.sched_getaffinity(0))
+    sockets = set()
+    for c in aff:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                sockets.add(f.read().strip())
+        except OSError:
+            pass
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = len(aff)
+    if quota is not None:
+        threads = min(threads, max(1, int(quota)))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return {"online": os.cpu_count(), "affinity": len(aff), "sockets": len(sockets) or None,
+            "cgroup_quota_cpus": quota, "omp_num_threads": omp or None, "threads": threads}
+
+
+def _timed_passes(fn, seconds: float, min_reps: int = 2):
+    fn()                                       # warm-up pass
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= min_reps:
+            return reps, el
+
+
+def cpu_sweep(O, CF, mats, seconds: float):
+    """GB/s of the oracle's threaded projection (4*nth row chunks, serial
+    below 64 rows: src/arch_qwen3.c:52-83) over the matrices of a config."""
     data = []
     for i, m in enumerate(mats):
         ws, xs = CF.matrix_seeds(O.substream, 0, i)
         data.append((m, O.blocks(m.qtype, ws, m.rows, m.cols), O.normal(xs, m.cols)))
     step_bytes = sum(algorithmic_bytes(m) for m in mats)
-    for m, w, x in data:                       # warm-up pass
-        O.project(m.qtype, w, m.rows, m.cols, x)
-    reps, t0 = 0, time.perf_counter()
-    while True:
+
+    def one():
         for m, w, x in data:
             O.project(m.qtype, w, m.rows, m.cols, x)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and reps >= 2:
+    reps, el = _timed_passes(one, seconds)
+    return step_bytes, reps, el
+
+
+def cpu_decode(O, CF, seconds: float):
+    """configs[2] on the CPU: the oracle decoder (the restated
+    src/arch_qwen3.c:178-252 on the pool, bit-identical to the compiled
+    reference) with first-index greedy picks (src/sampler.c:124-129) from
+    the 512-position prefill, timed as src/timing.c:52-54 defines decode
+    tok/s (generated ids / decode seconds); stops after `seconds` (at least
+    4 steps) or the 64 steps of the golden run, whose ids it must match."""
+    import numpy as np
+    shape = CF.QWEN3_06B
+    orc = O.OracleQwen3(O.SynthModel(shape, 0), CF.C3_PREFILL + CF.C3_STEPS + 1)
+    k, v = O.kv_prefill(O.substream, shape, 0, CF.C3_PREFILL)
+    orc.prefill_kv(k, v, CF.C3_PREFILL)
+    want = [int(t) for t in np.load(os.path.join(ROOT, "tests", "golden", "qwen3_06b.npz"),
+                                    allow_pickle=False)["tokens"]]
+    tok, toks = O.first_token(0, shape.vocab), []
+    t0 = time.perf_counter()
+    while len(toks) < CF.C3_STEPS:
+        lg = orc.forward(tok)
+        tok = int(O.orc.orc_argmax(O.ptr(lg), lg.size))
+        toks.append(tok)
+        if time.perf_counter() - t0 >= seconds and len(toks) >= 4:
             break
-    O.orc.orc_threads_shutdown()
+    el = time.perf_counter() - t0
+    del orc
+    return {"tok_s": round(len(toks) / el, 2), "steps": len(toks), "seconds": round(el, 2),
+            "tokens_match_reference": toks == want[:len(toks)]}
+
+
+def cpu_prefill_gemm(O, CF):
+    """configs[3] on the CPU: one pass of the six exact batched products
+    (the reference's ingot matmat order) with the pool injected over 8-row
+    strips (third_party/ingot/src/cpu.c:217-230), 512 tokens."""
+    flop, el = 0, 0.0
+    per = {}
+    for i, m in enumerate(CF.C4):
+        wseed, _ = CF.matrix_seeds(O.substream, 0, i)
+        w = O.blocks(m.qtype, wseed, m.rows, m.cols)
+        x = O.normal(O.substream(0, CF.PREFILL_X_INDEX + i), CF.C4_TOKENS * m.cols)
+        t0 = time.perf_counter()
+        O.matmat(m.qtype, w, m.rows, m.cols, x, CF.C4_TOKENS, threaded=True)
+        dt = time.perf_counter() - t0
+        f = 2 * m.rows * m.cols * CF.C4_TOKENS
+        per[m.name] = round(f / dt / 1e9, 2)
+        flop += f
+        el += dt
+    return {"gflop_s": round(flop / el / 1e9, 2), "seconds": round(el, 2),
+            "per_matrix_gflop_s": per}
+
+
+def cpu_baseline(CF, seconds: float = 10.0):
+    """The CPU oracle (the C11 restatement of the reference's as-built
+    kernels and decoder, bit-identical to it) on this host's cores: the
+    configs[1] sweep (the metric's value), configs[0], configs[2] decode and
+    configs[3]'s batched products, each on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    cpus = host_cpus()
+    threads = O.orc.orc_threads_init(cpus["threads"])
+    try:
+        step_bytes, reps, el = cpu_sweep(O, CF, CF.C2, seconds)
+        c1_bytes, c1_reps, c1_el = cpu_sweep(O, CF, CF.C1, max(1.0, seconds / 4))
+        decode = cpu_decode(O, CF, seconds)
+        gemm = cpu_prefill_gemm(O, CF)
+    finally:
+        O.orc.orc_threads_shutdown()
     return {"value": round(step_bytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{reps} passes of the configs[1] sweep ({step_bytes / 1e6:.1f} MB each) "
                       f"in {el:.1f} s, oracle restatement (bit-identical to the reference) with "
-                      f"4*nth row chunks on {threads} threads"}
+                      f"4*nth row chunks on {threads} threads",
+            "host": cpus,
+            "configs0_gbs": round(c1_bytes * c1_reps / c1_el / 1e9, 2),
+            "configs0_sample": f"{c1_reps} matvecs of Q4_K 1024x3072 in {c1_el:.1f} s",
+            "configs2_decode": decode,
+            "configs3_prefill_gemm": gemm}
 
 
 def pmc_probe(M, CF, launches: int = 8) -> None:
@@ -422,6 +592,9 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = head_bytes / (head_ms * 1e-3) / 1e9
 
+    log("[bench] configs[0] Q4_K matvec")
+    c1 = gpu_c1(M, CF)
+
     decode = None
     if not args.no_decode:
         log("[bench] configs[2] decode")
@@ -470,9 +643,7 @@ def main() -> int:
             "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": ("mynah_gemv_fast_group" if order != 0 else
-                       "mynah_gemv_group" if os.environ.get("MYNAH_GEMV_TYPED") == "0" else
-                       "mynah_gemv_group_q6k") + " (Q6_K 151936x1024 head)",
+            "kernel": M.gemv_kernel(CF.Q6_K, 151936, 1024) + " (Q6_K 151936x1024 head)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
@@ -483,6 +654,7 @@ def main() -> int:
             "avg_launch_ms": round(head_ms, 5),
         },
         "cpu_baseline": cpu,
+        "configs0": c1,
         "decode": decode,
         "prefill_gemm": prefill,
         "prefill_gemm_int8": prefill_int8,

@@ -168,6 +168,11 @@ int mynah_hip_matmat_mv_dev(int type, const void *w, size_t rows, size_t cols,
 enum { MYNAH_GEMV_EXACT = 0, MYNAH_GEMV_REORDERED = 1 };
 int mynah_hip_set_gemv_order(int order);
 int mynah_hip_gemv_order(void);
+/* The code-object name of the kernel one matvec of this type and shape
+ * launches in the given order (-1: the current one), from the same plan the
+ * launch makes; NULL (reason in mynah_hip_last_error) when it cannot run.
+ * No reference counterpart: it names what a profiler trace will show. */
+const char *mynah_hip_gemv_kernel(int type, size_t rows, size_t cols, int order);
 
 /* The int8 activation lane of Q4_K and Q5_K products (the reference's lane
  * of an AVX2 + FMA build of ingot, third_party/ingot/src/kernels.c:636-788,

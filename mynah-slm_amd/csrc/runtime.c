@@ -586,6 +586,28 @@ int mynah_gemv_group_geometry(mynah_gemv_group *grp, int order, uint32_t *thread
     return 0;
 }
 
+const char *mynah_hip_gemv_kernel(int type, size_t rows, size_t cols, int order) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return NULL;
+    if (type == MYNAH_Q4_0)
+        return kernel_names[rows < 32768u && env_long("MYNAH_Q40_PC", 1) != 0
+                                ? MYNAH_K_Q40_CHAIN_PC : MYNAH_K_Q40_CHAIN1];
+    if (type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
+        return kernel_names[MYNAH_K_Q4K_GEMV_INT8];
+    /* The plan reads shapes and pointer alignment only: stand-in addresses
+     * aligned like a device allocation. */
+    const uintptr_t fake = 4096;
+    mynah_gemv_group g;
+    memset(&g, 0, sizeof g);
+    g.n = 1;
+    if (mynah_gemv_desc_init(&g.d[0], type, (const void *)fake, rows, cols,
+                             (const float *)fake, (float *)fake) != 0)
+        return NULL;
+    gemv_plan p;
+    if (gemv_group_plan(d, &g, order, &p) != 0) return NULL;
+    return kernel_names[p.kernel];
+}
+
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
                             uint32_t *tiles_out, int order) {
     gemv_plan p;

@@ -96,6 +96,7 @@ def _load() -> C.CDLL:
         "mynah_hip_stream": (_P, []),
         "mynah_hip_set_gemv_order": (C.c_int, [C.c_int]),
         "mynah_hip_gemv_order": (C.c_int, []),
+        "mynah_hip_gemv_kernel": (C.c_char_p, [C.c_int, C.c_size_t, C.c_size_t, C.c_int]),
         "mynah_hip_event_create": (_P, []),
         "mynah_hip_event_record": (C.c_int, [_P, _P]),
         "mynah_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
@@ -356,6 +357,14 @@ def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int
     check(lib.mynah_hip_time_sweep(n, types, w, copies, rows, cols, x, y, steps, timed,
                                    C.byref(tot), C.byref(tim)), "time_sweep")
     return float(tot.value), float(tim.value)
+
+
+def gemv_kernel(qtype: int, rows: int, cols: int, order: int = -1) -> str:
+    """Name of the kernel one matvec of this shape launches (the plan only)."""
+    name = lib.mynah_hip_gemv_kernel(qtype, rows, cols, order)
+    if name is None:
+        raise HipError(f"gemv_kernel: {lib.mynah_hip_last_error().decode(errors='replace')}")
+    return name.decode()
 
 
 def time_matvec(qtype: int, w_ptrs, rows: int, cols: int, x: int, y: int, iters: int) -> float:

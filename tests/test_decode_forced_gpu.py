@@ -67,8 +67,9 @@ def rel_err(got, ref):
 
 def check_step(lg, g, i, stride=CF.FORCED_SAMPLE_STRIDE, exact=False):
     """One step's logits against the golden summary of step i: within 1e-4,
-    and in the exact modes bit for bit (the GEMVs keep the reference's order
-    and the softmax / sigmoid exponential is the C library's)."""
+    and in the exact modes bit for bit, the whole vocabulary by its SHA-256
+    (the GEMVs keep the reference's order and the softmax / sigmoid
+    exponential is the C library's)."""
     top, smp = lg[g["top_ids"][i]], lg[::stride]
     e_top = rel_err(top, g["top_vals"][i])
     e_smp = rel_err(smp, g["sample"][i])
@@ -76,6 +77,8 @@ def check_step(lg, g, i, stride=CF.FORCED_SAMPLE_STRIDE, exact=False):
     if exact:
         assert np.array_equal(top.view(np.uint32), g["top_vals"][i].view(np.uint32)), f"step {i}"
         assert np.array_equal(smp.view(np.uint32), g["sample"][i].view(np.uint32)), f"step {i}"
+        assert hashlib.sha256(np.ascontiguousarray(lg).tobytes()).hexdigest() == \
+            str(g["logits_sha"][i]), f"step {i}: whole logits vector"
     return max(e_top, e_smp)
 
 
@@ -198,5 +201,5 @@ def test_qwen3_4b_configs4_against_reference(M, mode):
     for j, stop in enumerate(int(s) for s in g["snapshot_steps"]):
         ids, last = dec.forced(inputs[done:stop + 1])
         assert ids == got[done:stop + 1]
-        check_step(last, g, j)
+        check_step(last, g, j, exact=mode == "exact")
         done = stop + 1

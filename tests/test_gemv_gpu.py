@@ -225,3 +225,19 @@ def test_reordered_order_within_f32_bound(M, qtype):
     exact = dq @ x.astype(np.float64)
     mag = np.abs(dq) @ np.abs(x.astype(np.float64))
     assert (np.abs(y - exact) <= (cols + 1) * 2.0 ** -24 * mag).all()
+
+
+def test_kernel_query_names_the_planned_kernel(M):
+    """mynah_hip_gemv_kernel answers from the launch's own plan: the exact
+    order's flat or streaming kernels, the reordered kernel, Q4_0's chains;
+    refused geometry gives NULL with the reason."""
+    exact = {"mynah_gemv_flat_q4k", "mynah_gemv_flat_q6k", "mynah_gemv_group",
+             "mynah_gemv_group_q4k", "mynah_gemv_group_q6k", "mynah_gemv_stream",
+             "mynah_gemv_stream_cvt"}
+    for qtype, rows, cols in ((12, 1024, 3072), (14, 151936, 1024), (14, 151936, 2560),
+                              (12, 9728, 2560), (8, 1024, 2048)):
+        assert M.gemv_kernel(qtype, rows, cols, 0) in exact
+        assert M.gemv_kernel(qtype, rows, cols, 1) == "mynah_gemv_fast_group"
+    assert M.gemv_kernel(2, 1024, 1024).startswith("mynah_q40_chain")
+    assert M.lib.mynah_hip_gemv_kernel(12, 1024, 100, 0) is None
+    assert b"geometry" in M.lib.mynah_hip_last_error()
