@@ -111,7 +111,8 @@ def gpu_c1(M, CF, launches: int = 256):
             M.gemv_kernel(m.qtype, m.rows, m.cols), "bytes_per_launch": nbytes,
             "weight_copies": copies, "launches": n, "avg_launch_ms": round(ms, 5),
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "copy_ceiling_gbs": round(copy_ceiling(M, nbytes), 1)}
+            "copy_ceiling_gbs": round(copy_ceiling(M, nbytes), 1),
+            "read_ceiling_gbs": round(read_ceiling(M, nbytes), 1)}
 
 
 def copy_ceiling(M, traffic: int, launches: int = 64) -> float:
@@ -140,10 +141,37 @@ def copy_ceiling(M, traffic: int, launches: int = 64) -> float:
     return 2 * half / (ms * 1e-3) / 1e9
 
 
+def read_ceiling(M, nbytes: int, launches: int = 64) -> float:
+    """GB/s a read-only stream (mynah_read16: every byte loaded once, nothing
+    written) reaches when each launch reads `nbytes`, launched back to back
+    from rotating sources (> 2x MALL) like the GEMVs: what one launch of a
+    GEMV's size can read, whatever it computes."""
+    size = max(256, nbytes // 256 * 256)
+    copies = max(2, -(-2 * MALL_BYTES // size))
+    src = [M.DeviceBuffer(size) for _ in range(copies)]
+    sink = M.DeviceBuffer(256)
+    for b in src:
+        M.check(M.lib.mynah_hip_memset(b.ptr, 1, size), "memset")
+    n = max(launches, 4 * copies)
+    for i in range(copies):
+        M.read_dev(src[i].ptr, size, sink.ptr)
+    a, e = M.Event(), M.Event()
+    a.record()
+    for i in range(n):
+        M.read_dev(src[i % copies].ptr, size, sink.ptr)
+    e.record()
+    M.sync()
+    ms = a.elapsed_ms(e) / n
+    for b in src + [sink]:
+        b.free()
+    return size / (ms * 1e-3) / 1e9
+
+
 def gpu_4b_classes(M, CF, launches: int = 64):
     """GB/s of each Qwen3-4B GEMV class, rotating copies totalling > 2x MALL,
-    and beside it the copy ceiling for the same traffic per launch."""
-    out, ceiling = {}, {}
+    and beside it the copy and read-only ceilings for the same bytes per
+    launch, and the kernel each class launches."""
+    out, ceiling, rceiling, kernels = {}, {}, {}, {}
     for i, m in enumerate(CF.QWEN3_4B_GEMV):
         wseed, xseed = CF.matrix_seeds(M.substream, 4, i)
         nbytes = algorithmic_bytes(m)
@@ -159,7 +187,9 @@ def gpu_4b_classes(M, CF, launches: int = 64):
         for b in w + [x, y]:
             b.free()
         ceiling[m.name] = round(copy_ceiling(M, nbytes, launches), 1)
-    return out, ceiling
+        rceiling[m.name] = round(read_ceiling(M, nbytes, launches), 1)
+        kernels[m.name] = M.gemv_kernel(m.qtype, m.rows, m.cols)
+    return out, ceiling, rceiling, kernels
 
 
 def forced_check(dec, g, k, v, npre):
@@ -560,6 +590,9 @@ def main() -> int:
     ap.add_argument("--decode-4b-only", action="store_true",
                     help="only configs[4]'s decode (2048-token prompt, then --steps greedy "
                          "steps, exact GEMV + split attention), printed as one JSON line")
+    ap.add_argument("--classes-only", action="store_true",
+                    help="only the Qwen3-4B GEMV classes with their copy and read-only "
+                         "ceilings, printed as one JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only the head GEMV + calibration copies, for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -580,6 +613,11 @@ def main() -> int:
         return 0
     if args.decode_only:
         print(json.dumps({"decode": gpu_decode(M, CF)}), flush=True)
+        return 0
+    if args.classes_only:
+        g, c, r, k = gpu_4b_classes(M, CF)
+        print(json.dumps({"qwen3_4b_gemv_gbs": g, "copy_ceiling_gbs": c, "read_ceiling_gbs": r,
+                          "kernels": k, "configs0": gpu_c1(M, CF)}), flush=True)
         return 0
     if args.decode_4b_only:
         print(json.dumps({"decode_4b": gpu_decode_4b(M, CF, args.steps)}), flush=True)
@@ -612,10 +650,10 @@ def main() -> int:
         log("[bench] configs[4] Qwen3-4B end to end")
         e2e_4b = gpu_qwen3_4b(M, CF)
 
-    extra_4b = ceiling_4b = None
+    extra_4b = ceiling_4b = rceiling_4b = kernels_4b = None
     if not args.no_4b:
         log("[bench] Qwen3-4B GEMV classes")
-        extra_4b, ceiling_4b = gpu_4b_classes(M, CF)
+        extra_4b, ceiling_4b, rceiling_4b, kernels_4b = gpu_4b_classes(M, CF)
 
     cpu = None
     if not args.no_cpu:
@@ -662,6 +700,8 @@ def main() -> int:
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
         "qwen3_4b_copy_ceiling_gbs": ceiling_4b,
+        "qwen3_4b_read_ceiling_gbs": rceiling_4b,
+        "qwen3_4b_gemv_kernels": kernels_4b,
     }
     print(json.dumps(line), flush=True)
     return 0

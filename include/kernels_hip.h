@@ -226,6 +226,11 @@ int   mynah_hip_sync(void *stream);
 /* Device-to-device copy by a plain 16-byte-vector kernel (buffers 16-byte
  * aligned, bytes a multiple of 16); the yardstick of the HBM counters. */
 int   mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream);
+/* A read-only stream over src (16-byte aligned, bytes a multiple of 16):
+ * every byte loaded once, nothing written but (practically never) one word
+ * of sink; the yardstick of what one launch reads at a size. No reference
+ * counterpart. */
+int   mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream);
 void *mynah_hip_stream(void);           /* the library's own stream */
 
 /* y[i] = expf(x[i]) for i < n with the bits of the reference's C library

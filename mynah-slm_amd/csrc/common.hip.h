@@ -30,6 +30,16 @@ MYNAH_DEV float ubyte_f(uint32_t v) {
     return r;
 }
 
+// ubyte_f (ASM) or the plain conversion (the backend picks the instruction).
+// Kernels with MFMA take the plain form: inline asm in a kernel makes the
+// compiler keep MFMA results in the accumulation registers, which costs a
+// v_accvgpr_read per result before it can be used.
+template <bool ASM, int K>
+MYNAH_DEV float ubyte_sel(uint32_t v) {
+    if constexpr (ASM) return ubyte_f<K>(v);
+    else return (float)((v >> (8 * K)) & 0xffu);
+}
+
 // Byte k of a dword as float (plain C; the backend picks the conversion).
 MYNAH_DEV float byte_f(uint32_t v, int k) { return (float)((v >> (8 * k)) & 0xffu); }
 

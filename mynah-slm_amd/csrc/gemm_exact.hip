@@ -76,7 +76,7 @@ MYNAH_DEV void gm_q4k_sm(uint4 hdr, uint32_t sb, float d, float dmin, float &ds,
 
 // Q4_K, natural order: piece p = values 16 p .. 16 p + 15, i.e. quant bytes
 // 16 (p & 1) .. + 15 of group p / 4, nibble (p / 2) & 1 (sub-block p / 2).
-struct GmQ4K {
+template <bool ASM = true> struct GmQ4KT {
     uint4 hdr, q;
     __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
         hdr = *(const uint4 *)blk;
@@ -91,19 +91,20 @@ struct GmQ4K {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t n = (w[k] >> shift) & 0x0f0f0f0fu;
-            dst[4 * k] = __builtin_fmaf(d1, ubyte_f<0>(n), -m1);
-            dst[4 * k + 1] = __builtin_fmaf(d1, ubyte_f<1>(n), -m1);
-            dst[4 * k + 2] = __builtin_fmaf(d1, ubyte_f<2>(n), -m1);
-            dst[4 * k + 3] = __builtin_fmaf(d1, ubyte_f<3>(n), -m1);
+            dst[4 * k] = __builtin_fmaf(d1, ubyte_sel<ASM, 0>(n), -m1);
+            dst[4 * k + 1] = __builtin_fmaf(d1, ubyte_sel<ASM, 1>(n), -m1);
+            dst[4 * k + 2] = __builtin_fmaf(d1, ubyte_sel<ASM, 2>(n), -m1);
+            dst[4 * k + 3] = __builtin_fmaf(d1, ubyte_sel<ASM, 3>(n), -m1);
         }
     }
 };
+using GmQ4K = GmQ4KT<true>;
 
 // Q4_K in the matvec order: the LDS order of group g is lo_0, hi_0, lo_1,
 // hi_1, ... (the low-nibble weight j and the high-nibble weight 32 + j of
 // the group, which the matvec sums one after the other). Piece p covers
 // quant bytes 8 (p & 3) .. + 7 of group p / 4, both nibbles.
-struct GmQ4KMv {
+template <bool ASM = true> struct GmQ4KMvT {
     uint4 hdr;
     uint2 q;
     __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
@@ -121,22 +122,23 @@ struct GmQ4KMv {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const uint32_t lo = w[k] & 0x0f0f0f0fu, hi = (w[k] >> 4) & 0x0f0f0f0fu;
-            dst[8 * k + 0] = __builtin_fmaf(dl, ubyte_f<0>(lo), -ml);
-            dst[8 * k + 1] = __builtin_fmaf(dh, ubyte_f<0>(hi), -mh);
-            dst[8 * k + 2] = __builtin_fmaf(dl, ubyte_f<1>(lo), -ml);
-            dst[8 * k + 3] = __builtin_fmaf(dh, ubyte_f<1>(hi), -mh);
-            dst[8 * k + 4] = __builtin_fmaf(dl, ubyte_f<2>(lo), -ml);
-            dst[8 * k + 5] = __builtin_fmaf(dh, ubyte_f<2>(hi), -mh);
-            dst[8 * k + 6] = __builtin_fmaf(dl, ubyte_f<3>(lo), -ml);
-            dst[8 * k + 7] = __builtin_fmaf(dh, ubyte_f<3>(hi), -mh);
+            dst[8 * k + 0] = __builtin_fmaf(dl, ubyte_sel<ASM, 0>(lo), -ml);
+            dst[8 * k + 1] = __builtin_fmaf(dh, ubyte_sel<ASM, 0>(hi), -mh);
+            dst[8 * k + 2] = __builtin_fmaf(dl, ubyte_sel<ASM, 1>(lo), -ml);
+            dst[8 * k + 3] = __builtin_fmaf(dh, ubyte_sel<ASM, 1>(hi), -mh);
+            dst[8 * k + 4] = __builtin_fmaf(dl, ubyte_sel<ASM, 2>(lo), -ml);
+            dst[8 * k + 5] = __builtin_fmaf(dh, ubyte_sel<ASM, 2>(hi), -mh);
+            dst[8 * k + 6] = __builtin_fmaf(dl, ubyte_sel<ASM, 3>(lo), -ml);
+            dst[8 * k + 7] = __builtin_fmaf(dh, ubyte_sel<ASM, 3>(hi), -mh);
         }
     }
 };
+using GmQ4KMv = GmQ4KMvT<true>;
 
 // Q5_K (kernels.c:1812-1833 q5_dequant_block, the decoder of its batched
 // core, 2573-2595): Q4_K's pieces, with the fifth bit of each weight from
 // qh: bytes 16 (p & 1) .. + 15 of qh, bit p / 2 (the sub-block).
-struct GmQ5K {
+template <bool ASM = true> struct GmQ5KT {
     uint4 hdr, q, h;
     __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
         hdr = *(const uint4 *)blk;
@@ -152,17 +154,18 @@ struct GmQ5K {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t n = ((w[k] >> shift) & 0x0f0f0f0fu) | (((hb[k] >> bit) & 0x01010101u) << 4);
-            dst[4 * k] = __builtin_fmaf(d1, ubyte_f<0>(n), -m1);
-            dst[4 * k + 1] = __builtin_fmaf(d1, ubyte_f<1>(n), -m1);
-            dst[4 * k + 2] = __builtin_fmaf(d1, ubyte_f<2>(n), -m1);
-            dst[4 * k + 3] = __builtin_fmaf(d1, ubyte_f<3>(n), -m1);
+            dst[4 * k] = __builtin_fmaf(d1, ubyte_sel<ASM, 0>(n), -m1);
+            dst[4 * k + 1] = __builtin_fmaf(d1, ubyte_sel<ASM, 1>(n), -m1);
+            dst[4 * k + 2] = __builtin_fmaf(d1, ubyte_sel<ASM, 2>(n), -m1);
+            dst[4 * k + 3] = __builtin_fmaf(d1, ubyte_sel<ASM, 3>(n), -m1);
         }
     }
 };
+using GmQ5K = GmQ5KT<true>;
 
 // Q5_K in the matvec order (kernels.c:1785-1810): Q4_KMv's pieces and LDS
 // order; qh bytes 8 (p & 3) .. + 7, bits 2 g (low) and 2 g + 1 (high).
-struct GmQ5KMv {
+template <bool ASM = true> struct GmQ5KMvT {
     uint4 hdr;
     uint2 q, h;
     __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
@@ -183,21 +186,22 @@ struct GmQ5KMv {
             const uint32_t lo = (w[k] & 0x0f0f0f0fu) | (((hb[k] >> (2u * g)) & 0x01010101u) << 4);
             const uint32_t hi =
                 ((w[k] >> 4) & 0x0f0f0f0fu) | (((hb[k] >> (2u * g + 1u)) & 0x01010101u) << 4);
-            dst[8 * k + 0] = __builtin_fmaf(dl, ubyte_f<0>(lo), -ml);
-            dst[8 * k + 1] = __builtin_fmaf(dh, ubyte_f<0>(hi), -mh);
-            dst[8 * k + 2] = __builtin_fmaf(dl, ubyte_f<1>(lo), -ml);
-            dst[8 * k + 3] = __builtin_fmaf(dh, ubyte_f<1>(hi), -mh);
-            dst[8 * k + 4] = __builtin_fmaf(dl, ubyte_f<2>(lo), -ml);
-            dst[8 * k + 5] = __builtin_fmaf(dh, ubyte_f<2>(hi), -mh);
-            dst[8 * k + 6] = __builtin_fmaf(dl, ubyte_f<3>(lo), -ml);
-            dst[8 * k + 7] = __builtin_fmaf(dh, ubyte_f<3>(hi), -mh);
+            dst[8 * k + 0] = __builtin_fmaf(dl, ubyte_sel<ASM, 0>(lo), -ml);
+            dst[8 * k + 1] = __builtin_fmaf(dh, ubyte_sel<ASM, 0>(hi), -mh);
+            dst[8 * k + 2] = __builtin_fmaf(dl, ubyte_sel<ASM, 1>(lo), -ml);
+            dst[8 * k + 3] = __builtin_fmaf(dh, ubyte_sel<ASM, 1>(hi), -mh);
+            dst[8 * k + 4] = __builtin_fmaf(dl, ubyte_sel<ASM, 2>(lo), -ml);
+            dst[8 * k + 5] = __builtin_fmaf(dh, ubyte_sel<ASM, 2>(hi), -mh);
+            dst[8 * k + 6] = __builtin_fmaf(dl, ubyte_sel<ASM, 3>(lo), -ml);
+            dst[8 * k + 7] = __builtin_fmaf(dh, ubyte_sel<ASM, 3>(hi), -mh);
         }
     }
 };
+using GmQ5KMv = GmQ5KMvT<true>;
 
 // Q6_K: piece p = values 16 p .. + 15 = weight 128 h + 32 k + l for
 // h = p / 8, k = (p / 2) & 3, l = 16 (p & 1) .. + 15; scale byte p.
-struct GmQ6K {
+template <bool ASM = true> struct GmQ6KT {
     uint32_t ql[4], qh[4], sd;   // sd: the int8 scale (low byte), d (high 16)
     __device__ __forceinline__ void load(const uint8_t *blk, uint32_t p) {
         const uint32_t h = p >> 3, k = (p >> 1) & 3u, l0 = 16u * (p & 1u);
@@ -217,17 +221,18 @@ struct GmQ6K {
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const uint32_t q6 = ((ql[m] >> ns) & 0x0f0f0f0fu) | (((qh[m] >> hs) & 0x03030303u) << 4);
-            dst[4 * m] = __builtin_fmaf(ds, ubyte_f<0>(q6), n32);
-            dst[4 * m + 1] = __builtin_fmaf(ds, ubyte_f<1>(q6), n32);
-            dst[4 * m + 2] = __builtin_fmaf(ds, ubyte_f<2>(q6), n32);
-            dst[4 * m + 3] = __builtin_fmaf(ds, ubyte_f<3>(q6), n32);
+            dst[4 * m] = __builtin_fmaf(ds, ubyte_sel<ASM, 0>(q6), n32);
+            dst[4 * m + 1] = __builtin_fmaf(ds, ubyte_sel<ASM, 1>(q6), n32);
+            dst[4 * m + 2] = __builtin_fmaf(ds, ubyte_sel<ASM, 2>(q6), n32);
+            dst[4 * m + 3] = __builtin_fmaf(ds, ubyte_sel<ASM, 3>(q6), n32);
         }
     }
 };
+using GmQ6K = GmQ6KT<true>;
 
 // Q8_0 (a 256-value unit = eight 34-byte blocks): piece p = values
 // 16 (p & 1) .. + 15 of block p / 2.
-struct GmQ80 {
+template <bool ASM = true> struct GmQ80T {
     uint32_t q[4], d;
     __device__ __forceinline__ void load(const uint8_t *blk8, uint32_t p) {
         const uint8_t *blk = blk8 + 34u * (p >> 1);
@@ -240,13 +245,14 @@ struct GmQ80 {
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const uint32_t v = q[m] ^ 0x80808080u;
-            dst[4 * m] = __builtin_fmaf(dd, ubyte_f<0>(v), n128);
-            dst[4 * m + 1] = __builtin_fmaf(dd, ubyte_f<1>(v), n128);
-            dst[4 * m + 2] = __builtin_fmaf(dd, ubyte_f<2>(v), n128);
-            dst[4 * m + 3] = __builtin_fmaf(dd, ubyte_f<3>(v), n128);
+            dst[4 * m] = __builtin_fmaf(dd, ubyte_sel<ASM, 0>(v), n128);
+            dst[4 * m + 1] = __builtin_fmaf(dd, ubyte_sel<ASM, 1>(v), n128);
+            dst[4 * m + 2] = __builtin_fmaf(dd, ubyte_sel<ASM, 2>(v), n128);
+            dst[4 * m + 3] = __builtin_fmaf(dd, ubyte_sel<ASM, 3>(v), n128);
         }
     }
 };
+using GmQ80 = GmQ80T<true>;
 
 // The x stage (64 tokens x 64 values) of unit u, stage st: 4 float4 per
 // thread, token idx / 16 and float4 idx % 16 for idx = tid + 256 k.

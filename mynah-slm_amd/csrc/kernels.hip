@@ -8,6 +8,7 @@
 #include "gemv_q40.hip"
 #include "gemv_fast.hip"
 #include "gemm_exact.hip"
+#include "gemm_mfma.hip"
 #include "decode.hip"
 #include "copy.hip"
 #include "int8.hip"

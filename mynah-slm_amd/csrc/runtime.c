@@ -494,7 +494,7 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
     if (chain) split = 0;
     /* Split super-blocks across quads when the launch is small enough that
      * four times the waves still fit the 1,024 SIMDs about twice. */
-    if (all_units > 32768u) split = 0;
+    if (all_units > (uint64_t)env_long("MYNAH_SPLIT_UNITS", 32768)) split = 0;
     const char *env = getenv("MYNAH_GEMV_SPLIT");
     if (env != NULL) split = split && env[0] != '0';
     /* The flat layout (gemv_exact.hip group_flat) for the one-lane exact
@@ -1049,6 +1049,27 @@ int mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream) {
     unsigned grid = (unsigned)(want < 8192 ? want : 8192);
     void *args[] = {&src, &dst, &n16};
     return mynah_launch(d, MYNAH_K_COPY16, grid, 1, 256, 0, mynah_stream_or_default(d, stream),
+                        args);
+}
+
+int mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (src == NULL || sink == NULL || bytes == 0 || bytes % 16 != 0 ||
+        ((uintptr_t)src & 15u) != 0 || ((uintptr_t)sink & 3u) != 0) {
+        mynah_set_error("read needs a 16-byte aligned source, a multiple of 16 bytes and a sink");
+        return -1;
+    }
+    uint64_t n16 = bytes / 16;
+    /* At least four workgroups per CU where the size allows, up to eight
+     * chunks per thread. */
+    uint64_t per = n16 / (256u * 4u * (uint64_t)d->cus);
+    if (per < 1) per = 1;
+    if (per > 8) per = 8;
+    uint64_t want = (n16 + 256u * per - 1) / (256u * per);
+    unsigned grid = (unsigned)(want < 65535 ? want : 65535);
+    void *args[] = {&src, &n16, &sink};
+    return mynah_launch(d, MYNAH_K_READ16, grid, 1, 256, 0, mynah_stream_or_default(d, stream),
                         args);
 }
 

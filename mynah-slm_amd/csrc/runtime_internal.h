@@ -26,6 +26,15 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_Q4K_GEMM_MV, "mynah_q4k_gemm_mv")        \
     X(MYNAH_K_Q6K_GEMM_MV, "mynah_q6k_gemm_mv")        \
     X(MYNAH_K_Q80_GEMM_MV, "mynah_q80_gemm_mv")        \
+    X(MYNAH_K_Q4K_GEMM_MFMA, "mynah_q4k_gemm_exact_mfma") \
+    X(MYNAH_K_Q5K_GEMM_MFMA, "mynah_q5k_gemm_exact_mfma") \
+    X(MYNAH_K_Q6K_GEMM_MFMA, "mynah_q6k_gemm_exact_mfma") \
+    X(MYNAH_K_Q80_GEMM_MFMA, "mynah_q80_gemm_exact_mfma") \
+    X(MYNAH_K_Q4K_GEMM_MV_MFMA, "mynah_q4k_gemm_mv_mfma") \
+    X(MYNAH_K_Q5K_GEMM_MV_MFMA, "mynah_q5k_gemm_mv_mfma") \
+    X(MYNAH_K_Q6K_GEMM_MV_MFMA, "mynah_q6k_gemm_mv_mfma") \
+    X(MYNAH_K_Q80_GEMM_MV_MFMA, "mynah_q80_gemm_mv_mfma") \
+    X(MYNAH_K_GEMM_FOLD, "mynah_gemm_fold")            \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
     X(MYNAH_K_GEMV_GROUP_Q6K, "mynah_gemv_group_q6k")  \
     X(MYNAH_K_GEMV_GROUP_Q4K, "mynah_gemv_group_q4k")  \
@@ -51,6 +60,7 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_PREFILL_SOFTMAX, "mynah_prefill_softmax") \
     X(MYNAH_K_PREFILL_PV, "mynah_prefill_pv")          \
     X(MYNAH_K_COPY16, "mynah_copy16")                  \
+    X(MYNAH_K_READ16, "mynah_read16")                  \
     X(MYNAH_K_EXPF, "mynah_expf_map")                  \
     X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
     X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \

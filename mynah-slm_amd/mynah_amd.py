@@ -102,6 +102,7 @@ def _load() -> C.CDLL:
         "mynah_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
         "mynah_hip_event_destroy": (C.c_int, [_P]),
         "mynah_hip_copy_dev": (C.c_int, [_P, _P, _SZ, _P]),
+        "mynah_hip_read_dev": (C.c_int, [_P, _SZ, _P, _P]),
         "mynah_hip_expf_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_time_sweep": (C.c_int, [C.c_int, _P, _P, C.c_int, _P, _P, _P, _P, C.c_int,
                                            C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
@@ -341,6 +342,10 @@ def dequant_dev(qtype: int, w: int, rows: int, cols: int, y: int, stream=None) -
 
 def copy_dev(dst: int, src: int, nbytes: int, stream=None) -> None:
     check(lib.mynah_hip_copy_dev(dst, src, nbytes, stream), "copy_dev")
+
+
+def read_dev(src: int, nbytes: int, sink: int, stream=None) -> None:
+    check(lib.mynah_hip_read_dev(src, nbytes, sink, stream), "read_dev")
 
 
 def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int):

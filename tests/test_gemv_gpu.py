@@ -241,3 +241,56 @@ def test_kernel_query_names_the_planned_kernel(M):
     assert M.gemv_kernel(2, 1024, 1024).startswith("mynah_q40_chain")
     assert M.lib.mynah_hip_gemv_kernel(12, 1024, 100, 0) is None
     assert b"geometry" in M.lib.mynah_hip_last_error()
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14, 8])
+@pytest.mark.parametrize("mv", [False, True])
+def test_mfma_gemm_equals_valu_gemm(M, qtype, mv):
+    """The exact GEMM with its products on MFMA (the default) against the
+    VALU kernels (MYNAH_GEMM_MFMA=0), bit for bit, with and without the
+    split over super-blocks (forced 3 ways, and off) and, in the matvec
+    order, the residual epilogue; ragged rows and token counts around the
+    64-token tile. The products of v_mfma_f32_16x16x1_4b_f32 with a zero
+    accumulator are v_mul_f32's (a -0 comes out +0, which no sum here can
+    see)."""
+    keys = ("MYNAH_GEMM_MFMA", "MYNAH_GEMM_SPLIT", "MYNAH_GEMM_WGS_PER_CU")
+    saved = {k: os.environ.get(k) for k in keys}
+
+    def run(env, rows, cols, tokens, res):
+        for k in keys:
+            os.environ.pop(k, None)
+        os.environ.update(env)
+        w = M.DeviceBuffer.from_array(M.synth_blocks(qtype, 5, rows, cols))
+        x = M.DeviceBuffer.from_array(M.synth_normal(9, tokens * cols))
+        y = M.DeviceBuffer(4 * rows * tokens)
+        r = M.DeviceBuffer.from_array(M.synth_normal(11, tokens * rows)) if res else None
+        try:
+            if mv:
+                M.check(M.lib.mynah_hip_matmat_mv_dev(qtype, w.ptr, rows, cols, x.ptr, y.ptr,
+                                                      tokens, r.ptr if r else None, None), "mv")
+            else:
+                M.check(M.lib.mynah_hip_matmat_dev(qtype, w.ptr, rows, cols, x.ptr, y.ptr,
+                                                   tokens, None), "matmat")
+            M.sync()
+            return y.download(np.float32, rows * tokens)
+        finally:
+            for b in (w, x, y, r):
+                if b is not None:
+                    b.free()
+
+    try:
+        for rows, cols, tokens in ((100, 512, 2), (64, 256, 65), (300, 1024, 130),
+                                   (2048, 2048, 512)):
+            for res in ((False, True) if mv else (False,)):
+                print(f"[case] type={qtype} mv={mv} {rows}x{cols} tokens={tokens} res={res}",
+                      flush=True)
+                ref = run({"MYNAH_GEMM_MFMA": "0"}, rows, cols, tokens, res)
+                for env in ({}, {"MYNAH_GEMM_SPLIT": "0"}, {"MYNAH_GEMM_SPLIT": "3"}):
+                    got = run(env, rows, cols, tokens, res)
+                    assert np.array_equal(bits(got), bits(ref)), (rows, cols, tokens, res, env)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
