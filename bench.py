@@ -590,6 +590,9 @@ def main() -> int:
     ap.add_argument("--decode-4b-only", action="store_true",
                     help="only configs[4]'s decode (2048-token prompt, then --steps greedy "
                          "steps, exact GEMV + split attention), printed as one JSON line")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the configs[3] GEMMs (exact, then the int8 lane), printed as "
+                         "one JSON line")
     ap.add_argument("--classes-only", action="store_true",
                     help="only the Qwen3-4B GEMV classes with their copy and read-only "
                          "ceilings, printed as one JSON line")
@@ -613,6 +616,10 @@ def main() -> int:
         return 0
     if args.decode_only:
         print(json.dumps({"decode": gpu_decode(M, CF)}), flush=True)
+        return 0
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": gpu_prefill_gemm(M, CF),
+                          "prefill_gemm_int8": gpu_prefill_gemm(M, CF, int8=True)}), flush=True)
         return 0
     if args.classes_only:
         g, c, r, k = gpu_4b_classes(M, CF)

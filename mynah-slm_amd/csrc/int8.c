@@ -19,6 +19,7 @@
 #include "runtime_internal.h"
 
 #include <pthread.h>
+#include <math.h>
 #include <stdlib.h>
 
 static int int8_mode = -1;
@@ -131,8 +132,30 @@ int mynah_q4k_int8_launch(mynah_device *d, int type, const void *w, size_t rows,
     }
     uint32_t c32 = (uint32_t)cols, t32 = (uint32_t)tokens, tile = token_tile(cols);
     void *args[] = {&w, &xq, &xs, &xsum, &y, &r32, &c32, &t32, &nb, &tile};
-    /* Workgroup tile (32 tr) rows x (32 tt) tokens. */
-    int tr = 2, tt = 2;
+    /* Workgroup tile (32 tr) rows x (32 tt) tokens: the largest tile whose
+     * workgroups fill whole rounds of the chip (>= 90 % of the last round
+     * busy), given how many of each fit a CU (LDS: the double-buffered
+     * operands, 60 KiB for 2 x 2 down to 30 KiB for 1 x 1); else the tile
+     * with the fullest last round. */
+    static const int cand[4][3] = {{2, 2, 2}, {2, 1, 3}, {1, 2, 3}, {1, 1, 5}};
+    int tr = 1, tt = 1;
+    double best = -1.0;
+    for (int c = 0; c < 4; c++) {
+        const double wgs = (double)((rows + 32u * cand[c][0] - 1) / (32u * cand[c][0])) *
+                           (double)((tokens + 32u * cand[c][1] - 1) / (32u * cand[c][1]));
+        const double rounds = wgs / ((double)d->cus * cand[c][2]);
+        const double fill = rounds / ceil(rounds);
+        if (fill >= 0.9) {
+            tr = cand[c][0];
+            tt = cand[c][1];
+            break;
+        }
+        if (fill > best) {
+            best = fill;
+            tr = cand[c][0];
+            tt = cand[c][1];
+        }
+    }
     const char *env = getenv("MYNAH_INT8_TILE");
     if (env != NULL && env[0] >= '1' && env[0] <= '2' && env[1] >= '1' && env[1] <= '2') {
         tr = env[0] - '0';

@@ -173,49 +173,89 @@ extern "C" __global__ __launch_bounds__(256) void mynah_q4k_gemv_int8(
 // quants 8 (l / 16) .. +7 of the sub-block (A operand) and token (l % 16) with
 // the same 8 activation positions (B operand), and receives the dots of rows
 // 4 (l / 16) + e, e = 0..3, for token l % 16. Sub-blocks 2g and 2g+1 are the
-// low and high nibbles of the same 8 quant bytes: one 8-byte load per group.
-// scale_j and offset_j of the workgroup's rows are computed once per
-// super-block into LDS (double buffered: one barrier per super-block), and
-// the next super-block's operands are fetched while the current one is
-// summed. The dots of sub-block j + 1 are issued before the epilogue of j.
+// low and high nibbles of the same 8 quant bytes: one 8-byte read per group.
+// Operands go through LDS: per super-block the workgroup copies its rows'
+// quant bytes (Q5_K: qh and qs), its tokens' activations, sub-block sums and
+// scales straight from global memory into LDS (global_load_lds_dwordx4 /
+// _dword: no registers, nothing for the compiler to move), double buffered,
+// the next super-block's copy in flight while the current one is summed;
+// scale_j and offset_j of the rows are computed into LDS from the block
+// headers. One barrier per super-block. Quants and activations sit in LDS
+// chunk-major ([16-byte chunk][row or token][16 bytes]), so the 16 rows or
+// tokens one operand read spans are 16 bytes apart and every read of a
+// sub-block is the same per-lane address plus a constant. The dots of
+// sub-block j + 1 are issued before the epilogue of j.
 // Q5_K (FMT 13, kernels.c:1155-1185 q5_k_quants): the same tiles, the quant
 // bytes at block offset 48 instead of 16, and each lane also holds the 8 qh
 // bytes of its 8 positions: bit j of qh[i] is the fifth bit (+16) of weight
 // i of sub-block j.
-template <int GI_TR, int GI_TT>
-struct GiOps {
-    unsigned long long a[GI_TR][4];   // quant bytes of group g of each row tile
-    unsigned long long h[GI_TR];      // Q5_K: the qh bytes of this lane's positions
-    unsigned long long q[GI_TT][8];   // activations of sub-block j of each token tile
-    int4 s[GI_TT][2];                 // the 8 sub-block sums of each token tile
-    float xs[GI_TT];                  // activation scale of each token tile
-    uint4 hdr;                        // the header this thread stages
-};
+// Bytes of one row's staged quant data per super-block: Q4_K qs (block bytes
+// 16 .. 143), Q5_K qh + qs (block bytes 16 .. 175).
+template <int FMT>
+constexpr uint32_t gi_qb() { return FMT == 13 ? 160u : 128u; }
 
-template <int FMT, int GI_TR, int GI_TT>
-MYNAH_DEV void gi_load(GiOps<GI_TR, GI_TT> &o, const uint8_t *const *arow, const int8_t *const *btok,
-                       const float *const *xsp, const int32_t *const *xsump,
-                       const uint8_t *hrow, uint32_t b) {
-    constexpr uint32_t UB = FMT == 13 ? 176u : 144u;
+typedef __attribute__((address_space(3))) void gi_lds_void;
+
+// Copy super-block b of the workgroup's rows and tokens into LDS buffer
+// (lq, lx, lsum, lxs); wave w takes every fourth 64-chunk piece. Rows and
+// tokens past the ends read the last one (their results are not stored).
+// Copy super-block b of the workgroup's rows and tokens into LDS buffer
+// (lq, lx, lsum, lxs): lq[c][r] = 16-byte chunk c of row r's staged bytes,
+// lx[c][t] = chunk c of token t's 256 activations, lsum[t] = its 8 sums,
+// lxs[t] = its scale. Each copy instruction fills 1 KiB (64 lanes x 16
+// bytes); wave w takes every fourth one. Rows and tokens past the ends read
+// the last one (their results are not stored).
+template <int FMT, int GI_ROWS, int GI_TOK>
+MYNAH_DEV void gi_stage_async(uint8_t *lq, int8_t *lx, int32_t *lsum, float *lxs,
+                              const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,
+                              const float *__restrict__ xs, const int32_t *__restrict__ xsum,
+                              uint32_t R0, uint32_t T0, uint32_t rows, uint32_t tokens,
+                              uint32_t cols, uint32_t nb, size_t rb, uint32_t b, uint32_t wave,
+                              uint32_t lane) {
+    constexpr uint32_t QB = gi_qb<FMT>(), CPR = QB / 16u, UB = FMT == 13 ? 176u : 144u;
+    constexpr uint32_t NQ = GI_ROWS * CPR / 64u, NX = GI_TOK * 16u / 64u, NS = GI_TOK * 2u / 64u;
+    // Workgroup-uniform bases; per-lane offsets stay below 4 GiB (at most 64
+    // rows or tokens of the tile).
+    const uint8_t *wb = w + (size_t)R0 * rb + (size_t)b * UB + 16u;
+    const int8_t *xb = xq + (size_t)T0 * cols + 256u * b;
+    const int32_t *sb = xsum + ((size_t)T0 * nb + b) * 8u;
+    const uint32_t rmax = rows - 1u - R0, tmax = tokens - 1u - T0;
 #pragma unroll
-    for (int i = 0; i < GI_TR; i++) {
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            o.a[i][g] = *(const unsigned long long *)(arow[i] + (size_t)b * UB + 32u * g);
-        // arow points at the lane's quant bytes (block + 48 + 8 lk); its qh
-        // bytes sit 32 bytes before them.
-        if (FMT == 13) o.h[i] = *(const unsigned long long *)(arow[i] + (size_t)b * UB - 32u);
+    for (uint32_t k = 0; k < (NQ + 3u) / 4u; k++) {
+        const uint32_t n = 4u * k + wave;
+        if (n < NQ) {
+            const uint32_t p = 64u * n + lane, c = p / GI_ROWS, r = p - c * GI_ROWS;
+            const uint32_t rr = r < rmax ? r : rmax;
+            __builtin_amdgcn_global_load_lds((const void *)(wb + (uint32_t)(rr * (uint32_t)rb +
+                                                                              16u * c)),
+                                             (gi_lds_void *)(lq + 1024u * n), 16, 0, 0);
+        }
     }
 #pragma unroll
-    for (int k = 0; k < GI_TT; k++) {
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            o.q[k][j] = *(const unsigned long long *)(btok[k] + 256u * b + 32u * j);
-        o.s[k][0] = ((const int4 *)(xsump[k] + 8u * b))[0];
-        o.s[k][1] = ((const int4 *)(xsump[k] + 8u * b))[1];
-        o.xs[k] = xsp[k][b];
+    for (uint32_t k = 0; k < (NX + 3u) / 4u; k++) {
+        const uint32_t n = 4u * k + wave;
+        if (n < NX) {
+            const uint32_t p = 64u * n + lane, c = p / GI_TOK, t = p - c * GI_TOK;
+            const uint32_t tt = t < tmax ? t : tmax;
+            __builtin_amdgcn_global_load_lds((const void *)(xb + (uint32_t)(tt * cols + 16u * c)),
+                                             (gi_lds_void *)(lx + 1024u * n), 16, 0, 0);
+        }
     }
-    o.hdr = *(const uint4 *)(hrow + (size_t)b * UB);
+#pragma unroll
+    for (uint32_t k = 0; k < (NS + 3u) / 4u; k++) {
+        const uint32_t n = 4u * k + wave;
+        if (n < NS) {
+            const uint32_t p = 64u * n + lane, t = p >> 1, tt = t < tmax ? t : tmax;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(sb + (uint32_t)(tt * nb * 8u + 4u * (p & 1u))),
+                (gi_lds_void *)(lsum + 256u * n), 16, 0, 0);
+        }
+    }
+    if (wave == 3u && lane < (uint32_t)GI_TOK) {
+        const uint32_t tt = lane < tmax ? lane : tmax;
+        __builtin_amdgcn_global_load_lds((const void *)(xs + (size_t)T0 * nb + b + tt * nb),
+                                         (gi_lds_void *)lxs, 4, 0, 0);
+    }
 }
 
 // Scale and offset of sub-blocks hj, hj + 1 of the staged row, into LDS.
@@ -232,38 +272,61 @@ MYNAH_DEV void gi_stage(float *buf, const uint4 hdr, uint32_t hj, uint32_t row) 
     buf[(9u + hj) * GI_ROWS + row] = dmin * (float)m1;
 }
 
-template <int FMT, int GI_TR, int GI_TT>
-MYNAH_DEV void gi_dots(i32x4 (&dt)[GI_TR][GI_TT], const GiOps<GI_TR, GI_TT> &o, int j) {
-#pragma unroll
-    for (int i = 0; i < GI_TR; i++) {
-        unsigned long long q =
-            ((j & 1) ? (o.a[i][j >> 1] >> 4) : o.a[i][j >> 1]) & 0x0f0f0f0f0f0f0f0full;
-        if (FMT == 13) q |= ((o.h[i] >> j) & 0x0101010101010101ull) << 4;
-#pragma unroll
-        for (int k = 0; k < GI_TT; k++) {
-            const i32x4 zero = {0, 0, 0, 0};
-            dt[i][k] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)q, (long)o.q[k][j], zero, 0,
-                                                             0, 0);
-        }
-    }
-}
-
-// One super-block's epilogue: tot[i][k][e] over j = 0..7. MIXED: some lane
-// has a token outside the groups of four, which takes the plain form.
+// One super-block's dots and epilogue from the LDS buffers: lane l's rows
+// 16 (GI_TR wr + i) + l % 16 and tokens 16 (GI_TT wt + k) + l % 16, quant and
+// activation positions 32 g + 8 (l / 16) .. +7 of group g / sub-block j;
+// tot[i][k][e] over j = 0..7 in order, then acc += tot * xs. MIXED: some
+// lane has a token outside the groups of four, which takes the plain form.
 template <int FMT, bool MIXED, int GI_TR, int GI_TT>
-MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT> &o,
-                        const float4 *sbuf,
-                        uint32_t wr, uint32_t lk, const bool (&fma_path)[GI_TT]) {
+MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const uint8_t *lq, const int8_t *lx,
+                        const int32_t *lsum, const float *lxs, const float4 *sbuf, uint32_t wr,
+                        uint32_t wt, uint32_t lane, const bool (&fma_path)[GI_TT]) {
 #pragma clang fp contract(off)
-    constexpr int GI_ROWS = 32 * GI_TR;
-    float xsm[GI_TT][8];
+    constexpr int GI_ROWS = 32 * GI_TR, GI_TOK = 32 * GI_TT;
+    const uint32_t lm = lane & 15u, lk = lane >> 4;
+    // Lane l reads the 8 bytes at position 8 (l / 16) of a 32-byte group:
+    // chunk 2 g + (l / 16) / 2 of its row / token, half (l / 16) % 2.
+    const uint32_t lo = 16u * (lk >> 1), hb = 8u * (lk & 1u);
+    const uint8_t *qrow[GI_TR];
+    const int8_t *xrow[GI_TT];
+    uint32_t tl[GI_TT];
+#pragma unroll
+    for (int i = 0; i < GI_TR; i++)
+        qrow[i] = lq + 16u * (16u * (GI_TR * wr + (uint32_t)i) + lm) + hb + lo * GI_ROWS;
 #pragma unroll
     for (int k = 0; k < GI_TT; k++) {
-        xsm[k][0] = (float)o.s[k][0].x; xsm[k][1] = (float)o.s[k][0].y;
-        xsm[k][2] = (float)o.s[k][0].z; xsm[k][3] = (float)o.s[k][0].w;
-        xsm[k][4] = (float)o.s[k][1].x; xsm[k][5] = (float)o.s[k][1].y;
-        xsm[k][6] = (float)o.s[k][1].z; xsm[k][7] = (float)o.s[k][1].w;
+        tl[k] = 16u * (GI_TT * wt + (uint32_t)k) + lm;
+        xrow[k] = lx + 16u * tl[k] + hb + lo * GI_TOK;
     }
+    unsigned long long qh[GI_TR];
+    if (FMT == 13) {
+#pragma unroll
+        for (int i = 0; i < GI_TR; i++) qh[i] = *(const unsigned long long *)qrow[i];
+    }
+    // Dots of sub-block j: the quant bytes of group j / 2 of each row tile
+    // (Q5_K: its qs start at chunk 2), nibble j % 2, times the activations
+    // of sub-block j of each token tile. The loop below stays rolled (runtime
+    // j), so no more than two sub-blocks' dots are ever live.
+    auto dots = [&](i32x4 (&dt)[GI_TR][GI_TT], uint32_t j) {
+        unsigned long long xb[GI_TT];
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++)
+            xb[k] = *(const unsigned long long *)(xrow[k] + 16u * GI_TOK * 2u * j);
+#pragma unroll
+        for (int i = 0; i < GI_TR; i++) {
+            const uint32_t c = (FMT == 13 ? 2u : 0u) + 2u * (j >> 1);
+            const unsigned long long qa =
+                *(const unsigned long long *)(qrow[i] + 16u * GI_ROWS * c);
+            unsigned long long q = (qa >> (4u * (j & 1u))) & 0x0f0f0f0f0f0f0f0full;
+            if (FMT == 13) q |= ((qh[i] >> j) & 0x0101010101010101ull) << 4;
+#pragma unroll
+            for (int k = 0; k < GI_TT; k++) {
+                const i32x4 zero = {0, 0, 0, 0};
+                dt[i][k] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)q, (long)xb[k], zero, 0, 0,
+                                                                 0);
+            }
+        }
+    };
     float tot[GI_TR][GI_TT][4];
 #pragma unroll
     for (int i = 0; i < GI_TR; i++)
@@ -272,20 +335,20 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT>
 #pragma unroll
             for (int e = 0; e < 4; e++) tot[i][k][e] = 0.0f;
     i32x4 cur[GI_TR][GI_TT], nxt[GI_TR][GI_TT];
-    gi_dots<FMT>(cur, o, 0);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        if (j < 7) gi_dots<FMT>(nxt, o, j + 1);
+    dots(cur, 0u);
+#pragma unroll 1
+    for (uint32_t j = 0; j < 8u; j++) {
+        if (j < 7u) dots(nxt, j + 1u);
 #pragma unroll
         for (int i = 0; i < GI_TR; i++) {
             const uint32_t slot = (16u * (GI_TR * wr + i)) / 4u + lk;
             const float4 sc = sbuf[j * (GI_ROWS / 4) + slot];
-            const float4 of = sbuf[(8 + j) * (GI_ROWS / 4) + slot];
+            const float4 of = sbuf[(8u + j) * (GI_ROWS / 4) + slot];
             const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
             const float ofv[4] = {of.x, of.y, of.z, of.w};
 #pragma unroll
             for (int k = 0; k < GI_TT; k++) {
-                const float xsj = xsm[k][j];
+                const float xsj = (float)lsum[8u * tl[k] + j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const float dv = (float)cur[i][k][e];
@@ -299,19 +362,19 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const GiOps<GI_TR, GI_TT>
                 }
             }
         }
-        if (j < 7) {
 #pragma unroll
-            for (int i = 0; i < GI_TR; i++)
+        for (int i = 0; i < GI_TR; i++)
 #pragma unroll
-                for (int k = 0; k < GI_TT; k++) cur[i][k] = nxt[i][k];
-        }
+            for (int k = 0; k < GI_TT; k++) cur[i][k] = nxt[i][k];
     }
 #pragma unroll
     for (int i = 0; i < GI_TR; i++)
 #pragma unroll
-        for (int k = 0; k < GI_TT; k++)
+        for (int k = 0; k < GI_TT; k++) {
+            const float xsv = lxs[tl[k]];
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[i][k][e] = acc[i][k][e] + tot[i][k][e] * o.xs[k];
+            for (int e = 0; e < 4; e++) acc[i][k][e] = acc[i][k][e] + tot[i][k][e] * xsv;
+        }
 }
 
 template <int FMT, int GI_TR, int GI_TT>
@@ -320,6 +383,11 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
                          float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens,
                          uint32_t nb, uint32_t tile) {
     constexpr int GI_ROWS = 32 * GI_TR, GI_TOK = 32 * GI_TT;
+    constexpr uint32_t QB = gi_qb<FMT>();
+    __shared__ __attribute__((aligned(16))) uint8_t lq[2][GI_ROWS * QB];
+    __shared__ __attribute__((aligned(16))) int8_t lx[2][GI_TOK * 256];
+    __shared__ __attribute__((aligned(16))) int32_t lsum[2][GI_TOK * 8];
+    __shared__ __attribute__((aligned(16))) float lxs[2][GI_TOK];
     __shared__ float4 so[2][16 * GI_ROWS / 4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t wr = wave & 1u, wt = wave >> 1;
@@ -327,41 +395,28 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
     const size_t rb = (size_t)nb * (FMT == 13 ? 176u : 144u);
     const uint32_t lm = lane & 15u, lk = lane >> 4;
 
-    // Operand rows and tokens of this lane (clamped for loads; stores check).
-    const uint8_t *arow[GI_TR];
-    const int8_t *btok[GI_TT];
-    const float *xsp[GI_TT];
-    const int32_t *xsump[GI_TT];
     uint32_t tok[GI_TT];
     bool fma_path[GI_TT];
     bool all_fma = true;
-#pragma unroll
-    for (int i = 0; i < GI_TR; i++) {
-        uint32_t r = R0 + 16u * (GI_TR * wr + i) + lm;
-        r = r < rows ? r : rows - 1u;
-        arow[i] = w + (size_t)r * rb + (FMT == 13 ? 48u : 16u) + 8u * lk;
-    }
 #pragma unroll
     for (int k = 0; k < GI_TT; k++) {
         const uint32_t t = T0 + 16u * (GI_TT * wt + k) + lm;
         tok[k] = t;
         const uint32_t tc = t < tokens ? t : tokens - 1u;
-        btok[k] = xq + (size_t)tc * cols + 8u * lk;
-        xsp[k] = xs + (size_t)tc * nb;
-        xsump[k] = xsum + (size_t)tc * nb * 8u;
         const uint32_t t0 = tc - tc % tile;
         const uint32_t cnt = tokens - t0 < tile ? tokens - t0 : tile;
         fma_path[k] = tc - t0 < (cnt & ~3u);
         all_fma = all_fma && fma_path[k];
     }
     const bool mixed = !__all(all_fma);
-    // Staging: thread tid owns row tid / 4 of the workgroup, sub-blocks
+    // Scale staging: thread tid owns row tid / 4 of the workgroup, sub-blocks
     // 2 (tid % 4) and 2 (tid % 4) + 1 (threads beyond 4 GI_ROWS stage nothing).
     const uint32_t srow = tid >> 2, hj = 2u * (tid & 3u);
     const bool stager = srow < GI_ROWS;
     uint32_t hr = R0 + (stager ? srow : 0u);
     hr = hr < rows ? hr : rows - 1u;
     const uint8_t *hrow = w + (size_t)hr * rb;
+    constexpr uint32_t UB = FMT == 13 ? 176u : 144u;
 
     float acc[GI_TR][GI_TT][4];
 #pragma unroll
@@ -371,18 +426,32 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[i][k][e] = 0.0f;
 
-    GiOps<GI_TR, GI_TT> cur, nxt;
-    gi_load<FMT>(cur, arow, btok, xsp, xsump, hrow, 0);
-    if (stager) gi_stage<GI_ROWS>((float *)so[0], cur.hdr, hj, srow);
+    gi_stage_async<FMT, GI_ROWS, GI_TOK>(lq[0], lx[0], lsum[0], lxs[0], w, xq, xs, xsum, R0, T0,
+                                         rows, tokens, cols, nb, rb, 0u, wave, lane);
+    uint4 hdr = *(const uint4 *)hrow;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (stager) gi_stage<GI_ROWS>((float *)so[0], hdr, hj, srow);
     __syncthreads();
     for (uint32_t b = 0; b < nb; b++) {
+        const uint32_t c = b & 1u;
         const bool more = b + 1u < nb;
-        if (more) gi_load<FMT>(nxt, arow, btok, xsp, xsump, hrow, b + 1u);
-        if (mixed) gi_block<FMT, true>(acc, cur, so[b & 1u], wr, lk, fma_path);
-        else gi_block<FMT, false>(acc, cur, so[b & 1u], wr, lk, fma_path);
-        if (more && stager) gi_stage<GI_ROWS>((float *)so[(b + 1u) & 1u], nxt.hdr, hj, srow);
+        if (more) {
+            gi_stage_async<FMT, GI_ROWS, GI_TOK>(lq[c ^ 1u], lx[c ^ 1u], lsum[c ^ 1u],
+                                                 lxs[c ^ 1u], w, xq, xs, xsum, R0, T0, rows,
+                                                 tokens, cols, nb, rb, b + 1u, wave, lane);
+            hdr = *(const uint4 *)(hrow + (size_t)(b + 1u) * UB);
+        }
+        if (mixed)
+            gi_block<FMT, true>(acc, lq[c], lx[c], lsum[c], lxs[c], so[c], wr, wt, lane,
+                                fma_path);
+        else
+            gi_block<FMT, false>(acc, lq[c], lx[c], lsum[c], lxs[c], so[c], wr, wt, lane,
+                                 fma_path);
+        if (more) {
+            __builtin_amdgcn_s_waitcnt(0);
+            if (stager) gi_stage<GI_ROWS>((float *)so[c ^ 1u], hdr, hj, srow);
+        }
         __syncthreads();
-        if (more) cur = nxt;
     }
 
 #pragma unroll
@@ -400,7 +469,7 @@ MYNAH_DEV void gemm_int8(const uint8_t *__restrict__ w, const int8_t *__restrict
 }
 
 #define GEMM_INT8(NAME, FMT, TR, TT)                                                         \
-    extern "C" __global__ __launch_bounds__(256) void NAME##_##TR##TT(                       \
+    extern "C" __global__ __launch_bounds__(256, 2) void NAME##_##TR##TT(                    \
         const uint8_t *__restrict__ w, const int8_t *__restrict__ xq,                        \
         const float *__restrict__ xs, const int32_t *__restrict__ xsum,                      \
         float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t nb,   \
