@@ -62,11 +62,14 @@ MYNAH_DEV float q4k_group(const uint32_t *q, float d, float dmin, uint32_t s0, u
     float sa, ma, sb, mb;
     q4k_sm<2 * G>(s0, s1, s2, sa, ma);
     q4k_sm<2 * G + 1>(s0, s1, s2, sb, mb);
-    const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
+    // The high nibbles stay in place (16 q): (db / 16) (16 q) - ob is the
+    // same real number as db q - ob, and db / 16 is exact, so one fma still
+    // gives the reference's rounding, without a shift per word.
+    const float da = d * sa, db = d * sb * 0.0625f, oa = dmin * ma, ob = dmin * mb;
 #pragma unroll
     for (int m = 0; m < 8; m++) {
         const uint32_t v = q[8 * G + m];
-        const uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo = v & 0x0f0f0f0fu, hi = v & 0xf0f0f0f0u;
         const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
         const float qh[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
         const float4 xa4 = *(const float4 *)(x + 64 * G + 4 * m);
@@ -482,11 +485,12 @@ template <> struct RawSeg<12> {
         float sa, ma, sb, mb;
         q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g, sa, ma);
         q4k_sm_rt(hdr.y, hdr.z, hdr.w, 2u * g + 1u, sb, mb);
-        const float da = d * sa, db = d * sb, oa = dmin * ma, ob = dmin * mb;
+        // High nibbles in place, scale / 16 (exact), as in q4k_group.
+        const float da = d * sa, db = d * sb * 0.0625f, oa = dmin * ma, ob = dmin * mb;
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
         for (int m = 0; m < 8; m++) {
-            const uint32_t lo = q[m] & 0x0f0f0f0fu, hi = (q[m] >> 4) & 0x0f0f0f0fu;
+            const uint32_t lo = q[m] & 0x0f0f0f0fu, hi = q[m] & 0xf0f0f0f0u;
             const float ql[4] = {ubyte_f<0>(lo), ubyte_f<1>(lo), ubyte_f<2>(lo), ubyte_f<3>(lo)};
             const float qh[4] = {ubyte_f<0>(hi), ubyte_f<1>(hi), ubyte_f<2>(hi), ubyte_f<3>(hi)};
             const float4 xa4 = *(const float4 *)(x + 4 * m);
