@@ -183,7 +183,17 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
 mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_tensor *table,
                                  size_t count, const void *blob, uint64_t blob_bytes,
                                  uint32_t n_ctx, char *err, size_t errsz) {
-    if (c == NULL || table == NULL || blob == NULL || n_ctx == 0) {
+    const uint64_t at = 0;
+    return mynah_qwen3_new_parts(c, table, count, &blob, &blob_bytes, &at, 1, blob_bytes, n_ctx,
+                                 err, errsz);
+}
+
+mynah_qwen3 *mynah_qwen3_new_parts(const mynah_qwen3_shape *c, const mynah_synth_tensor *table,
+                                   size_t count, const void *const *parts,
+                                   const uint64_t *part_bytes, const uint64_t *part_at,
+                                   uint32_t n_parts, uint64_t blob_bytes, uint32_t n_ctx,
+                                   char *err, size_t errsz) {
+    if (c == NULL || table == NULL || parts == NULL || n_parts == 0 || n_ctx == 0) {
         fail(err, errsz, "null argument", NULL);
         return NULL;
     }
@@ -212,8 +222,17 @@ mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_t
     s->layers = (dlayer *)calloc(c->n_layers, sizeof *s->layers);
     int ok = s->layers != NULL;
 
+    /* The parts (the shards' data sections of a split checkpoint; one part
+     * otherwise) go to their places in one device blob, unchanged; the gaps
+     * between them are never read. */
     s->blob = (unsigned char *)dalloc(blob_bytes, &ok);
-    if (ok && hipMemcpy(s->blob, blob, blob_bytes, hipMemcpyHostToDevice) != hipSuccess) ok = 0;
+    for (uint32_t i = 0; ok && i < n_parts; i++) {
+        if (parts[i] == NULL || part_at[i] > blob_bytes || part_bytes[i] > blob_bytes - part_at[i])
+            ok = 0;
+        else if (part_bytes[i] != 0 && hipMemcpy(s->blob + part_at[i], parts[i], part_bytes[i],
+                                                 hipMemcpyHostToDevice) != hipSuccess)
+            ok = 0;
+    }
     if (!ok) {
         fail(err, errsz, "cannot upload the model", NULL);
         mynah_hip_qwen3_free(s);

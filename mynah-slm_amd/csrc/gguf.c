@@ -50,20 +50,28 @@ typedef struct {
 typedef struct {
     const char *name;
     uint64_t nlen;
-    uint32_t rank, type;
+    uint32_t rank, type, shard;
     uint64_t ne[GG_MAX_DIMS];
-    uint64_t offset, nbytes;
+    uint64_t offset, nbytes;        /* offset within its shard's data section */
 } gg_tensor;
 
-struct mynah_gguf {
+/* One mapped file of a checkpoint; `concat` is where its data section sits
+ * in the concatenation of all shards' data sections (mynah_gguf_shard_data). */
+typedef struct {
     unsigned char *map;
     size_t size;
     uint32_t version;
-    uint64_t n_kv, n_tensors, alignment;
-    gg_kv *kv;
-    gg_tensor *t;
+    uint64_t alignment;
     const unsigned char *data;
-    uint64_t data_bytes;
+    uint64_t data_bytes, concat;
+} gg_shard;
+
+struct mynah_gguf {
+    gg_shard *sh;
+    uint32_t n_sh;
+    uint64_t n_kv, n_tensors, concat_bytes;
+    gg_kv *kv;                      /* the first shard's metadata */
+    gg_tensor *t;                   /* every shard's tensors, in shard order */
 };
 
 static void gg_err(char *err, size_t errsz, const char *fmt, ...) {
@@ -279,10 +287,233 @@ static int read_scalar(uint32_t type, const unsigned char *p, uint64_t *u, doubl
 
 void mynah_gguf_close(mynah_gguf *g) {
     if (g == NULL) return;
-    if (g->map) munmap(g->map, g->size);
+    for (uint32_t i = 0; i < g->n_sh; i++)
+        if (g->sh[i].map) munmap(g->sh[i].map, g->sh[i].size);
+    free(g->sh);
     free(g->kv);
     free(g->t);
     free(g);
+}
+
+/* The last general.alignment among kv[0 .. n) that reads as a number, else
+ * `dflt` (ingot's header scan). */
+static uint64_t alignment_of(const gg_kv *kv, uint64_t n, uint64_t dflt) {
+    uint64_t a = dflt;
+    for (uint64_t i = 0; i < n; i++) {
+        uint64_t v;
+        double f;
+        if (name_is(kv[i].key, kv[i].klen, "general.alignment", 17) &&
+            read_scalar(kv[i].type, kv[i].val, &v, &f) == 0)
+            a = v;
+    }
+    return a;
+}
+
+/* Map `path` as shard `index` of g and parse it: header, metadata (kept for
+ * the first shard; a later shard's is read with the same checks and only its
+ * general.alignment used, a missing or zero one meaning 32, as ingot's
+ * shard_parse does), tensor infos appended to g's table, data section. */
+static int parse_shard(mynah_gguf *g, uint32_t index, const char *path, char *err,
+                       size_t errsz) {
+    gg_shard *sh = &g->sh[index];
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        gg_err(err, errsz, "cannot open '%s'", path);
+        return -1;
+    }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 24) {
+        close(fd);
+        gg_err(err, errsz, "'%s' is shorter than a GGUF header", path);
+        return -1;
+    }
+    sh->size = (size_t)st.st_size;
+    void *m = mmap(NULL, sh->size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (m == MAP_FAILED) {
+        gg_err(err, errsz, "cannot map '%s'", path);
+        return -1;
+    }
+    sh->map = (unsigned char *)m;
+    g->n_sh = index + 1;
+    gg_cur c = {sh->map, sh->map + sh->size};
+    uint32_t magic;
+    uint64_t n_tensors, n_kv;
+    if (rd_le32(&c, &magic) || magic != GG_MAGIC) {
+        gg_err(err, errsz, "'%s' does not start with the GGUF magic", path);
+        return -1;
+    }
+    if (rd_le32(&c, &sh->version) || sh->version < 2 || sh->version > 3) {
+        gg_err(err, errsz, "'%s': GGUF version %u (this reader takes 2 and 3)", path, sh->version);
+        return -1;
+    }
+    /* A metadata entry takes at least 13 bytes and a tensor info 24, so the
+     * counts are bounded by the file before anything is allocated for them. */
+    if (rd_le64(&c, &n_tensors) || rd_le64(&c, &n_kv) || n_tensors > GG_MAX_COUNT ||
+        n_kv > GG_MAX_COUNT || n_kv * 13 + n_tensors * 24 > sh->size - 24) {
+        gg_err(err, errsz, "'%s': the header counts more entries than the file can hold", path);
+        return -1;
+    }
+    gg_kv *kv = (gg_kv *)calloc(n_kv ? n_kv : 1, sizeof *kv);
+    gg_tensor *grown = (gg_tensor *)realloc(g->t, (size_t)(g->n_tensors + n_tensors + 1) *
+                                                      sizeof *g->t);
+    if (kv == NULL || grown == NULL) {
+        free(kv);
+        if (grown) g->t = grown;
+        gg_err(err, errsz, "out of memory");
+        return -1;
+    }
+    g->t = grown;
+    for (uint64_t i = 0; i < n_kv; i++)
+        if (read_entry(&c, &kv[i], i, err, errsz)) {
+            free(kv);
+            return -1;
+        }
+    sh->alignment = alignment_of(kv, n_kv, 32);
+    if (index == 0) {
+        g->kv = kv;
+        g->n_kv = n_kv;
+    } else {
+        free(kv);
+        if (sh->alignment == 0) sh->alignment = 32;
+    }
+    /* Checked here rather than where ingot checks it (when the data section
+     * is placed); a file is refused either way. */
+    if (sh->alignment == 0 || sh->alignment > (1u << 20) ||
+        (sh->alignment & (sh->alignment - 1))) {
+        gg_err(err, errsz, "'%s': general.alignment %llu is not a power of two up to 1 MiB",
+               path, (unsigned long long)sh->alignment);
+        return -1;
+    }
+    const uint64_t base = g->n_tensors;
+    for (uint64_t i = 0; i < n_tensors; i++) {
+        gg_tensor *t = &g->t[base + i];
+        memset(t, 0, sizeof *t);
+        t->shard = index;
+        if (rd_string(&c, &t->name, &t->nlen) || rd_le32(&c, &t->rank)) {
+            gg_err(err, errsz, "tensor entry %llu is cut short by the end of the file", (unsigned long long)i);
+            return -1;
+        }
+        const int nl = (int)(t->nlen < 200 ? t->nlen : 200);
+        if (t->rank > GG_MAX_DIMS) {
+            gg_err(err, errsz, "tensor '%.*s': rank %u is above %d", nl, t->name, t->rank,
+                   GG_MAX_DIMS);
+            return -1;
+        }
+        uint64_t nelem = 1;
+        for (uint32_t d = 0; d < t->rank; d++) {
+            if (rd_le64(&c, &t->ne[d]) || t->ne[d] == 0 || nelem > UINT64_MAX / t->ne[d]) {
+                gg_err(err, errsz, "tensor '%.*s': a zero or overflowing dimension", nl, t->name);
+                return -1;
+            }
+            nelem *= t->ne[d];
+        }
+        for (uint32_t d = t->rank; d < GG_MAX_DIMS; d++) t->ne[d] = 1;
+        if (rd_le32(&c, &t->type) || rd_le64(&c, &t->offset)) {
+            gg_err(err, errsz, "tensor '%.*s': its entry is cut short", nl, t->name);
+            return -1;
+        }
+        uint64_t be, bb;
+        if (type_geometry(t->type, &be, &bb)) {
+            gg_err(err, errsz, "tensor '%.*s': ggml type %u is unknown", nl, t->name, t->type);
+            return -1;
+        }
+        /* Quantized blocks lie along ne[0] and may not straddle rows. */
+        if ((be > 1 && (t->rank == 0 || t->ne[0] % be != 0)) || (nelem / be) > UINT64_MAX / bb) {
+            gg_err(err, errsz, "tensor '%.*s': %llu values is not whole blocks of type %u", nl,
+                   t->name, (unsigned long long)t->ne[0], t->type);
+            return -1;
+        }
+        t->nbytes = nelem / be * bb;
+        if (t->offset % sh->alignment != 0) {
+            gg_err(err, errsz, "tensor '%.*s': data offset %llu is off the %llu-byte alignment", nl, t->name,
+                   (unsigned long long)t->offset, (unsigned long long)sh->alignment);
+            return -1;
+        }
+        g->n_tensors = base + i + 1;
+    }
+    const uint64_t head = (uint64_t)(c.p - sh->map);
+    const uint64_t data_off = (head + sh->alignment - 1) & ~(sh->alignment - 1);
+    if (data_off > sh->size) {
+        gg_err(err, errsz, "'%s': the data section starts past the end of the file", path);
+        return -1;
+    }
+    sh->data = sh->map + data_off;
+    sh->data_bytes = sh->size - data_off;
+    for (uint64_t i = base; i < g->n_tensors; i++) {
+        const gg_tensor *t = &g->t[i];
+        if (t->offset > sh->data_bytes || t->nbytes > sh->data_bytes - t->offset) {
+            gg_err(err, errsz, "tensor '%.*s': data ends past the end of '%s'",
+                   (int)(t->nlen < 200 ? t->nlen : 200), t->name, path);
+            return -1;
+        }
+    }
+    return 0;
+}
+
+/* 1 (with the message) when two tensors share a name, compared as C strings
+ * (up to a first NUL); an open-addressing hash of the names, so a table of
+ * millions of entries costs linear time. */
+static int dup_name(const mynah_gguf *g, char *err, size_t errsz) {
+    if (g->n_tensors < 2) return 0;
+    uint64_t cap = 16;
+    while (cap < 2 * g->n_tensors) cap *= 2;
+    uint64_t *slot = (uint64_t *)calloc((size_t)cap, sizeof *slot);   /* index + 1 */
+    if (slot == NULL) {
+        gg_err(err, errsz, "out of memory");
+        return 1;
+    }
+    int dup = 0;
+    for (uint64_t i = 0; i < g->n_tensors && !dup; i++) {
+        const gg_tensor *t = &g->t[i];
+        const size_t tl = strnlen(t->name, (size_t)t->nlen);
+        uint64_t h = 0xcbf29ce484222325ull;
+        for (size_t k = 0; k < tl; k++) h = (h ^ (unsigned char)t->name[k]) * 0x100000001b3ull;
+        for (uint64_t p = h & (cap - 1);; p = (p + 1) & (cap - 1)) {
+            if (slot[p] == 0) {
+                slot[p] = i + 1;
+                break;
+            }
+            const gg_tensor *o = &g->t[slot[p] - 1];
+            if (strnlen(o->name, (size_t)o->nlen) == tl && memcmp(o->name, t->name, tl) == 0) {
+                gg_err(err, errsz, "tensor '%.*s' appears more than once",
+                       (int)(tl < 200 ? tl : 200), t->name);
+                dup = 1;
+                break;
+            }
+        }
+    }
+    free(slot);
+    return dup;
+}
+
+/* Open the `n` files of one checkpoint as shards 0 .. n - 1. A tensor name
+ * present twice (in one file or across shards) makes every lookup
+ * ambiguous, and the reference's reader refuses it; so does this one. */
+static mynah_gguf *open_paths(char *const *paths, uint32_t n, char *err, size_t errsz) {
+    mynah_gguf *g = (mynah_gguf *)calloc(1, sizeof *g);
+    if (g == NULL || (g->sh = (gg_shard *)calloc(n, sizeof *g->sh)) == NULL) {
+        free(g);
+        gg_err(err, errsz, "out of memory");
+        return NULL;
+    }
+    for (uint32_t i = 0; i < n; i++)
+        if (parse_shard(g, i, paths[i], err, errsz)) goto fail;
+    if (dup_name(g, err, errsz)) goto fail;
+    /* The shards' data sections laid end to end, each from a multiple of 256
+     * bytes and of its own alignment. */
+    uint64_t at = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const uint64_t a = g->sh[i].alignment > 256 ? g->sh[i].alignment : 256;
+        at = (at + a - 1) & ~(a - 1);
+        g->sh[i].concat = at;
+        at += g->sh[i].data_bytes;
+    }
+    g->concat_bytes = at;
+    return g;
+fail:
+    mynah_gguf_close(g);
+    return NULL;
 }
 
 mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
@@ -290,143 +521,65 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
         gg_err(err, errsz, "null path");
         return NULL;
     }
-    const int fd = open(path, O_RDONLY | O_CLOEXEC);
-    if (fd < 0) {
-        gg_err(err, errsz, "cannot open '%s'", path);
+    char *one = (char *)path;
+    return open_paths(&one, 1, err, errsz);
+}
+
+/* <prefix>-NNNNN-of-MMMMM.gguf with 1 <= NNNNN <= MMMMM <= 999 and MMMMM >= 2
+ * (llama.cpp's split naming, read as third_party/ingot/src/gguf.c:466-509
+ * reads it): the number of shards and the length of the prefix, else 0. */
+static uint32_t split_name(const char *path, size_t *prefix) {
+    const size_t len = strlen(path), tl = 15, sl = 5;      /* "-NNNNN-of-MMMMM", ".gguf" */
+    if (len < tl + sl || strcmp(path + len - sl, ".gguf") != 0) return 0;
+    const char *t = path + len - sl - tl;
+    if (t[0] != '-' || t[6] != '-' || t[7] != 'o' || t[8] != 'f' || t[9] != '-') return 0;
+    unsigned no = 0, total = 0;
+    for (int i = 1; i <= 5; i++) {
+        if (t[i] < '0' || t[i] > '9') return 0;
+        no = no * 10u + (unsigned)(t[i] - '0');
+    }
+    for (int i = 10; i <= 14; i++) {
+        if (t[i] < '0' || t[i] > '9') return 0;
+        total = total * 10u + (unsigned)(t[i] - '0');
+    }
+    if (total < 2 || total > 999 || no < 1 || no > total) return 0;
+    *prefix = (size_t)(t - path);
+    return total;
+}
+
+mynah_gguf *mynah_gguf_open_split(const char *path, char *err, size_t errsz) {
+    if (path == NULL) {
+        gg_err(err, errsz, "null path");
         return NULL;
     }
-    struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size < 24) {
-        close(fd);
-        gg_err(err, errsz, "'%s' is shorter than a GGUF header", path);
-        return NULL;
+    size_t prefix = 0;
+    const uint32_t n = split_name(path, &prefix);
+    if (n == 0) return mynah_gguf_open(path, err, errsz);
+    char **paths = (char **)calloc(n, sizeof *paths);
+    const size_t plen = prefix + 15 + 5 + 1;
+    mynah_gguf *g = NULL;
+    if (paths == NULL) goto oom;
+    for (uint32_t i = 0; i < n; i++) {
+        if ((paths[i] = (char *)malloc(plen)) == NULL) goto oom;
+        memcpy(paths[i], path, prefix);
+        snprintf(paths[i] + prefix, plen - prefix, "-%05u-of-%05u.gguf", i + 1, n);
     }
-    mynah_gguf *g = (mynah_gguf *)calloc(1, sizeof *g);
-    if (g == NULL) {
-        close(fd);
-        gg_err(err, errsz, "out of memory");
-        return NULL;
-    }
-    g->size = (size_t)st.st_size;
-    void *m = mmap(NULL, g->size, PROT_READ, MAP_PRIVATE, fd, 0);
-    close(fd);
-    if (m == MAP_FAILED) {
-        free(g);
-        gg_err(err, errsz, "cannot map '%s'", path);
-        return NULL;
-    }
-    g->map = (unsigned char *)m;
-    gg_cur c = {g->map, g->map + g->size};
-    uint32_t magic;
-    if (rd_le32(&c, &magic) || magic != GG_MAGIC) {
-        gg_err(err, errsz, "'%s' does not start with the GGUF magic", path);
-        goto fail;
-    }
-    if (rd_le32(&c, &g->version) || g->version < 2 || g->version > 3) {
-        gg_err(err, errsz, "'%s': GGUF version %u (this reader takes 2 and 3)", path, g->version);
-        goto fail;
-    }
-    /* A metadata entry takes at least 13 bytes and a tensor info 24, so the
-     * counts are bounded by the file before anything is allocated for them. */
-    if (rd_le64(&c, &g->n_tensors) || rd_le64(&c, &g->n_kv) || g->n_tensors > GG_MAX_COUNT ||
-        g->n_kv > GG_MAX_COUNT || g->n_kv * 13 + g->n_tensors * 24 > g->size - 24) {
-        gg_err(err, errsz, "'%s': the header counts more entries than the file can hold", path);
-        goto fail;
-    }
-    g->kv = (gg_kv *)calloc(g->n_kv ? g->n_kv : 1, sizeof *g->kv);
-    g->t = (gg_tensor *)calloc(g->n_tensors ? g->n_tensors : 1, sizeof *g->t);
-    if (g->kv == NULL || g->t == NULL) {
-        gg_err(err, errsz, "out of memory");
-        goto fail;
-    }
-    for (uint64_t i = 0; i < g->n_kv; i++)
-        if (read_entry(&c, &g->kv[i], i, err, errsz)) goto fail;
-    /* The last general.alignment that reads as a number sets the alignment
-     * (ingot's header scan); it must be a power of two up to 1 MiB. */
-    g->alignment = 32;
-    for (uint64_t i = 0; i < g->n_kv; i++) {
-        uint64_t v;
-        double f;
-        if (name_is(g->kv[i].key, g->kv[i].klen, "general.alignment", 17) &&
-            read_scalar(g->kv[i].type, g->kv[i].val, &v, &f) == 0)
-            g->alignment = v;
-    }
-    if (g->alignment == 0 || g->alignment > (1u << 20) || (g->alignment & (g->alignment - 1))) {
-        gg_err(err, errsz, "'%s': general.alignment %llu is not a power of two up to 1 MiB",
-               path, (unsigned long long)g->alignment);
-        goto fail;
-    }
-    for (uint64_t i = 0; i < g->n_tensors; i++) {
-        gg_tensor *t = &g->t[i];
-        if (rd_string(&c, &t->name, &t->nlen) || rd_le32(&c, &t->rank)) {
-            gg_err(err, errsz, "tensor entry %llu is cut short by the end of the file", (unsigned long long)i);
-            goto fail;
-        }
-        const int nl = (int)(t->nlen < 200 ? t->nlen : 200);
-        if (t->rank > GG_MAX_DIMS) {
-            gg_err(err, errsz, "tensor '%.*s': rank %u is above %d", nl, t->name, t->rank,
-                   GG_MAX_DIMS);
-            goto fail;
-        }
-        uint64_t nelem = 1;
-        for (uint32_t d = 0; d < t->rank; d++) {
-            if (rd_le64(&c, &t->ne[d]) || t->ne[d] == 0 || nelem > UINT64_MAX / t->ne[d]) {
-                gg_err(err, errsz, "tensor '%.*s': a zero or overflowing dimension", nl, t->name);
-                goto fail;
-            }
-            nelem *= t->ne[d];
-        }
-        for (uint32_t d = t->rank; d < GG_MAX_DIMS; d++) t->ne[d] = 1;
-        if (rd_le32(&c, &t->type) || rd_le64(&c, &t->offset)) {
-            gg_err(err, errsz, "tensor '%.*s': its entry is cut short", nl, t->name);
-            goto fail;
-        }
-        uint64_t be, bb;
-        if (type_geometry(t->type, &be, &bb)) {
-            gg_err(err, errsz, "tensor '%.*s': ggml type %u is unknown", nl, t->name, t->type);
-            goto fail;
-        }
-        /* Quantized blocks lie along ne[0] and may not straddle rows. */
-        if ((be > 1 && (t->rank == 0 || t->ne[0] % be != 0)) || (nelem / be) > UINT64_MAX / bb) {
-            gg_err(err, errsz, "tensor '%.*s': %llu values is not whole blocks of type %u", nl,
-                   t->name, (unsigned long long)t->ne[0], t->type);
-            goto fail;
-        }
-        t->nbytes = nelem / be * bb;
-        if (t->offset % g->alignment != 0) {
-            gg_err(err, errsz, "tensor '%.*s': data offset %llu is off the %llu-byte alignment", nl, t->name,
-                   (unsigned long long)t->offset, (unsigned long long)g->alignment);
-            goto fail;
-        }
-    }
-    {
-        const uint64_t head = (uint64_t)(c.p - g->map);
-        const uint64_t data_off = (head + g->alignment - 1) & ~(g->alignment - 1);
-        if (data_off > g->size) {
-            gg_err(err, errsz, "'%s': the data section starts past the end of the file", path);
-            goto fail;
-        }
-        g->data = g->map + data_off;
-        g->data_bytes = g->size - data_off;
-        for (uint64_t i = 0; i < g->n_tensors; i++) {
-            const gg_tensor *t = &g->t[i];
-            if (t->offset > g->data_bytes || t->nbytes > g->data_bytes - t->offset) {
-                gg_err(err, errsz, "tensor '%.*s': data ends past the end of '%s'",
-                       (int)(t->nlen < 200 ? t->nlen : 200), t->name, path);
-                goto fail;
-            }
-        }
-    }
+    g = open_paths(paths, n, err, errsz);
+    goto done;
+oom:
+    gg_err(err, errsz, "out of memory");
+done:
+    if (paths)
+        for (uint32_t i = 0; i < n; i++) free(paths[i]);
+    free(paths);
     return g;
-fail:
-    mynah_gguf_close(g);
-    return NULL;
 }
 
 /* ── queries ────────────────────────────────────────────────────────────── */
 
-uint32_t mynah_gguf_version(const mynah_gguf *g) { return g ? g->version : 0; }
-uint64_t mynah_gguf_alignment(const mynah_gguf *g) { return g ? g->alignment : 0; }
+uint32_t mynah_gguf_version(const mynah_gguf *g) { return g ? g->sh[0].version : 0; }
+uint64_t mynah_gguf_alignment(const mynah_gguf *g) { return g ? g->sh[0].alignment : 0; }
+uint32_t mynah_gguf_n_shards(const mynah_gguf *g) { return g ? g->n_sh : 0; }
 uint64_t mynah_gguf_n_kv(const mynah_gguf *g) { return g ? g->n_kv : 0; }
 uint64_t mynah_gguf_n_tensors(const mynah_gguf *g) { return g ? g->n_tensors : 0; }
 
@@ -572,7 +725,7 @@ int mynah_gguf_tensor_table(const mynah_gguf *g, mynah_synth_tensor *table, size
             d->cols = t->ne[0];
             d->rows = 1;
             for (uint32_t k = 1; k < GG_MAX_DIMS; k++) d->rows *= t->ne[k];
-            d->offset = t->offset;
+            d->offset = g->sh[t->shard].concat + t->offset;
             d->nbytes = t->nbytes;
         }
         n++;
@@ -582,13 +735,30 @@ int mynah_gguf_tensor_table(const mynah_gguf *g, mynah_synth_tensor *table, size
 }
 
 const void *mynah_gguf_data(const mynah_gguf *g, uint64_t *bytes) {
-    if (g == NULL) return NULL;
-    if (bytes) *bytes = g->data_bytes;
-    return g->data;
+    if (g == NULL || g->n_sh != 1) return NULL;
+    if (bytes) *bytes = g->sh[0].data_bytes;
+    return g->sh[0].data;
+}
+
+const void *mynah_gguf_shard_data(const mynah_gguf *g, uint32_t shard, uint64_t *bytes,
+                                  uint64_t *concat) {
+    if (g == NULL || shard >= g->n_sh) return NULL;
+    if (bytes) *bytes = g->sh[shard].data_bytes;
+    if (concat) *concat = g->sh[shard].concat;
+    return g->sh[shard].data;
+}
+
+int mynah_gguf_tensor_place(const mynah_gguf *g, uint64_t index, uint32_t *shard,
+                            uint64_t *offset) {
+    if (g == NULL || index >= g->n_tensors) return -1;
+    if (shard) *shard = g->t[index].shard;
+    if (offset) *offset = g->t[index].offset;
+    return 0;
 }
 
 mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *err, size_t errsz) {
-    mynah_gguf *g = mynah_gguf_open(path, err, errsz);
+    /* src/model.c:183 opens every checkpoint through the split-aware open. */
+    mynah_gguf *g = mynah_gguf_open_split(path, err, errsz);
     if (g == NULL) return NULL;
     mynah_qwen3_shape shape;
     uint32_t n_train = 0;
@@ -597,19 +767,26 @@ mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *e
         size_t count = 0;
         mynah_gguf_tensor_table(g, NULL, 0, &count);
         mynah_synth_tensor *table = (mynah_synth_tensor *)calloc(count ? count : 1, sizeof *table);
-        if (table == NULL) {
+        const void **parts = (const void **)calloc(g->n_sh, sizeof *parts);
+        uint64_t *bytes = (uint64_t *)calloc(g->n_sh, sizeof *bytes);
+        uint64_t *at = (uint64_t *)calloc(g->n_sh, sizeof *at);
+        if (table == NULL || parts == NULL || bytes == NULL || at == NULL) {
             gg_err(err, errsz, "out of memory");
         } else {
             mynah_gguf_tensor_table(g, table, count, &count);
+            for (uint32_t i = 0; i < g->n_sh; i++)
+                parts[i] = mynah_gguf_shard_data(g, i, &bytes[i], &at[i]);
             /* The reference's server asks for the model's own context
              * (server/main.c:426); a zero context_length means one position
              * here, which the decoder refuses like any empty context. */
             if (n_ctx == 0) n_ctx = n_train;
-            uint64_t bytes = 0;
-            const void *data = mynah_gguf_data(g, &bytes);
-            s = mynah_hip_qwen3_new(&shape, table, count, data, bytes, n_ctx, err, errsz);
-            free(table);
+            s = mynah_qwen3_new_parts(&shape, table, count, parts, bytes, at, g->n_sh,
+                                      g->concat_bytes, n_ctx, err, errsz);
         }
+        free(table);
+        free(parts);
+        free(bytes);
+        free(at);
     }
     mynah_gguf_close(g);
     return s;

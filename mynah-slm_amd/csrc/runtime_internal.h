@@ -194,4 +194,14 @@ int mynah_matmat_mv_launch(mynah_device *d, int type, const void *w, size_t rows
                            const float *x, float *y, size_t tokens, const float *res,
                            hipStream_t stream);
 
+/* mynah_hip_qwen3_new over a blob of blob_bytes assembled from n_parts
+ * host parts, part i (part_bytes[i] bytes) at offset part_at[i]: the data
+ * sections of a split checkpoint's shards (gguf.c). */
+#include "mynah_decode.h"
+mynah_qwen3 *mynah_qwen3_new_parts(const mynah_qwen3_shape *c, const mynah_synth_tensor *table,
+                                   size_t count, const void *const *parts,
+                                   const uint64_t *part_bytes, const uint64_t *part_at,
+                                   uint32_t n_parts, uint64_t blob_bytes, uint32_t n_ctx,
+                                   char *err, size_t errsz);
+
 #endif

@@ -137,6 +137,12 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_prompt": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, _P,
                                              C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mynah_gguf_open": (_P, [C.c_char_p, C.c_char_p, _SZ]),
+        "mynah_gguf_open_split": (_P, [C.c_char_p, C.c_char_p, _SZ]),
+        "mynah_gguf_n_shards": (C.c_uint32, [_P]),
+        "mynah_gguf_shard_data": (_P, [_P, C.c_uint32, C.POINTER(C.c_uint64),
+                                       C.POINTER(C.c_uint64)]),
+        "mynah_gguf_tensor_place": (C.c_int, [_P, C.c_uint64, C.POINTER(C.c_uint32),
+                                              C.POINTER(C.c_uint64)]),
         "mynah_gguf_close": (None, [_P]),
         "mynah_gguf_version": (C.c_uint32, [_P]),
         "mynah_gguf_alignment": (C.c_uint64, [_P]),
@@ -441,11 +447,41 @@ class GgufShape:
 class GgufFile:
     """A memory-mapped GGUF v2 / v3 file (include/mynah_gguf.h)."""
 
-    def __init__(self, path: str):
+    def __init__(self, path: str, split: bool = False):
+        """split: open a <prefix>-0000k-of-0000n.gguf checkpoint whole
+        (mynah_gguf_open_split)."""
         err = C.create_string_buffer(512)
-        self.h = lib.mynah_gguf_open(os.fsencode(path), err, 512)
+        fn = lib.mynah_gguf_open_split if split else lib.mynah_gguf_open
+        self.h = fn(os.fsencode(path), err, 512)
         if not self.h:
             raise HipError(f"gguf_open: {err.value.decode(errors='replace')}")
+
+    @property
+    def n_shards(self) -> int:
+        return int(lib.mynah_gguf_n_shards(self.h))
+
+    def places(self):
+        """[(shard, offset within the shard's data section)] of every tensor."""
+        out, sh, off = [], C.c_uint32(), C.c_uint64()
+        for i in range(self.n_tensors):
+            check(lib.mynah_gguf_tensor_place(self.h, i, C.byref(sh), C.byref(off)), "place")
+            out.append((int(sh.value), int(off.value)))
+        return out
+
+    def shard_size(self, shard: int) -> int:
+        """Bytes of shard `shard`'s data section (to the end of its file)."""
+        size, at = C.c_uint64(), C.c_uint64()
+        if not lib.mynah_gguf_shard_data(self.h, shard, C.byref(size), C.byref(at)):
+            raise HipError("shard_size: no such shard")
+        return int(size.value)
+
+    def shard_bytes(self, shard: int, offset: int, nbytes: int) -> bytes:
+        """nbytes of shard `shard`'s data section from `offset`."""
+        size, at = C.c_uint64(), C.c_uint64()
+        p = lib.mynah_gguf_shard_data(self.h, shard, C.byref(size), C.byref(at))
+        if not p or offset + nbytes > size.value:
+            raise HipError("shard_bytes: out of range")
+        return C.string_at(p + offset, nbytes)
 
     @property
     def version(self) -> int:
@@ -549,7 +585,7 @@ class Qwen3Decoder:
     def from_gguf(cls, path: str, n_ctx: int = 0) -> "Qwen3Decoder":
         """The decoder over a GGUF checkpoint (mynah_slm_load, src/model.c:177):
         n_ctx 0 takes the file's context_length."""
-        with GgufFile(path) as g:
+        with GgufFile(path, split=True) as g:
             shape, _ = g.qwen3_shape()
         self = cls.__new__(cls)
         self.model = types.SimpleNamespace(shape=shape, path=path)

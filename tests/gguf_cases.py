@@ -1,13 +1,15 @@
 """GGUF files the reader tests share with tests/golden/make_gguf_golden.py.
 
-Two families, each a name -> bytes builder:
+Three families, each keyed by name:
   OPEN_CASES    a small container with metadata of every value type and
                 tensors of several ggml types, valid and broken one field at a
                 time (the malformations of the reference's own reader test,
                 third_party/ingot/tests/test_gguf.c:304-410, and more);
   CONFIG_CASES  a one-layer Qwen3-shaped file whose metadata is varied the ways
                 src/model.c:71-125 (load_config) and :177-228 (tensor binding)
-                tell apart.
+                tell apart;
+  SPLIT_CASES   split checkpoints (files and the name to open), read by
+                ingot_gguf_open_split (gguf.h:62-66, gguf.c:466-570).
 The golden script records, per case, whether the compiled reference's reader
 (ingot_gguf_open) and loader (mynah_slm_load) accept it and which config it
 reads; the tests hold this repository's reader to the same answers.
@@ -132,6 +134,13 @@ def _open_cases():
     lo = w.pos[("offset", last[0])]
     cases["last_offset_one_block_late"] = lambda: _patch(
         b, lo, "<Q", struct.unpack_from("<Q", b, lo)[0] + 32)
+
+    def duplicate_name():
+        d = mini_writer()
+        d.tensors.append(("f16.weight",) + tuple(d.tensors[0][1:]))
+        return d.to_bytes()
+
+    cases["duplicate_tensor_name"] = duplicate_name
     return cases
 
 
@@ -227,3 +236,80 @@ OPEN_CASES = _open_cases()
 CONFIG_CASES = _config_cases()
 CONFIG_FIELDS = ("n_layers", "d_model", "d_ff", "n_heads", "n_kv_heads", "head_dim", "n_ctx",
                  "vocab", "rms_eps", "rope_theta")
+
+
+# ── split checkpoints ──────────────────────────────────────────────────────
+
+def _split_files(w, n=3, prefix="m", later_kvs=(), alignments=None):
+    shards = GW.split_writers(w, n, later_kvs, alignments)
+    return [[GW.split_name(prefix, i, n), s.to_bytes()] for i, s in enumerate(shards)], shards
+
+
+def _split_cases():
+    """name -> () -> (files [[file name, bytes]], the name to open): split
+    checkpoints (<prefix>-0000k-of-0000n.gguf, gguf.h:62-66) whole and
+    broken one shard at a time."""
+    cases = {}
+    later = (("general.architecture", KV_STRING, "mini", None),)
+
+    def three():
+        return _split_files(mini_writer(), 3, later_kvs=later)[0]
+
+    cases["three_shards"] = lambda: (three(), GW.split_name("m", 0, 3))
+    cases["open_via_second"] = lambda: (three(), GW.split_name("m", 1, 3))
+    cases["open_via_last"] = lambda: (three(), GW.split_name("m", 2, 3))
+    cases["two_shards_v2"] = lambda: (_split_files(mini_writer(version=2), 2)[0],
+                                      GW.split_name("m", 0, 2))
+    cases["later_alignment_64"] = lambda: (
+        _split_files(mini_writer(), 3, alignments=[32, 64, 16])[0], GW.split_name("m", 0, 3))
+
+    def later_align(value):
+        files, shards = _split_files(mini_writer(), 3)
+        b = shards[1].to_bytes()
+        files[1][1] = _patch(b, shards[1].pos[("kv", "general.alignment")], "<I", value)
+        return files
+
+    cases["later_alignment_0"] = lambda: (later_align(0), GW.split_name("m", 0, 3))
+    cases["later_alignment_48"] = lambda: (later_align(48), GW.split_name("m", 0, 3))
+
+    def later_no_alignment_key():
+        w = mini_writer()
+        shards = GW.split_writers(w, 3)
+        shards[2].append_alignment = False
+        return [[GW.split_name("m", i, 3), s.to_bytes()] for i, s in enumerate(shards)]
+
+    cases["later_no_alignment_key"] = lambda: (later_no_alignment_key(), GW.split_name("m", 0, 3))
+    cases["missing_shard"] = lambda: (three()[:2], GW.split_name("m", 0, 3))
+
+    def duplicate_across():
+        w = mini_writer()
+        shards = GW.split_writers(w, 3)
+        shards[2].tensors.append(shards[0].tensors[0])
+        return [[GW.split_name("m", i, 3), s.to_bytes()] for i, s in enumerate(shards)]
+
+    cases["duplicate_across_shards"] = lambda: (duplicate_across(), GW.split_name("m", 0, 3))
+
+    def broken_later(patch):
+        files, shards = _split_files(mini_writer(), 3)
+        files[2][1] = patch(shards[2], files[2][1])
+        return files
+
+    cases["later_bad_kv_type"] = lambda: (broken_later(
+        lambda s, b: _patch(b, s.pos[("kv", "split.no")] - 4, "<I", 13)),
+        GW.split_name("m", 0, 3))
+    cases["later_version_1"] = lambda: (broken_later(lambda s, b: _patch(b, 4, "<I", 1)),
+                                        GW.split_name("m", 0, 3))
+    cases["later_truncated"] = lambda: (broken_later(lambda s, b: b[:s.pos["data"] - 1]),
+                                        GW.split_name("m", 0, 3))
+    cases["later_payload_past_eof"] = lambda: (broken_later(
+        lambda s, b: _patch(b, s.pos[("offset", s.tensors[-1][0])], "<Q", 1 << 20)),
+        GW.split_name("m", 0, 3))
+    cases["one_of_one_is_plain"] = lambda: ([[GW.split_name("m", 0, 1), mini_writer().to_bytes()]],
+                                            GW.split_name("m", 0, 1))
+    cases["number_past_total_is_plain"] = lambda: (
+        [["m-00004-of-00003.gguf", mini_writer().to_bytes()]], "m-00004-of-00003.gguf")
+    cases["plain_name"] = lambda: ([["m.gguf", mini_writer().to_bytes()]], "m.gguf")
+    return cases
+
+
+SPLIT_CASES = _split_cases()

@@ -120,3 +120,29 @@ def qwen3_writer(shape, table, count: int, blob, n_ctx: int) -> GgufWriter:
 
 def qwen3_gguf(shape, table, count: int, blob, n_ctx: int) -> bytes:
     return qwen3_writer(shape, table, count, blob, n_ctx).to_bytes()
+
+
+def split_writers(w: GgufWriter, n: int, later_kvs=(), alignments=None) -> list:
+    """w's tensors spread over n shards, a contiguous run each, in order (as
+    llama.cpp's gguf-split writes them): shard 0 carries w's metadata, later
+    shards only `later_kvs`;
+    every shard also gets split.no / split.count / split.tensors.count
+    (u16, u16, i32) like gguf-split's. alignments[i] sets shard i's."""
+    per = -(-len(w.tensors) // n)
+    out = []
+    for i in range(n):
+        a = alignments[i] if alignments else w.alignment
+        s = GgufWriter(version=w.version, alignment=a, append_alignment=w.append_alignment)
+        if i == 0:
+            s.kvs = list(w.kvs)
+        else:
+            s.kvs = list(later_kvs)
+        s.kv("split.no", KV_U16, i).kv("split.count", KV_U16, n)
+        s.kv("split.tensors.count", KV_I32, len(w.tensors))
+        s.tensors = w.tensors[i * per:(i + 1) * per]
+        out.append(s)
+    return out
+
+
+def split_name(prefix: str, i: int, n: int) -> str:
+    return f"{prefix}-{i + 1:05d}-of-{n:05d}.gguf"

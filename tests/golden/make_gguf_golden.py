@@ -14,7 +14,9 @@ Records, as plain JSON data:
                metadata count, alignment, data base, tensor table, and the
                u64 / f64 / string / array-length reads of every key;
   config       for every CONFIG_CASES file, mynah_slm_load's config (null when
-               it refuses the file).
+               it refuses the file);
+  split        for every SPLIT_CASES checkpoint, what ingot_gguf_open_split
+               reads (null when it refuses it), each tensor row with its shard.
 """
 from __future__ import annotations
 
@@ -62,12 +64,23 @@ def main() -> None:
             with open(path, "wb") as f:
                 f.write(build())
             out["config"][name] = O.ref_qwen3_config(ref, path)
+        out["split"] = {}
+        for name, build in GC.SPLIT_CASES.items():
+            files, opened = build()
+            sd = os.path.join(d, "split_" + name)
+            os.makedirs(sd)
+            for fname, data in files:
+                with open(os.path.join(sd, fname), "wb") as f:
+                    f.write(data)
+            out["split"][name] = O.ref_gguf_read(ref, os.path.join(sd, opened), keys, split=True)
     with open(os.path.join(HERE, "gguf_cases.json"), "w") as f:
         json.dump(out, f, indent=1, sort_keys=True)
         f.write("\n")
     print("accepted:", sum(v is not None for v in out["open"].values()), "of",
           len(out["open"]), "open cases;", sum(v is not None for v in out["config"].values()),
-          "of", len(out["config"]), "config cases")
+          "of", len(out["config"]), "config cases;",
+          sum(v is not None for v in out["split"].values()), "of", len(out["split"]),
+          "split cases")
 
 
 if __name__ == "__main__":

@@ -153,6 +153,7 @@ def load_ref():
                                     _SZ]),
         # ingot's GGUF reader (third_party/ingot/include/ingot/gguf.h:60-130)
         "ingot_gguf_open": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
+        "ingot_gguf_open_split": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
         "ingot_gguf_close": (None, [_P]),
         "ingot_gguf_version": (C.c_uint32, [_P]),
         "ingot_gguf_alignment": (C.c_uint64, [_P]),
@@ -497,13 +498,16 @@ def ref_run(ref, model: SynthModel, n_ctx, steps, k=None, v=None, n_prefill=0, p
     return [int(t) for t in greedy], logits
 
 
-def ref_gguf_read(ref, path: str, keys=()):
+def ref_gguf_read(ref, path: str, keys=(), split: bool = False):
     """What the reference's reader makes of the file at `path`: None when
-    ingot_gguf_open refuses it, else its header, tensor table and, for each of
-    `keys`, the u64 / f64 / string / array-length reads (None where refused)."""
+    ingot_gguf_open (split: ingot_gguf_open_split) refuses it, else its
+    header, tensor table (split: each row also carrying the tensor's shard)
+    and, for each of `keys`, the u64 / f64 / string / array-length reads
+    (None where refused)."""
     g = _P()
     err = C.create_string_buffer(512)
-    if ref.ingot_gguf_open(C.byref(g), os.fsencode(path), err, 512) != 0:
+    opener = ref.ingot_gguf_open_split if split else ref.ingot_gguf_open
+    if opener(C.byref(g), os.fsencode(path), err, 512) != 0:
         assert g.value is None and err.value
         return None
     try:
@@ -512,8 +516,9 @@ def ref_gguf_read(ref, path: str, keys=()):
                "data_base": int(ref.ingot_gguf_data_base(g, 0)), "tensors": [], "kv": {}}
         for i in range(ref.ingot_gguf_count(g)):
             t = ref.ingot_gguf_at(g, i).contents
-            out["tensors"].append([t.name.decode(), t.type, t.rank, list(t.ne[:t.rank]),
-                                   int(t.offset), int(t.nbytes)])
+            row = [t.name.decode(), t.type, t.rank, list(t.ne[:t.rank]), int(t.offset),
+                   int(t.nbytes)]
+            out["tensors"].append(row + [int(t.shard)] if split else row)
         for key in keys:
             kv = ref.ingot_gguf_kv_find(g, key.encode())
             if not kv:

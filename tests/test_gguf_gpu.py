@@ -136,3 +136,26 @@ def test_refusals(M, tiny, tmp_path):
         M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model)), (1 << 20) + 1)
     with pytest.raises(M.HipError):
         M.Qwen3Decoder.from_gguf(str(tmp_path / "absent.gguf"))
+
+
+def test_split_checkpoint_decodes_like_the_single_file(M, tiny, tmp_path):
+    """The tiny model as a three-shard checkpoint (its tensors spread in
+    order, the later shards with their own alignments, 64 and 16) opened
+    through its second shard's name: the same logits bit for bit as the
+    single file, step after step (src/model.c:183 opens both the same way)."""
+    print("[case] split GGUF (3 shards) vs single file, 6 steps", flush=True)
+    model, k, v, first = tiny
+    w = tiny_writer(model)
+    d = tmp_path / "split"
+    d.mkdir()
+    for i, s in enumerate(GW.split_writers(w, 3, alignments=[32, 64, 16])):
+        (d / GW.split_name("tiny", i, 3)).write_bytes(s.to_bytes())
+    a = M.Qwen3Decoder.from_gguf(str(d / GW.split_name("tiny", 1, 3)), 24)
+    b = M.Qwen3Decoder.from_gguf(write(tmp_path, "one", w), 24)
+    for dec in (a, b):
+        dec.set_kv(k, v, N_PRE)
+    tok = first
+    for _ in range(6):
+        la, lb = a.forward(tok), b.forward(tok)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        tok = int(np.argmax(la))
