@@ -155,7 +155,8 @@ int mynah_hip_dequant_dev(int type, const void *w, size_t rows, size_t cols,
  * GEMM speed (the prompt prefill's projections). res (optional, may equal
  * y): y = res + W x, the reference's residual add (src/arch_qwen3.c:224).
  * No reference counterpart (the reference's batched product sums in its
- * own batched order). cols % 256 == 0; device pointers; asynchronous. */
+ * own batched order). cols % 256 == 0 (Q4_0: cols % 32 == 0, its batched
+ * order being the matvec's); device pointers; asynchronous. */
 int mynah_hip_matmat_mv_dev(int type, const void *w, size_t rows, size_t cols,
                             const float *x, float *y, size_t tokens, const float *res,
                             void *stream);

@@ -83,9 +83,8 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
  * token by token, src/arch_qwen3.c:3-7). Tokens run in chunks of up to 2048
  * (MYNAH_PREFILL_CHUNK) through matvec-order GEMMs, per-row RMSNorm and
  * SwiGLU, and per-query attention; the chunk buffers are allocated on first
- * use. A model with Q4_0 projections (no batched Q4_0 GEMM) runs one
- * decode step per token instead, which gives the same bits. 0, or -1 when
- * the tokens do not fit the context. */
+ * use; Q4_0 projections take the Q4_0 chains, whose batched order is the
+ * matvec's. 0, or -1 when the tokens do not fit the context. */
 int mynah_hip_qwen3_prefill(mynah_qwen3 *s, const uint32_t *tokens, uint32_t n);
 
 /* How mynah_hip_qwen3_prompt fills the cache with the prompt:

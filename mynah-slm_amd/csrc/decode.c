@@ -75,7 +75,6 @@ struct mynah_qwen3 {
      * rows of X, normalised X, Q (rotated in place), attention output,
      * gate (then SwiGLU) and up activations, scores, and the tokens. */
     int prefill_mode;               /* MYNAH_PREFILL_BATCHED or MYNAH_PREFILL_STEPS */
-    int has_q40;                    /* a Q4_0 projection: prompts prefill token by token */
     uint32_t pf_cap;
     float *pf_x, *pf_xn, *pf_q, *pf_att, *pf_g, *pf_u, *pf_s;
     uint32_t *pf_tok;
@@ -274,10 +273,6 @@ mynah_qwen3 *mynah_qwen3_new_parts(const mynah_qwen3_shape *c, const mynah_synth
                         L->wk.type == 0 || L->wv.type == 0 || L->wo.type == 0 ||
                         L->down.type == 0))
             rc = fail(err, errsz, "projection types must be quantized, gate/up alike", n);
-        if (rc == 0 && (L->wq.type == MYNAH_Q4_0 || L->wk.type == MYNAH_Q4_0 ||
-                        L->wv.type == MYNAH_Q4_0 || L->wo.type == MYNAH_Q4_0 ||
-                        L->gate.type == MYNAH_Q4_0 || L->down.type == MYNAH_Q4_0))
-            s->has_q40 = 1;
     }
     if (rc == 0 && s->head.type == 0)
         rc = fail(err, errsz, "the output head must be quantized", NULL);
@@ -782,13 +777,6 @@ int mynah_hip_qwen3_prefill(mynah_qwen3 *s, const uint32_t *tokens, uint32_t n) 
             mynah_set_error("token %u out of range", tokens[i]);
             return -1;
         }
-    /* The batched GEMMs have no Q4_0 form: such a model fills the cache
-     * with the per-token step (the same bits). */
-    if (s->has_q40) {
-        for (uint32_t i = 0; i < n; i++)
-            if (mynah_hip_qwen3_forward(s, tokens[i], NULL) != 0) return -1;
-        return 0;
-    }
     const uint32_t cap = prefill_chunk_cap();
     if (n > 0 && prefill_alloc(s, n < cap ? n : cap) != 0) return -1;
     hipStream_t st = d->stream;
@@ -885,10 +873,7 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
             mynah_set_error("token %u out of range", prompt[i]);
             return -1;
         }
-    /* The batched prefill's matvec-order GEMMs have no Q4_0 form; a model
-     * with Q4_0 projections fills the cache with the per-token step, which
-     * gives the same bits. */
-    if (n_prompt > 1 && s->prefill_mode == MYNAH_PREFILL_BATCHED && !s->has_q40)
+    if (n_prompt > 1 && s->prefill_mode == MYNAH_PREFILL_BATCHED)
         return prompt_batched(s, d, prompt, n_prompt, n_steps, tokens_out, prefill_ms, decode_ms);
     if (n_prompt > 1 &&
         hipMemcpy(s->forced, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice) != hipSuccess) {

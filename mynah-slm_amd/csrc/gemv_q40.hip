@@ -16,7 +16,8 @@
 // workgroup), T tokens per lane as T
 // independent chains interleaved (T = 1 for the matvec; 2, 4 or 8 batched,
 // the most that still leaves enough waves to fill the chip), grid.y
-// over token groups. The row is streamed in chunks of 8 blocks (256 values,
+// over token groups; res (may be NULL or equal y) is added to each finished
+// chain, the residual add of the batched prefill. The row is streamed in chunks of 8 blocks (256 values,
 // 144 bytes): a chunk's words are loaded one chunk ahead of their use, and
 // the matching 256 x values of each token are staged in LDS and read as
 // broadcasts. The chains are latency-bound (cols dependent adds each); the
@@ -29,9 +30,9 @@
 #define Q40_WORDS 37            // dwords covering a chunk at either 2-byte skew
 
 template <int T>
-MYNAH_DEV void q40_chain(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                         float *__restrict__ y, uint32_t rows, uint32_t cols, uint32_t tokens,
-                         uint32_t row_bytes) {
+MYNAH_DEV void q40_chain(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,
+                         uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,
+                         const float *res) {
 #pragma clang fp contract(off)
     __shared__ float4 xs[T][64];
     const uint32_t lane = threadIdx.x;
@@ -123,7 +124,10 @@ MYNAH_DEV void q40_chain(const uint8_t *__restrict__ w, const float *__restrict_
     if (row < rows) {
 #pragma unroll
         for (int t = 0; t < T; t++)
-            if (t0 + (uint32_t)t < tokens) y[(size_t)(t0 + (uint32_t)t) * rows + row] = acc[t];
+            if (t0 + (uint32_t)t < tokens) {
+                const size_t o = (size_t)(t0 + (uint32_t)t) * rows + row;
+                y[o] = res ? res[o] + acc[t] : acc[t];
+            }
     }
 }
 
@@ -231,25 +235,29 @@ mynah_q40_chain_pc(const uint8_t *__restrict__ w, const float *__restrict__ x,
 }
 
 extern "C" __global__ void __launch_bounds__(64)
-mynah_q40_chain1(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
-                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
-    q40_chain<1>(w, x, y, rows, cols, tokens, row_bytes);
+mynah_q40_chain1(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,
+                 const float *res) {
+    q40_chain<1>(w, x, y, rows, cols, tokens, row_bytes, res);
 }
 
 extern "C" __global__ void __launch_bounds__(64)
-mynah_q40_chain2(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
-                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
-    q40_chain<2>(w, x, y, rows, cols, tokens, row_bytes);
+mynah_q40_chain2(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,
+                 const float *res) {
+    q40_chain<2>(w, x, y, rows, cols, tokens, row_bytes, res);
 }
 
 extern "C" __global__ void __launch_bounds__(64)
-mynah_q40_chain4(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
-                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
-    q40_chain<4>(w, x, y, rows, cols, tokens, row_bytes);
+mynah_q40_chain4(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,
+                 const float *res) {
+    q40_chain<4>(w, x, y, rows, cols, tokens, row_bytes, res);
 }
 
 extern "C" __global__ void __launch_bounds__(64)
-mynah_q40_chain8(const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y,
-                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes) {
-    q40_chain<8>(w, x, y, rows, cols, tokens, row_bytes);
+mynah_q40_chain8(const uint8_t *__restrict__ w, const float *__restrict__ x, float *y,
+                 uint32_t rows, uint32_t cols, uint32_t tokens, uint32_t row_bytes,
+                 const float *res) {
+    q40_chain<8>(w, x, y, rows, cols, tokens, row_bytes, res);
 }

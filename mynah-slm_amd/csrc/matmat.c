@@ -96,7 +96,7 @@ int mynah_matmat_launch(mynah_device *d, int type, const void *w, size_t rows, s
         return mynah_int8_product(d, type, w, rows, cols, x, y, tokens, stream);
     /* Q4_0 has no batched kernel in the reference: its generic path runs the
      * matvec's chain per token (generic.c:76-93), and so does this one. */
-    if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, tokens, stream);
+    if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, tokens, NULL, stream);
     /* The reference's batched core works in 256-wide units for every type
      * and refuses anything else (kernels.c:1087-1088, 2641-2648). */
     if (cols % 256 != 0) {
@@ -128,9 +128,15 @@ int mynah_matmat_mv_launch(mynah_device *d, int type, const void *w, size_t rows
                            hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(type, rows, cols, &rb) != 0) return -1;
+    /* Q4_0's matvec and batched product share one order (a single running
+     * sum per output, kernels.c:2467-2484, generic.c:76-93): the batched
+     * chains are the matvec-order GEMM. */
     if (type == MYNAH_Q4_0) {
-        mynah_set_error("no matvec-order GEMM for Q4_0");
-        return -1;
+        if (tokens == 0 || tokens > 0xffffffffu) {
+            mynah_set_error("matvec-order GEMM needs 1 <= tokens < 2^32");
+            return -1;
+        }
+        return mynah_q40_launch(d, w, rows, cols, x, y, tokens, res, stream);
     }
     if (cols % 256 != 0 || tokens == 0 || tokens > 0xffffffffu || rb > 0xffffffffu) {
         mynah_set_error("matvec-order GEMM needs cols %% 256 == 0 and 1 <= tokens < 2^32");

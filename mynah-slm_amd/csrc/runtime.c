@@ -204,7 +204,7 @@ static int gemv_launch(mynah_device *d, int type, const void *w, size_t rows, si
      * (third_party/ingot/src/kernels.c:819-834). */
     if (allow_int8 && type == MYNAH_Q4_K && mynah_int8_mode() == MYNAH_INT8_ALL)
         return mynah_int8_product(d, MYNAH_Q4_K, w, rows, cols, x, y, 1, stream);
-    if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, 1, stream);
+    if (type == MYNAH_Q4_0) return mynah_q40_launch(d, w, rows, cols, x, y, 1, NULL, stream);
     if (type != MYNAH_Q8_0 && cols % 256 != 0) {
         mynah_set_error("cols must be a multiple of 256");
         return -1;
@@ -236,7 +236,7 @@ int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, siz
 static long env_long(const char *name, long dflt);
 
 int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
-                     float *y, size_t tokens, hipStream_t stream) {
+                     float *y, size_t tokens, const float *res, hipStream_t stream) {
     size_t rb;
     if (mynah_geometry(MYNAH_Q4_0, rows, cols, &rb) != 0) return -1;
     /* Batched: T token chains per lane, the largest of 8, 4, 2 that still
@@ -261,11 +261,11 @@ int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, c
      * weight). With more rows the one-wave kernel already fills the chip and
      * does less work in all (151936 x 1024: 35 against 53 us).
      * MYNAH_Q40_PC=0 always takes the one-wave kernel. */
-    if (tokens == 1 && rows < 32768u && env_long("MYNAH_Q40_PC", 1) != 0) {
+    if (tokens == 1 && res == NULL && rows < 32768u && env_long("MYNAH_Q40_PC", 1) != 0) {
         void *args[] = {&w, &x, &y, &r32, &c32, &rb32};
         return mynah_launch(d, MYNAH_K_Q40_CHAIN_PC, grid, 1, 256, 0, stream, args);
     }
-    void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32};
+    void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32, &res};
     const int k = per == 1 ? MYNAH_K_Q40_CHAIN1 : per == 2 ? MYNAH_K_Q40_CHAIN2
                 : per == 4 ? MYNAH_K_Q40_CHAIN4 : MYNAH_K_Q40_CHAIN8;
     return mynah_launch(d, k, grid, (unsigned)groups, 64, 0, stream, args);

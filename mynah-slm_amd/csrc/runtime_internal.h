@@ -109,9 +109,10 @@ static inline int mynah_w_misaligned(int type, const void *w) {
     return ((uintptr_t)w & m) != 0;
 }
 /* Q4_0 products (gemv_q40.hip): y[t][r] for tokens >= 1, the reference's
- * single running sum per (row, token). */
+ * single running sum per (row, token) — the matvec's order and the batched
+ * product's alike. res (NULL, or may equal y): y = res + that sum. */
 int mynah_q40_launch(mynah_device *d, const void *w, size_t rows, size_t cols, const float *x,
-                     float *y, size_t tokens, hipStream_t stream);
+                     float *y, size_t tokens, const float *res, hipStream_t stream);
 
 int mynah_gemv_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,
                       const float *x, float *y, hipStream_t stream);

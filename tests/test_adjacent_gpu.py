@@ -5,11 +5,12 @@ compiled reference (test_oracle_adjacent.py): the Q5_K matvec in the order of
 the reference's scalar lane (grouped kernel, both the one-lane and the
 split-quad layouts), its batched product in the batched core's order, the
 Q4_0 matvec and batched product as one running sum per (row, token), and
-both dequants. The decoder takes Q5_K tensors (embedding, tied head, paired
-gate/up, K/V, residual projections): its logits match the oracle decoder
-within the decode tolerance, its greedy ids equal, and its batched prefill
-leaves the step-by-step cache bit for bit. Q4_0 tensors are refused by the
-decoder (no fused kernel), and misaligned or ragged operands by the ABI.
+both dequants. The decoder takes Q5_K and Q4_0 tensors (embedding, tied
+head, paired gate/up, K/V, residual projections): its logits match the
+oracle decoder within the decode tolerance, its greedy ids equal, and its
+batched prefill (Q4_0 through the token chains, whose batched order is the
+matvec's) leaves the step-by-step cache bit for bit. Misaligned or ragged
+operands are refused by the ABI.
 """
 from __future__ import annotations
 
@@ -158,8 +159,12 @@ def test_device_twins_and_refusals(M):
             assert M.lib.mynah_hip_matvec_dev(t, wd.ptr, rows, cols - 16, xd.ptr, yd.ptr,
                                               None) == -1
             if t == 2:
-                assert M.lib.mynah_hip_matmat_mv_dev(2, wd.ptr, rows, cols, xd.ptr, yd.ptr,
-                                                     tokens, None, None) == -1
+                # Q4_0's matvec-order GEMM is its batched product.
+                M.check(M.lib.mynah_hip_matmat_mv_dev(2, wd.ptr, rows, cols, xd.ptr, yd.ptr,
+                                                      tokens, None, None), "matmat_mv")
+                M.sync()
+                assert np.array_equal(bits(yd.download(np.float32, rows * tokens)),
+                                      bits(O.matmat(t, w, rows, cols, x, tokens)))
         finally:
             for b in (wd, xd, yd):
                 b.free()
@@ -253,9 +258,8 @@ def test_decoder_with_block_type(M, qtype):
 
 @pytest.mark.parametrize("qtype", DECODER_TYPES)
 def test_decoder_batched_prefill_is_bit_identical(M, qtype):
-    """Q5_K takes the batched prefill; a model with Q4_0 projections prefills
-    token by token whatever the mode asks. Either way the cache and the next
-    logits equal the per-token path's bits."""
+    """The batched prefill of a model with Q5_K or Q4_0 projections: the
+    cache and the next logits equal the per-token path's bits."""
     print(f"[case] type {qtype} decoder: batched prefill vs steps", flush=True)
     model = Variant(M, Q5K_TENSORS, qtype=qtype)
     prompt = O.uniform(21, 40, CF.QWEN3_TINY.vocab)
@@ -292,6 +296,25 @@ def test_decoder_all_q40_projections(M):
         assert rel_err(a, b) <= TOL
         tok = int(np.argmax(b))
         assert int(np.argmax(a)) == tok
+
+
+@pytest.mark.parametrize("chunk", ["2048", "16"])
+def test_all_q40_batched_prefill(M, monkeypatch, chunk):
+    """Every projection Q4_0: a 70-token prompt prefilled in batches (one
+    chunk, and 16-token chunks) leaves the per-token cache and next logits
+    bit for bit; the chains take 8, 4 or 2 tokens per lane by batch size."""
+    monkeypatch.setenv("MYNAH_PREFILL_CHUNK", chunk)
+    print(f"[case] all-Q4_0 tiny decoder: batched prefill (chunk {chunk}) vs steps", flush=True)
+    model = Variant(M, ALL_PROJECTIONS, qtype=2)
+    prompt = O.uniform(23, 70, CF.QWEN3_TINY.vocab)
+    a, b = M.Qwen3Decoder(model, 80), M.Qwen3Decoder(model, 80)
+    for t in prompt:
+        a.forward(int(t), want_logits=False)
+    b.prefill(prompt)
+    ka, va = a.get_kv(prompt.size)
+    kb, vb = b.get_kv(prompt.size)
+    assert np.array_equal(bits(ka), bits(kb)) and np.array_equal(bits(va), bits(vb))
+    assert np.array_equal(bits(a.forward(5)), bits(b.forward(5)))
 
 
 @pytest.mark.parametrize("qtype", DECODER_TYPES)

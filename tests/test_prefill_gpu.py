@@ -7,11 +7,12 @@ the same tokens one decode step at a time (mynah_hip_qwen3_forward without
 logits, exact GEMV order, exact attention), which is itself within the
 reference's 1e-4 metric of the compiled reference and gives its greedy ids
 (test_decode_gpu.py). Checked here: the matvec-order GEMM against the oracle
-matvec of every token (bit-exact, Q4_K / Q6_K / Q8_0, with and without the
+matvec of every token (bit-exact, Q4_K / Q6_K / Q8_0 / Q4_0, with and without the
 residual epilogue); the whole K/V cache and the next step's logits after a
 batched prefill against the step-by-step fill (bit-exact), for the tiny
 model across chunk sizes 1, 7, 64 and 512 and a prefill starting after a
-synthetic cache, for Qwen3-0.6B, and the prompt() loop's greedy ids.
+synthetic cache, for Qwen3-0.6B, for Qwen3-4B over a 2048-token prompt in
+one default-size (2048) chunk, and the prompt() loop's greedy ids.
 """
 from __future__ import annotations
 
@@ -53,7 +54,7 @@ def bits(a):
     return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("qtype", [12, 14, 8])
+@pytest.mark.parametrize("qtype", [12, 14, 8, 2])
 @pytest.mark.parametrize("rows,cols,tokens", [(96, 1024, 5), (130, 2048, 64), (64, 512, 131)])
 def test_matmat_mv_equals_matvec(M, qtype, rows, cols, tokens):
     print(f"[case] matmat_mv type={qtype} {rows}x{cols} tokens={tokens}", flush=True)
@@ -125,6 +126,18 @@ def test_qwen3_06b_prefill_equals_steps(M):
     prompt = M.synth_uniform(M.substream(7, 4), 100, shape.vocab)
     a, b = fill_both(M, model, prompt, 104)
     assert_same_state(a, b, int(prompt[1]))
+
+
+def test_qwen3_4b_prefill_default_chunk_equals_steps(M):
+    """configs[4]'s prompt length at the default chunk: one 2048-token
+    batch against 2048 decode steps."""
+    os.environ.pop("MYNAH_PREFILL_CHUNK", None)
+    shape = CF.QWEN3_4B
+    print("[case] Qwen3-4B prefill of 2048 tokens, default chunk", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    prompt = M.synth_uniform(M.substream(7, 6), 2048, shape.vocab)
+    a, b = fill_both(M, model, prompt, 2056)
+    assert_same_state(a, b, int(prompt[5]))
 
 
 def test_prompt_batched_equals_steps(M):
