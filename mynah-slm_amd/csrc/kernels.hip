@@ -4,6 +4,7 @@
 // SPDX-License-Identifier: MIT
 #include "dequant.hip"
 #include "gemv_exact.hip"
+#include "gemv_pc.hip"
 #include "gemv_stream.hip"
 #include "gemv_q40.hip"
 #include "gemv_fast.hip"

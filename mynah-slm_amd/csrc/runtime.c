@@ -452,6 +452,41 @@ static int gemv_flat_plan(const mynah_device *d, mynah_gemv_group *grp, gemv_pla
     return 0;
 }
 
+/* Producer/consumer layout (gemv_pc.hip) for all-Q4_K launches: a
+ * workgroup of one adding wave and four producing waves owns R = min(64,
+ * 64 / Ut) whole rows, one super-block per adding lane. Returns 1 when the
+ * launch does not qualify (rows longer than 64 super-blocks, or LDS over
+ * 64 KiB). */
+static int gemv_pc_plan(mynah_gemv_group *grp, gemv_plan *p) {
+    uint32_t tiles = 0;
+    size_t lds = 0;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        mynah_gemv_desc *g = &grp->d[i];
+        const uint32_t ut = g->w2 ? 2u * g->units : g->units;
+        if (g->type != MYNAH_Q4_K || ut > 64u) return 1;
+        const uint32_t r = 64u / ut;
+        const size_t slots = 2u * (size_t)r * ut * 68u;
+        const size_t tail = g->norm_w && g->cols > slots ? g->cols : slots;
+        const size_t need = ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
+                             (((size_t)r * (ut | 1u) + 3u) & ~(size_t)3u) + tail) * 4u;
+        if (need > lds) lds = need;
+    }
+    if (lds > 64u * 1024u) return 1;
+    for (uint32_t i = 0; i < grp->n; i++) {
+        mynah_gemv_desc *g = &grp->d[i];
+        const uint32_t r = 64u / (g->w2 ? 2u * g->units : g->units);
+        g->pad = r;
+        g->tile0 = tiles;
+        tiles += (g->rows + r - 1u) / r;
+    }
+    p->grid = tiles;
+    p->lds = lds;
+    p->threads = 320u;
+    p->shape = 0;
+    p->kernel = MYNAH_K_GEMV_PC_Q4K;
+    return 0;
+}
+
 /* Plan a grouped GEMV in the given order (-1: the library's current one):
  * exact (lane = row x unit slot, unit sums folded in order; a single large
  * matrix with long rows takes the streaming kernel) or reordered (8-lane row
@@ -489,6 +524,17 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         }
     }
     if (exact && !chain && gemv_stream_plan(d, grp, p) == 0) return 0;
+    /* The producer/consumer layout for small all-Q4_K launches, whose
+     * one-lane chains leave most SIMDs idle: MYNAH_GEMV_PC=1 wherever it
+     * fits, 0 never; by default between MYNAH_PC_MIN_UNITS and
+     * MYNAH_PC_MAX_UNITS super-blocks per launch. */
+    if (exact && !chain) {
+        const long pc = env_long("MYNAH_GEMV_PC", -1);
+        const int want = pc == 1 || (pc < 0 &&
+                         all_units >= (uint64_t)env_long("MYNAH_PC_MIN_UNITS", 1L << 62) &&
+                         all_units <= (uint64_t)env_long("MYNAH_PC_MAX_UNITS", 0));
+        if (want && gemv_pc_plan(grp, p) == 0) return 0;
+    }
     /* A Q4_0 row is one running sum: with a Q4_0 matrix in the launch every
      * lane owns a whole row (K = 1, one wave of 64 rows per workgroup). */
     if (chain) split = 0;

@@ -40,6 +40,7 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_GEMV_GROUP_Q4K, "mynah_gemv_group_q4k")  \
     X(MYNAH_K_GEMV_FLAT_Q4K, "mynah_gemv_flat_q4k")    \
     X(MYNAH_K_GEMV_FLAT_Q6K, "mynah_gemv_flat_q6k")    \
+    X(MYNAH_K_GEMV_PC_Q4K, "mynah_gemv_pc_q4k")        \
     X(MYNAH_K_GEMV_STREAM, "mynah_gemv_stream")        \
     X(MYNAH_K_GEMV_STREAM_CVT, "mynah_gemv_stream_cvt") \
     X(MYNAH_K_GEMV_FAST_GROUP, "mynah_gemv_fast_group") \

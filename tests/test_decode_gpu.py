@@ -139,6 +139,35 @@ def test_fast_order_same_tokens(M):
         M.check(M.lib.mynah_hip_set_gemv_order(0), "order")
 
 
+@pytest.mark.parametrize("shape", [CF.QWEN3_TINY, CF.QWEN3_06B], ids=["tiny", "0.6B"])
+def test_producer_consumer_gemv_decoder_bit_identical(M, monkeypatch, shape):
+    """Every Q4_K projection launch in the producer/consumer layout (forced
+    with MYNAH_GEMV_PC=1: q/k/v with the input RMSNorm, o and down with the
+    residual, the gate/up pair with SwiGLU, K/V into the cache slot): each
+    step's logits bit-identical to the default decoder's, stepwise and
+    graph-replayed."""
+    npre, steps = 40, 12
+    print(f"[case] producer/consumer GEMV decoder d={shape.d_model}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    monkeypatch.setenv("MYNAH_GEMV_PC", "1")
+    a = M.Qwen3Decoder(model, npre + steps + 1)
+    a.set_kv(k, v, npre)
+    la = [a.forward(t) for t in range(first, first + steps)]
+    a.reset()
+    a.set_kv(k, v, npre)
+    ta, _ = a.generate(first, steps)
+    monkeypatch.setenv("MYNAH_GEMV_PC", "0")
+    b = M.Qwen3Decoder(model, npre + steps + 1)
+    b.set_kv(k, v, npre)
+    for i, t in enumerate(range(first, first + steps)):
+        assert np.array_equal(la[i].view(np.uint32), b.forward(t).view(np.uint32)), f"step {i}"
+    b.reset()
+    b.set_kv(k, v, npre)
+    assert b.generate(first, steps)[0] == ta
+
+
 def test_split_attention_every_step_against_oracle(M):
     """Split attention (per-chunk softmax partials, one launch per layer):
     logits within 1e-4 of the oracle on every step, over chunk boundaries."""

@@ -96,6 +96,23 @@ def test_qwen3_4b_shapes(M, m):
     assert same(y, O.project(m.qtype, w, m.rows, m.cols, x))
 
 
+PC_SHAPES = [(4096, 2560), (1024, 2560), (2560, 4096), (9728, 2560), (2560, 9728),
+             (1000, 256), (37, 256 * 40), (130, 256 * 33), (3, 2560)]
+
+
+@pytest.mark.parametrize("rows,cols", PC_SHAPES)
+def test_producer_consumer_layout_bit_exact(M, monkeypatch, rows, cols):
+    """The producer/consumer Q4_K GEMV (gemv_pc.hip, forced on with
+    MYNAH_GEMV_PC=1): the Qwen3-4B shapes, one-unit rows (64 rows per
+    workgroup), rows of 40 and 33 units (one row per workgroup) and a
+    ragged last workgroup, against the oracle bit for bit."""
+    monkeypatch.setenv("MYNAH_GEMV_PC", "1")
+    assert M.gemv_kernel(12, rows, cols, 0) == "mynah_gemv_pc_q4k"
+    w, x = case(M, 12, rows, cols, seed=13)
+    ref = O.project(12, w, rows, cols, x)
+    assert same(M.matvec(12, w, rows, cols, x), ref)
+
+
 @pytest.mark.parametrize("qtype", [12, 14, 8])
 def test_dequant_bit_exact(M, qtype):
     rows, cols = 77, 1536
@@ -231,7 +248,7 @@ def test_kernel_query_names_the_planned_kernel(M):
     """mynah_hip_gemv_kernel answers from the launch's own plan: the exact
     order's flat or streaming kernels, the reordered kernel, Q4_0's chains;
     refused geometry gives NULL with the reason."""
-    exact = {"mynah_gemv_flat_q4k", "mynah_gemv_flat_q6k", "mynah_gemv_group",
+    exact = {"mynah_gemv_flat_q4k", "mynah_gemv_flat_q6k", "mynah_gemv_group", "mynah_gemv_pc_q4k",
              "mynah_gemv_group_q4k", "mynah_gemv_group_q6k", "mynah_gemv_stream",
              "mynah_gemv_stream_cvt"}
     for qtype, rows, cols in ((12, 1024, 3072), (14, 151936, 1024), (14, 151936, 2560),
