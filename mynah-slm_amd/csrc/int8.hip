@@ -334,11 +334,11 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const uint8_t *lq, const 
         for (int k = 0; k < GI_TT; k++)
 #pragma unroll
             for (int e = 0; e < 4; e++) tot[i][k][e] = 0.0f;
-    i32x4 cur[GI_TR][GI_TT], nxt[GI_TR][GI_TT];
-    dots(cur, 0u);
-#pragma unroll 1
-    for (uint32_t j = 0; j < 8u; j++) {
-        if (j < 7u) dots(nxt, j + 1u);
+    // tot = fma(-xsum_j, offset_j, fma(dot_j, scale_j, tot)) for sub-block j.
+    auto epi = [&](const i32x4 (&dt)[GI_TR][GI_TT], uint32_t j) {
+        float xsj[GI_TT];
+#pragma unroll
+        for (int k = 0; k < GI_TT; k++) xsj[k] = (float)lsum[8u * tl[k] + j];
 #pragma unroll
         for (int i = 0; i < GI_TR; i++) {
             const uint32_t slot = (16u * (GI_TR * wr + i)) / 4u + lk;
@@ -348,24 +348,30 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const uint8_t *lq, const 
             const float ofv[4] = {of.x, of.y, of.z, of.w};
 #pragma unroll
             for (int k = 0; k < GI_TT; k++) {
-                const float xsj = (float)lsum[8u * tl[k] + j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float dv = (float)cur[i][k][e];
+                    const float dv = (float)dt[i][k][e];
                     float f = __builtin_fmaf(dv, scv[e], tot[i][k][e]);
-                    f = __builtin_fmaf(-xsj, ofv[e], f);
+                    f = __builtin_fmaf(-xsj[k], ofv[e], f);
                     if (MIXED) {
-                        const float p = tot[i][k][e] + (scv[e] * dv - ofv[e] * xsj);
+                        const float p = tot[i][k][e] + (scv[e] * dv - ofv[e] * xsj[k]);
                         f = fma_path[k] ? f : p;
                     }
                     tot[i][k][e] = f;
                 }
             }
         }
-#pragma unroll
-        for (int i = 0; i < GI_TR; i++)
-#pragma unroll
-            for (int k = 0; k < GI_TT; k++) cur[i][k] = nxt[i][k];
+    };
+    // Two register sets of dots, alternating: the dots of sub-block j + 1
+    // are issued before the epilogue of j, with no copies between them.
+    i32x4 da[GI_TR][GI_TT], db[GI_TR][GI_TT];
+    dots(da, 0u);
+#pragma unroll 1
+    for (uint32_t j = 0; j < 8u; j += 2u) {
+        dots(db, j + 1u);
+        epi(da, j);
+        if (j + 2u < 8u) dots(da, j + 2u);
+        epi(db, j + 1u);
     }
 #pragma unroll
     for (int i = 0; i < GI_TR; i++)
