@@ -11,8 +11,9 @@ matvec of every token (bit-exact, Q4_K / Q6_K / Q8_0 / Q4_0, with and without th
 residual epilogue); the whole K/V cache and the next step's logits after a
 batched prefill against the step-by-step fill (bit-exact), for the tiny
 model across chunk sizes 1, 7, 64 and 512 and a prefill starting after a
-synthetic cache, for Qwen3-0.6B, for Qwen3-4B over a 2048-token prompt in
-one default-size (2048) chunk, and the prompt() loop's greedy ids.
+synthetic cache, for Qwen3-0.6B, and the prompt() loop's greedy ids (the
+Qwen3-4B 2048-token prefill at the default chunk is in
+test_decode_forced_gpu.py).
 """
 from __future__ import annotations
 
@@ -126,18 +127,6 @@ def test_qwen3_06b_prefill_equals_steps(M):
     prompt = M.synth_uniform(M.substream(7, 4), 100, shape.vocab)
     a, b = fill_both(M, model, prompt, 104)
     assert_same_state(a, b, int(prompt[1]))
-
-
-def test_qwen3_4b_prefill_default_chunk_equals_steps(M):
-    """configs[4]'s prompt length at the default chunk: one 2048-token
-    batch against 2048 decode steps."""
-    os.environ.pop("MYNAH_PREFILL_CHUNK", None)
-    shape = CF.QWEN3_4B
-    print("[case] Qwen3-4B prefill of 2048 tokens, default chunk", flush=True)
-    model = M.SynthQwen3(shape, 0)
-    prompt = M.synth_uniform(M.substream(7, 6), 2048, shape.vocab)
-    a, b = fill_both(M, model, prompt, 2056)
-    assert_same_state(a, b, int(prompt[5]))
 
 
 def test_prompt_batched_equals_steps(M):
