@@ -104,7 +104,8 @@ int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);
  *     order; two launches per layer;
  *   MYNAH_ATTN_SPLIT: positions split across workgroups, per-chunk softmax
  *     partials combined by a second small launch; short FMA chains; differs
- *     from the reference by f32 rounding only. */
+ *     from the reference by f32 rounding only; refused (-1) for n_ctx above
+ *     524,288 (the combine's per-chunk weights fill 64 KiB of LDS there). */
 enum { MYNAH_ATTN_EXACT = 0, MYNAH_ATTN_SPLIT = 1 };
 int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode);
 

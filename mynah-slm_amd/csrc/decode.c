@@ -1159,6 +1159,13 @@ int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode) {
         mynah_set_error("attention mode %d", mode);
         return -1;
     }
+    /* The combine keeps one weight per chunk in LDS (64 KiB: 16,384 chunks
+     * of MYNAH_AS_CH positions). */
+    if (mode == MYNAH_ATTN_SPLIT && (size_t)s->nch_max * sizeof(float) > 64u * 1024u) {
+        mynah_set_error("split attention holds at most %u positions (n_ctx %u)",
+                        16384u * MYNAH_AS_CH, s->n_ctx);
+        return -1;
+    }
     s->attn_mode = mode;
     return 0;
 }

@@ -19,7 +19,11 @@
 // that starts at +0 never holds (only -0 + -0 gives -0). Each product is then
 // added to its running sum with its own v_add_f32 (no contraction), in
 // column order — the same roundings as the VALU kernel, at one VALU
-// instruction per product instead of two.
+// instruction per product instead of two. The instruction's accumulate form
+// (D = A B + C) cannot carry the sums: on gfx950 it rounds once, like fma
+// (equal to fmaf on 16.8 million single and chained cases, and unlike a
+// multiply then an add on a third of them), where the reference rounds the
+// product and the sum separately.
 //
 // Tiling: a workgroup of 256 threads owns 64 rows x 64 tokens; wave w the
 // tokens 16 w .. 16 w + 15. Per column step k lane l feeds A = w[row l][k]
@@ -30,7 +34,10 @@
 // stage at a time with the decoders of gemm_exact.hip (16 values per
 // thread), x is copied beside them (for the Q4_K / Q5_K matvec order in the
 // interleaved order), and the next stage is fetched into registers while the
-// current one is summed.
+// current one is summed. Within a stage each column's products land in their
+// own registers and the next column's MFMA is issued before this column's
+// adds (scheduling barriers pin that order), so the matrix core and the VALU
+// work at the same time.
 //
 // Split K (gridDim.z > 1): workgroup z takes the units [z U / Z, (z + 1) U /
 // Z) and stores every unit's sum to part[u][token][row] instead of folding
@@ -114,16 +121,33 @@ MYNAH_DEV void gemm_mfma(const uint8_t *__restrict__ w, const float *__restrict_
                 raw.load(wrow + UB * nu, 4u * nst + dp);
                 gm_fetch_x(xr, x, tid, tok0, tokens, cols, nu, nst);
             }
+            // Software-pipelined by one column: the products of column k + 1
+            // are issued (into their own registers) before the 16 adds of
+            // column k, so the matrix core works while the VALU adds.
+            float4 a4 = *(const float4 *)&wl[lane][0];
+            float4 b4 = *(const float4 *)&xl[tb][0];
+            gf_f32x16 pc = __builtin_amdgcn_mfma_f32_16x16x1f32(a4.x, b4.x, zero, 0, 0, 0);
 #pragma unroll
             for (uint32_t i = 0; i < GF_STAGE; i += 4) {
-                const float4 a4 = *(const float4 *)&wl[lane][i];
-                const float4 b4 = *(const float4 *)&xl[tb][i];
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+                float4 an = a4, bn = b4;
+                if (i + 4u < GF_STAGE) {
+                    an = *(const float4 *)&wl[lane][i + 4u];
+                    bn = *(const float4 *)&xl[tb][i + 4u];
+                }
+                const float av[5] = {a4.x, a4.y, a4.z, a4.w, an.x};
+                const float bv[5] = {b4.x, b4.y, b4.z, b4.w, bn.x};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const gf_f32x16 p =
-                        __builtin_amdgcn_mfma_f32_16x16x1f32(av[c], bv[c], zero, 0, 0, 0);
-                    s = s + p;
+                    gf_f32x16 pn = zero;
+                    if (c < 3 || i + 4u < GF_STAGE)
+                        pn = __builtin_amdgcn_mfma_f32_16x16x1f32(av[c + 1], bv[c + 1],
+                                                                  zero, 0, 0, 0);
+                    // Nothing crosses these: the next column's MFMA stays
+                    // ahead of this column's adds.
+                    __builtin_amdgcn_sched_barrier(0);
+                    s = s + pc;
+                    __builtin_amdgcn_sched_barrier(0);
+                    pc = pn;
                 }
                 if (ORD == 1 && FMT == 8 && (i & 31u) == 28u) {
                     // Q8_0 matvec order: each 32-value block's sum joins the
@@ -131,6 +155,8 @@ MYNAH_DEV void gemm_mfma(const uint8_t *__restrict__ w, const float *__restrict_
                     acc = acc + s;
                     s = zero;
                 }
+                a4 = an;
+                b4 = bn;
             }
             __syncthreads();
         }

@@ -98,3 +98,18 @@ def test_prefill_past_4096_equals_stepwise(M):
     assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32))
     assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_split_attention_refused_past_its_combine_limit(M):
+    """n_ctx 524,289 needs 16,385 chunks, one more than the combine's 64 KiB
+    of per-chunk weights: the split mode is refused before any launch and
+    the exact mode (the default) still decodes."""
+    shape = CF.QWEN3_TINY
+    print("[case] tiny decoder at n_ctx 524289: split attention refused", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    dec = M.Qwen3Decoder(model, 524289)
+    with pytest.raises(M.HipError, match="split attention holds at most 524288"):
+        dec.set_attention(M.ATTN_SPLIT)
+    lg = dec.forward(O.first_token(0, shape.vocab))
+    assert np.isfinite(lg).all() and dec.n_past == 1
+    dec.close()
