@@ -21,9 +21,12 @@ reference's), `prefill_gemm` (configs[3], the exact batched GEMM at 512
 tokens), `prefill_gemm_int8` (the same with Q4_K on the int8 activation
 lane, the batched default of the reference's AVX2 build),
 `qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
-greedy steps on Qwen3-4B), `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class) and
-`qwen3_4b_copy_ceiling_gbs` (a plain copy moving the same HBM bytes per launch:
-what any kernel launched back to back reaches at that size).
+greedy steps on Qwen3-4B), `qwen3_4b_gemv_gbs` (each Qwen3-4B GEMV class),
+`qwen3_4b_copy_ceiling_gbs` / `qwen3_4b_read_ceiling_gbs` (a plain copy and a
+read-only stream moving the same HBM bytes per launch: what any kernel
+launched back to back reaches at that size) and `valu` (the time per wave64
+f32 add with every SIMD issuing adds only, and the exact GEMM's ceiling that
+follows from one add per product).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -562,6 +565,19 @@ def pmc_probe(M, CF, launches: int = 8) -> None:
         f"4 copies of {nbytes} bytes (mynah_copy16)")
 
 
+def valu_yardstick(M, prefill) -> dict:
+    """The exact orders pay one non-packed v_add_f32 per product: the time per
+    wave64 add (every SIMD issuing only adds) bounds the exact GEMM at
+    2 flops x 64 lanes / t per SIMD. Measured twice, the faster kept."""
+    ns, simds = min(M.valu_add_rate() for _ in range(2))
+    ceiling = 2.0 * 64.0 / (ns * 1e-9) * simds / 1e12
+    out = {"f32_add_ns_per_wave64_per_simd": round(ns, 4), "simds": simds,
+           "exact_gemm_ceiling_tflop_s": round(ceiling, 1)}
+    if prefill is not None:
+        out["exact_gemm_frac_of_ceiling"] = round(prefill["tflop_s"] / ceiling, 3)
+    return out
+
+
 def traffic_for(name: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
@@ -618,8 +634,10 @@ def main() -> int:
         print(json.dumps({"decode": gpu_decode(M, CF)}), flush=True)
         return 0
     if args.gemm_only:
-        print(json.dumps({"prefill_gemm": gpu_prefill_gemm(M, CF),
-                          "prefill_gemm_int8": gpu_prefill_gemm(M, CF, int8=True)}), flush=True)
+        pg = gpu_prefill_gemm(M, CF)
+        print(json.dumps({"prefill_gemm": pg,
+                          "prefill_gemm_int8": gpu_prefill_gemm(M, CF, int8=True),
+                          "valu": valu_yardstick(M, pg)}), flush=True)
         return 0
     if args.classes_only:
         g, c, r, k = gpu_4b_classes(M, CF)
@@ -661,6 +679,9 @@ def main() -> int:
     if not args.no_4b:
         log("[bench] Qwen3-4B GEMV classes")
         extra_4b, ceiling_4b, rceiling_4b, kernels_4b = gpu_4b_classes(M, CF)
+
+    log("[bench] VALU add rate")
+    valu = valu_yardstick(M, prefill)
 
     cpu = None
     if not args.no_cpu:
@@ -709,6 +730,7 @@ def main() -> int:
         "qwen3_4b_copy_ceiling_gbs": ceiling_4b,
         "qwen3_4b_read_ceiling_gbs": rceiling_4b,
         "qwen3_4b_gemv_kernels": kernels_4b,
+        "valu": valu,
     }
     print(json.dumps(line), flush=True)
     return 0

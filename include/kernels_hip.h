@@ -232,6 +232,12 @@ int   mynah_hip_copy_dev(void *dst, const void *src, size_t bytes, void *stream)
  * of sink; the yardstick of what one launch reads at a size. No reference
  * counterpart. */
 int   mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream);
+/* The VALU yardstick (no reference counterpart): time per wave64 v_add_f32
+ * per SIMD, in ns, with every SIMD issuing nothing but independent f32 adds
+ * (eight waves per SIMD, `iters` x 8 adds per lane) — the price of one
+ * product in the exact summation orders; *simds (optional) gets the
+ * device's SIMD count. Synchronous; allocates 4 bytes. */
+int   mynah_hip_valu_add_rate(uint32_t iters, float *ns_per_instr, uint32_t *simds);
 void *mynah_hip_stream(void);           /* the library's own stream */
 
 /* y[i] = expf(x[i]) for i < n with the bits of the reference's C library

@@ -52,3 +52,24 @@ mynah_expf_map(const float *__restrict__ x, float *__restrict__ y, uint64_t n) {
          i += (uint64_t)gridDim.x * blockDim.x)
         y[i] = mynah_expf(x[i]);
 }
+
+// The VALU yardstick: every lane runs eight independent chains of `iters`
+// dependent v_add_f32 (non-packed), so with eight waves per SIMD the SIMD
+// issues nothing but f32 adds: the time per wave64 add is what the exact
+// summation orders (one add per product, in a fixed order) pay per product.
+// The result is stored only in the (impossible) case that it equals `never`.
+extern "C" __global__ void __launch_bounds__(256)
+mynah_valu_add_rate(uint32_t iters, float c, float never, float *__restrict__ sink) {
+#pragma clang fp contract(off)
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) a[i] = (float)threadIdx.x * 0.001f + (float)i;
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[i] = a[i] + c;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s = s + a[i];
+    if (s == never) sink[0] = s;
+}

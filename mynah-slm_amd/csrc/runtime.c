@@ -1119,6 +1119,44 @@ int mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream) 
                         args);
 }
 
+int mynah_hip_valu_add_rate(uint32_t iters, float *ns_per_instr, uint32_t *simds) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (ns_per_instr == NULL || iters == 0) {
+        mynah_set_error("valu rate: null output or zero iterations");
+        return -1;
+    }
+    /* Eight waves per SIMD: 4-wave workgroups, two per SIMD's worth. */
+    const unsigned grid = 8u * (unsigned)d->cus;
+    float *sink = NULL;
+    HIP_OK(hipMalloc((void **)&sink, 4), "hipMalloc(valu rate sink)");
+    float c = 1.0001f, never = -1.0f;
+    hipEvent_t e0 = NULL, e1 = NULL;
+    int rc = -1;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        void *args[] = {&iters, &c, &never, &sink};
+        float ms = 0.0f;
+        rc = mynah_launch(d, MYNAH_K_VALU_ADD_RATE, grid, 1, 256, 0, d->stream, args);
+        rc = rc ? rc : (hipEventRecord(e0, d->stream) == hipSuccess ? 0 : -1);
+        rc = rc ? rc : mynah_launch(d, MYNAH_K_VALU_ADD_RATE, grid, 1, 256, 0, d->stream, args);
+        rc = rc ? rc : (hipEventRecord(e1, d->stream) == hipSuccess ? 0 : -1);
+        rc = rc ? rc : (hipEventSynchronize(e1) == hipSuccess ? 0 : -1);
+        rc = rc ? rc : (hipEventElapsedTime(&ms, e0, e1) == hipSuccess ? 0 : -1);
+        /* wave64 adds per SIMD: 8 waves x iters x 8 chains */
+        if (rc == 0) {
+            *ns_per_instr = ms * 1e6f / (8.0f * (float)iters * 8.0f);
+            if (simds) *simds = 4u * (uint32_t)d->cus;
+        }
+        else mynah_set_error("valu rate: launch or event failed");
+    } else {
+        mynah_set_error("valu rate: hipEventCreate failed");
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(sink);
+    return rc;
+}
+
 int mynah_hip_expf_dev(const float *x, float *y, size_t n, void *stream) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;

@@ -103,6 +103,8 @@ def _load() -> C.CDLL:
         "mynah_hip_event_destroy": (C.c_int, [_P]),
         "mynah_hip_copy_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_read_dev": (C.c_int, [_P, _SZ, _P, _P]),
+        "mynah_hip_valu_add_rate": (C.c_int, [C.c_uint32, C.POINTER(C.c_float),
+                                              C.POINTER(C.c_uint32)]),
         "mynah_hip_expf_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_time_sweep": (C.c_int, [C.c_int, _P, _P, C.c_int, _P, _P, _P, _P, C.c_int,
                                            C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
@@ -352,6 +354,14 @@ def copy_dev(dst: int, src: int, nbytes: int, stream=None) -> None:
 
 def read_dev(src: int, nbytes: int, sink: int, stream=None) -> None:
     check(lib.mynah_hip_read_dev(src, nbytes, sink, stream), "read_dev")
+
+
+def valu_add_rate(iters: int = 20000):
+    """(ns per wave64 v_add_f32 per SIMD with every SIMD issuing only f32
+    adds, the device's SIMD count)."""
+    ns, simds = C.c_float(0.0), C.c_uint32(0)
+    check(lib.mynah_hip_valu_add_rate(iters, C.byref(ns), C.byref(simds)), "valu_add_rate")
+    return float(ns.value), int(simds.value)
 
 
 def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int):

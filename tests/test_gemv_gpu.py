@@ -311,3 +311,11 @@ def test_mfma_gemm_equals_valu_gemm(M, qtype, mv):
                 os.environ.pop(k, None)
             else:
                 os.environ[k] = v
+
+
+def test_valu_add_yardstick(M):
+    """The VALU yardstick runs and reports a plausible time per wave64 add
+    (a non-packed f32 add takes 4 cycles of a 16-lane SIMD: 1.6-2.5 ns at the
+    MI355X's clocks) and the device's SIMD count."""
+    ns, simds = M.valu_add_rate(2000)
+    assert 0.5 < ns < 10.0 and simds % 4 == 0 and simds >= 4
