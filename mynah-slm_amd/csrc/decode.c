@@ -396,8 +396,14 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             uint32_t nchm = s->nch_max, kvd = s->kv_dim;
             uint32_t group = c->n_heads / c->n_kv_heads;
             float eps = c->rms_eps, scale = s->scale;
+            /* Chunks live at this step's position stay live in every later
+             * step (the graphs replay forward), so they load K/V before the
+             * position arrives. */
+            uint32_t nctx = s->n_ctx;
+            uint32_t spec = (s->n_past + MYNAH_AS_CH) / MYNAH_AS_CH;
+            if (spec > nchm) spec = nchm;
             void *args[] = {&q, &kl, &vl, &qn, &kn, &rcos, &rsin, &pos, &pm, &pl, &po, &nchm, &kvd,
-                            &group, &eps, &scale};
+                            &group, &eps, &scale, &nctx, &spec};
             rc = mynah_launch(d, MYNAH_K_ATTN_SPLIT, c->n_kv_heads, s->nch_max, 128 * group, 0, st,
                               args);
             if (rc) break;

@@ -464,7 +464,8 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                  const float *__restrict__ k_norm, const float *__restrict__ rope_cos,
                  const float *__restrict__ rope_sin, const uint32_t *__restrict__ pos_ptr,
                  float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po,
-                 uint32_t nch_max, uint32_t kv_dim, uint32_t group, float eps, float scale) {
+                 uint32_t nch_max, uint32_t kv_dim, uint32_t group, float eps, float scale,
+                 uint32_t n_ctx, uint32_t spec_chunks) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float qn[8][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
@@ -473,22 +474,26 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     __shared__ __attribute__((aligned(16))) float ee[8][AS_CH];
     const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
     const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * AS_CH;
-    if (t0 >= n_kv) return;
+    // Chunks below spec_chunks were live when the launch was enqueued and the
+    // position only grows, so their K/V loads go out before the position
+    // arrives; the others first learn whether they hold any position at all.
+    const bool spec = c < spec_chunks;
+    if (!spec && t0 >= n_kv) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nthr = blockDim.x;
     const uint32_t nw = nthr >> 6;                  // 2 * group waves
-    const bool has_pos = pos < t0 + AS_CH;
     // Every load of the workgroup is issued before the first wait: K for the
-    // dot lanes, the V rows of the chunk, and for wave w < group query head w
-    // (wave group: the new key when this chunk holds pos) with its norm
-    // weights and the rotation of position pos.
+    // dot lanes and the V rows of the chunk (rows clamped into the cache;
+    // positions at or past pos are masked below), and for wave w < group
+    // query head w (wave group: the new key when this chunk holds pos) with
+    // its norm weights and the rotation of position pos.
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t ppp = 4u * nw;                   // positions per pass
     float kv[AS_PASS][8];
 #pragma unroll
     for (int ps = 0; ps < AS_PASS; ps++) {
         const uint32_t t = t0 + ppp * (uint32_t)ps + 4u * wave + r;
-        const bool live = t < pos && ppp * (uint32_t)ps < AS_CH;
-        const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
+        const uint32_t row = t < n_ctx ? t : n_ctx - 1u;
+        const float *krow = k_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + l;
 #pragma unroll
         for (int j = 0; j < 8; j++) kv[ps][j] = krow[16 * j];
     }
@@ -497,9 +502,17 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
         const uint32_t i = tid + nthr * (uint32_t)k;
         const uint32_t tr = i >> 5, q4 = i & 31u, t = t0 + tr;
-        vr[k] = (i < AS_CH * 32u && t < n_kv)
-                    ? *(const float4 *)(v_layer + (size_t)t * kv_dim + (size_t)kvh * 128u + 4u * q4)
+        const uint32_t row = t < n_ctx ? t : n_ctx - 1u;
+        vr[k] = i < AS_CH * 32u
+                    ? *(const float4 *)(v_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + 4u * q4)
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if (t0 >= n_kv) return;       // a speculative chunk past the position (after a reset)
+    const bool has_pos = pos < t0 + AS_CH;
+#pragma unroll
+    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
+        const uint32_t t = t0 + ((tid + nthr * (uint32_t)k) >> 5);
+        if (t >= n_kv) vr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const bool qwave = wave < group, kwave = wave == group && has_pos;
     float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
@@ -627,15 +640,24 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
         pv[k][0] = c < nch_max ? pob[(size_t)c * cstride] : 0.0f;
         pv[k][1] = c < nch_max ? pob[(size_t)c * cstride + 64u] : 0.0f;
     }
+    // Chunk tid's max and exp sum, also in flight before the position.
+    const float pm0 = tid < nch_max ? pm[base + (size_t)tid * group] : 0.0f;
+    const double pl0 = tid < nch_max ? pl[base + (size_t)tid * group] : 0.0;
     const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
     float m = -__builtin_inff();
-    for (uint32_t c = tid; c < nch; c += 256u) m = fmaxf(m, pm[base + (size_t)c * group]);
+    if (tid < nch) m = fmaxf(m, pm0);
+    for (uint32_t c = tid + 256u; c < nch; c += 256u) m = fmaxf(m, pm[base + (size_t)c * group]);
     m = wave_max_f(m);
     if (lane == 0) smax[wave] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
     double l = 0.0;
-    for (uint32_t c = tid; c < nch; c += 256u) {
+    if (tid < nch) {
+        const float w = mynah_expf(pm0 - M);
+        wsc[tid] = w;
+        l += (double)w * pl0;
+    }
+    for (uint32_t c = tid + 256u; c < nch; c += 256u) {
         const float w = mynah_expf(pm[base + (size_t)c * group] - M);
         wsc[c] = w;
         l += (double)w * pl[base + (size_t)c * group];
