@@ -77,6 +77,16 @@ MYNAH_DEV double readlane_d(double v, int lane) {
     return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
 }
 
+// Positions per workgroup of the split decode attention (= MYNAH_AS_CH in
+// runtime_internal.h).
+#define AS_CH 32
+
+// Wave-wide float max (all lanes get the result).
+MYNAH_DEV float wave_max_f(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
 // Sum over the 64 lanes of a (fully active) wave in double, every lane
 // receiving the total: DPP within quads (xor 1, xor 2) and rows (rotate by
 // 4, 8), then the four row sums read as scalars.

@@ -32,12 +32,6 @@ MYNAH_DEV float row16_dot(float acc) {
 
 #define DEC_WG 256
 
-// Wave-wide double sum / float max (all lanes get the result).
-MYNAH_DEV float wave_max_f(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
-}
-
 // Per-head RMSNorm then split-half RoPE of one head vector by one wave
 // (src/kernels.c:130-137, 173-189): s from the double sum of squares,
 // x = x * (s * w), then x[i] = a c - b s, x[i + hd/2] = b c + a s. src may
@@ -443,7 +437,6 @@ mynah_attn_out_long(const float *__restrict__ v_layer, const float *__restrict__
 // weighted sum. Split: grid (n_kv_heads, ceil(n_ctx / AS_CH)), block 128 *
 // group; group <= 8, hd == 128. Partials: pm, pl [n_kv][nch_max][group], po
 // [n_kv][nch_max][group][128].
-#define AS_CH 32                                  // = MYNAH_AS_CH (runtime_internal.h)
 #define AS_PASS ((AS_CH + 15) / 16)                 // K passes of 16 positions (group >= 2)
 // Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
 // x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as

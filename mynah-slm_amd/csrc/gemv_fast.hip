@@ -291,6 +291,7 @@ mynah_gemv_fast_group(const GemvGroup grp) {
     extern __shared__ __attribute__((aligned(16))) float lds_f[];
     __shared__ double shd[4];
     __shared__ float wp[4][2][8];
+    if (gemv_prefetch_tail(grp.pf)) return;
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;

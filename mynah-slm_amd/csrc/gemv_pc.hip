@@ -170,6 +170,7 @@ extern "C" __global__ void __launch_bounds__(320)
 mynah_gemv_pc_q4k(const GemvGroup grp) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ double shd[16];
+    if (gemv_prefetch_tail(grp.pf)) return;
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;

@@ -338,6 +338,7 @@ static long env_long(const char *name, long dflt) {
 typedef struct {
     int kernel;
     uint32_t grid, threads, shape;
+    uint32_t tile_rows;      /* rows per workgroup; 0: each descriptor's pad */
     size_t lds;
     mynah_stream_desc sd;
 } gemv_plan;
@@ -374,6 +375,7 @@ static int gemv_stream_plan(const mynah_device *d, const mynah_gemv_group *grp, 
     p->sd = sd;
     p->kernel = env_long("MYNAH_GEMV_MIX", 0) ? MYNAH_K_GEMV_STREAM : MYNAH_K_GEMV_STREAM_CVT;
     p->grid = (uint32_t)wgs;
+    p->tile_rows = 0;
     p->threads = 256;
     p->lds = lds;
     p->shape = 0;
@@ -431,7 +433,8 @@ static int gemv_flat_plan(const mynah_device *d, mynah_gemv_group *grp, gemv_pla
         g->tile0 = tiles;
         tiles += (g->rows + r - 1u) / r;
         const size_t need = ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
-                             (size_t)r * (ut | 1u) + (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
+                             (size_t)r * (ut | 1u) +
+                             (g->norm_w || grp->af.on ? (size_t)g->cols : 0u)) * 4u;
         if (need > lds) lds = need;
         all_q4k = all_q4k && g->type == MYNAH_Q4_K;
         all_q6k = all_q6k && g->type == MYNAH_Q6_K;
@@ -441,6 +444,7 @@ static int gemv_flat_plan(const mynah_device *d, mynah_gemv_group *grp, gemv_pla
         return -1;
     }
     p->grid = tiles;
+    p->tile_rows = 0;
     p->lds = lds;
     p->threads = T;
     p->shape = 1u << 25;
@@ -480,6 +484,7 @@ static int gemv_pc_plan(mynah_gemv_group *grp, gemv_plan *p) {
         tiles += (g->rows + r - 1u) / r;
     }
     p->grid = tiles;
+    p->tile_rows = 0;
     p->lds = lds;
     p->threads = 320u;
     p->shape = 0;
@@ -580,7 +585,7 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         /* Q4_0 keeps no unit partials in LDS. */
         const size_t parts = g->type == MYNAH_Q4_0 ? 0u : (size_t)tile_rows * (ut | 1u);
         const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) + parts +
-                                     (g->norm_w ? (size_t)g->cols : 0u)) * 4u
+                                     (g->norm_w || grp->af.on ? (size_t)g->cols : 0u)) * 4u
                                   : ((size_t)g->cols + g->cols / 16 + g->cols / 8 +
                                      (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
         if (need > lds) lds = need;
@@ -592,6 +597,7 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         return -1;
     }
     p->grid = tiles;
+    p->tile_rows = tile_rows;
     p->lds = lds;
     if (!exact) {
         p->kernel = MYNAH_K_GEMV_FAST_GROUP;
@@ -654,18 +660,102 @@ const char *mynah_hip_gemv_kernel(int type, size_t rows, size_t cols, int order)
     return kernel_names[p.kernel];
 }
 
+/* Launches that mynah_gemv_group_fold can run with attention partials
+ * folded into the input: one matrix, the exact split or flat layout of any
+ * type but Q4_0, at most 512 threads. */
+static int plan_folds(const gemv_plan *p, const mynah_gemv_group *grp) {
+    const int k = p->kernel;
+    if (k != MYNAH_K_GEMV_GROUP && k != MYNAH_K_GEMV_GROUP_Q4K && k != MYNAH_K_GEMV_GROUP_Q6K &&
+        k != MYNAH_K_GEMV_FLAT_Q4K && k != MYNAH_K_GEMV_FLAT_Q6K)
+        return 0;
+    return grp->n == 1 && grp->d[0].type != MYNAH_Q4_0 && p->threads <= 512u &&
+           grp->d[0].cols <= 8u * p->threads && grp->d[0].cols / 128u <= 4u * (p->threads / 64u);
+}
+
+int mynah_gemv_group_can_fold(mynah_gemv_group *grp, int order) {
+    mynah_device *d = mynah_dev();
+    gemv_plan p;
+    if (d == NULL || gemv_group_plan(d, grp, order, &p) != 0) return -1;
+    return plan_folds(&p, grp);
+}
+
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
                             uint32_t *tiles_out, int order) {
     gemv_plan p;
     if (gemv_group_plan(d, grp, order, &p) != 0) return -1;
+    if (grp->af.on) {
+        const mynah_attn_fold *a = &grp->af;
+        if (!plan_folds(&p, grp) || a->nch_max == 0 || a->nch_max > 64u || a->group == 0 ||
+            a->n_heads % a->group != 0 || (uint64_t)a->n_heads * 128u != grp->d[0].cols ||
+            a->spec > a->nch_max || a->n_heads > 4u * (p.threads / 64u) ||
+            grp->d[0].cols > 8u * p.threads) {
+            mynah_set_error("attention fold does not fit this launch");
+            return -1;
+        }
+        p.kernel = MYNAH_K_GEMV_GROUP_FOLD;
+    }
     if (tiles_out) *tiles_out = p.grid;
     if (p.kernel == MYNAH_K_GEMV_STREAM || p.kernel == MYNAH_K_GEMV_STREAM_CVT) {
         void *args[] = {&p.sd};
         return mynah_launch(d, p.kernel, p.grid, 1, p.threads, p.lds, stream, args);
     }
     grp->shape = p.shape;
+    grp->pf.host_tiles = p.grid;
+    if (grp->pf.wgs % 8u != 0 || grp->pf.n > MYNAH_PF_SEGS) {
+        mynah_set_error("prefetch of %u workgroups, %u segments", grp->pf.wgs, grp->pf.n);
+        return -1;
+    }
     void *args[] = {grp};
-    return mynah_launch(d, p.kernel, p.grid, 1, p.threads, p.lds, stream, args);
+    return mynah_launch(d, p.kernel, p.grid + grp->pf.wgs, 1, p.threads, p.lds, stream, args);
+}
+
+int mynah_gemv_prefetch_plan(const mynah_gemv_group *next, int order, uint32_t wgs,
+                             uint32_t bytes_per_wg, uint64_t max_bytes, uint32_t step_log2,
+                             mynah_gemv_prefetch *pf) {
+    memset(pf, 0, sizeof *pf);
+    if (wgs == 0 && bytes_per_wg == 0) return 0;
+    if (wgs % 8u != 0 || step_log2 < 2u || step_log2 > 12u) {
+        mynah_set_error("prefetch of %u workgroups, step 2^%u", wgs, step_log2);
+        return -1;
+    }
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    mynah_gemv_group g = *next;
+    gemv_plan p;
+    if (gemv_group_plan(d, &g, order, &p) != 0) return -1;
+    if (p.kernel == MYNAH_K_GEMV_STREAM || p.kernel == MYNAH_K_GEMV_STREAM_CVT) return 0;
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < g.n; i++) {
+        const mynah_gemv_desc *e = &g.d[i];
+        const uint32_t r = p.tile_rows ? p.tile_rows : e->pad;
+        const uint32_t end = i + 1 < g.n ? g.d[i + 1].tile0 : p.grid;
+        const uint64_t bytes = (uint64_t)e->rows * e->row_bytes;
+        if (r == 0 || bytes > 0xffffffffull || (uint64_t)r * e->row_bytes > 0xffffffffull) {
+            memset(pf, 0, sizeof *pf);
+            return 0;
+        }
+        const void *w[2] = {e->w, e->w2};
+        for (int k = 0; k < 2 && n < MYNAH_PF_SEGS; k++) {
+            if (w[k] == NULL) continue;
+            pf->base[n] = w[k];
+            pf->t0[n] = e->tile0;
+            pf->nt[n] = end - e->tile0;
+            pf->bpt[n] = r * e->row_bytes;
+            pf->bytes[n] = (uint32_t)bytes;
+            n++;
+        }
+    }
+    uint64_t total = 0;
+    for (uint32_t k = 0; k < n; k++) total += pf->bytes[k];
+    if (total > max_bytes) n = 0;
+    if (bytes_per_wg != 0) {
+        const uint64_t w = (total + bytes_per_wg - 1u) / bytes_per_wg;
+        wgs = w >= 1024u ? 1024u : (uint32_t)((w + 7u) & ~7ull);
+    }
+    pf->n = n;
+    pf->wgs = n ? wgs : 0u;
+    pf->step_log2 = step_log2;
+    return 0;
 }
 
 int mynah_dequant_launch(mynah_device *d, int type, const void *w, size_t rows, size_t cols,

@@ -168,6 +168,72 @@ def test_producer_consumer_gemv_decoder_bit_identical(M, monkeypatch, shape):
     assert b.generate(first, steps)[0] == ta
 
 
+def _split_runs(M, model, shape, k, v, npre, first, steps):
+    d = M.Qwen3Decoder(model, npre + steps + 1)
+    d.set_attention(M.ATTN_SPLIT)
+    d.set_kv(k, v, npre)
+    logits = [d.forward(t) for t in range(first, first + steps)]
+    d.reset()
+    d.set_kv(k, v, npre)
+    toks, _ = d.generate(first, steps)
+    lg = d.forward(toks[-1])
+    d.close()
+    return logits, toks, lg
+
+
+@pytest.mark.parametrize("shape,npre", [(CF.QWEN3_TINY, 60), (CF.QWEN3_06B, 500)],
+                         ids=["tiny", "0.6B"])
+def test_folded_attention_combine_bit_identical(M, monkeypatch, shape, npre):
+    """Split attention with the chunk partials folded by the output
+    projection's staging (the default while they are cheap to re-read:
+    short contexts) against the separate
+    combine launch (MYNAH_ATTN_FOLD=0): every step's logits bit-identical,
+    stepwise and graph-replayed, across a chunk boundary (the fold forced
+    on whatever the partials cost)."""
+    steps = 12
+    print(f"[case] folded combine d={shape.d_model} npre={npre}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    monkeypatch.setenv("MYNAH_ATTN_FOLD", "1")
+    monkeypatch.setenv("MYNAH_FOLD_MAX_BYTES", str(1 << 40))
+    la, ta, ga = _split_runs(M, model, shape, k, v, npre, first, steps)
+    monkeypatch.setenv("MYNAH_ATTN_FOLD", "0")
+    lb, tb, gb = _split_runs(M, model, shape, k, v, npre, first, steps)
+    for i in range(steps):
+        assert np.array_equal(la[i].view(np.uint32), lb[i].view(np.uint32)), f"step {i}"
+    assert ta == tb
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
+
+
+@pytest.mark.parametrize("env", [{"MYNAH_PREFETCH_WGS": "128", "MYNAH_PREFETCH_BPW": "0"},
+                                 {"MYNAH_PREFETCH_BPW": "8192", "MYNAH_PREFETCH_MAX": "0"},
+                                 {"MYNAH_PREFETCH_BPW": "1024", "MYNAH_PREFETCH_STEP": "6"}],
+                         ids=["wgs128", "bpw8192_all", "bpw1024_step64"])
+def test_prefetching_decoder_bit_identical(M, monkeypatch, env):
+    """Decode GEMVs carrying workgroups that prefetch the next GEMV's weights
+    into L2 (every next GEMV prefetched, by workgroup count or bytes per
+    workgroup): logits and ids bit-identical to the decoder without them
+    (MYNAH_PREFETCH_BPW=0; 0.6B, split attention, stepwise and
+    graph-replayed)."""
+    shape, npre, steps = CF.QWEN3_06B, 100, 8
+    print(f"[case] prefetch {env}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    for e, val in env.items():
+        monkeypatch.setenv(e, val)
+    la, ta, ga = _split_runs(M, model, shape, k, v, npre, first, steps)
+    for e in env:
+        monkeypatch.delenv(e)
+    monkeypatch.setenv("MYNAH_PREFETCH_BPW", "0")
+    lb, tb, gb = _split_runs(M, model, shape, k, v, npre, first, steps)
+    for i in range(steps):
+        assert np.array_equal(la[i].view(np.uint32), lb[i].view(np.uint32)), f"step {i}"
+    assert ta == tb
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
+
+
 def test_split_attention_every_step_against_oracle(M):
     """Split attention (per-chunk softmax partials, one launch per layer):
     logits within 1e-4 of the oracle on every step, over chunk boundaries."""
