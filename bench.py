@@ -261,7 +261,7 @@ def gpu_decode(M, CF):
     return out
 
 
-def gpu_prefill_gemm(M, CF, reps: int = 5, int8: bool = False):
+def gpu_prefill_gemm(M, CF, reps: int = 20, int8: bool = False):
     """the prefill GEMMs at Qwen3-1.7B shapes, 512 tokens.
     int8=False: the exact batched order (bit-identical to the reference's
     exact matmat). int8=True: the Q4_K products take the int8 activation lane
@@ -279,7 +279,7 @@ def gpu_prefill_gemm(M, CF, reps: int = 5, int8: bool = False):
             M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
             M.sync()
             a, b = M.Event(), M.Event()
-            n = reps * (8 if int8 else 1)
+            n = reps * (4 if int8 else 1)
             a.record()
             for _ in range(n):
                 M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)

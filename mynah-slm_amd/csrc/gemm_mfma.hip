@@ -40,10 +40,12 @@
 // work at the same time.
 //
 // Split K (gridDim.z > 1): workgroup z takes the units [z U / Z, (z + 1) U /
-// Z) and stores every unit's sum to part[u][token][row] instead of folding
-// it; mynah_gemm_fold then folds the unit sums of each output in unit order
-// from 0 (and adds res), the row total the single launch would give. Not for
-// the Q8_0 matvec order, whose row total takes every 32-value block sum.
+// Z); z = 0 stores the running row total of its units (from 0, in order) to
+// part[0][token][row], every other z stores each unit's sum to
+// part[u][token][row]; mynah_gemm_fold then continues the total from slot 0
+// over the later units in order (and adds res), the row total the single
+// launch would give. Not for the Q8_0 matvec order, whose row total takes
+// every 32-value block sum.
 //
 // SPDX-License-Identifier: MIT
 #include "common.hip.h"
@@ -161,7 +163,7 @@ MYNAH_DEV void gemm_mfma(const uint8_t *__restrict__ w, const float *__restrict_
             __syncthreads();
         }
         if (!(ORD == 1 && FMT == 8)) {
-            if (split) {
+            if (split && z > 0u) {
                 // Unit u's sums, for the in-order fold.
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
@@ -175,7 +177,19 @@ MYNAH_DEV void gemm_mfma(const uint8_t *__restrict__ w, const float *__restrict_
             }
         }
     }
-    if (split) return;
+    if (split) {
+        // The first split's units start the row total: its running sum from
+        // 0 is what the fold would reach after them, stored in slot 0.
+        if (z == 0u) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = row0 + gf_row(r, lane);
+                const uint32_t t = tok0 + tb;
+                if (row < rows && t < tokens) part[(size_t)t * rows + row] = acc[r];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const uint32_t row = row0 + gf_row(r, lane);
@@ -208,18 +222,27 @@ GEMM_MFMA_ENTRY(mynah_q5k_gemm_mv_mfma, GmQ5KMvT<false>, 176u, 1, 13)
 GEMM_MFMA_ENTRY(mynah_q6k_gemm_mv_mfma, GmQ6KT<false>, 210u, 1, 14)
 GEMM_MFMA_ENTRY(mynah_q80_gemm_mv_mfma, GmQ80T<false>, 272u, 1, 8)
 
-// The in-order fold of split-K unit sums: y[t][r] = (res[t][r] +) the sum of
-// part[u][t][r] for u = 0 .. units - 1 taken in order from 0 — the row total
-// of the reference's order. One thread per output, consecutive rows
-// consecutive threads.
+// The in-order fold of split-K unit sums: y[t][r] = (res[t][r] +) the row
+// total continued from part[0][t][r] (the first split's running total over
+// its units 0 .. first - 1) over part[u][t][r], u = first .. units - 1, in
+// order — the row total of the reference's order. One thread per output,
+// consecutive rows consecutive threads; the loads go out four at a time.
 extern "C" __global__ void __launch_bounds__(256)
 mynah_gemm_fold(const float *__restrict__ part, const float *res, float *y, uint32_t rows,
-                uint32_t tokens, uint32_t units) {
+                uint32_t tokens, uint32_t first, uint32_t units) {
 #pragma clang fp contract(off)
     const uint64_t n = (uint64_t)rows * tokens;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float acc = 0.0f;
-    for (uint32_t u = 0; u < units; u++) acc = acc + part[(size_t)u * n + i];
+    float acc = part[i];
+    uint32_t u = first;
+    for (; u + 4u <= units; u += 4u) {
+        float v[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) v[k] = part[(size_t)(u + k) * n + i];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) acc = acc + v[k];
+    }
+    for (; u < units; u++) acc = acc + part[(size_t)u * n + i];
     y[i] = res ? res[i] + acc : acc;
 }

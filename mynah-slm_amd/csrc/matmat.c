@@ -25,7 +25,8 @@ static long env_long(const char *name, long dflt) {
  * bits). A launch of at most one 64 x 64 tile per CU splits the
  * super-blocks over gridDim.z, up to MYNAH_GEMM_WGS_PER_CU (default 4)
  * workgroups per CU (MYNAH_GEMM_SPLIT=0 never, N at most N ways), and folds
- * the per-super-block sums in order afterwards (mynah_gemm_fold). */
+ * the first split's running total and the later per-super-block sums in
+ * order afterwards (mynah_gemm_fold). */
 static int gemm_mfma_launch(mynah_device *d, int type, int ord, const void *w, size_t rows,
                             size_t cols, size_t rb, const float *x, float *y, size_t tokens,
                             const float *res, hipStream_t stream) {
@@ -66,8 +67,8 @@ static int gemm_mfma_launch(mynah_device *d, int type, int ord, const void *w, s
     void *args[] = {&w, &x, &y, &r32, &c32, &t32, &rb32, &res, &part};
     int rc = mynah_launch3(d, kid[ord][ti], gx, gy, nz, 256, 0, stream, args);
     if (rc == 0) {
-        uint32_t u32 = units;
-        void *fargs[] = {&part, &res, &y, &r32, &t32, &u32};
+        uint32_t u32 = units, first = units / nz;   /* the units of split 0 */
+        void *fargs[] = {&part, &res, &y, &r32, &t32, &first, &u32};
         rc = mynah_launch(d, MYNAH_K_GEMM_FOLD, (unsigned)((n + 255) / 256), 1, 256, 0, stream,
                           fargs);
     }
