@@ -367,12 +367,15 @@ MYNAH_DEV void gi_block(float (&acc)[GI_TR][GI_TT][4], const uint8_t *lq, const 
     i32x4 da[GI_TR][GI_TT], db[GI_TR][GI_TT];
     dots(da, 0u);
 #pragma unroll 1
-    for (uint32_t j = 0; j < 8u; j += 2u) {
+    for (uint32_t j = 0; j < 6u; j += 2u) {
         dots(db, j + 1u);
         epi(da, j);
-        if (j + 2u < 8u) dots(da, j + 2u);
+        dots(da, j + 2u);
         epi(db, j + 1u);
     }
+    dots(db, 7u);
+    epi(da, 6u);
+    epi(db, 7u);
 #pragma unroll
     for (int i = 0; i < GI_TR; i++)
 #pragma unroll
