@@ -87,6 +87,26 @@ MYNAH_DEV float wave_max_f(float v) {
     return v;
 }
 
+// A float moved across lanes by one DPP control.
+template <int CTRL>
+MYNAH_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Wave-wide float max by DPP within rows, then the four row maxima (a max
+// is the same in any order).
+MYNAH_DEV float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 // Sum over the 64 lanes of a (fully active) wave in double, every lane
 // receiving the total: DPP within quads (xor 1, xor 2) and rows (rotate by
 // 4, 8), then the four row sums read as scalars.

@@ -474,11 +474,11 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     if (!spec && t0 >= n_kv) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nthr = blockDim.x;
     const uint32_t nw = nthr >> 6;                  // 2 * group waves
-    // Every load of the workgroup is issued before the first wait: K for the
-    // dot lanes and the V rows of the chunk (rows clamped into the cache;
-    // positions at or past pos are masked below), and for wave w < group
-    // query head w (wave group: the new key when this chunk holds pos) with
-    // its norm weights and the rotation of position pos.
+    // The K rows of the dot lanes and the V rows of the chunk are loaded
+    // first (rows clamped into the cache; positions at or past pos are
+    // masked below), then for wave w < group query head w with its norm
+    // weights; after the position, the new key (wave group, when this chunk
+    // holds pos) and the rotation of position pos.
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t ppp = 4u * nw;                   // positions per pass
     float kv[AS_PASS][8];
@@ -500,6 +500,17 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                     ? *(const float4 *)(v_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + 4u * q4)
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    // The query heads and their norm weights do not depend on the position
+    // either.
+    const bool qwave = wave < group;
+    float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    if (qwave) {
+        const float *src = q + (size_t)(kvh * group + wave) * 128u;
+        x0 = src[lane];
+        x1 = src[lane + 64u];
+        w0 = q_norm[lane];
+        w1 = q_norm[lane + 64u];
+    }
     if (t0 >= n_kv) return;       // a speculative chunk past the position (after a reset)
     const bool has_pos = pos < t0 + AS_CH;
 #pragma unroll
@@ -507,16 +518,15 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         const uint32_t t = t0 + ((tid + nthr * (uint32_t)k) >> 5);
         if (t >= n_kv) vr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const bool qwave = wave < group, kwave = wave == group && has_pos;
+    const bool kwave = wave == group && has_pos;
     float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
-    float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, cs = 0.0f, sn = 0.0f;
+    if (kwave) {
+        x0 = kpos[lane];
+        x1 = kpos[lane + 64u];
+        w0 = k_norm[lane];
+        w1 = k_norm[lane + 64u];
+    }
     if (qwave || kwave) {
-        const float *src = qwave ? q + (size_t)(kvh * group + wave) * 128u : kpos;
-        const float *w = qwave ? q_norm : k_norm;
-        x0 = src[lane];
-        x1 = src[lane + 64u];
-        w0 = w[lane];
-        w1 = w[lane + 64u];
         cs = rope_cos[(size_t)pos * 64u + lane];
         sn = rope_sin[(size_t)pos * 64u + lane];
     }
@@ -604,7 +614,9 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
 // Thread c (and c + 256, ...) takes chunk c's max and exp sum: M = max m_c,
 // w_c = expf(m_c - M) (kept in LDS), L = sum_c w_c l_c in double (each
 // wave's share, then the four shares in wave order); inv = (float)(1 / L).
-// Wave w then sums o_w = fma(w_c * inv, o_c, o_w) over its chunks c = w,
+// Up to 64 chunks all of them sit in wave 0, which computes M and L alone
+// (same values: the other waves contribute -inf and 0.0), one barrier
+// fewer. Wave w then sums o_w = fma(w_c * inv, o_c, o_w) over its chunks c = w,
 // w + 4, ... in order, lane l holding dimensions l and l + 64, and the four
 // partial vectors are added in wave order. The first AC_PRE chunks of every
 // wave are loaded before the position arrives (every slot below nch_max is
@@ -620,6 +632,7 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
     extern __shared__ float wsc[];
     __shared__ float smax[AC_WAVES];
     __shared__ double ssum[AC_WAVES];
+    __shared__ float sinv;
     __shared__ float spart[AC_WAVES - 1][128];
     const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
@@ -637,28 +650,49 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
     const float pm0 = tid < nch_max ? pm[base + (size_t)tid * group] : 0.0f;
     const double pl0 = tid < nch_max ? pl[base + (size_t)tid * group] : 0.0;
     const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
-    float m = -__builtin_inff();
-    if (tid < nch) m = fmaxf(m, pm0);
-    for (uint32_t c = tid + 256u; c < nch; c += 256u) m = fmaxf(m, pm[base + (size_t)c * group]);
-    m = wave_max_f(m);
-    if (lane == 0) smax[wave] = m;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
-    double l = 0.0;
-    if (tid < nch) {
-        const float w = mynah_expf(pm0 - M);
-        wsc[tid] = w;
-        l += (double)w * pl0;
+    float inv;
+    if (nch <= 64u) {
+        // Every chunk is in wave 0: it alone finds M and L, the other waves'
+        // maxima being -inf and their double sums 0 (added all the same).
+        if (wave == 0u) {
+            float m = -__builtin_inff();
+            if (lane < nch) m = fmaxf(m, pm0);
+            const float M = wave_max_dpp(m);
+            double l = 0.0;
+            if (lane < nch) {
+                const float w = mynah_expf(pm0 - M);
+                wsc[lane] = w;
+                l += (double)w * pl0;
+            }
+            l = wave_sum_d(l);
+            if (lane == 0) sinv = (float)(1.0 / (((l + 0.0) + 0.0) + 0.0));
+        }
+        __syncthreads();
+        inv = sinv;
+    } else {
+        float m = -__builtin_inff();
+        if (tid < nch) m = fmaxf(m, pm0);
+        for (uint32_t c = tid + 256u; c < nch; c += 256u) m = fmaxf(m, pm[base + (size_t)c * group]);
+        m = wave_max_f(m);
+        if (lane == 0) smax[wave] = m;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+        double l = 0.0;
+        if (tid < nch) {
+            const float w = mynah_expf(pm0 - M);
+            wsc[tid] = w;
+            l += (double)w * pl0;
+        }
+        for (uint32_t c = tid + 256u; c < nch; c += 256u) {
+            const float w = mynah_expf(pm[base + (size_t)c * group] - M);
+            wsc[c] = w;
+            l += (double)w * pl[base + (size_t)c * group];
+        }
+        l = wave_sum_d(l);
+        if (lane == 0) ssum[wave] = l;
+        __syncthreads();
+        inv = (float)(1.0 / (((ssum[0] + ssum[1]) + ssum[2]) + ssum[3]));
     }
-    for (uint32_t c = tid + 256u; c < nch; c += 256u) {
-        const float w = mynah_expf(pm[base + (size_t)c * group] - M);
-        wsc[c] = w;
-        l += (double)w * pl[base + (size_t)c * group];
-    }
-    l = wave_sum_d(l);
-    if (lane == 0) ssum[wave] = l;
-    __syncthreads();
-    const float inv = (float)(1.0 / (((ssum[0] + ssum[1]) + ssum[2]) + ssum[3]));
     float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
     for (uint32_t k = 0; k < AC_PRE; k++) {     // static indices keep pv in registers

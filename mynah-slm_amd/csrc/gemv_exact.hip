@@ -487,26 +487,6 @@ MYNAH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ no
     }
 }
 
-// A float moved across lanes by one DPP control.
-template <int CTRL>
-MYNAH_DEV float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Wave-wide float max by DPP within rows, then the four row maxima (a max
-// is the same in any order).
-MYNAH_DEV float wave_max_dpp(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x124>(v));
-    v = fmaxf(v, dpp_f<0x128>(v));
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
 // Stage the attention output that mynah_attn_combine would write, from the
 // split partials, into the padded LDS copy (the layout stage_x writes).
 // Per query head h (wave h mod waves, lane c holding chunk c): M = max m_c,
