@@ -87,6 +87,17 @@ MYNAH_DEV float wave_max_f(float v) {
     return v;
 }
 
+// Calls f(Index<0>), ..., f(Index<N - 1>): register arrays indexed by
+// these stay in registers from the start (no loop to unroll first).
+template <uint32_t I> struct Index { static constexpr uint32_t value = I; };
+template <uint32_t N, class F>
+MYNAH_DEV void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(Index<N - 1>{});
+    }
+}
+
 // A float moved across lanes by one DPP control.
 template <int CTRL>
 MYNAH_DEV float dpp_f(float v) {

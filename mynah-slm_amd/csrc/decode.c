@@ -509,7 +509,12 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             const float *cpm = pm, *cpo = po;
             const double *cpl = pl;
             void *args2[] = {&pos, &cpm, &cpl, &cpo, &out, &nchm, &group};
-            if (!fold)
+            /* Up to MYNAH_AC1_MAX chunks one wave per query head combines
+             * (no barrier), past that four (MYNAH_ATTN_COMBINE1=0: always
+             * four); same bits. */
+            if (!fold && s->nch_max <= MYNAH_AC1_MAX && env_or("MYNAH_ATTN_COMBINE1", 1) != 0)
+                rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE1, c->n_heads, 1, 64, 0, st, args2);
+            else if (!fold)
                 rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_heads, 1, 256,
                                   (size_t)s->nch_max * sizeof(float), st, args2);
         } else {

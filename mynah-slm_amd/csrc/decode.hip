@@ -737,6 +737,58 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
 }
 
 
+// The combine of one query head by one wave, for launches of at most
+// AC1_MAX chunks: the operations of mynah_attn_combine in the same order
+// (every chunk in lane c of one wave: M by a wave max, L = the wave's double
+// sum plus the three empty waves' 0.0, then the four fma chains over the
+// chunks c = 0, 1, 2, 3 mod 4 with weights w_c * inv, added in that order),
+// with no barrier: the weights reach every lane by readlane. Every partial
+// of the launch's nch_max chunks is loaded before the position arrives.
+// Grid n_heads, block 64.
+#define AC1_MAX 32                                 // = MYNAH_AC1_MAX (runtime_internal.h)
+extern "C" __global__ void __launch_bounds__(64)
+mynah_attn_combine1(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
+                    const double *__restrict__ pl, const float *__restrict__ po,
+                    float *__restrict__ out, uint32_t nch_max, uint32_t group) {
+#pragma clang fp contract(off)
+    const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
+    const uint32_t lane = threadIdx.x;
+    const size_t base = (size_t)kvh * nch_max * group + h;
+    const float *pob = po + base * 128u + lane;
+    const size_t cstride = (size_t)group * 128u;
+    float pv[AC1_MAX][2];
+    static_for<AC1_MAX>([&](auto C) {
+        constexpr uint32_t c = decltype(C)::value;
+        pv[c][0] = c < nch_max ? pob[(size_t)c * cstride] : 0.0f;
+        pv[c][1] = c < nch_max ? pob[(size_t)c * cstride + 64u] : 0.0f;
+    });
+    const float pm0 = lane < nch_max ? pm[base + (size_t)lane * group] : 0.0f;
+    const double pl0 = lane < nch_max ? pl[base + (size_t)lane * group] : 0.0;
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
+    float m = -__builtin_inff();
+    if (lane < nch) m = fmaxf(m, pm0);
+    const float M = wave_max_dpp(m);
+    float w = 0.0f;
+    double l = 0.0;
+    if (lane < nch) {
+        w = mynah_expf(pm0 - M);
+        l += (double)w * pl0;
+    }
+    l = wave_sum_d(l);
+    const float inv = (float)(1.0 / (((l + 0.0) + 0.0) + 0.0));
+    float o[4][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}};
+    static_for<AC1_MAX>([&](auto C) {
+        constexpr uint32_t c = decltype(C)::value;
+        if (c < nch) {
+            const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c)) * inv;
+            o[c & 3u][0] = __builtin_fmaf(sc, pv[c][0], o[c & 3u][0]);
+            o[c & 3u][1] = __builtin_fmaf(sc, pv[c][1], o[c & 3u][1]);
+        }
+    });
+    out[(size_t)head * 128u + lane] = ((o[0][0] + o[1][0]) + o[2][0]) + o[3][0];
+    out[(size_t)head * 128u + 64u + lane] = ((o[0][1] + o[1][1]) + o[2][1]) + o[3][1];
+}
+
 // src/kernels.c:118-128 (the final norm before the head,
 // src/arch_qwen3.c:239): s = (float)(1 / sqrt(sum(x^2) / n + eps)) with the
 // sum in double; out = (x * s) * w. One workgroup.

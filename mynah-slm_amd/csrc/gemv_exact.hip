@@ -508,17 +508,6 @@ MYNAH_DEV void fold_fma(float4 &o, float sc, const float4 &v) {
     o.w = __builtin_fmaf(sc, v.w, o.w);
 }
 
-// Calls f(Index<0>), ..., f(Index<N - 1>): register arrays indexed by
-// these stay in registers from the start (no loop to unroll first).
-template <uint32_t I> struct Index { static constexpr uint32_t value = I; };
-template <uint32_t N, class F>
-MYNAH_DEV void static_for(F &&f) {
-    if constexpr (N > 0) {
-        static_for<N - 1>(f);
-        f(Index<N - 1>{});
-    }
-}
-
 MYNAH_DEV void stage_fold(const AttnFold &af, uint32_t cols, float *lds, float *lw) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nw = blockDim.x >> 6;

@@ -51,6 +51,7 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_ATTN_OUT_LONG, "mynah_attn_out_long")    \
     X(MYNAH_K_ATTN_SPLIT, "mynah_attn_split")          \
     X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
+    X(MYNAH_K_ATTN_COMBINE1, "mynah_attn_combine1")    \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
     X(MYNAH_K_EMBED, "mynah_embed_row")                \
@@ -84,6 +85,8 @@ enum {
 
 /* Positions per workgroup of the split attention (decode.hip AS_CH). */
 #define MYNAH_AS_CH 32
+/* Most chunks mynah_attn_combine1 (one wave per query head) takes. */
+#define MYNAH_AC1_MAX 32
 
 typedef struct {
     int loaded;
