@@ -737,56 +737,96 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
 }
 
 
-// The combine of one query head by one wave, for launches of at most
-// AC1_MAX chunks: the operations of mynah_attn_combine in the same order
-// (every chunk in lane c of one wave: M by a wave max, L = the wave's double
-// sum plus the three empty waves' 0.0, then the four fma chains over the
-// chunks c = 0, 1, 2, 3 mod 4 with weights w_c * inv, added in that order),
-// with no barrier: the weights reach every lane by readlane. Every partial
-// of the launch's nch_max chunks is loaded before the position arrives.
-// Grid n_heads, block 64.
+// The combine of one query head without a barrier, for launches of at most
+// MAXC chunks: the operations of mynah_attn_combine in the same order.
+// Chunk c's max and exp sum sit in lane c % 64 (set c / 64) of every wave:
+// M by wave maxima, L = ((s_0 + s_1) + 0.0) + 0.0 with s_k the wave's double
+// sum over set k (the combine's per-wave sums; its third and fourth waves
+// hold no chunk), then the four fma chains over the chunks c = 0, 1, 2, 3
+// mod 4 with weights w_c * inv (read from their lanes), added in that order.
+// DPL dimensions per lane: 2 (one wave per head, dimensions l and l + 64)
+// or 1 (two waves, wave w dimension 64 w + l, each on its own). Every
+// partial of the launch's chunks is loaded before the position arrives.
+// Grid n_heads, block 128 / DPL.
+template <int MAXC, int DPL>
+MYNAH_DEV void attn_combine_waves(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
+                                  const double *__restrict__ pl, const float *__restrict__ po,
+                                  float *__restrict__ out, uint32_t nch_max, uint32_t group) {
+#pragma clang fp contract(off)
+    constexpr uint32_t SETS = (MAXC + 63) / 64;
+    const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
+    const uint32_t lane = threadIdx.x & 63u, dim0 = DPL == 1 ? 64u * (threadIdx.x >> 6) : 0u;
+    const size_t base = (size_t)kvh * nch_max * group + h;
+    const float *pob = po + base * 128u + dim0 + lane;
+    const size_t cstride = (size_t)group * 128u;
+    float pv[MAXC][DPL];
+    static_for<MAXC>([&](auto C) {
+        constexpr uint32_t c = decltype(C)::value;
+        static_for<DPL>([&](auto D) {
+            constexpr uint32_t e = decltype(D)::value;
+            pv[c][e] = c < nch_max ? pob[(size_t)c * cstride + 64u * e] : 0.0f;
+        });
+    });
+    float pmv[SETS];
+    double plv[SETS];
+    static_for<SETS>([&](auto K) {
+        constexpr uint32_t k = decltype(K)::value;
+        const uint32_t c = 64u * k + lane;
+        pmv[k] = c < nch_max ? pm[base + (size_t)c * group] : 0.0f;
+        plv[k] = c < nch_max ? pl[base + (size_t)c * group] : 0.0;
+    });
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
+    float m = -__builtin_inff();
+    static_for<SETS>([&](auto K) {
+        constexpr uint32_t k = decltype(K)::value;
+        if (64u * k + lane < nch) m = fmaxf(m, pmv[k]);
+    });
+    const float M = wave_max_dpp(m);
+    float w[SETS];
+    double L = 0.0;
+    static_for<SETS>([&](auto K) {
+        constexpr uint32_t k = decltype(K)::value;
+        double l = 0.0;
+        w[k] = 0.0f;
+        if (64u * k + lane < nch) {
+            w[k] = mynah_expf(pmv[k] - M);
+            l += (double)w[k] * plv[k];
+        }
+        const double sk = wave_sum_d(l);
+        L = k == 0 ? sk : L + sk;
+    });
+    for (uint32_t k = SETS; k < 4u; k++) L = L + 0.0;
+    const float inv = (float)(1.0 / L);
+    float o[4][DPL];
+    static_for<4>([&](auto K) {
+        static_for<DPL>([&](auto D) { o[decltype(K)::value][decltype(D)::value] = 0.0f; });
+    });
+    static_for<MAXC>([&](auto C) {
+        constexpr uint32_t c = decltype(C)::value;
+        if (c < nch) {
+            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[c / 64u]), c % 64u));
+            const float sc = wc * inv;
+            static_for<DPL>([&](auto D) {
+                constexpr uint32_t e = decltype(D)::value;
+                o[c & 3u][e] = __builtin_fmaf(sc, pv[c][e], o[c & 3u][e]);
+            });
+        }
+    });
+    static_for<DPL>([&](auto D) {
+        constexpr uint32_t e = decltype(D)::value;
+        out[(size_t)head * 128u + dim0 + 64u * e + lane] = ((o[0][e] + o[1][e]) + o[2][e]) + o[3][e];
+    });
+}
+
+// One wave per query head up to AC1_MAX chunks. (Two waves, one dimension
+// per lane, up to 128 chunks, measured slower than the four-wave combine at
+// the 4B's 69 chunks: 459 -> 452 tok/s.)
 #define AC1_MAX 32                                 // = MYNAH_AC1_MAX (runtime_internal.h)
 extern "C" __global__ void __launch_bounds__(64)
 mynah_attn_combine1(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                     const double *__restrict__ pl, const float *__restrict__ po,
                     float *__restrict__ out, uint32_t nch_max, uint32_t group) {
-#pragma clang fp contract(off)
-    const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
-    const uint32_t lane = threadIdx.x;
-    const size_t base = (size_t)kvh * nch_max * group + h;
-    const float *pob = po + base * 128u + lane;
-    const size_t cstride = (size_t)group * 128u;
-    float pv[AC1_MAX][2];
-    static_for<AC1_MAX>([&](auto C) {
-        constexpr uint32_t c = decltype(C)::value;
-        pv[c][0] = c < nch_max ? pob[(size_t)c * cstride] : 0.0f;
-        pv[c][1] = c < nch_max ? pob[(size_t)c * cstride + 64u] : 0.0f;
-    });
-    const float pm0 = lane < nch_max ? pm[base + (size_t)lane * group] : 0.0f;
-    const double pl0 = lane < nch_max ? pl[base + (size_t)lane * group] : 0.0;
-    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
-    float m = -__builtin_inff();
-    if (lane < nch) m = fmaxf(m, pm0);
-    const float M = wave_max_dpp(m);
-    float w = 0.0f;
-    double l = 0.0;
-    if (lane < nch) {
-        w = mynah_expf(pm0 - M);
-        l += (double)w * pl0;
-    }
-    l = wave_sum_d(l);
-    const float inv = (float)(1.0 / (((l + 0.0) + 0.0) + 0.0));
-    float o[4][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}, {0.0f, 0.0f}};
-    static_for<AC1_MAX>([&](auto C) {
-        constexpr uint32_t c = decltype(C)::value;
-        if (c < nch) {
-            const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c)) * inv;
-            o[c & 3u][0] = __builtin_fmaf(sc, pv[c][0], o[c & 3u][0]);
-            o[c & 3u][1] = __builtin_fmaf(sc, pv[c][1], o[c & 3u][1]);
-        }
-    });
-    out[(size_t)head * 128u + lane] = ((o[0][0] + o[1][0]) + o[2][0]) + o[3][0];
-    out[(size_t)head * 128u + 64u + lane] = ((o[0][1] + o[1][1]) + o[2][1]) + o[3][1];
+    attn_combine_waves<AC1_MAX, 2>(pos_ptr, pm, pl, po, out, nch_max, group);
 }
 
 // src/kernels.c:118-128 (the final norm before the head,

@@ -206,13 +206,14 @@ def test_folded_attention_combine_bit_identical(M, monkeypatch, shape, npre):
     assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape,npre", [(CF.QWEN3_TINY, 60), (CF.QWEN3_06B, 500)],
-                         ids=["tiny", "0.6B"])
+@pytest.mark.parametrize("shape,npre", [(CF.QWEN3_TINY, 60), (CF.QWEN3_06B, 500),
+                                        (CF.QWEN3_TINY, 1000)],
+                         ids=["tiny", "0.6B", "tiny-32ch"])
 def test_one_wave_combine_bit_identical(M, monkeypatch, shape, npre):
     """The split attention's combine by one wave per query head (up to 32
-    chunks, no barrier) against the four-wave combine
-    (MYNAH_ATTN_COMBINE1=0), the fold off in both: every step's logits
-    bit-identical, stepwise and graph-replayed, across a chunk boundary."""
+    chunks, no barrier; the last case has exactly 32) against the four-wave
+    combine (MYNAH_ATTN_COMBINE1=0), the fold off in both: every step's
+    logits bit-identical, stepwise and graph-replayed."""
     steps = 12
     print(f"[case] one-wave combine d={shape.d_model} npre={npre}", flush=True)
     model = M.SynthQwen3(shape, 0)
