@@ -130,11 +130,11 @@ MYNAH_DEV double wave_sum_d(double v) {
 }
 
 // Workgroup-wide double sum; every thread gets the result. `sh` holds one
-// double per wave (blockDim.x <= 1024).
+// double per wave (blockDim.x <= 1024) and is written with no barrier in
+// front: a kernel calls this at most once per `sh` (every caller does).
 MYNAH_DEV double block_sum_d(double v, double *sh) {
     v = wave_sum_d(v);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    __syncthreads();
     if (lane == 0) sh[wave] = v;
     __syncthreads();
     double t = 0.0;
