@@ -1125,78 +1125,116 @@ mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride) {
 // (0 past each query's own last position, which leaves its chain unchanged:
 // fma(v, 0, o) = o for finite v and o != -0, and o never becomes -0 from
 // +0) and the V rows (rows past the tile's last position hold row 0, finite)
-// are staged in LDS; the next chunk's V rows are fetched into registers
-// while this one is summed. Grid (n_kv_heads,
+// are staged in LDS; the next chunk's V rows and probabilities are fetched
+// into registers while this one is summed. Grid (n_kv_heads,
 // ceil(T / PV_Q)), block 512.
 #define PV_Q 8
 #define PV_CH 64
-extern "C" __global__ void __launch_bounds__(512)
-mynah_prefill_pv(const float *__restrict__ v_layer, const float *__restrict__ probs,
-                 float *__restrict__ out, uint32_t p0, uint32_t T, uint32_t sstride,
-                 uint32_t kv_dim, uint32_t group) {
+// G = group (2 .. 8, the decoder's limits): each thread owns NPT = 2 G
+// (query, head) pairs, all compile-time indices; pairs of a short last tile
+// have probabilities 0 (their outputs are not stored).
+template <uint32_t G>
+MYNAH_DEV void prefill_pv_tile(const float *__restrict__ v_layer, const float *__restrict__ probs,
+                               float *__restrict__ out, uint32_t p0, uint32_t T, uint32_t sstride,
+                               uint32_t kv_dim, float (*pl)[PV_CH], float (*vl)[128]) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float pl[PV_Q * 8][PV_CH];
-    __shared__ __attribute__((aligned(16))) float vl[PV_CH][128];
+    constexpr uint32_t NPT = PV_Q * G / 4u, NPR = PV_Q * G * PV_CH / 512u;
     const uint32_t kvh = blockIdx.x, q0 = blockIdx.y * PV_Q;
     const uint32_t nq = T - q0 < PV_Q ? T - q0 : PV_Q;
-    const uint32_t npair = nq * group, n_heads = gridDim.x * group;
+    const uint32_t npair = nq * G, n_heads = gridDim.x * G;
     const uint32_t tid = threadIdx.x, d = tid & 127u, c = tid >> 7;
     const uint32_t n_end = p0 + q0 + nq;            // positions of the last query
     const float *vbase = v_layer + (size_t)kvh * 128u;
     // V fetch role: float4 f = tid + 512 k of the chunk: row f / 32, column
-    // 4 (f % 32); rows past n_end read row 0 (never used).
+    // 4 (f % 32); rows past n_end read row 0 (never used). Probability fetch
+    // role: entry i = tid + 512 k of the chunk's PV_Q G x PV_CH (pair i /
+    // PV_CH, position i % PV_CH), 0 past the pair's query or past npair.
     float4 vr[4];
-    auto fetch = [&](uint32_t t0) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t f = tid + 512u * (uint32_t)k, r = t0 + (f >> 5);
-            vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
-        }
-    };
-    float o[16];
-#pragma unroll
-    for (int k = 0; k < 16; k++) o[k] = 0.0f;
-    fetch(0);
+    float pr_r[NPR];
+    float o[NPT];
+    static_for<NPT>([&](auto K) { o[decltype(K)::value] = 0.0f; });
     for (uint32_t t0 = 0; t0 < n_end; t0 += PV_CH) {
+        if (t0 == 0) {
+            static_for<4>([&](auto K) {
+                constexpr uint32_t k = decltype(K)::value;
+                const uint32_t f = tid + 512u * k, r = f >> 5;
+                vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
+            });
+            static_for<NPR>([&](auto K) {
+                constexpr uint32_t k = decltype(K)::value;
+                const uint32_t i = tid + 512u * k, pr = i / PV_CH, t = i % PV_CH;
+                const uint32_t qi = pr / G, h = pr % G;
+                pr_r[k] = pr < npair && t < p0 + q0 + qi + 1u
+                              ? probs[((size_t)(q0 + qi) * n_heads + kvh * G + h) * sstride + t]
+                              : 0.0f;
+            });
+        }
         __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t f = tid + 512u * (uint32_t)k;
+        static_for<4>([&](auto K) {
+            constexpr uint32_t k = decltype(K)::value;
+            const uint32_t f = tid + 512u * k;
             *(float4 *)&vl[f >> 5][4u * (f & 31u)] = vr[k];
-        }
-        for (uint32_t i = tid; i < npair * PV_CH; i += blockDim.x) {
-            const uint32_t pr = i / PV_CH, j = i % PV_CH, t = t0 + j;
-            const uint32_t qi = pr / group, h = pr % group;
-            const uint32_t n_kv = p0 + q0 + qi + 1u;
-            pl[pr][j] = t < n_kv ? probs[((size_t)(q0 + qi) * n_heads + kvh * group + h) * sstride + t]
-                                 : 0.0f;
-        }
+        });
+        static_for<NPR>([&](auto K) {
+            constexpr uint32_t k = decltype(K)::value;
+            const uint32_t i = tid + 512u * k;
+            pl[i / PV_CH][i % PV_CH] = pr_r[k];
+        });
         __syncthreads();
-        if (t0 + PV_CH < n_end) fetch(t0 + PV_CH);
+        const uint32_t t1 = t0 + PV_CH;
+        if (t1 < n_end) {
+            static_for<4>([&](auto K) {
+                constexpr uint32_t k = decltype(K)::value;
+                const uint32_t f = tid + 512u * k, r = t1 + (f >> 5);
+                vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
+            });
+            static_for<NPR>([&](auto K) {
+                constexpr uint32_t k = decltype(K)::value;
+                const uint32_t i = tid + 512u * k, pr = i / PV_CH, t = t1 + i % PV_CH;
+                const uint32_t qi = pr / G, h = pr % G;
+                pr_r[k] = pr < npair && t < p0 + q0 + qi + 1u
+                              ? probs[((size_t)(q0 + qi) * n_heads + kvh * G + h) * sstride + t]
+                              : 0.0f;
+            });
+        }
         // Four positions per step (rounded up: the padding has p = 0).
         const uint32_t tn = n_end - t0 < PV_CH ? n_end - t0 : PV_CH;
         for (uint32_t j = 0; j < tn; j += 4) {
             const float v0 = vl[j][d], v1 = vl[j + 1][d], v2 = vl[j + 2][d], v3 = vl[j + 3][d];
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const uint32_t pr = c + 4u * (uint32_t)k;
-                if (pr < npair) {
-                    const float4 pp = *(const float4 *)&pl[pr][j];
-                    float acc = o[k];
-                    acc = __builtin_fmaf(v0, pp.x, acc);
-                    acc = __builtin_fmaf(v1, pp.y, acc);
-                    acc = __builtin_fmaf(v2, pp.z, acc);
-                    o[k] = __builtin_fmaf(v3, pp.w, acc);
-                }
-            }
+            static_for<NPT>([&](auto K) {
+                constexpr uint32_t k = decltype(K)::value;
+                const float4 pp = *(const float4 *)&pl[c + 4u * k][j];
+                float acc = o[k];
+                acc = __builtin_fmaf(v0, pp.x, acc);
+                acc = __builtin_fmaf(v1, pp.y, acc);
+                acc = __builtin_fmaf(v2, pp.z, acc);
+                o[k] = __builtin_fmaf(v3, pp.w, acc);
+            });
         }
     }
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const uint32_t pr = c + 4u * (uint32_t)k;
+    static_for<NPT>([&](auto K) {
+        constexpr uint32_t k = decltype(K)::value;
+        const uint32_t pr = c + 4u * k;
         if (pr < npair) {
-            const uint32_t qi = pr / group, h = pr % group;
-            out[((size_t)(q0 + qi) * n_heads + kvh * group + h) * 128u + d] = o[k];
+            const uint32_t qi = pr / G, h = pr % G;
+            out[((size_t)(q0 + qi) * n_heads + kvh * G + h) * 128u + d] = o[k];
         }
+    });
+}
+
+extern "C" __global__ void __launch_bounds__(512)
+mynah_prefill_pv(const float *__restrict__ v_layer, const float *__restrict__ probs,
+                 float *__restrict__ out, uint32_t p0, uint32_t T, uint32_t sstride,
+                 uint32_t kv_dim, uint32_t group) {
+    __shared__ __attribute__((aligned(16))) float pl[PV_Q * 8][PV_CH];
+    __shared__ __attribute__((aligned(16))) float vl[PV_CH][128];
+    switch (group) {
+    case 2u: prefill_pv_tile<2>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    case 3u: prefill_pv_tile<3>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    case 4u: prefill_pv_tile<4>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    case 5u: prefill_pv_tile<5>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    case 6u: prefill_pv_tile<6>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    case 7u: prefill_pv_tile<7>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
+    default: prefill_pv_tile<8>(v_layer, probs, out, p0, T, sstride, kv_dim, pl, vl); break;
     }
 }

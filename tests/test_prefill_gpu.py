@@ -120,6 +120,20 @@ def test_tiny_prefill_after_cache(M, chunk):
     assert_same_state(a, b, int(prompt[0]))
 
 
+@pytest.mark.parametrize("group", [3, 5, 6, 7, 8])
+def test_prefill_equals_steps_every_group(M, chunk, group):
+    """Query heads per key head 3 .. 8 (Qwen3-14B has 5): the batched
+    prefill (its PV tiles compiled per group) leaves K/V and the next
+    logits bit-identical to token-by-token steps."""
+    chunk(40)
+    shape = CF.Qwen3Shape(2, 512, 768, 2 * group, 2, 128, 4096)
+    print(f"[case] prefill group={group}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    prompt = M.synth_uniform(M.substream(7, 5), 75, shape.vocab)
+    a, b = fill_both(M, model, prompt, 80)
+    assert_same_state(a, b, int(prompt[2]))
+
+
 def test_qwen3_06b_prefill_equals_steps(M):
     shape = CF.QWEN3_06B
     print("[case] Qwen3-0.6B prefill of 100 tokens", flush=True)
