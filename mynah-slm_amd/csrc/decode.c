@@ -446,23 +446,6 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
     mynah_gemv_group lg[LG_COUNT], next_qkv;
     int rc = 0;
     for (int k = 0; k < LG_COUNT && rc == 0; k++) rc = layer_group(s, 0, k, &lg[k]);
-    /* Split attention up to 64 chunks: the output projection folds the
-     * chunks' partials itself (the combine's operations, same bits) instead
-     * of a combine launch, when its workgroups re-read at most
-     * MYNAH_FOLD_MAX_BYTES (default 12 MiB) of partials between them: each
-     * workgroup reads every head's partials, which costs more than the
-     * saved launch past about a dozen chunks at 0.6B (measured: +1.4 % at
-     * 40-100 positions, +0.8 % at 220, -0.7 % at 512). MYNAH_ATTN_FOLD=0
-     * keeps the combine launch. */
-    int fold = rc == 0 && s->attn_mode == MYNAH_ATTN_SPLIT && s->nch_max <= 64u &&
-               env_or("MYNAH_ATTN_FOLD", 1) != 0 &&
-               mynah_gemv_group_can_fold(&lg[LG_O], -1) == 1;
-    if (fold) {
-        uint32_t o_wgs = 0;
-        const uint64_t reread = (uint64_t)c->n_heads * s->nch_max * 128u * 4u;
-        fold = mynah_gemv_group_geometry(&lg[LG_O], -1, NULL, &o_wgs) == 0 &&
-               reread * o_wgs <= (uint64_t)env_or("MYNAH_FOLD_MAX_BYTES", 12L << 20);
-    }
     for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
         const dlayer *L = &s->layers[l];
         float *kl = s->k_cache + l * per_layer, *vl = s->v_cache + l * per_layer;
@@ -472,13 +455,6 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             for (int k = LG_O; k < LG_COUNT && rc == 0; k++) rc = layer_group(s, l, k, &lg[k]);
         }
         if (rc == 0 && more) rc = layer_group(s, l + 1, LG_QKV, &next_qkv);
-        if (rc == 0 && fold) {
-            uint32_t spec = (s->n_past + MYNAH_AS_CH) / MYNAH_AS_CH;
-            if (spec > s->nch_max) spec = s->nch_max;
-            const mynah_attn_fold af = {pos, s->pm, s->pl, s->po, s->nch_max,
-                                        c->n_heads / c->n_kv_heads, c->n_heads, 1, spec, 0};
-            lg[LG_O].af = af;
-        }
         for (int k = 0; k < LG_COUNT && rc == 0 && (pf_wgs || pf_b); k++) {
             const mynah_gemv_group *nx = k + 1 < LG_COUNT ? &lg[k + 1] : more ? &next_qkv : NULL;
             if (nx) rc = mynah_gemv_prefetch_plan(nx, -1, pf_wgs, pf_b, pf_m, pf_step, &lg[k].pf);
@@ -512,9 +488,9 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             /* Up to MYNAH_AC1_MAX chunks one wave per query head combines
              * (no barrier), past that four (MYNAH_ATTN_COMBINE1=0: always
              * four); same bits. */
-            if (!fold && s->nch_max <= MYNAH_AC1_MAX && env_or("MYNAH_ATTN_COMBINE1", 1) != 0)
+            if (s->nch_max <= MYNAH_AC1_MAX && env_or("MYNAH_ATTN_COMBINE1", 1) != 0)
                 rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE1, c->n_heads, 1, 64, 0, st, args2);
-            else if (!fold)
+            else
                 rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_heads, 1, 256,
                                   (size_t)s->nch_max * sizeof(float), st, args2);
         } else {

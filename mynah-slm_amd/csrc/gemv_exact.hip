@@ -377,27 +377,10 @@ struct GemvPrefetch {
     uint32_t n, wgs, host_tiles, step_log2;
 };
 
-// The split decode attention's partials, folded by the launch that reads
-// the attention output (the output projection) while it stages its input,
-// in place of a separate combine launch: the operations of
-// mynah_attn_combine (decode.hip) in the same order, so the staged input
-// has the bits that launch writes. on = 0: the input is read from x.
-// Partials pm, pl [n_kv][nch_max][group], po [n_kv][nch_max][group][128];
-// nch_max <= 64, n_heads * 128 = cols, spec <= nch_max.
-struct AttnFold {
-    const uint32_t *pos;
-    const float *pm;
-    const double *pl;
-    const float *po;
-    uint32_t nch_max, group, n_heads, on;
-    uint32_t spec, pad;       // chunks live when the launch was enqueued
-};
-
 struct GemvGroup {
     uint32_t n, shape;
     GemvDesc d[EX_GROUP_MAX];
     GemvPrefetch pf;
-    AttnFold af;
 };
 
 // Where the prefetched bytes end up: stored only when the touched bytes sum
@@ -487,138 +470,6 @@ MYNAH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ no
     }
 }
 
-// Stage the attention output that mynah_attn_combine would write, from the
-// split partials, into the padded LDS copy (the layout stage_x writes).
-// Per query head h (wave h mod waves, lane c holding chunk c): M = max m_c,
-// w_c = expf(m_c - M), L = the wave's double sum of w_c l_c (then + 0.0
-// three times: the combine adds its three empty waves' sums), inv =
-// (float)(1 / L). Per output float4: four fma chains over the chunks c = 0,
-// 1, 2, 3 (mod 4) in chunk order with weights w_c * inv, added in that
-// order. Every load of the chunks live when the launch was enqueued (the
-// first FOLD_PRE of them per output) goes out before the position. Needs
-// n_heads <= FOLD_HP * waves, cols <= 8 * threads; lw holds n_heads * 65
-// floats. Every thread of the workgroup calls it; the caller synchronises
-// before reading the copy.
-#define FOLD_HP 4
-#define FOLD_PRE 12
-MYNAH_DEV void fold_fma(float4 &o, float sc, const float4 &v) {
-    o.x = __builtin_fmaf(sc, v.x, o.x);
-    o.y = __builtin_fmaf(sc, v.y, o.y);
-    o.z = __builtin_fmaf(sc, v.z, o.z);
-    o.w = __builtin_fmaf(sc, v.w, o.w);
-}
-
-MYNAH_DEV void stage_fold(const AttnFold &af, uint32_t cols, float *lds, float *lw) {
-#pragma clang fp contract(off)
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nw = blockDim.x >> 6;
-    const uint32_t H = af.n_heads, G = af.group, NM = af.nch_max;
-    float *wsc = lw, *winv = lw + 64u * H;
-    // Chunk maxima and exp sums of this wave's heads, lane = chunk.
-    float pmv[FOLD_HP];
-    double plv[FOLD_HP];
-    static_for<FOLD_HP>([&](auto K) {
-        constexpr uint32_t k = decltype(K)::value;
-        const uint32_t h = wave + nw * k, kvh = h / G;
-        const size_t slot = ((size_t)kvh * NM + lane) * G + (h - kvh * G);
-        const bool ok = h < H && lane < NM;
-        pmv[k] = ok ? af.pm[slot] : 0.0f;
-        plv[k] = ok ? af.pl[slot] : 0.0;
-    });
-    // The thread's two output float4s q0, q1 (q1 clamped into the vector)
-    // and the partials of their first FOLD_PRE chunks (chunk indices clamped
-    // below nch_max; chunks at or past pre are loaded again below).
-    const uint32_t n4 = cols / 4u, pre = af.spec < FOLD_PRE ? af.spec : FOLD_PRE;
-    const uint32_t cs = G * 32u;                   // float4s from one chunk to the next
-    const uint32_t q0 = tid, q1r = tid + blockDim.x, q1 = q1r < n4 ? q1r : n4 - 1u;
-    const uint32_t h0 = q0 >> 5, h1 = q1 >> 5, k0 = h0 / G, k1 = h1 / G;
-    const float4 *pb0 = (const float4 *)(af.po + ((size_t)k0 * NM * G + (h0 - k0 * G)) * 128u) + (q0 & 31u);
-    const float4 *pb1 = (const float4 *)(af.po + ((size_t)k1 * NM * G + (h1 - k1 * G)) * 128u) + (q1 & 31u);
-    float4 v0[FOLD_PRE], v1[FOLD_PRE];
-    static_for<FOLD_PRE>([&](auto C) {
-        constexpr uint32_t c = decltype(C)::value;
-        const uint32_t cc = c < NM ? c : NM - 1u;
-        v0[c] = pb0[(size_t)cc * cs];
-        v1[c] = pb1[(size_t)cc * cs];
-    });
-    const uint32_t n_kv = af.pos[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
-    float M[FOLD_HP];
-    static_for<FOLD_HP>([&](auto K) {
-        constexpr uint32_t k = decltype(K)::value;
-        float m = -__builtin_inff();
-        if (lane < nch) m = fmaxf(m, pmv[k]);
-        M[k] = wave_max_dpp(m);
-    });
-    double L[FOLD_HP];
-    static_for<FOLD_HP>([&](auto K) {
-        constexpr uint32_t k = decltype(K)::value;
-        const uint32_t h = wave + nw * k;
-        double l = 0.0;
-        if (h < H && lane < nch) {
-            const float w = mynah_expf(pmv[k] - M[k]);
-            wsc[64u * h + lane] = w;
-            l += (double)w * plv[k];
-        }
-        L[k] = wave_sum_d(l);
-    });
-    static_for<FOLD_HP>([&](auto K) {
-        constexpr uint32_t k = decltype(K)::value;
-        const uint32_t h = wave + nw * k;
-        if (lane == 0 && h < H) winv[h] = (float)(1.0 / (((L[k] + 0.0) + 0.0) + 0.0));
-    });
-    // Chunks past those live at enqueue (pre) that are live now.
-    if (pre < FOLD_PRE && pre < nch) {
-        static_for<FOLD_PRE>([&](auto C) {
-            constexpr uint32_t c = decltype(C)::value;
-            if (c >= pre && c < nch) {
-                v0[c] = pb0[(size_t)c * cs];
-                v1[c] = pb1[(size_t)c * cs];
-            }
-        });
-    }
-    __syncthreads();
-    const float inv0 = winv[h0], inv1 = winv[h1];
-    const float *w0 = wsc + 64u * h0, *w1 = wsc + 64u * h1;
-    float4 o0[4], o1[4];
-    static_for<4>([&](auto K) {
-        constexpr uint32_t k = decltype(K)::value;
-        o0[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        o1[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    });
-    static_for<FOLD_PRE>([&](auto C) {
-        constexpr uint32_t c = decltype(C)::value;
-        if (c < nch) {
-            fold_fma(o0[c & 3u], w0[c] * inv0, v0[c]);
-            fold_fma(o1[c & 3u], w1[c] * inv1, v1[c]);
-        }
-    });
-    for (uint32_t c = FOLD_PRE; c < nch; c += 4u) {
-        float4 x0[4], x1[4];
-        static_for<4>([&](auto K) {
-            constexpr uint32_t k = decltype(K)::value;
-            const uint32_t cc = c + k < nch ? c + k : c;
-            x0[k] = pb0[(size_t)cc * cs];
-            x1[k] = pb1[(size_t)cc * cs];
-        });
-        static_for<4>([&](auto K) {
-            constexpr uint32_t k = decltype(K)::value;
-            if (c + k < nch) {
-                fold_fma(o0[k], w0[c + k] * inv0, x0[k]);
-                fold_fma(o1[k], w1[c + k] * inv1, x1[k]);
-            }
-        });
-    }
-    float4 r0, r1;
-    r0.x = ((o0[0].x + o0[1].x) + o0[2].x) + o0[3].x;
-    r0.y = ((o0[0].y + o0[1].y) + o0[2].y) + o0[3].y;
-    r0.z = ((o0[0].z + o0[1].z) + o0[2].z) + o0[3].z;
-    r0.w = ((o0[0].w + o0[1].w) + o0[2].w) + o0[3].w;
-    r1.x = ((o1[0].x + o1[1].x) + o1[2].x) + o1[3].x;
-    r1.y = ((o1[0].y + o1[1].y) + o1[2].y) + o1[3].y;
-    r1.z = ((o1[0].z + o1[1].z) + o1[2].z) + o1[3].z;
-    r1.w = ((o1[0].w + o1[1].w) + o1[2].w) + o1[3].w;
-    if (q0 < n4) *(float4 *)(lds + 4u * q0 + 4u * (q0 >> 6)) = r0;
-    if (q1r < n4) *(float4 *)(lds + 4u * q1 + 4u * (q1 >> 6)) = r1;
-}
 
 template <int FMT> struct Raw;
 template <> struct Raw<12> {
@@ -823,9 +674,8 @@ MYNAH_DEV const float *unit_x(const float *lx, uint32_t u) {
     return lx + 260u * u;
 }
 
-template <int FMT, bool SEG, class RawT = Raw<FMT>, bool FOLD = false>
-MYNAH_DEV void group_split(const GemvDesc &g, const AttnFold &af, uint32_t t, uint32_t shape,
-                           float *lds, double *shd) {
+template <int FMT, bool SEG, class RawT = Raw<FMT>>
+MYNAH_DEV void group_split(const GemvDesc &g, uint32_t t, uint32_t shape, float *lds, double *shd) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t lk = shape & 31u, ws_n = (shape >> 8) & 31u, wr_n = (shape >> 16) & 31u;
@@ -859,8 +709,7 @@ MYNAH_DEV void group_split(const GemvDesc &g, const AttnFold &af, uint32_t t, ui
 
     // Stage x (or RMSNorm(x) * norm_w) into the padded LDS copy.
     const uint32_t cols = g.cols;
-    if constexpr (FOLD) stage_fold(af, cols, lds, lds + xpad_floats(cols) + rpg * pstride);
-    else stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + rpg * pstride, shd);
+    stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + rpg * pstride, shd);
     __syncthreads();
 
     float *part = lds + xpad_floats(cols);
@@ -908,9 +757,8 @@ MYNAH_DEV void group_split(const GemvDesc &g, const AttnFold &af, uint32_t t, ui
 // of a row are folded in unit order by one thread (R <= 64: the first wave),
 // followed by the epilogues of group_split. Every lane busy but the last
 // few of the workgroup, and x staged once per R rows.
-template <int FMT, class RawT = Raw<FMT>, bool FOLD = false>
-MYNAH_DEV void group_flat(const GemvDesc &g, const AttnFold &af, uint32_t t, float *lds,
-                          double *shd) {
+template <int FMT, class RawT = Raw<FMT>>
+MYNAH_DEV void group_flat(const GemvDesc &g, uint32_t t, float *lds, double *shd) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t R = g.pad;
@@ -934,8 +782,7 @@ MYNAH_DEV void group_flat(const GemvDesc &g, const AttnFold &af, uint32_t t, flo
     const uint32_t yoff = g.ypos ? g.ypos[0] * g.ystride : 0u;
 
     const uint32_t cols = g.cols;
-    if constexpr (FOLD) stage_fold(af, cols, lds, lds + xpad_floats(cols) + R * pstride);
-    else stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + R * pstride, shd);
+    stage_x(g.x, g.norm_w, cols, g.eps, lds, lds + xpad_floats(cols) + R * pstride, shd);
     __syncthreads();
 
     float *part = lds + xpad_floats(cols);
@@ -1036,54 +883,24 @@ mynah_gemv_group(const GemvGroup grp) {
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
     const GemvDesc &g = grp.d[i];
     if (grp.shape & (1u << 25)) {
-        if (g.type == 12u) group_flat<12>(g, grp.af, t, lds, shd);
-        else if (g.type == 13u) group_flat<13>(g, grp.af, t, lds, shd);
-        else if (g.type == 14u) group_flat<14>(g, grp.af, t, lds, shd);
-        else group_flat<8>(g, grp.af, t, lds, shd);
+        if (g.type == 12u) group_flat<12>(g, t, lds, shd);
+        else if (g.type == 13u) group_flat<13>(g, t, lds, shd);
+        else if (g.type == 14u) group_flat<14>(g, t, lds, shd);
+        else group_flat<8>(g, t, lds, shd);
     } else if (grp.shape & (1u << 24)) {
-        if (g.type == 12u) group_split<12, true>(g, grp.af, t, grp.shape, lds, shd);
-        else if (g.type == 13u) group_split<13, true>(g, grp.af, t, grp.shape, lds, shd);
-        else group_split<14, true>(g, grp.af, t, grp.shape, lds, shd);
+        if (g.type == 12u) group_split<12, true>(g, t, grp.shape, lds, shd);
+        else if (g.type == 13u) group_split<13, true>(g, t, grp.shape, lds, shd);
+        else group_split<14, true>(g, t, grp.shape, lds, shd);
     } else if (g.type == 12u) {
-        group_split<12, false>(g, grp.af, t, grp.shape, lds, shd);
+        group_split<12, false>(g, t, grp.shape, lds, shd);
     } else if (g.type == 13u) {
-        group_split<13, false>(g, grp.af, t, grp.shape, lds, shd);
+        group_split<13, false>(g, t, grp.shape, lds, shd);
     } else if (g.type == 14u) {
-        group_split<14, false>(g, grp.af, t, grp.shape, lds, shd);
+        group_split<14, false>(g, t, grp.shape, lds, shd);
     } else if (g.type == 2u) {
         group_chain_q40(g, t, lds, shd);
     } else {
-        group_split<8, false>(g, grp.af, t, grp.shape, lds, shd);
-    }
-}
-
-// A launch whose input is the split attention's output, folded from the
-// partials while staging (stage_fold; grp.af): the layouts of
-// mynah_gemv_group for the super-block types and Q8_0, at most 512 threads.
-extern "C" __global__ void __launch_bounds__(512)
-mynah_gemv_group_fold(const GemvGroup grp) {
-    extern __shared__ __attribute__((aligned(16))) float lds[];
-    __shared__ double shd[16];
-    if (gemv_prefetch_tail(grp.pf)) return;
-    const uint32_t t = blockIdx.x;
-    const GemvDesc &g = grp.d[0];
-    if (grp.shape & (1u << 25)) {
-        if (g.type == 12u) group_flat<12, Raw<12>, true>(g, grp.af, t, lds, shd);
-        else if (g.type == 13u) group_flat<13, Raw<13>, true>(g, grp.af, t, lds, shd);
-        else if (g.type == 14u) group_flat<14, Raw<14>, true>(g, grp.af, t, lds, shd);
-        else group_flat<8, Raw<8>, true>(g, grp.af, t, lds, shd);
-    } else if (grp.shape & (1u << 24)) {
-        if (g.type == 12u) group_split<12, true, Raw<12>, true>(g, grp.af, t, grp.shape, lds, shd);
-        else if (g.type == 13u) group_split<13, true, Raw<13>, true>(g, grp.af, t, grp.shape, lds, shd);
-        else group_split<14, true, Raw<14>, true>(g, grp.af, t, grp.shape, lds, shd);
-    } else if (g.type == 12u) {
-        group_split<12, false, Raw<12>, true>(g, grp.af, t, grp.shape, lds, shd);
-    } else if (g.type == 13u) {
-        group_split<13, false, Raw<13>, true>(g, grp.af, t, grp.shape, lds, shd);
-    } else if (g.type == 14u) {
-        group_split<14, false, Raw<14>, true>(g, grp.af, t, grp.shape, lds, shd);
-    } else {
-        group_split<8, false, Raw<8>, true>(g, grp.af, t, grp.shape, lds, shd);
+        group_split<8, false>(g, t, grp.shape, lds, shd);
     }
 }
 
@@ -1098,7 +915,7 @@ mynah_gemv_group_q4k(const GemvGroup grp) {
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
-    group_split<12, false>(grp.d[i], grp.af, t, grp.shape, lds, shd);
+    group_split<12, false>(grp.d[i], t, grp.shape, lds, shd);
 }
 
 // Launches whose every matrix is Q6_K, in the one-lane-per-super-block
@@ -1112,7 +929,7 @@ mynah_gemv_group_q6k(const GemvGroup grp) {
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
-    group_split<14, false, RawQ6Lean>(grp.d[i], grp.af, t, grp.shape, lds, shd);
+    group_split<14, false, RawQ6Lean>(grp.d[i], t, grp.shape, lds, shd);
 }
 
 // The flat layout for launches whose every matrix is Q4_K (up to 512
@@ -1125,7 +942,7 @@ mynah_gemv_flat_q4k(const GemvGroup grp) {
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
-    group_flat<12>(grp.d[i], grp.af, t, lds, shd);
+    group_flat<12>(grp.d[i], t, lds, shd);
 }
 
 extern "C" __global__ void __launch_bounds__(512, 5)
@@ -1136,5 +953,5 @@ mynah_gemv_flat_q6k(const GemvGroup grp) {
     const uint32_t t = blockIdx.x;
     uint32_t i = 0;
     while (i + 1 < grp.n && t >= grp.d[i + 1].tile0) i++;
-    group_flat<14, RawQ6Lean>(grp.d[i], grp.af, t, lds, shd);
+    group_flat<14, RawQ6Lean>(grp.d[i], t, lds, shd);
 }

@@ -434,7 +434,7 @@ static int gemv_flat_plan(const mynah_device *d, mynah_gemv_group *grp, gemv_pla
         tiles += (g->rows + r - 1u) / r;
         const size_t need = ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) +
                              (size_t)r * (ut | 1u) +
-                             (g->norm_w || grp->af.on ? (size_t)g->cols : 0u)) * 4u;
+                             (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
         if (need > lds) lds = need;
         all_q4k = all_q4k && g->type == MYNAH_Q4_K;
         all_q6k = all_q6k && g->type == MYNAH_Q6_K;
@@ -585,7 +585,7 @@ static int gemv_group_plan(const mynah_device *d, mynah_gemv_group *grp, int ord
         /* Q4_0 keeps no unit partials in LDS. */
         const size_t parts = g->type == MYNAH_Q4_0 ? 0u : (size_t)tile_rows * (ut | 1u);
         const size_t need = exact ? ((size_t)g->cols + 4u * ((g->cols + 255u) / 256u) + parts +
-                                     (g->norm_w || grp->af.on ? (size_t)g->cols : 0u)) * 4u
+                                     (g->norm_w ? (size_t)g->cols : 0u)) * 4u
                                   : ((size_t)g->cols + g->cols / 16 + g->cols / 8 +
                                      (g->norm_w ? (size_t)g->cols : 0u)) * 4u;
         if (need > lds) lds = need;
@@ -660,40 +660,10 @@ const char *mynah_hip_gemv_kernel(int type, size_t rows, size_t cols, int order)
     return kernel_names[p.kernel];
 }
 
-/* Launches that mynah_gemv_group_fold can run with attention partials
- * folded into the input: one matrix, the exact split or flat layout of any
- * type but Q4_0, at most 512 threads. */
-static int plan_folds(const gemv_plan *p, const mynah_gemv_group *grp) {
-    const int k = p->kernel;
-    if (k != MYNAH_K_GEMV_GROUP && k != MYNAH_K_GEMV_GROUP_Q4K && k != MYNAH_K_GEMV_GROUP_Q6K &&
-        k != MYNAH_K_GEMV_FLAT_Q4K && k != MYNAH_K_GEMV_FLAT_Q6K)
-        return 0;
-    return grp->n == 1 && grp->d[0].type != MYNAH_Q4_0 && p->threads <= 512u &&
-           grp->d[0].cols <= 8u * p->threads && grp->d[0].cols / 128u <= 4u * (p->threads / 64u);
-}
-
-int mynah_gemv_group_can_fold(mynah_gemv_group *grp, int order) {
-    mynah_device *d = mynah_dev();
-    gemv_plan p;
-    if (d == NULL || gemv_group_plan(d, grp, order, &p) != 0) return -1;
-    return plan_folds(&p, grp);
-}
-
 int mynah_gemv_group_launch(mynah_device *d, mynah_gemv_group *grp, hipStream_t stream,
                             uint32_t *tiles_out, int order) {
     gemv_plan p;
     if (gemv_group_plan(d, grp, order, &p) != 0) return -1;
-    if (grp->af.on) {
-        const mynah_attn_fold *a = &grp->af;
-        if (!plan_folds(&p, grp) || a->nch_max == 0 || a->nch_max > 64u || a->group == 0 ||
-            a->n_heads % a->group != 0 || (uint64_t)a->n_heads * 128u != grp->d[0].cols ||
-            a->spec > a->nch_max || a->n_heads > 4u * (p.threads / 64u) ||
-            grp->d[0].cols > 8u * p.threads) {
-            mynah_set_error("attention fold does not fit this launch");
-            return -1;
-        }
-        p.kernel = MYNAH_K_GEMV_GROUP_FOLD;
-    }
     if (tiles_out) *tiles_out = p.grid;
     if (p.kernel == MYNAH_K_GEMV_STREAM || p.kernel == MYNAH_K_GEMV_STREAM_CVT) {
         void *args[] = {&p.sd};

@@ -36,7 +36,6 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_Q80_GEMM_MV_MFMA, "mynah_q80_gemm_mv_mfma") \
     X(MYNAH_K_GEMM_FOLD, "mynah_gemm_fold")            \
     X(MYNAH_K_GEMV_GROUP, "mynah_gemv_group")          \
-    X(MYNAH_K_GEMV_GROUP_FOLD, "mynah_gemv_group_fold") \
     X(MYNAH_K_GEMV_GROUP_Q6K, "mynah_gemv_group_q6k")  \
     X(MYNAH_K_GEMV_GROUP_Q4K, "mynah_gemv_group_q4k")  \
     X(MYNAH_K_GEMV_FLAT_Q4K, "mynah_gemv_flat_q4k")    \
@@ -181,24 +180,10 @@ typedef struct {
     uint32_t n, wgs, host_tiles, step_log2;
 } mynah_gemv_prefetch;
 
-/* Host mirror of gemv_exact.hip AttnFold: the split attention's partials
- * folded into the input of the launch (on = 1) instead of a combine launch.
- * Requires nch_max <= 64, spec <= nch_max, n_heads * 128 = cols of the one
- * descriptor, n_heads <= 4 * waves and cols <= 8 * threads. */
-typedef struct {
-    const uint32_t *pos;
-    const float *pm;
-    const double *pl;
-    const float *po;
-    uint32_t nch_max, group, n_heads, on;
-    uint32_t spec, pad;       /* chunks live when the launch is enqueued */
-} mynah_attn_fold;
-
 typedef struct {
     uint32_t n, shape;        /* shape: set by the launch */
     mynah_gemv_desc d[MYNAH_GROUP_MAX];
     mynah_gemv_prefetch pf;
-    mynah_attn_fold af;
 } mynah_gemv_group;
 
 /* Fill tile0 and launch. Each desc needs w, x, y, rows, type and (from
@@ -219,9 +204,6 @@ int mynah_gemv_group_threads(mynah_gemv_group *grp, int order, uint32_t *threads
  * array a one-member group with `keys` writes. */
 int mynah_gemv_group_geometry(mynah_gemv_group *grp, int order, uint32_t *threads,
                               uint32_t *grid);
-/* 1 when the launch of grp in `order` runs a kernel that folds attention
- * partials into its input (af), 0 when not, -1 on error. */
-int mynah_gemv_group_can_fold(mynah_gemv_group *grp, int order);
 /* Fill *pf so that a launch carrying it prefetches the weights of `next`
  * (planned in `order`) with wgs workgroups (a multiple of 8), or with one
  * workgroup per bytes_per_wg bytes (rounded up to a multiple of 8, at most

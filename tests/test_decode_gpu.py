@@ -181,45 +181,19 @@ def _split_runs(M, model, shape, k, v, npre, first, steps):
     return logits, toks, lg
 
 
-@pytest.mark.parametrize("shape,npre", [(CF.QWEN3_TINY, 60), (CF.QWEN3_06B, 500)],
-                         ids=["tiny", "0.6B"])
-def test_folded_attention_combine_bit_identical(M, monkeypatch, shape, npre):
-    """Split attention with the chunk partials folded by the output
-    projection's staging (the default while they are cheap to re-read:
-    short contexts) against the separate
-    combine launch (MYNAH_ATTN_FOLD=0): every step's logits bit-identical,
-    stepwise and graph-replayed, across a chunk boundary (the fold forced
-    on whatever the partials cost)."""
-    steps = 12
-    print(f"[case] folded combine d={shape.d_model} npre={npre}", flush=True)
-    model = M.SynthQwen3(shape, 0)
-    k, v = O.kv_prefill(O.substream, shape, 0, npre)
-    first = O.first_token(0, shape.vocab)
-    monkeypatch.setenv("MYNAH_ATTN_FOLD", "1")
-    monkeypatch.setenv("MYNAH_FOLD_MAX_BYTES", str(1 << 40))
-    la, ta, ga = _split_runs(M, model, shape, k, v, npre, first, steps)
-    monkeypatch.setenv("MYNAH_ATTN_FOLD", "0")
-    lb, tb, gb = _split_runs(M, model, shape, k, v, npre, first, steps)
-    for i in range(steps):
-        assert np.array_equal(la[i].view(np.uint32), lb[i].view(np.uint32)), f"step {i}"
-    assert ta == tb
-    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
-
-
 @pytest.mark.parametrize("shape,npre", [(CF.QWEN3_TINY, 60), (CF.QWEN3_06B, 500),
                                         (CF.QWEN3_TINY, 1000)],
                          ids=["tiny", "0.6B", "tiny-32ch"])
 def test_one_wave_combine_bit_identical(M, monkeypatch, shape, npre):
     """The split attention's combine by one wave per query head (up to 32
     chunks, no barrier; the last case has exactly 32) against the four-wave
-    combine (MYNAH_ATTN_COMBINE1=0), the fold off in both: every step's
-    logits bit-identical, stepwise and graph-replayed."""
+    combine (MYNAH_ATTN_COMBINE1=0): every step's logits bit-identical,
+    stepwise and graph-replayed."""
     steps = 12
     print(f"[case] one-wave combine d={shape.d_model} npre={npre}", flush=True)
     model = M.SynthQwen3(shape, 0)
     k, v = O.kv_prefill(O.substream, shape, 0, npre)
     first = O.first_token(0, shape.vocab)
-    monkeypatch.setenv("MYNAH_ATTN_FOLD", "0")
     monkeypatch.setenv("MYNAH_ATTN_COMBINE1", "1")
     la, ta, ga = _split_runs(M, model, shape, k, v, npre, first, steps)
     monkeypatch.setenv("MYNAH_ATTN_COMBINE1", "0")
