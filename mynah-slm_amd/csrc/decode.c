@@ -415,14 +415,15 @@ static long env_or(const char *name, long dflt) {
     return (e != NULL && e[0] != '\0') ? strtol(e, NULL, 10) : dflt;
 }
 
-/* L2 prefetch between the decode GEMVs: each grouped launch of a step
+/* L2 prefetch of the decode GEMVs' weights: each grouped launch of a step
  * carries one workgroup per MYNAH_PREFETCH_BPW bytes (default 8192; 0
- * none), or MYNAH_PREFETCH_WGS workgroups (a multiple of 8), that pull the
- * next GEMV's weights into the L2 of the XCDs that will read them, one byte
- * touched per 2^MYNAH_PREFETCH_STEP bytes (default 7, the L2 line). Next
- * GEMVs above MYNAH_PREFETCH_MAX bytes (default 6 MiB, about what the L2s
- * keep beside the K/V traffic) are not prefetched: measured, 0.6B decode
- * 974 -> 993 tok/s, and the 4B's larger GEMVs lost a little. */
+ * none), or MYNAH_PREFETCH_WGS workgroups (a multiple of 8), that pull a
+ * later GEMV's weights into the L2 of the XCDs that will read them, one
+ * byte touched per 2^MYNAH_PREFETCH_STEP bytes (default 7, the L2 line):
+ * the same GEMV of the next layer when a layer fits the L2s (below), else
+ * the next GEMV, skipping those above MYNAH_PREFETCH_MAX bytes (default
+ * 6 MiB, about what the L2s keep beside the K/V traffic; measured, 0.6B
+ * decode 974 -> 993 tok/s, the 4B's larger GEMVs lost a little). */
 static uint32_t prefetch_wgs(void) {
     const long v = env_or("MYNAH_PREFETCH_WGS", 0);
     return v > 0 && v <= 4096 ? (uint32_t)(v & ~7L) : 0u;
@@ -446,6 +447,18 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
     mynah_gemv_group lg[LG_COUNT], next_qkv;
     int rc = 0;
     for (int k = 0; k < LG_COUNT && rc == 0; k++) rc = layer_group(s, 0, k, &lg[k]);
+    /* Whole layers of at most MYNAH_PREFETCH_LAYER_MAX bytes (default
+     * 16 MiB, half the eight L2s) are prefetched a layer ahead, larger ones
+     * GEMV by GEMV (0.6B: 1,017 -> 1,028 tok/s; at 4B's 67 MB layers a
+     * layer ahead lost 1-2 %). */
+    uint64_t layer_bytes = 0;
+    for (int k = 0; k < LG_COUNT; k++)
+        for (uint32_t i = 0; i < lg[k].n; i++)
+            layer_bytes += (uint64_t)lg[k].d[i].rows * lg[k].d[i].row_bytes *
+                           (lg[k].d[i].w2 ? 2u : 1u);
+    const long pf_lmax = env_or("MYNAH_PREFETCH_LAYER_MAX", 16L << 20);
+    const int pf_ahead = (pf_wgs || pf_b) && c->n_layers > 1 && pf_lmax > 0 &&
+                         layer_bytes <= (uint64_t)pf_lmax;
     for (uint32_t l = 0; l < c->n_layers && rc == 0; l++) {
         const dlayer *L = &s->layers[l];
         float *kl = s->k_cache + l * per_layer, *vl = s->v_cache + l * per_layer;
@@ -455,7 +468,18 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             for (int k = LG_O; k < LG_COUNT && rc == 0; k++) rc = layer_group(s, l, k, &lg[k]);
         }
         if (rc == 0 && more) rc = layer_group(s, l + 1, LG_QKV, &next_qkv);
-        for (int k = 0; k < LG_COUNT && rc == 0 && (pf_wgs || pf_b); k++) {
+        if (pf_ahead && more) {
+            /* A layer ahead: each launch fetches the same launch of the next
+             * layer, whose weights then wait in the L2s for a whole layer. */
+            for (int k = 0; k < LG_COUNT && rc == 0; k++) {
+                mynah_gemv_group nxl;
+                rc = k == LG_QKV ? 0 : layer_group(s, l + 1, k, &nxl);
+                if (rc == 0)
+                    rc = mynah_gemv_prefetch_plan(k == LG_QKV ? &next_qkv : &nxl, -1, pf_wgs,
+                                                  pf_b, UINT64_MAX, pf_step, &lg[k].pf);
+            }
+        }
+        for (int k = 0; k < LG_COUNT && rc == 0 && !pf_ahead && (pf_wgs || pf_b); k++) {
             const mynah_gemv_group *nx = k + 1 < LG_COUNT ? &lg[k + 1] : more ? &next_qkv : NULL;
             if (nx) rc = mynah_gemv_prefetch_plan(nx, -1, pf_wgs, pf_b, pf_m, pf_step, &lg[k].pf);
         }

@@ -205,15 +205,19 @@ def test_one_wave_combine_bit_identical(M, monkeypatch, shape, npre):
 
 
 @pytest.mark.parametrize("env", [{"MYNAH_PREFETCH_WGS": "128", "MYNAH_PREFETCH_BPW": "0"},
-                                 {"MYNAH_PREFETCH_BPW": "8192", "MYNAH_PREFETCH_MAX": "0"},
-                                 {"MYNAH_PREFETCH_BPW": "1024", "MYNAH_PREFETCH_STEP": "6"}],
-                         ids=["wgs128", "bpw8192_all", "bpw1024_step64"])
+                                 {"MYNAH_PREFETCH_BPW": "8192"},
+                                 {"MYNAH_PREFETCH_BPW": "1024", "MYNAH_PREFETCH_STEP": "6"},
+                                 {"MYNAH_PREFETCH_BPW": "8192", "MYNAH_PREFETCH_MAX": "0",
+                                  "MYNAH_PREFETCH_LAYER_MAX": "0"}],
+                         ids=["ahead_wgs128", "ahead_bpw8192", "ahead_bpw1024_step64",
+                              "next_bpw8192_all"])
 def test_prefetching_decoder_bit_identical(M, monkeypatch, env):
-    """Decode GEMVs carrying workgroups that prefetch the next GEMV's weights
-    into L2 (every next GEMV prefetched, by workgroup count or bytes per
-    workgroup): logits and ids bit-identical to the decoder without them
-    (MYNAH_PREFETCH_BPW=0; 0.6B, split attention, stepwise and
-    graph-replayed)."""
+    """Decode GEMVs carrying workgroups that prefetch weights into L2 — the
+    same GEMV of the next layer (the 0.6B default: its layers fit the L2s)
+    or, with MYNAH_PREFETCH_LAYER_MAX=0, the next GEMV (every one, no size
+    cap) — by workgroup count or bytes per workgroup: logits and ids
+    bit-identical to the decoder without them (MYNAH_PREFETCH_BPW=0; 0.6B,
+    split attention, stepwise and graph-replayed)."""
     shape, npre, steps = CF.QWEN3_06B, 100, 8
     print(f"[case] prefetch {env}", flush=True)
     model = M.SynthQwen3(shape, 0)
