@@ -53,6 +53,7 @@ struct mynah_qwen3 {
     dtensor embed, out_norm, head;
     dlayer *layers;
     float *k_cache, *v_cache, *rope_cos, *rope_sin;
+    float *rope_now;          /* cos | sin of the position the next step writes (2 x hd / 2) */
     float *x, *q, *attn, *act, *logits, *scores;
     uint32_t *counters;             /* token, pos, step, forced-token count */
     uint32_t *forced;               /* prompt tokens replayed before greedy steps */
@@ -168,7 +169,8 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
         if (s->exec[v]) (void)hipGraphExecDestroy(s->exec[v]);
         if (s->graph[v]) (void)hipGraphDestroy(s->graph[v]);
     }
-    void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->x, s->q,
+    void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->rope_now,
+                    s->x, s->q,
                     s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->forced, s->pm, s->pl,
                     s->po, s->pf_x, s->pf_xn, s->pf_q, s->pf_att, s->pf_g, s->pf_u, s->pf_s,
                     s->pf_tok};
@@ -287,6 +289,7 @@ mynah_qwen3 *mynah_qwen3_new_parts(const mynah_qwen3_shape *c, const mynah_synth
     s->v_cache = (float *)dalloc(kv * 4, &ok);
     s->rope_cos = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
     s->rope_sin = (float *)dalloc((size_t)n_ctx * half * 4, &ok);
+    s->rope_now = (float *)dalloc(2 * half * 4, &ok);
     s->x = (float *)dalloc(dm * 4, &ok);
     s->q = (float *)dalloc((size_t)s->q_dim * 4, &ok);
     s->attn = (float *)dalloc((size_t)s->q_dim * 4, &ok);
@@ -489,7 +492,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
         if (s->attn_mode == MYNAH_ATTN_SPLIT) {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;
-            const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+            const float *rnow = s->rope_now;
             float *pm = s->pm, *po = s->po, *out = s->attn;
             double *pl = s->pl;
             uint32_t nchm = s->nch_max, kvd = s->kv_dim;
@@ -501,7 +504,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             uint32_t nctx = s->n_ctx;
             uint32_t spec = (s->n_past + MYNAH_AS_CH) / MYNAH_AS_CH;
             if (spec > nchm) spec = nchm;
-            void *args[] = {&q, &kl, &vl, &qn, &kn, &rcos, &rsin, &pos, &pm, &pl, &po, &nchm, &kvd,
+            void *args[] = {&q, &kl, &vl, &qn, &kn, &rnow, &pos, &pm, &pl, &po, &nchm, &kvd,
                             &group, &eps, &scale, &nctx, &spec};
             rc = mynah_launch(d, MYNAH_K_ATTN_SPLIT, c->n_kv_heads, s->nch_max, 128 * group, 0, st,
                               args);
@@ -574,8 +577,10 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
         uint32_t dm = c->d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
         const uint32_t *forced = s->forced, *nforced = NFORCED(s);
         uint32_t vocab = c->vocab;
+        const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+        float *rnow = s->rope_now;
         void *args[] = {&keys, &n, &tok, &toks, &pos, &step, &maxs, &tab, &x, &dm, &ty, &rb,
-                        &forced, &nforced, &vocab};
+                        &forced, &nforced, &vocab, &rcos, &rsin, &rnow};
         rc = mynah_launch(d, MYNAH_K_ARGMAX, 1, 1, 1024, 0, st, args);
     }
     return rc;
@@ -588,7 +593,11 @@ static int embed_current(mynah_qwen3 *s, mynah_device *d) {
     uint32_t *tok = TOKEN(s);
     float *x = s->x;
     uint32_t dm = s->c.d_model, ty = (uint32_t)s->embed.type, rb = (uint32_t)s->embed.row_bytes;
-    void *args[] = {&tab, &tok, &x, &dm, &ty, &rb};
+    const uint32_t *pos = POS(s);
+    const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+    float *rnow = s->rope_now;
+    uint32_t nctx = s->n_ctx;
+    void *args[] = {&tab, &tok, &x, &dm, &ty, &rb, &pos, &rcos, &rsin, &rnow, &nctx};
     return mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, d->stream, args);
 }
 

@@ -454,8 +454,8 @@ MYNAH_DEV void norm_rope_reg(float x0, float x1, float w0, float w1, float c, fl
 extern "C" __global__ void __launch_bounds__(1024)
 mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                  const float *__restrict__ v_layer, const float *__restrict__ q_norm,
-                 const float *__restrict__ k_norm, const float *__restrict__ rope_cos,
-                 const float *__restrict__ rope_sin, const uint32_t *__restrict__ pos_ptr,
+                 const float *__restrict__ k_norm, const float *__restrict__ rope_now,
+                 const uint32_t *__restrict__ pos_ptr,
                  float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po,
                  uint32_t nch_max, uint32_t kv_dim, uint32_t group, float eps, float scale,
                  uint32_t n_ctx, uint32_t spec_chunks) {
@@ -500,8 +500,9 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                     ? *(const float4 *)(v_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + 4u * q4)
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    // The query heads and their norm weights do not depend on the position
-    // either.
+    // The query heads, their norm weights and the rotation of the position
+    // (rope_now: its cos and sin rows, copied there by the launch that set
+    // the position) do not depend on the position's value either.
     const bool qwave = wave < group;
     float x0 = 0.0f, x1 = 0.0f, w0 = 0.0f, w1 = 0.0f, cs = 0.0f, sn = 0.0f;
     if (qwave) {
@@ -510,6 +511,10 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         x1 = src[lane + 64u];
         w0 = q_norm[lane];
         w1 = q_norm[lane + 64u];
+    }
+    if (wave <= group) {
+        cs = rope_now[lane];
+        sn = rope_now[64u + lane];
     }
     if (t0 >= n_kv) return;       // a speculative chunk past the position (after a reset)
     const bool has_pos = pos < t0 + AS_CH;
@@ -525,10 +530,6 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         x1 = kpos[lane + 64u];
         w0 = k_norm[lane];
         w1 = k_norm[lane + 64u];
-    }
-    if (qwave || kwave) {
-        cs = rope_cos[(size_t)pos * 64u + lane];
-        sn = rope_sin[(size_t)pos * 64u + lane];
     }
 #pragma unroll
     for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
@@ -930,9 +931,18 @@ mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_key
                      uint32_t *__restrict__ pos, uint32_t *__restrict__ step, uint32_t max_steps,
                      const uint8_t *__restrict__ table, float *__restrict__ x, uint32_t d,
                      uint32_t type, uint32_t row_bytes, const uint32_t *__restrict__ forced,
-                     const uint32_t *__restrict__ n_forced, uint32_t vocab) {
+                     const uint32_t *__restrict__ n_forced, uint32_t vocab,
+                     const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
+                     float *__restrict__ rope_now) {
     __shared__ unsigned long long wk[16];
-    __shared__ uint32_t sidx;
+    __shared__ uint32_t sidx, spos;
+    // The counters go out with the keys.
+    uint32_t s = 0, nf = 0, p = 0;
+    if (threadIdx.x == 0) {
+        s = step[0];
+        nf = n_forced[0];
+        p = pos[0];
+    }
     unsigned long long best = 0ull;
     for (uint32_t i = threadIdx.x; i < n_keys; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
     best = wave_max_u64(best);
@@ -941,17 +951,23 @@ mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_key
     if (threadIdx.x == 0) {
         for (uint32_t k = 1; k < (blockDim.x + 63u) / 64u; k++) best = wk[k] > best ? wk[k] : best;
         const uint32_t idx = ~(uint32_t)(best & 0xffffffffull);
-        const uint32_t s = step[0];
-        uint32_t next = s + 1u < n_forced[0] ? forced[s + 1u] : idx;
+        uint32_t next = s + 1u < nf ? forced[s + 1u] : idx;
         if (next >= vocab) next = 0u;       // no keys (a prefill step) and nothing forced
         token[0] = next;
         if (s < max_steps) tokens[s] = idx;
         step[0] = s + 1u;
-        pos[0] = pos[0] + 1u;
+        pos[0] = p + 1u;
         sidx = next;
+        spos = p + 1u;
     }
     __syncthreads();
-    const uint32_t idx = sidx;
+    const uint32_t idx = sidx, np = spos;
+    // The rotation of the next position for the next step's attention
+    // (max_steps = the context length = the rope tables' rows).
+    if (threadIdx.x < 64u && np < max_steps) {
+        rope_now[threadIdx.x] = rope_cos[(size_t)np * 64u + threadIdx.x];
+        rope_now[64u + threadIdx.x] = rope_sin[(size_t)np * 64u + threadIdx.x];
+    }
     for (uint32_t c = threadIdx.x; c < d / 32u; c += blockDim.x) embed_group(table, idx, x, c, type, row_bytes);
 }
 
@@ -960,8 +976,18 @@ mynah_argmax_advance(const unsigned long long *__restrict__ keys, uint32_t n_key
 // 32 values.
 extern "C" __global__ void __launch_bounds__(DEC_WG)
 mynah_embed_row(const uint8_t *__restrict__ table, const uint32_t *__restrict__ token_ptr,
-                float *__restrict__ x, uint32_t d, uint32_t type, uint32_t row_bytes) {
+                float *__restrict__ x, uint32_t d, uint32_t type, uint32_t row_bytes,
+                const uint32_t *__restrict__ pos_ptr, const float *__restrict__ rope_cos,
+                const float *__restrict__ rope_sin, float *__restrict__ rope_now, uint32_t n_ctx) {
     const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;   // 32-value group
+    // The rotation of the current position, for the split attention.
+    if (c < 64u) {
+        const uint32_t p = pos_ptr[0];
+        if (p < n_ctx) {
+            rope_now[c] = rope_cos[(size_t)p * 64u + c];
+            rope_now[64u + c] = rope_sin[(size_t)p * 64u + c];
+        }
+    }
     if (c >= d / 32u) return;
     embed_group(table, token_ptr[0], x, c, type, row_bytes);
 }
