@@ -511,7 +511,10 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             if (rc) break;
             const float *cpm = pm, *cpo = po;
             const double *cpl = pl;
-            void *args2[] = {&pos, &cpm, &cpl, &cpo, &out, &nchm, &group};
+            /* The four-wave combine finds M and L in wave 0 up to 128 chunks
+             * (MYNAH_COMBINE_WAVE0=0: never; same bits). */
+            uint32_t w0max = env_or("MYNAH_COMBINE_WAVE0", 1) != 0 ? 128u : 0u;
+            void *args2[] = {&pos, &cpm, &cpl, &cpo, &out, &nchm, &group, &w0max};
             /* Up to MYNAH_AC1_MAX chunks one wave per query head combines
              * (no barrier), past that four (MYNAH_ATTN_COMBINE1=0: always
              * four); same bits. */

@@ -615,9 +615,9 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
 // Thread c (and c + 256, ...) takes chunk c's max and exp sum: M = max m_c,
 // w_c = expf(m_c - M) (kept in LDS), L = sum_c w_c l_c in double (each
 // wave's share, then the four shares in wave order); inv = (float)(1 / L).
-// Up to 64 chunks all of them sit in wave 0, which computes M and L alone
-// (same values: the other waves contribute -inf and 0.0), one barrier
-// fewer. Wave w then sums o_w = fma(w_c * inv, o_c, o_w) over its chunks c = w,
+// Up to 128 chunks wave 0 computes M and L alone (lane l holding chunks l
+// and 64 + l; same values: its two double sums are the first two waves'
+// sums, the others contribute -inf and 0.0), one barrier fewer. Wave w then sums o_w = fma(w_c * inv, o_c, o_w) over its chunks c = w,
 // w + 4, ... in order, lane l holding dimensions l and l + 64, and the four
 // partial vectors are added in wave order. The first AC_PRE chunks of every
 // wave are loaded before the position arrives (every slot below nch_max is
@@ -628,7 +628,7 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
 extern "C" __global__ void __launch_bounds__(256)
 mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                    const double *__restrict__ pl, const float *__restrict__ po,
-                   float *__restrict__ out, uint32_t nch_max, uint32_t group) {
+                   float *__restrict__ out, uint32_t nch_max, uint32_t group, uint32_t wave0_max) {
 #pragma clang fp contract(off)
     extern __shared__ float wsc[];
     __shared__ float smax[AC_WAVES];
@@ -650,23 +650,35 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
     // Chunk tid's max and exp sum, also in flight before the position.
     const float pm0 = tid < nch_max ? pm[base + (size_t)tid * group] : 0.0f;
     const double pl0 = tid < nch_max ? pl[base + (size_t)tid * group] : 0.0;
+    // Wave 0 also holds chunk 64 + lane for the max and sum.
+    const uint32_t c1 = 64u + lane;
+    const float pm1 = wave == 0u && c1 < nch_max ? pm[base + (size_t)c1 * group] : 0.0f;
+    const double pl1 = wave == 0u && c1 < nch_max ? pl[base + (size_t)c1 * group] : 0.0;
     const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
     float inv;
-    if (nch <= 64u) {
-        // Every chunk is in wave 0: it alone finds M and L, the other waves'
-        // maxima being -inf and their double sums 0 (added all the same).
+    if (nch <= wave0_max) {          // wave0_max <= 128
+        // Wave 0 alone finds M and L: lane l holds chunks l and 64 + l, whose
+        // double sums are the combine's first two wave sums (the other
+        // waves' maxima being -inf and their sums 0, added all the same).
         if (wave == 0u) {
             float m = -__builtin_inff();
             if (lane < nch) m = fmaxf(m, pm0);
+            if (64u + lane < nch) m = fmaxf(m, pm1);
             const float M = wave_max_dpp(m);
-            double l = 0.0;
+            double l = 0.0, l1 = 0.0;
             if (lane < nch) {
                 const float w = mynah_expf(pm0 - M);
                 wsc[lane] = w;
                 l += (double)w * pl0;
             }
+            if (64u + lane < nch) {
+                const float w = mynah_expf(pm1 - M);
+                wsc[64u + lane] = w;
+                l1 += (double)w * pl1;
+            }
             l = wave_sum_d(l);
-            if (lane == 0) sinv = (float)(1.0 / (((l + 0.0) + 0.0) + 0.0));
+            l1 = wave_sum_d(l1);
+            if (lane == 0) sinv = (float)(1.0 / (((l + l1) + 0.0) + 0.0));
         }
         __syncthreads();
         inv = sinv;

@@ -204,6 +204,28 @@ def test_one_wave_combine_bit_identical(M, monkeypatch, shape, npre):
     assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
 
 
+@pytest.mark.parametrize("npre", [1500, 2105], ids=["48ch", "67ch"])
+def test_four_wave_combine_wave0_sums_bit_identical(M, monkeypatch, npre):
+    """The four-wave combine (past 32 chunks) finding the maximum and the
+    double sum in wave 0 alone — up to 128 chunks, two per lane from the
+    65th — against its all-waves form (MYNAH_COMBINE_WAVE0=0): every step's
+    logits bit-identical, stepwise and graph-replayed, at 48 chunks and
+    across the 67th chunk's boundary (tiny model)."""
+    shape, steps = CF.QWEN3_TINY, 12
+    print(f"[case] wave-0 combine sums npre={npre}", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    monkeypatch.setenv("MYNAH_COMBINE_WAVE0", "1")
+    la, ta, ga = _split_runs(M, model, shape, k, v, npre, first, steps)
+    monkeypatch.setenv("MYNAH_COMBINE_WAVE0", "0")
+    lb, tb, gb = _split_runs(M, model, shape, k, v, npre, first, steps)
+    for i in range(steps):
+        assert np.array_equal(la[i].view(np.uint32), lb[i].view(np.uint32)), f"step {i}"
+    assert ta == tb
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
+
+
 @pytest.mark.parametrize("env", [{"MYNAH_PREFETCH_WGS": "128", "MYNAH_PREFETCH_BPW": "0"},
                                  {"MYNAH_PREFETCH_BPW": "8192"},
                                  {"MYNAH_PREFETCH_BPW": "1024", "MYNAH_PREFETCH_STEP": "6"},
