@@ -1187,7 +1187,16 @@ MYNAH_DEV void prefill_pv_tile(const float *__restrict__ v_layer, const float *_
     // 4 (f % 32); rows past n_end read row 0 (never used). Probability fetch
     // role: entry i = tid + 512 k of the chunk's PV_Q G x PV_CH (pair i /
     // PV_CH, position i % PV_CH), 0 past the pair's query or past npair.
-    float4 vr[4];
+    // Four named registers rather than an array: an array of float4 written
+    // through the compile-time loop stays in private memory.
+    float4 vr0, vr1, vr2, vr3;
+    auto vr = [&](auto K) -> float4 & {
+        constexpr uint32_t k = decltype(K)::value;
+        if constexpr (k == 0) return vr0;
+        else if constexpr (k == 1) return vr1;
+        else if constexpr (k == 2) return vr2;
+        else return vr3;
+    };
     float pr_r[NPR];
     float o[NPT];
     static_for<NPT>([&](auto K) { o[decltype(K)::value] = 0.0f; });
@@ -1196,7 +1205,7 @@ MYNAH_DEV void prefill_pv_tile(const float *__restrict__ v_layer, const float *_
             static_for<4>([&](auto K) {
                 constexpr uint32_t k = decltype(K)::value;
                 const uint32_t f = tid + 512u * k, r = f >> 5;
-                vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
+                vr(K) = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
             });
             static_for<NPR>([&](auto K) {
                 constexpr uint32_t k = decltype(K)::value;
@@ -1211,7 +1220,7 @@ MYNAH_DEV void prefill_pv_tile(const float *__restrict__ v_layer, const float *_
         static_for<4>([&](auto K) {
             constexpr uint32_t k = decltype(K)::value;
             const uint32_t f = tid + 512u * k;
-            *(float4 *)&vl[f >> 5][4u * (f & 31u)] = vr[k];
+            *(float4 *)&vl[f >> 5][4u * (f & 31u)] = vr(K);
         });
         static_for<NPR>([&](auto K) {
             constexpr uint32_t k = decltype(K)::value;
@@ -1224,7 +1233,7 @@ MYNAH_DEV void prefill_pv_tile(const float *__restrict__ v_layer, const float *_
             static_for<4>([&](auto K) {
                 constexpr uint32_t k = decltype(K)::value;
                 const uint32_t f = tid + 512u * k, r = t1 + (f >> 5);
-                vr[k] = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
+                vr(K) = *(const float4 *)(vbase + (size_t)(r < n_end ? r : 0u) * kv_dim + 4u * (f & 31u));
             });
             static_for<NPR>([&](auto K) {
                 constexpr uint32_t k = decltype(K)::value;
