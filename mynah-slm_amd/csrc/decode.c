@@ -827,8 +827,9 @@ static int enqueue_prefill_chunk(mynah_qwen3 *s, mynah_device *d, hipStream_t st
             uint32_t sstride = s->sstride, kvd = s->kv_dim, grp = group;
             uint32_t tt = T;
             void *args[] = {&qn, &kc, &sc, &p0, &tt, &sstride, &kvd, &grp, &scale};
-            rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 63) / 64,
-                               (T + 7) / 8, 256, 0, st, args);
+            /* 256 positions by 16 queries per workgroup, the queries in LDS */
+            rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 255) / 256,
+                               (T + 15) / 16, 256, (size_t)16 * group * 512, st, args);
             if (rc) break;
             void *args2[] = {&sc, &p0, &sstride};
             rc = mynah_launch(d, MYNAH_K_PREFILL_SOFTMAX, T, c->n_heads, 64, 0, st, args2);

@@ -1086,63 +1086,73 @@ mynah_prefill_rope(float *__restrict__ q, float *__restrict__ k_layer,
 }
 
 // Scores of PS_Q consecutive query rows q0 .. q0 + PS_Q - 1 (positions
-// p0 + q0 + i) against a chunk of PS_POS positions, with the dot of the
-// decode kernel (attn_scores_body): lane (r, l) of wave w holds
-// k_t[16 j + l] of positions t = t0 + 16 w + 4 i + r (i < 4), accumulates
-// fma(q[16 j + l], k_t[16 j + l]) over j and the 16 lanes combine in the
-// reference's AVX2 order (row16_dot). The K rows are loaded once for the
-// tile; a query scores only positions up to its own. Grid (n_kv_heads,
+// p0 + q0 + i) against a chunk of PS_POS positions, each lane one position:
+// lane l of wave w holds the whole key row of position t = t0 + 64 w + l in
+// registers and computes, for every (query, head) pair of the tile, the
+// reference's AVX2 dot (src/kernels.c:39-62) in its own registers: the 16
+// FMA chains a[i] = fma(q[16 j + i], k_t[16 j + i], a[i]) over j = 0..7 (a[i]
+// is s0[i] for i < 8, s1[i - 8] otherwise), then tt[i] = a[i] + a[i + 8],
+// v[i] = tt[i] + tt[i + 4], dot = (v0 + v1) + (v2 + v3) -- the operations of
+// the decode kernel's 16-lane form (row16_dot), bit for bit. The query
+// values are wave-uniform LDS reads; the scores of a wave are 64 consecutive
+// floats. A query scores only positions up to its own. Grid (n_kv_heads,
 // ceil((p0 + T) / PS_POS), ceil(T / PS_Q)), block 256; group <= 8.
-#define PS_Q 8
-#define PS_POS 64
+#define PS_Q 16
+#define PS_POS 256
 extern "C" __global__ void __launch_bounds__(256)
 mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_layer,
                      float *__restrict__ scores, uint32_t p0, uint32_t T, uint32_t sstride,
                      uint32_t kv_dim, uint32_t group, float scale) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float ql[PS_Q][8][128];
+    // Queries of the tile, [query][head][128]: PS_Q * group * 512 bytes of
+    // dynamic LDS.
+    extern __shared__ __attribute__((aligned(16))) float ql[];
     const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * PS_POS, q0 = blockIdx.z * PS_Q;
     const uint32_t nq = T - q0 < PS_Q ? T - q0 : PS_Q;
     const uint32_t last = p0 + q0 + nq - 1u;          // position of the tile's last query
     if (t0 > last) return;
     const uint32_t n_heads = gridDim.x * group, q_dim = n_heads * 128u;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t r = lane >> 4, l = lane & 15u;
-    uint32_t tp[4];
-    float kv[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        tp[i] = t0 + 16u * wave + 4u * (uint32_t)i + r;
-        const float *krow =
-            k_layer + (size_t)(tp[i] <= last ? tp[i] : 0u) * kv_dim + (size_t)kvh * 128u + l;
-#pragma unroll
-        for (int j = 0; j < 8; j++) kv[i][j] = krow[16 * j];
-    }
-    // Query values stored lane-major: ql[qi][h][8 l + j] = q[16 j + l], so a
-    // lane's eight values are two float4.
-    for (uint32_t i = threadIdx.x; i < nq * group * 128u; i += blockDim.x) {
-        const uint32_t qi = i / (group * 128u), rem = i % (group * 128u), e = rem & 127u;
-        ql[qi][rem >> 7][8u * (e & 15u) + (e >> 4)] =
-            qn[(size_t)(q0 + qi) * q_dim + (size_t)kvh * group * 128u + rem];
+    const uint32_t tw = t0 + 64u * wave, t = tw + lane;
+    // Rows past the tile's last query read row 0 (finite, never stored).
+    const float4 *krow = (const float4 *)(k_layer + (size_t)(t <= last ? t : 0u) * kv_dim +
+                                          (size_t)kvh * 128u);
+    float4 k4[32];
+    static_for<32>([&](auto I) { k4[decltype(I)::value] = krow[decltype(I)::value]; });
+    for (uint32_t i = threadIdx.x; i < nq * group * 32u; i += blockDim.x) {
+        const uint32_t qi = i / (group * 32u), rem = i % (group * 32u);
+        *(float4 *)&ql[(qi * group + (rem >> 5)) * 128u + 4u * (rem & 31u)] =
+            *(const float4 *)&qn[(size_t)(q0 + qi) * q_dim + (size_t)kvh * group * 128u + 4u * rem];
     }
     __syncthreads();
     for (uint32_t qi = 0; qi < nq; qi++) {
         const uint32_t pos = p0 + q0 + qi;
-        if (t0 + 16u * wave > pos) continue;            // wave-uniform
+        if (tw > pos) continue;                         // wave-uniform
         float *srow = scores + (size_t)(q0 + qi) * n_heads * sstride;
         for (uint32_t h = 0; h < group; h++) {
-            const float4 qa = *(const float4 *)&ql[qi][h][8u * l];
-            const float4 qb = *(const float4 *)&ql[qi][h][8u * l + 4u];
-            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-            float* hrow = srow + (size_t)(kvh * group + h) * sstride;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qv[j], kv[i][j], acc);
-                const float dot = row16_dot(acc);
-                if (l == 0 && tp[i] <= pos) hrow[tp[i]] = dot * scale;
-            }
+            const float4 *qh = (const float4 *)&ql[(qi * group + h) * 128u];
+            float a[16];
+            static_for<16>([&](auto I) { a[decltype(I)::value] = 0.0f; });
+            static_for<8>([&](auto J) {
+                constexpr uint32_t j = decltype(J)::value;
+                static_for<4>([&](auto M) {
+                    constexpr uint32_t m = decltype(M)::value;
+                    const float4 qv = qh[4u * j + m], kv = k4[4u * j + m];
+                    a[4u * m + 0u] = __builtin_fmaf(qv.x, kv.x, a[4u * m + 0u]);
+                    a[4u * m + 1u] = __builtin_fmaf(qv.y, kv.y, a[4u * m + 1u]);
+                    a[4u * m + 2u] = __builtin_fmaf(qv.z, kv.z, a[4u * m + 2u]);
+                    a[4u * m + 3u] = __builtin_fmaf(qv.w, kv.w, a[4u * m + 3u]);
+                });
+            });
+            float tt[8];
+            static_for<8>([&](auto I) {
+                constexpr uint32_t i = decltype(I)::value;
+                tt[i] = a[i] + a[i + 8u];
+            });
+            const float v0 = tt[0] + tt[4], v1 = tt[1] + tt[5], v2 = tt[2] + tt[6],
+                        v3 = tt[3] + tt[7];
+            const float dot = (v0 + v1) + (v2 + v3);
+            if (t <= pos) srow[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
         }
     }
 }
