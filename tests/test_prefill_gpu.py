@@ -134,6 +134,20 @@ def test_prefill_equals_steps_every_group(M, chunk, group):
     assert_same_state(a, b, int(prompt[2]))
 
 
+def test_prefill_after_cache_crosses_score_tiles(M, chunk):
+    """Group 8 (the scores tile's largest query block in LDS), prefill of
+    100 tokens from position 200 of a synthetic cache: the queries' rows
+    cross the 256-position score tiles, and the last 16-query tile holds 4."""
+    chunk(100)
+    shape = CF.Qwen3Shape(2, 512, 768, 16, 2, 128, 4096)
+    print("[case] prefill group=8 from position 200", flush=True)
+    model = M.SynthQwen3(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, 200)
+    prompt = M.synth_uniform(M.substream(7, 6), 100, shape.vocab)
+    a, b = fill_both(M, model, prompt, 320, kv=(k, v, 200))
+    assert_same_state(a, b, int(prompt[4]))
+
+
 def test_qwen3_06b_prefill_equals_steps(M):
     shape = CF.QWEN3_06B
     print("[case] Qwen3-0.6B prefill of 100 tokens", flush=True)
