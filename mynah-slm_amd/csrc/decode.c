@@ -831,8 +831,9 @@ static int enqueue_prefill_chunk(mynah_qwen3 *s, mynah_device *d, hipStream_t st
             rc = mynah_launch3(d, MYNAH_K_PREFILL_SCORES, c->n_kv_heads, (p0 + T + 255) / 256,
                                (T + 15) / 16, 256, (size_t)16 * group * 512, st, args);
             if (rc) break;
-            void *args2[] = {&sc, &p0, &sstride};
-            rc = mynah_launch(d, MYNAH_K_PREFILL_SOFTMAX, T, c->n_heads, 64, 0, st, args2);
+            uint32_t nh = c->n_heads;
+            void *args2[] = {&sc, &p0, &sstride, &nh};
+            rc = mynah_launch(d, MYNAH_K_PREFILL_SOFTMAX, T, (nh + 3) / 4, 256, 0, st, args2);
             if (rc) break;
             const float *vc = vl, *pr = s->pf_s;
             float *out = s->pf_att;

@@ -1157,11 +1157,14 @@ mynah_prefill_scores(const float *__restrict__ qn, const float *__restrict__ k_l
     }
 }
 
-// Softmax of query row t = blockIdx.x, head blockIdx.y (positions 0 ..
-// p0 + t), written back over its scores: grid (T, n_heads), one wave.
-extern "C" __global__ void __launch_bounds__(64)
-mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride) {
-    float *row = scores + ((size_t)blockIdx.x * gridDim.y + blockIdx.y) * sstride;
+// Softmax of query row t = blockIdx.x, head 4 blockIdx.y + wave (positions
+// 0 .. p0 + t), written back over its scores: grid (T, ceil(n_heads / 4)),
+// four waves, one row each.
+extern "C" __global__ void __launch_bounds__(256)
+mynah_prefill_softmax(float *scores, uint32_t p0, uint32_t sstride, uint32_t n_heads) {
+    const uint32_t h = blockIdx.y * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (h >= n_heads) return;
+    float *row = scores + ((size_t)blockIdx.x * n_heads + h) * sstride;
     softmax_any(row, p0 + blockIdx.x + 1u, row);
 }
 
