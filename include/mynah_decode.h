@@ -66,6 +66,10 @@ int mynah_hip_qwen3_set_kv(mynah_qwen3 *s, const float *k, const float *v, uint3
 int mynah_hip_qwen3_get_kv(const mynah_qwen3 *s, float *k, float *v, uint32_t n_pos);
 
 uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s);
+/* Test hook, no reference counterpart: the attention output of the last
+ * layer of the most recent step (n_heads * head_dim floats, the `out` of
+ * src/kernels.c:228-250 for that layer), into host memory. */
+int mynah_hip_qwen3_read_attn(const mynah_qwen3 *s, float *out);
 /* src/generate.c:13-86 with greedy sampling: the prompt's tokens fill the
  * cache (all but the last without logits, the head is skipped), then
  * n_steps greedy steps start from the last prompt token; tokens_out gets the

@@ -432,6 +432,19 @@ static uint32_t prefetch_wgs(void) {
     return v > 0 && v <= 4096 ? (uint32_t)(v & ~7L) : 0u;
 }
 
+/* The exact attention's PV kernel for this state, or -1 for the eight-lane
+ * kernels (MYNAH_ATTN_PV=0, or head_dim other than 128). Up to 4096
+ * positions the softmax runs inside it, with 1024 scores per float4 column
+ * of its four loader waves (1 to 4 columns by n_ctx); longer contexts read
+ * the probabilities from the scores rows, normalised in place first. */
+static int pv_kernel(const mynah_qwen3 *s) {
+    if (env_or("MYNAH_ATTN_PV", 1) == 0 || s->c.head_dim != 128) return -1;
+    if (s->n_ctx > 4096) return MYNAH_K_ATTN_PV_M;
+    static const int by_cols[4] = {MYNAH_K_ATTN_PV_1, MYNAH_K_ATTN_PV_2, MYNAH_K_ATTN_PV_3,
+                                   MYNAH_K_ATTN_PV_4};
+    return by_cols[(s->n_ctx - 1u) / 1024u];
+}
+
 static uint32_t prefetch_step(void) {
     const long v = env_or("MYNAH_PREFETCH_STEP", 7);
     return v >= 2 && v <= 12 ? (uint32_t)v : 7u;
@@ -539,7 +552,19 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             float *out = s->attn;
             const float *scc = s->scores;
             void *args2[] = {&vl, &scc, &pos, &out, &sstride, &kvd, &group};
-            if ((size_t)group * sstride * 4 <= EXACT_LDS_SCORES) {
+            const int pv = pv_kernel(s);
+            if (pv >= 0) {
+                /* A PV chain in every lane (MYNAH_ATTN_PV=0: the eight-lane
+                 * kernels below; same bits). */
+                uint32_t nkv = c->n_kv_heads;
+                void *args3[] = {&vl, &scc, &pos, &out, &sstride, &kvd, &nkv, &group};
+                if (pv == MYNAH_K_ATTN_PV_M) {
+                    void *args1[] = {&sc, &pos, &sstride};
+                    rc = mynah_launch(d, MYNAH_K_ATTN_SOFTMAX, c->n_heads, 1, 64, 0, st, args1);
+                }
+                rc = rc ? rc : mynah_launch(d, pv, c->n_heads * (128u / MYNAH_PV_SW), 1, 320, 0,
+                                            st, args3);
+            } else if ((size_t)group * sstride * 4 <= EXACT_LDS_SCORES) {
                 rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, 64 * group,
                                   (size_t)group * sstride * 4, st, args2);
             } else {
@@ -1254,6 +1279,21 @@ int mynah_hip_qwen3_get_kv(const mynah_qwen3 *s, float *k, float *v, uint32_t n_
 }
 
 uint32_t mynah_hip_qwen3_n_past(const mynah_qwen3 *s) { return s ? s->n_past : 0; }
+
+int mynah_hip_qwen3_read_attn(const mynah_qwen3 *s, float *out) {
+    if (s == NULL || out == NULL) {
+        mynah_set_error("null argument");
+        return -1;
+    }
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (hipStreamSynchronize(d->stream) != hipSuccess ||
+        hipMemcpy(out, s->attn, (size_t)s->q_dim * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        mynah_set_error("attention output download failed");
+        return -1;
+    }
+    return 0;
+}
 
 void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
     if (s) s->n_past = 0;

@@ -180,24 +180,38 @@ MYNAH_DEV float ao_fma4(float4 v, float4 p, float o) {
 }
 
 // Softmax of one scores row over positions 0 .. n_kv - 1 by one wave
-// (src/kernels.c:207-220): the scores are loaded into registers (lane l
-// holds positions 4 l + 256 k .. + 3, n_kv <= 4096), then the f32 max, expf,
-// the double sum and the product with the f32 reciprocal of the sum; p gets
-// the probabilities of the float4s that hold positions < n_kv (positions
-// past n_kv in the last float4 get 0). p may equal sc_row (every score is
-// read before any probability is written).
-MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
-#pragma clang fp contract(off)
+// (src/kernels.c:207-220), in two parts. softmax_load: lane l takes the
+// float4s l, l + 64, ... (KS of them, n_kv <= 256 KS) into registers, the
+// index clamped to the row's last float4 that holds a position; straight-line
+// loads, so the wave waits for them once and not behind each other.
+// softmax_finish: positions past n_kv become -inf, then the f32 max, expf
+// (2^(i/32) table at `tab`), the double sum and the product with the f32
+// reciprocal of the sum; p gets the probabilities of the float4s that hold
+// positions < n_kv (positions past n_kv in the last float4 get 0). p may
+// equal sc_row (every score is read before any probability is written).
+template <int KS = AO_SK>
+MYNAH_DEV void softmax_load(float4 *sv, const float *sc_row, uint32_t n_kv) {
     const uint32_t lane = threadIdx.x & 63u;
     const float4 *sc = (const float4 *)sc_row;
+    const uint32_t n4 = (n_kv + 3u) / 4u;
+#pragma unroll
+    for (int k = 0; k < KS; k++) {
+        const uint32_t i = lane + 64u * (uint32_t)k;
+        sv[k] = sc[i < n4 ? i : n4 - 1u];
+    }
+}
+
+template <int KS = AO_SK>
+MYNAH_DEV void softmax_finish(float4 *sv, uint32_t n_kv, float *p, const uint64_t *tab) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n4 = (n_kv + 3u) / 4u, kmax = (n4 + 63u) / 64u;
     const float ninf = -__builtin_inff();
-    float4 sv[AO_SK];
 #pragma unroll
-    for (int k = 0; k < AO_SK; k++) {
+    for (int k = 0; k < KS; k++) {
         if ((uint32_t)k < kmax) {
             const uint32_t i = lane + 64u * (uint32_t)k, t = 4u * i;
-            float4 v = i < n4 ? sc[i] : make_float4(ninf, ninf, ninf, ninf);
+            float4 v = i < n4 ? sv[k] : make_float4(ninf, ninf, ninf, ninf);
             if (t + 1u >= n_kv) v.y = ninf;
             if (t + 2u >= n_kv) v.z = ninf;
             if (t + 3u >= n_kv) v.w = ninf;
@@ -206,19 +220,19 @@ MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
     }
     float m = ninf;
 #pragma unroll
-    for (int k = 0; k < AO_SK; k++)
+    for (int k = 0; k < KS; k++)
         if ((uint32_t)k < kmax)
             m = fmaxf(fmaxf(fmaxf(m, sv[k].x), fmaxf(sv[k].y, sv[k].z)), sv[k].w);
     m = wave_max_f(m);
     double acc = 0.0;
 #pragma unroll
-    for (int k = 0; k < AO_SK; k++) {
+    for (int k = 0; k < KS; k++) {
         if ((uint32_t)k < kmax) {
             float4 e;
-            e.x = mynah_expf(sv[k].x - m);
-            e.y = mynah_expf(sv[k].y - m);
-            e.z = mynah_expf(sv[k].z - m);
-            e.w = mynah_expf(sv[k].w - m);
+            e.x = mynah_expf_t(sv[k].x - m, tab);
+            e.y = mynah_expf_t(sv[k].y - m, tab);
+            e.z = mynah_expf_t(sv[k].z - m, tab);
+            e.w = mynah_expf_t(sv[k].w - m, tab);
             acc += (double)e.x;
             acc += (double)e.y;
             acc += (double)e.z;
@@ -230,7 +244,7 @@ MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
     const float inv = (float)(1.0 / sum);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < AO_SK; k++) {
+    for (int k = 0; k < KS; k++) {
         if ((uint32_t)k < kmax) {
             const uint32_t i = lane + 64u * (uint32_t)k;
             const float4 e = sv[k];
@@ -238,6 +252,12 @@ MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
                 *(float4 *)(p + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
         }
     }
+}
+
+MYNAH_DEV void softmax_row(const float *sc_row, uint32_t n_kv, float *p) {
+    float4 sv[AO_SK];
+    softmax_load(sv, sc_row, n_kv);
+    softmax_finish(sv, n_kv, p, mynah_exp2_tab);
 }
 
 // softmax_row for rows of any length, by one wave, through memory instead of
@@ -422,6 +442,284 @@ mynah_attn_out_long(const float *__restrict__ v_layer, const float *__restrict__
     }
     if (chain) out[(size_t)(kvh * group + wave) * 128u + AO_DV * blockIdx.y + lane] = o;
 }
+
+// Calls f(Index<C>), f(Index<C + 1>), ... while the index is below n (and
+// N): a run of steps written out, each with its constants, that stops at n.
+template <uint32_t C, uint32_t N, class F>
+MYNAH_DEV void steps_until(uint32_t n, F &&f) {
+    if constexpr (C < N) {
+        if (C >= n) return;
+        f(Index<C>{});
+        steps_until<C + 1u, N>(n, f);
+    }
+}
+
+// ── exact attention: a PV chain in every lane ──────────────────────────────
+// The reference's weighted sum (src/kernels.c:83-100, 252-272) is, for every
+// (query head, dimension), one chain o = fma(v_t[d], p_t, o) over t = 0 ..
+// n_kv - 1 in order: n_kv dependent FMAs that no reordering may shorten (a
+// dependent v_fmac_f32 costs about 8.7 cycles on gfx950). A workgroup takes
+// one query head and a slice of PV_SW = 16 of its dimensions: lane l of wave
+// 0 carries the chain of dimension l % PV_SW (lanes PV_SW and up repeat the
+// first ones and are not stored), reading V (rows of PV_SW floats in LDS)
+// and four probabilities per ds_read_b128 (every lane the same address),
+// eight groups of four positions ahead. V of the slice streams through a
+// ring of three LDS chunks of PV_CH positions, filled by four loader waves
+// that keep up to PV_WIN chunks in flight in registers, one barrier per
+// chunk; narrow slices keep each CU's share of V (and its load issue) small
+// beside the chain. The probabilities are either computed by the loader
+// waves into LDS (PMEM = false, n_kv <= 1024 KS: the softmax of
+// src/kernels.c:207-220 over the four waves — f32 max, expf, a double sum
+// per lane, per wave (wave_sum_d) and then of the four waves in order,
+// product with the f32 reciprocal) or read, normalised by
+// mynah_attn_softmax, from the scores rows and staged per chunk beside V
+// (PMEM = true, any length). Grid n_heads * 128 / PV_SW: workgroup b takes
+// key head kvh = b % n_kv_heads, query head kvh * group + (b / n_kv_heads) %
+// group and slice b / (n_kv_heads * group), so every workgroup of a key head
+// runs on the XCD b % 8 names when n_kv_heads is 8 and shares its V rows in
+// that L2; block 320; hd == 128.
+#define PV_SW 16
+#define PV_CH (4096 / PV_SW)
+#define PV_NBUF 3
+#define PV_WIN 4
+// A native 4-float vector: arrays of it stay in registers (copies of the
+// HIP float4 struct become memcpy calls that can pin an array in scratch).
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// v_layer and sp carry no __restrict__: loads from restrict-qualified
+// read-only memory may be moved across barriers, which would undo the
+// loaders' placement of their fetches.
+template <bool PMEM, int KS>
+MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
+                            float *__restrict__ out, uint32_t sstride, uint32_t kv_dim,
+                            uint32_t n_kv_heads, uint32_t group) {
+#pragma clang fp contract(off)
+    constexpr uint32_t RQ = PV_SW / 4u;                    // float4 per row of the slice
+    constexpr uint32_t NV = PV_CH * PV_SW / 4u / 256u;     // float4 of V per loader thread per chunk
+    __shared__ __attribute__((aligned(16))) v4f vbuf[PV_NBUF][PV_CH * RQ];   // [t][PV_SW]
+    __shared__ __attribute__((aligned(16))) float pl[PMEM ? PV_NBUF * PV_CH : 1024 * KS];
+    __shared__ uint64_t etab[4][32];
+    __shared__ float wmax[4];
+    __shared__ double wsum[4];
+    const uint32_t n_kv = pos + 1u;
+    const uint32_t b = blockIdx.x, kvh = b % n_kv_heads, rest = b / n_kv_heads;
+    const uint32_t head = kvh * group + rest % group, slice = rest / group;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t nc = (n_kv + PV_CH - 1u) / PV_CH;
+    const float *prow = sp + (size_t)head * sstride;
+
+    if (wave == 0) {
+        if constexpr (!PMEM) {
+            __syncthreads();                              // wave maxima
+            __syncthreads();                              // wave sums
+        }
+        __syncthreads();                                  // p, chunks 0 and 1 staged
+        const uint32_t d = lane % PV_SW;
+        float acc = 0.0f;
+        // Group m of chunk c: positions PV_CH c + 4 m .. + 3 of this lane's
+        // dimension and their probabilities.
+        auto vsrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
+            const float *vc = (const float *)vbuf[c % PV_NBUF] + 4u * PV_SW * m + d;
+            return make_float4(vc[0], vc[PV_SW], vc[2u * PV_SW], vc[3u * PV_SW]);
+        };
+        auto psrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
+            return *(const float4 *)(PMEM ? pl + (c % PV_NBUF) * PV_CH + 4u * m
+                                          : pl + c * PV_CH + 4u * m);
+        };
+        auto fma4 = [&](const float4 v, const float4 p) __attribute__((always_inline)) {
+            acc = __builtin_fmaf(v.x, p.x, acc);
+            acc = __builtin_fmaf(v.y, p.y, acc);
+            acc = __builtin_fmaf(v.z, p.z, acc);
+            acc = __builtin_fmaf(v.w, p.w, acc);
+        };
+        // Full chunks: eight groups of reads in flight, ahead into chunk
+        // c + 1, whose buffer was staged before the last barrier (for c + 1
+        // past the end the reads are of a stale buffer and unused).
+        float4 rv[8], rp[8];
+#pragma unroll
+        for (uint32_t m = 0; m < 8u; m++) {
+            rv[m] = vsrc(0, m);
+            rp[m] = psrc(0, m);
+        }
+        for (uint32_t c = 0; c < nc; c++) {
+            const uint32_t tn = n_kv - c * PV_CH < PV_CH ? n_kv - c * PV_CH : PV_CH;
+            if (tn == PV_CH) {
+                static_for<PV_CH / 4u>([&](auto mi) __attribute__((always_inline)) {
+                    constexpr uint32_t m = decltype(mi)::value, r = m % 8u;
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma4(rv[r], rp[r]);
+                    if constexpr (m + 8u < PV_CH / 4u) {
+                        rv[r] = vsrc(c, m + 8u);
+                        rp[r] = psrc(c, m + 8u);
+                    } else {
+                        rv[r] = vsrc(c + 1u, m + 8u - PV_CH / 4u);
+                        rp[r] = psrc(c + 1u, m + 8u - PV_CH / 4u);
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                // The last chunk, partial: straight from LDS.
+                const float *vc = (const float *)vbuf[c % PV_NBUF] + d;
+                const float *pc = PMEM ? pl + (c % PV_NBUF) * PV_CH : pl + c * PV_CH;
+                for (uint32_t t = 0; t < tn; t++) acc = __builtin_fmaf(vc[PV_SW * t], pc[t], acc);
+            }
+            __syncthreads();
+        }
+        if (lane < PV_SW) out[(size_t)head * 128u + slice * PV_SW + lane] = acc;
+        return;
+    }
+
+    // Loader waves 1 .. 4: chunk c is fetched into register slot c % PV_WIN
+    // PV_WIN chunks before it is stored into buffer c % PV_NBUF (two
+    // iterations before the chain reads it). Rows past the position read the
+    // last row, whose copies the chain never reads, so the loads have no
+    // branch and the waits count them exactly.
+    const uint32_t lt = tid - 64u, lw = wave - 1u;
+    const float *vcol = v_layer + (size_t)kvh * 128u + slice * PV_SW;
+    v4f vr[PV_WIN][NV], pr[PV_WIN];
+    auto fetch = [&](v4f *v4, v4f &p4, uint32_t c) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t q = 0; q < NV; q++) {
+            const uint32_t i = lt + 256u * q, t = c * PV_CH + i / RQ;
+            const uint32_t tt = t < n_kv ? t : n_kv - 1u;
+            v4[q] = *(const v4f *)(vcol + (size_t)tt * kv_dim + 4u * (i % RQ));
+        }
+        if constexpr (PMEM) {
+            const uint32_t t4 = c * PV_CH + 4u * (lt % (PV_CH / 4u)), last = (n_kv - 1u) & ~3u;
+            p4 = *(const v4f *)(prow + (t4 < n_kv ? t4 : last));
+        }
+    };
+    auto store = [&](const v4f *v4, const v4f &p4, uint32_t c) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t q = 0; q < NV; q++) vbuf[c % PV_NBUF][lt + 256u * q] = v4[q];
+        if constexpr (PMEM) {
+            if (lt < PV_CH / 4u) *(v4f *)(pl + (c % PV_NBUF) * PV_CH + 4u * lt) = p4;
+        }
+    };
+    if constexpr (!PMEM) {
+        // The expf table, the scores (float4 lt + 256 k of the row, index
+        // clamped into the row's positions) and the first two chunks of V go
+        // out first; the rest of V once the scores are in.
+        const float4 *sc = (const float4 *)prow;
+        const uint32_t n4 = (n_kv + 3u) / 4u;
+        const float ninf = -__builtin_inff();
+        float4 sv[KS];
+        const uint64_t tv = mynah_exp2_tab[lane & 31u];
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const uint32_t i = lt + 256u * (uint32_t)k;
+            sv[k] = sc[i < n4 ? i : n4 - 1u];
+        }
+        fetch(vr[0], pr[0], 0);
+        fetch(vr[1], pr[1], 1);
+        etab[lw][lane & 31u] = tv;                        // lanes l and l + 32 write the same value
+        // Every column at once, no branch: positions at or past n_kv are
+        // -inf, whose exponential is 0 and adds nothing to the sums.
+        float m = ninf;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const uint32_t t = 4u * (lt + 256u * (uint32_t)k);
+            float4 v = sv[k];
+            v.x = t < n_kv ? v.x : ninf;
+            v.y = t + 1u < n_kv ? v.y : ninf;
+            v.z = t + 2u < n_kv ? v.z : ninf;
+            v.w = t + 3u < n_kv ? v.w : ninf;
+            sv[k] = v;
+            m = fmaxf(fmaxf(fmaxf(m, v.x), fmaxf(v.y, v.z)), v.w);
+        }
+        m = wave_max_dpp(m);
+        if (lane == 0) wmax[lw] = m;
+        __syncthreads();
+        static_for<PV_WIN - 2u>([&](auto w) __attribute__((always_inline)) {
+            constexpr uint32_t W = decltype(w)::value + 2u;
+            fetch(vr[W], pr[W], W);
+        });
+        m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        double acc = 0.0;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            float4 e;
+            e.x = mynah_expf_t(sv[k].x - m, etab[lw]);
+            e.y = mynah_expf_t(sv[k].y - m, etab[lw]);
+            e.z = mynah_expf_t(sv[k].z - m, etab[lw]);
+            e.w = mynah_expf_t(sv[k].w - m, etab[lw]);
+            sv[k] = e;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            acc += (double)sv[k].x;
+            acc += (double)sv[k].y;
+            acc += (double)sv[k].z;
+            acc += (double)sv[k].w;
+        }
+        acc = wave_sum_d(acc);
+        if (lane == 0) wsum[lw] = acc;
+        __syncthreads();
+        const float inv = (float)(1.0 / (((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]));
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const uint32_t i = lt + 256u * (uint32_t)k;
+            if (i < n4) {
+                const float4 e = sv[k];
+                *(float4 *)(pl + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
+            }
+        }
+    } else {
+        static_for<PV_WIN>([&](auto w) __attribute__((always_inline)) {
+            constexpr uint32_t W = decltype(w)::value;
+            fetch(vr[W], pr[W], W);
+        });
+    }
+    store(vr[0], pr[0], 0);
+    store(vr[1], pr[1], 1);
+    fetch(vr[0], pr[0], PV_WIN);
+    fetch(vr[1], pr[1], PV_WIN + 1u);
+    __syncthreads();
+    // One barrier per chunk of the chain (nc in all); chunk c + 2 goes where
+    // chunk c - 1 was and its slot takes chunk c + 2 + PV_WIN. With the
+    // probabilities in LDS the chunks are at most 4 KS and the steps are
+    // written out one by one (a loop's back edge would make the compiler
+    // wait for every fetch in flight at its head); otherwise a loop of
+    // rounds of PV_WIN steps, each slot index a constant.
+    auto step = [&](auto wi, uint32_t c) __attribute__((always_inline)) {
+        constexpr uint32_t S = (decltype(wi)::value + 2u) % PV_WIN;
+        store(vr[S], pr[S], c + 2u);
+        fetch(vr[S], pr[S], c + 2u + PV_WIN);
+        __syncthreads();
+    };
+    if constexpr (!PMEM) {
+        steps_until<0, 1024u * KS / PV_CH>(nc, [&](auto ci) __attribute__((always_inline)) {
+            constexpr uint32_t c = decltype(ci)::value;
+            step(Index<c % PV_WIN>{}, c);
+        });
+    } else {
+        for (uint32_t c0 = 0;; c0 += PV_WIN) {
+            bool more = true;
+            static_for<PV_WIN>([&](auto wi) __attribute__((always_inline)) {
+                const uint32_t c = c0 + decltype(wi)::value;
+                if (more && c >= nc) more = false;
+                if (more) step(wi, c);
+            });
+            if (!more) return;
+        }
+    }
+}
+
+#define PV_KERNEL(PMEM, KS, NAME)                                                             \
+    extern "C" __global__ void __launch_bounds__(320)                                         \
+    NAME(const float *v_layer, const float *sp, const uint32_t *__restrict__ pos_ptr,         \
+         float *__restrict__ out, uint32_t sstride, uint32_t kv_dim, uint32_t n_kv_heads,     \
+         uint32_t group) {                                                                    \
+        attn_pv_body<PMEM, KS>(v_layer, sp, pos_ptr[0], out, sstride, kv_dim, n_kv_heads,     \
+                               group);                                                        \
+    }
+// Probabilities in LDS: KS float4 of scores per loader thread cover n_ctx <= 1024 KS.
+PV_KERNEL(false, 1, mynah_attn_pv_1)
+PV_KERNEL(false, 2, mynah_attn_pv_2)
+PV_KERNEL(false, 3, mynah_attn_pv_3)
+PV_KERNEL(false, 4, mynah_attn_pv_4)
+// Probabilities from memory (any length).
+PV_KERNEL(true, 1, mynah_attn_pv_m)
 
 // ── attention with the positions split across workgroups ───────────────────
 // The same operations as mynah_attn_scores + mynah_attn_out, except that the

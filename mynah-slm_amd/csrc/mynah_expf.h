@@ -53,16 +53,13 @@ MYNAH_EXPF_TAB uint64_t mynah_exp2_tab[32] = {
 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull
 };
 
-MYNAH_EXPF_FN float mynah_expf(float x) {
+/* mynah_expf with the table read through `tab` (the 32 entries of
+ * mynah_exp2_tab, e.g. a copy in GPU shared memory, whose reads do not wait
+ * behind the wave's outstanding global loads). */
+MYNAH_EXPF_FN float mynah_expf_t(float x, const uint64_t *tab) {
     uint32_t xb;
     __builtin_memcpy(&xb, &x, 4);
     const uint32_t abstop = (xb >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                 /* |x| >= 88 or NaN */
-        if (xb == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_inff();
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
     const double shift = 0x1.8p+52, inv_ln2_32 = 0x1.71547652b82fep+0 * 32.0;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
@@ -73,14 +70,27 @@ MYNAH_EXPF_FN float mynah_expf(float x) {
     __builtin_memcpy(&ki, &kd, 8);
     kd -= shift;
     const double r = MYNAH_FMA64(inv_ln2_32, xd, -kd);
-    const uint64_t t = mynah_exp2_tab[ki % 32u] + (ki << 47);
+    const uint64_t t = tab[ki % 32u] + (ki << 47);
     double s;
     __builtin_memcpy(&s, &t, 8);
     const double z = MYNAH_FMA64(c0, r, c1), r2 = r * r;
     double y = MYNAH_FMA64(c2, r, 1.0);
     y = MYNAH_FMA64(z, r2, y);
     y = y * s;
-    return (float)y;
+    /* The special cases of |x| >= 88 or NaN, taken after the main path
+     * (whose result they replace; its table index is in range whatever x
+     * is), so that no lane branches: -inf -> 0 before NaN and +inf -> x + x,
+     * before overflow -> +inf, before underflow -> +0. */
+    float out = (float)y;
+    if (abstop >= 0x42bu) {
+        out = x < -0x1.9fe368p6f ? 0.0f : out;
+        out = x > 0x1.62e42ep6f ? __builtin_inff() : out;
+        out = abstop >= 0x7f8u ? x + x : out;
+        out = xb == 0xff800000u ? 0.0f : out;
+    }
+    return out;
 }
+
+MYNAH_EXPF_FN float mynah_expf(float x) { return mynah_expf_t(x, mynah_exp2_tab); }
 
 #endif

@@ -877,6 +877,10 @@ static int host_call(host_op op, int type, const void *w, size_t rows, size_t co
     const size_t ybytes = (op == OP_DEQUANT ? rows * cols : tokens * rows) * sizeof(float);
     const void *wd = lookup(w, wbytes);
     hipStream_t s = d->stream;
+    /* The reference reads blocks at any address (test_quant.c:208-295); a
+     * registered copy keeps the host address's skew, so a tensor that sits
+     * off the kernels' word alignment is staged into an aligned buffer. */
+    if (wd != NULL && mynah_w_misaligned(type, wd)) wd = NULL;
     if (wd == NULL) {
         if (grow(&stage_w, &cap_w, wbytes) != 0) goto out;
         if (hipMemcpyAsync(stage_w, w, wbytes, hipMemcpyHostToDevice, s) != hipSuccess) {

@@ -48,6 +48,11 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_ATTN_OUT, "mynah_attn_out")              \
     X(MYNAH_K_ATTN_SOFTMAX, "mynah_attn_softmax")      \
     X(MYNAH_K_ATTN_OUT_LONG, "mynah_attn_out_long")    \
+    X(MYNAH_K_ATTN_PV_1, "mynah_attn_pv_1")            \
+    X(MYNAH_K_ATTN_PV_2, "mynah_attn_pv_2")            \
+    X(MYNAH_K_ATTN_PV_3, "mynah_attn_pv_3")            \
+    X(MYNAH_K_ATTN_PV_4, "mynah_attn_pv_4")            \
+    X(MYNAH_K_ATTN_PV_M, "mynah_attn_pv_m")            \
     X(MYNAH_K_ATTN_SPLIT, "mynah_attn_split")          \
     X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
     X(MYNAH_K_ATTN_COMBINE1, "mynah_attn_combine1")    \
@@ -83,6 +88,9 @@ enum {
 #define MYNAH_MAX_DEVICES 16
 
 /* Positions per workgroup of the split attention (decode.hip AS_CH). */
+/* Dimensions per workgroup of the exact attention's PV kernel (= PV_SW in
+ * decode.hip). */
+#define MYNAH_PV_SW 16
 #define MYNAH_AS_CH 32
 /* Most chunks mynah_attn_combine1 (one wave per query head) takes. */
 #define MYNAH_AC1_MAX 32

@@ -134,6 +134,7 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_prefill": (C.c_int, [_P, _P, C.c_uint32]),
         "mynah_hip_qwen3_set_prefill": (C.c_int, [_P, C.c_int]),
         "mynah_hip_qwen3_n_past": (C.c_uint32, [_P]),
+        "mynah_hip_qwen3_read_attn": (C.c_int, [_P, _P]),
         "mynah_hip_qwen3_uses_graph": (C.c_int, [_P]),
         "mynah_hip_qwen3_set_attention": (C.c_int, [_P, C.c_int]),
         "mynah_hip_qwen3_prompt": (C.c_int, [_P, _P, C.c_uint32, C.c_uint32, _P,
@@ -604,6 +605,13 @@ class Qwen3Decoder:
         if not self.h:
             raise HipError(f"qwen3_from_gguf: {err.value.decode(errors='replace')}")
         return self
+
+    def read_attn(self) -> np.ndarray:
+        """The last layer's attention output of the most recent step."""
+        sh = self.model.shape
+        out = np.empty(sh.n_heads * sh.head_dim, np.float32)
+        check(lib.mynah_hip_qwen3_read_attn(self.h, ptr(out)), "read_attn")
+        return out
 
     def set_kv(self, k: np.ndarray, v: np.ndarray, n_pos: int) -> None:
         k = np.ascontiguousarray(k, np.float32)

@@ -93,6 +93,8 @@ float *orc_qwen3_k_cache(orc_qwen3 *s);
 float *orc_qwen3_v_cache(orc_qwen3 *s);
 void  orc_qwen3_set_n_past(orc_qwen3 *s, uint32_t n_past);
 uint32_t orc_qwen3_n_past(const orc_qwen3 *s);
+const float *orc_qwen3_last_q(const orc_qwen3 *s);
+const float *orc_qwen3_last_attn(const orc_qwen3 *s);
 /* mynah_slm_forward: 0, or -1 when the context is full. */
 int   orc_qwen3_forward(orc_qwen3 *s, uint32_t token, float *logits);
 

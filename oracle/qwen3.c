@@ -208,6 +208,10 @@ float *orc_qwen3_k_cache(orc_qwen3 *s) { return s->k_cache; }
 float *orc_qwen3_v_cache(orc_qwen3 *s) { return s->v_cache; }
 void orc_qwen3_set_n_past(orc_qwen3 *s, uint32_t n) { s->n_past = n; }
 uint32_t orc_qwen3_n_past(const orc_qwen3 *s) { return s->n_past; }
+/* The last layer's normalised, rotated query heads and attention output of
+ * the most recent step (n_heads * head_dim floats each). */
+const float *orc_qwen3_last_q(const orc_qwen3 *s) { return s->q; }
+const float *orc_qwen3_last_attn(const orc_qwen3 *s) { return s->attn; }
 
 int orc_qwen3_forward(orc_qwen3 *s, uint32_t token, float *logits) {
     const orc_qwen3_config *c = &s->c;

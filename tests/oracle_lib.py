@@ -98,6 +98,8 @@ def _load_oracle() -> C.CDLL:
         "orc_qwen3_v_cache": (C.POINTER(C.c_float), [_P]),
         "orc_qwen3_set_n_past": (None, [_P, C.c_uint32]),
         "orc_qwen3_n_past": (C.c_uint32, [_P]),
+        "orc_qwen3_last_q": (C.POINTER(C.c_float), [_P]),
+        "orc_qwen3_last_attn": (C.POINTER(C.c_float), [_P]),
         "orc_qwen3_forward": (C.c_int, [_P, C.c_uint32, _P]),
         "orc_argmax": (C.c_uint32, [_P, _SZ]),
         "orc_sampler_new": (_P, [C.POINTER(SamplerParams), C.c_uint32]),
@@ -354,6 +356,18 @@ class OracleQwen3:
         logits = np.empty(self.model.shape.vocab, np.float32)
         assert orc.orc_qwen3_forward(self.h, token, ptr(logits)) == 0
         return logits
+
+    def last_attn(self) -> np.ndarray:
+        """The last layer's attention output of the most recent step."""
+        s = self.model.shape
+        n = s.n_heads * s.head_dim
+        return np.ctypeslib.as_array(orc.orc_qwen3_last_attn(self.h), shape=(n,)).copy()
+
+    def last_q(self) -> np.ndarray:
+        """The last layer's normalised, rotated query heads of the most recent step."""
+        s = self.model.shape
+        n = s.n_heads * s.head_dim
+        return np.ctypeslib.as_array(orc.orc_qwen3_last_q(self.h), shape=(n,)).copy()
 
     def greedy(self, first: int, steps: int):
         toks, tok, first_logits = [], first, None
