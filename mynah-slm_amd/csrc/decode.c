@@ -539,15 +539,20 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
         } else {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;
-            const float *rcos = s->rope_cos, *rsin = s->rope_sin;
+            const float *rnow = s->rope_now;
             float *sc = s->scores;
             uint32_t nctx = s->n_ctx, kvd = s->kv_dim, sstride = s->sstride;
             uint32_t group = c->n_heads / c->n_kv_heads;
             float eps = c->rms_eps, scale = s->scale;
-            void *args[] = {&q, &kl, &qn, &kn, &rcos, &rsin, &pos, &sc, &nctx, &sstride, &kvd,
-                            &group, &eps, &scale};
-            rc = mynah_launch(d, MYNAH_K_ATTN_SCORES, c->n_kv_heads, (s->n_ctx + 15) / 16, 256, 0,
-                              st, args);
+            /* 16-position chunks live at this step's position stay live in
+             * every later step (the graphs replay forward), so they load
+             * their key rows before the position arrives. */
+            const uint32_t nsc = (s->n_ctx + 15) / 16;
+            uint32_t spec = (s->n_past + 16) / 16;
+            if (spec > nsc) spec = nsc;
+            void *args[] = {&q, &kl, &qn, &kn, &rnow, &pos, &sc, &nctx, &sstride, &kvd,
+                            &group, &eps, &scale, &spec};
+            rc = mynah_launch(d, MYNAH_K_ATTN_SCORES, c->n_kv_heads, nsc, 256, 0, st, args);
             if (rc) break;
             float *out = s->attn;
             const float *scc = s->scores;

@@ -56,6 +56,19 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
     }
 }
 
+// Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
+// x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
+// head_norm_rope, with the pair (i, i + 64) rotated in registers.
+MYNAH_DEV void norm_rope_reg(float x0, float x1, float w0, float w1, float c, float sn, float eps,
+                             float &y0, float &y1) {
+#pragma clang fp contract(off)
+    const double sum = wave_sum_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
+    const float s = (float)(1.0 / sqrt(sum / 128.0 + (double)eps));
+    const float a = x0 * (s * w0), b = x1 * (s * w1);
+    y0 = a * c - b * sn;
+    y1 = b * c + a * sn;
+}
+
 // Attention scores for one key head and a chunk of SC_POS positions
 // (src/kernels.c:228-250 first loop, with src/arch_qwen3.c:209-218 folded in).
 // Lane (r, l) of wave w handles position t = t0 + 4 w + r and the dot-product
@@ -63,54 +76,84 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
 // k_t[16 j + l] for j = 0..7 and accumulates fma(q[16 j + l], k_t[16 j + l])
 // over j, which is s0[l] for l < 8 and s1[l - 8] otherwise; the 16 lanes of a
 // position then combine exactly as the reference does: tt = s0 + s1, v[l] =
-// tt[l] + tt[l + 4], dot = (v0 + v1) + (v2 + v3). Before that, wave g
-// normalises and rotates query head kvh * group + g into LDS, and the
-// workgroup whose chunk holds `pos` normalises and rotates the new key in the
-// cache slot (the only writer of that slot; its own score uses the rotated
-// key from LDS). Scores rows are `sstride` floats apart. Grid (n_kv_heads,
-// ceil(n_ctx / SC_POS)), block 256; group <= 8, hd == 128.
+// tt[l] + tt[l + 4], dot = (v0 + v1) + (v2 + v3). The query heads kvh * group
+// + h are normalised and rotated (src/kernels.c:130-137, 173-189) in
+// registers by wave h % 4 into LDS, and the workgroup whose chunk holds `pos`
+// normalises and rotates the new key in the cache slot (the only writer of
+// that slot; its own score uses the rotated key from LDS). Nothing before the
+// position's arrival depends on it: chunks below spec_chunks (those live when
+// the launch was enqueued; the position only grows) load their key rows
+// (clamped into the cache) at once, the query heads, their norm weights and
+// the rotation of the position (rope_now, its cos and sin rows, copied there
+// by the launch that set the position) likewise; the other chunks first learn
+// whether they hold any position. Scores rows are `sstride` floats apart.
+// Grid (n_kv_heads, ceil(n_ctx / SC_POS)), block 256; group <= 8, hd == 128.
 #define SC_POS 16
 MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__ k_layer,
                                 const float *__restrict__ q_norm, const float *__restrict__ k_norm,
-                                const float *__restrict__ rope_cos,
-                                const float *__restrict__ rope_sin, uint32_t pos,
-                                float *__restrict__ scores, uint32_t sstride, uint32_t kv_dim,
-                                uint32_t group, float eps, float scale) {
+                                const float *__restrict__ rope_now,
+                                const uint32_t *__restrict__ pos_ptr, float *__restrict__ scores,
+                                uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group,
+                                float eps, float scale, uint32_t spec_chunks) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float qn[8][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
-    __shared__ float tmp[9][128];
-    const uint32_t n_kv = pos + 1u;
-    const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * SC_POS;
-    if (t0 >= n_kv) return;
+    const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * SC_POS;
+    if (c >= spec_chunks && t0 >= pos_ptr[0] + 1u) return;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t t = t0 + 4u * wave + r;
-    const bool live = t < pos;                      // the new key is rotated below
-    const float *krow = k_layer + (size_t)(live ? t : 0u) * kv_dim + (size_t)kvh * 128u + l;
+    const uint32_t row = t < n_ctx ? t : n_ctx - 1u;
+    const float *krow = k_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + l;
     float kv[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) kv[j] = krow[16 * j];
-    {
-        const float *cs = rope_cos + (size_t)pos * 64u, *sn = rope_sin + (size_t)pos * 64u;
-        const bool has_pos = pos < t0 + SC_POS;
-        const uint32_t ntask = group + (has_pos ? 1u : 0u);
-        for (uint32_t task = wave; task < ntask; task += 4u) {
-            if (task < group) {
-                head_norm_rope(q + (size_t)(kvh * group + task) * 128u, qn[task], q_norm, cs, sn,
-                               128u, eps, tmp[task]);
-            } else {
-                float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
-                head_norm_rope(kpos, kn, k_norm, cs, sn, 128u, eps, tmp[8]);
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                for (uint32_t i = lane; i < 128u; i += 64u) kpos[i] = kn[i];
-            }
+    // Query heads wave and wave + 4 (those below group), their norm weights
+    // and the rotation of the position.
+    float x0[2], x1[2];
+    const float w0 = q_norm[lane], w1 = q_norm[lane + 64u];
+    const float cs = rope_now[lane], sn = rope_now[64u + lane];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const uint32_t h = wave + 4u * (uint32_t)e;
+        const float *src = q + (size_t)(kvh * group + (h < group ? h : 0u)) * 128u;
+        x0[e] = src[lane];
+        x1[e] = src[lane + 64u];
+    }
+    const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
+    if (t0 >= n_kv) return;       // a speculative chunk past the position (after a reset)
+    const bool has_pos = pos < t0 + SC_POS;
+    // The new key: wave group % 4 (after its query heads, if any).
+    const uint32_t kw = group % 4u;
+    float *kpos = k_layer + (size_t)pos * kv_dim + (size_t)kvh * 128u;
+    float k0 = 0.0f, k1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+    if (has_pos && wave == kw) {
+        k0 = kpos[lane];
+        k1 = kpos[lane + 64u];
+        kw0 = k_norm[lane];
+        kw1 = k_norm[lane + 64u];
+    }
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const uint32_t h = wave + 4u * (uint32_t)e;
+        if (h < group) {
+            float y0, y1;
+            norm_rope_reg(x0[e], x1[e], w0, w1, cs, sn, eps, y0, y1);
+            qn[h][lane] = y0;
+            qn[h][lane + 64u] = y1;
         }
+    }
+    if (has_pos && wave == kw) {
+        float y0, y1;
+        norm_rope_reg(k0, k1, kw0, kw1, cs, sn, eps, y0, y1);
+        kn[lane] = y0;
+        kn[lane + 64u] = y1;
+        kpos[lane] = y0;
+        kpos[lane + 64u] = y1;
     }
     __syncthreads();
     if (t < n_kv) {
-        if (!live) {
+        if (t >= pos) {
 #pragma unroll
             for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
         }
@@ -127,13 +170,11 @@ MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__
 extern "C" __global__ void __launch_bounds__(256)
 mynah_attn_scores(const float *__restrict__ q, float *__restrict__ k_layer,
                   const float *__restrict__ q_norm, const float *__restrict__ k_norm,
-                  const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
-                  const uint32_t *__restrict__ pos_ptr, float *__restrict__ scores,
-                  uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim, uint32_t group, float eps,
-                  float scale) {
-    (void)n_ctx;
-    attn_scores_body(q, k_layer, q_norm, k_norm, rope_cos, rope_sin, pos_ptr[0], scores,
-                           sstride, kv_dim, group, eps, scale);
+                  const float *__restrict__ rope_now, const uint32_t *__restrict__ pos_ptr,
+                  float *__restrict__ scores, uint32_t n_ctx, uint32_t sstride, uint32_t kv_dim,
+                  uint32_t group, float eps, float scale, uint32_t spec_chunks) {
+    attn_scores_body(q, k_layer, q_norm, k_norm, rope_now, pos_ptr, scores, n_ctx, sstride,
+                     kv_dim, group, eps, scale, spec_chunks);
 }
 
 // Softmax and weighted sum of V for one key head and AO_DV = 8 output
@@ -459,13 +500,13 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // (query head, dimension), one chain o = fma(v_t[d], p_t, o) over t = 0 ..
 // n_kv - 1 in order: n_kv dependent FMAs that no reordering may shorten (a
 // dependent v_fmac_f32 costs about 8.7 cycles on gfx950). A workgroup takes
-// one query head and a slice of PV_SW = 16 of its dimensions: lane l of wave
-// 0 carries the chain of dimension l % PV_SW (lanes PV_SW and up repeat the
-// first ones and are not stored), reading V (rows of PV_SW floats in LDS)
+// one query head and a slice of DPV_SW = 16 of its dimensions: lane l of wave
+// 0 carries the chain of dimension l % DPV_SW (lanes DPV_SW and up repeat the
+// first ones and are not stored), reading V (rows of DPV_SW floats in LDS)
 // and four probabilities per ds_read_b128 (every lane the same address),
 // eight groups of four positions ahead. V of the slice streams through a
-// ring of three LDS chunks of PV_CH positions, filled by four loader waves
-// that keep up to PV_WIN chunks in flight in registers, one barrier per
+// ring of three LDS chunks of DPV_CH positions, filled by four loader waves
+// that keep up to DPV_WIN chunks in flight in registers, one barrier per
 // chunk; narrow slices keep each CU's share of V (and its load issue) small
 // beside the chain. The probabilities are either computed by the loader
 // waves into LDS (PMEM = false, n_kv <= 1024 KS: the softmax of
@@ -473,15 +514,15 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // per lane, per wave (wave_sum_d) and then of the four waves in order,
 // product with the f32 reciprocal) or read, normalised by
 // mynah_attn_softmax, from the scores rows and staged per chunk beside V
-// (PMEM = true, any length). Grid n_heads * 128 / PV_SW: workgroup b takes
+// (PMEM = true, any length). Grid n_heads * 128 / DPV_SW: workgroup b takes
 // key head kvh = b % n_kv_heads, query head kvh * group + (b / n_kv_heads) %
 // group and slice b / (n_kv_heads * group), so every workgroup of a key head
 // runs on the XCD b % 8 names when n_kv_heads is 8 and shares its V rows in
 // that L2; block 320; hd == 128.
-#define PV_SW 16
-#define PV_CH (4096 / PV_SW)
-#define PV_NBUF 3
-#define PV_WIN 4
+#define DPV_SW 16
+#define DPV_CH (4096 / DPV_SW)
+#define DPV_NBUF 3
+#define DPV_WIN 4
 // A native 4-float vector: arrays of it stay in registers (copies of the
 // HIP float4 struct become memcpy calls that can pin an array in scratch).
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -494,10 +535,10 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
                             float *__restrict__ out, uint32_t sstride, uint32_t kv_dim,
                             uint32_t n_kv_heads, uint32_t group) {
 #pragma clang fp contract(off)
-    constexpr uint32_t RQ = PV_SW / 4u;                    // float4 per row of the slice
-    constexpr uint32_t NV = PV_CH * PV_SW / 4u / 256u;     // float4 of V per loader thread per chunk
-    __shared__ __attribute__((aligned(16))) v4f vbuf[PV_NBUF][PV_CH * RQ];   // [t][PV_SW]
-    __shared__ __attribute__((aligned(16))) float pl[PMEM ? PV_NBUF * PV_CH : 1024 * KS];
+    constexpr uint32_t RQ = DPV_SW / 4u;                    // float4 per row of the slice
+    constexpr uint32_t NV = DPV_CH * DPV_SW / 4u / 256u;     // float4 of V per loader thread per chunk
+    __shared__ __attribute__((aligned(16))) v4f vbuf[DPV_NBUF][DPV_CH * RQ];   // [t][DPV_SW]
+    __shared__ __attribute__((aligned(16))) float pl[PMEM ? DPV_NBUF * DPV_CH : 1024 * KS];
     __shared__ uint64_t etab[4][32];
     __shared__ float wmax[4];
     __shared__ double wsum[4];
@@ -505,7 +546,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     const uint32_t b = blockIdx.x, kvh = b % n_kv_heads, rest = b / n_kv_heads;
     const uint32_t head = kvh * group + rest % group, slice = rest / group;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-    const uint32_t nc = (n_kv + PV_CH - 1u) / PV_CH;
+    const uint32_t nc = (n_kv + DPV_CH - 1u) / DPV_CH;
     const float *prow = sp + (size_t)head * sstride;
 
     if (wave == 0) {
@@ -514,17 +555,17 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
             __syncthreads();                              // wave sums
         }
         __syncthreads();                                  // p, chunks 0 and 1 staged
-        const uint32_t d = lane % PV_SW;
+        const uint32_t d = lane % DPV_SW;
         float acc = 0.0f;
-        // Group m of chunk c: positions PV_CH c + 4 m .. + 3 of this lane's
+        // Group m of chunk c: positions DPV_CH c + 4 m .. + 3 of this lane's
         // dimension and their probabilities.
         auto vsrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
-            const float *vc = (const float *)vbuf[c % PV_NBUF] + 4u * PV_SW * m + d;
-            return make_float4(vc[0], vc[PV_SW], vc[2u * PV_SW], vc[3u * PV_SW]);
+            const float *vc = (const float *)vbuf[c % DPV_NBUF] + 4u * DPV_SW * m + d;
+            return make_float4(vc[0], vc[DPV_SW], vc[2u * DPV_SW], vc[3u * DPV_SW]);
         };
         auto psrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
-            return *(const float4 *)(PMEM ? pl + (c % PV_NBUF) * PV_CH + 4u * m
-                                          : pl + c * PV_CH + 4u * m);
+            return *(const float4 *)(PMEM ? pl + (c % DPV_NBUF) * DPV_CH + 4u * m
+                                          : pl + c * DPV_CH + 4u * m);
         };
         auto fma4 = [&](const float4 v, const float4 p) __attribute__((always_inline)) {
             acc = __builtin_fmaf(v.x, p.x, acc);
@@ -542,58 +583,58 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
             rp[m] = psrc(0, m);
         }
         for (uint32_t c = 0; c < nc; c++) {
-            const uint32_t tn = n_kv - c * PV_CH < PV_CH ? n_kv - c * PV_CH : PV_CH;
-            if (tn == PV_CH) {
-                static_for<PV_CH / 4u>([&](auto mi) __attribute__((always_inline)) {
+            const uint32_t tn = n_kv - c * DPV_CH < DPV_CH ? n_kv - c * DPV_CH : DPV_CH;
+            if (tn == DPV_CH) {
+                static_for<DPV_CH / 4u>([&](auto mi) __attribute__((always_inline)) {
                     constexpr uint32_t m = decltype(mi)::value, r = m % 8u;
                     __builtin_amdgcn_sched_barrier(0);
                     fma4(rv[r], rp[r]);
-                    if constexpr (m + 8u < PV_CH / 4u) {
+                    if constexpr (m + 8u < DPV_CH / 4u) {
                         rv[r] = vsrc(c, m + 8u);
                         rp[r] = psrc(c, m + 8u);
                     } else {
-                        rv[r] = vsrc(c + 1u, m + 8u - PV_CH / 4u);
-                        rp[r] = psrc(c + 1u, m + 8u - PV_CH / 4u);
+                        rv[r] = vsrc(c + 1u, m + 8u - DPV_CH / 4u);
+                        rp[r] = psrc(c + 1u, m + 8u - DPV_CH / 4u);
                     }
                 });
                 __builtin_amdgcn_sched_barrier(0);
             } else {
                 // The last chunk, partial: straight from LDS.
-                const float *vc = (const float *)vbuf[c % PV_NBUF] + d;
-                const float *pc = PMEM ? pl + (c % PV_NBUF) * PV_CH : pl + c * PV_CH;
-                for (uint32_t t = 0; t < tn; t++) acc = __builtin_fmaf(vc[PV_SW * t], pc[t], acc);
+                const float *vc = (const float *)vbuf[c % DPV_NBUF] + d;
+                const float *pc = PMEM ? pl + (c % DPV_NBUF) * DPV_CH : pl + c * DPV_CH;
+                for (uint32_t t = 0; t < tn; t++) acc = __builtin_fmaf(vc[DPV_SW * t], pc[t], acc);
             }
             __syncthreads();
         }
-        if (lane < PV_SW) out[(size_t)head * 128u + slice * PV_SW + lane] = acc;
+        if (lane < DPV_SW) out[(size_t)head * 128u + slice * DPV_SW + lane] = acc;
         return;
     }
 
-    // Loader waves 1 .. 4: chunk c is fetched into register slot c % PV_WIN
-    // PV_WIN chunks before it is stored into buffer c % PV_NBUF (two
+    // Loader waves 1 .. 4: chunk c is fetched into register slot c % DPV_WIN
+    // DPV_WIN chunks before it is stored into buffer c % DPV_NBUF (two
     // iterations before the chain reads it). Rows past the position read the
     // last row, whose copies the chain never reads, so the loads have no
     // branch and the waits count them exactly.
     const uint32_t lt = tid - 64u, lw = wave - 1u;
-    const float *vcol = v_layer + (size_t)kvh * 128u + slice * PV_SW;
-    v4f vr[PV_WIN][NV], pr[PV_WIN];
+    const float *vcol = v_layer + (size_t)kvh * 128u + slice * DPV_SW;
+    v4f vr[DPV_WIN][NV], pr[DPV_WIN];
     auto fetch = [&](v4f *v4, v4f &p4, uint32_t c) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t q = 0; q < NV; q++) {
-            const uint32_t i = lt + 256u * q, t = c * PV_CH + i / RQ;
+            const uint32_t i = lt + 256u * q, t = c * DPV_CH + i / RQ;
             const uint32_t tt = t < n_kv ? t : n_kv - 1u;
             v4[q] = *(const v4f *)(vcol + (size_t)tt * kv_dim + 4u * (i % RQ));
         }
         if constexpr (PMEM) {
-            const uint32_t t4 = c * PV_CH + 4u * (lt % (PV_CH / 4u)), last = (n_kv - 1u) & ~3u;
+            const uint32_t t4 = c * DPV_CH + 4u * (lt % (DPV_CH / 4u)), last = (n_kv - 1u) & ~3u;
             p4 = *(const v4f *)(prow + (t4 < n_kv ? t4 : last));
         }
     };
     auto store = [&](const v4f *v4, const v4f &p4, uint32_t c) __attribute__((always_inline)) {
 #pragma unroll
-        for (uint32_t q = 0; q < NV; q++) vbuf[c % PV_NBUF][lt + 256u * q] = v4[q];
+        for (uint32_t q = 0; q < NV; q++) vbuf[c % DPV_NBUF][lt + 256u * q] = v4[q];
         if constexpr (PMEM) {
-            if (lt < PV_CH / 4u) *(v4f *)(pl + (c % PV_NBUF) * PV_CH + 4u * lt) = p4;
+            if (lt < DPV_CH / 4u) *(v4f *)(pl + (c % DPV_NBUF) * DPV_CH + 4u * lt) = p4;
         }
     };
     if constexpr (!PMEM) {
@@ -630,7 +671,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         m = wave_max_dpp(m);
         if (lane == 0) wmax[lw] = m;
         __syncthreads();
-        static_for<PV_WIN - 2u>([&](auto w) __attribute__((always_inline)) {
+        static_for<DPV_WIN - 2u>([&](auto w) __attribute__((always_inline)) {
             constexpr uint32_t W = decltype(w)::value + 2u;
             fetch(vr[W], pr[W], W);
         });
@@ -665,37 +706,37 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
             }
         }
     } else {
-        static_for<PV_WIN>([&](auto w) __attribute__((always_inline)) {
+        static_for<DPV_WIN>([&](auto w) __attribute__((always_inline)) {
             constexpr uint32_t W = decltype(w)::value;
             fetch(vr[W], pr[W], W);
         });
     }
     store(vr[0], pr[0], 0);
     store(vr[1], pr[1], 1);
-    fetch(vr[0], pr[0], PV_WIN);
-    fetch(vr[1], pr[1], PV_WIN + 1u);
+    fetch(vr[0], pr[0], DPV_WIN);
+    fetch(vr[1], pr[1], DPV_WIN + 1u);
     __syncthreads();
     // One barrier per chunk of the chain (nc in all); chunk c + 2 goes where
-    // chunk c - 1 was and its slot takes chunk c + 2 + PV_WIN. With the
+    // chunk c - 1 was and its slot takes chunk c + 2 + DPV_WIN. With the
     // probabilities in LDS the chunks are at most 4 KS and the steps are
     // written out one by one (a loop's back edge would make the compiler
     // wait for every fetch in flight at its head); otherwise a loop of
-    // rounds of PV_WIN steps, each slot index a constant.
+    // rounds of DPV_WIN steps, each slot index a constant.
     auto step = [&](auto wi, uint32_t c) __attribute__((always_inline)) {
-        constexpr uint32_t S = (decltype(wi)::value + 2u) % PV_WIN;
+        constexpr uint32_t S = (decltype(wi)::value + 2u) % DPV_WIN;
         store(vr[S], pr[S], c + 2u);
-        fetch(vr[S], pr[S], c + 2u + PV_WIN);
+        fetch(vr[S], pr[S], c + 2u + DPV_WIN);
         __syncthreads();
     };
     if constexpr (!PMEM) {
-        steps_until<0, 1024u * KS / PV_CH>(nc, [&](auto ci) __attribute__((always_inline)) {
+        steps_until<0, 1024u * KS / DPV_CH>(nc, [&](auto ci) __attribute__((always_inline)) {
             constexpr uint32_t c = decltype(ci)::value;
-            step(Index<c % PV_WIN>{}, c);
+            step(Index<c % DPV_WIN>{}, c);
         });
     } else {
-        for (uint32_t c0 = 0;; c0 += PV_WIN) {
+        for (uint32_t c0 = 0;; c0 += DPV_WIN) {
             bool more = true;
-            static_for<PV_WIN>([&](auto wi) __attribute__((always_inline)) {
+            static_for<DPV_WIN>([&](auto wi) __attribute__((always_inline)) {
                 const uint32_t c = c0 + decltype(wi)::value;
                 if (more && c >= nc) more = false;
                 if (more) step(wi, c);
@@ -705,7 +746,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     }
 }
 
-#define PV_KERNEL(PMEM, KS, NAME)                                                             \
+#define DPV_KERNEL(PMEM, KS, NAME)                                                             \
     extern "C" __global__ void __launch_bounds__(320)                                         \
     NAME(const float *v_layer, const float *sp, const uint32_t *__restrict__ pos_ptr,         \
          float *__restrict__ out, uint32_t sstride, uint32_t kv_dim, uint32_t n_kv_heads,     \
@@ -714,12 +755,12 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
                                group);                                                        \
     }
 // Probabilities in LDS: KS float4 of scores per loader thread cover n_ctx <= 1024 KS.
-PV_KERNEL(false, 1, mynah_attn_pv_1)
-PV_KERNEL(false, 2, mynah_attn_pv_2)
-PV_KERNEL(false, 3, mynah_attn_pv_3)
-PV_KERNEL(false, 4, mynah_attn_pv_4)
+DPV_KERNEL(false, 1, mynah_attn_pv_1)
+DPV_KERNEL(false, 2, mynah_attn_pv_2)
+DPV_KERNEL(false, 3, mynah_attn_pv_3)
+DPV_KERNEL(false, 4, mynah_attn_pv_4)
 // Probabilities from memory (any length).
-PV_KERNEL(true, 1, mynah_attn_pv_m)
+DPV_KERNEL(true, 1, mynah_attn_pv_m)
 
 // ── attention with the positions split across workgroups ───────────────────
 // The same operations as mynah_attn_scores + mynah_attn_out, except that the
@@ -736,19 +777,6 @@ PV_KERNEL(true, 1, mynah_attn_pv_m)
 // group; group <= 8, hd == 128. Partials: pm, pl [n_kv][nch_max][group], po
 // [n_kv][nch_max][group][128].
 #define AS_PASS ((AS_CH + 15) / 16)                 // K passes of 16 positions (group >= 2)
-// Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
-// x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
-// head_norm_rope, with the pair (i, i + 64) rotated in registers.
-MYNAH_DEV void norm_rope_reg(float x0, float x1, float w0, float w1, float c, float sn, float eps,
-                             float &y0, float &y1) {
-#pragma clang fp contract(off)
-    const double sum = wave_sum_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
-    const float s = (float)(1.0 / sqrt(sum / 128.0 + (double)eps));
-    const float a = x0 * (s * w0), b = x1 * (s * w1);
-    y0 = a * c - b * sn;
-    y1 = b * c + a * sn;
-}
-
 extern "C" __global__ void __launch_bounds__(1024)
 mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
                  const float *__restrict__ v_layer, const float *__restrict__ q_norm,
