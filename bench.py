@@ -212,7 +212,9 @@ def forced_check(dec, g, k, v, npre):
     return {"greedy_ids_match": greedy == [int(t) for t in g["greedy"]],
             "last_logits_bit_identical":
                 hashlib.sha256(last.tobytes()).hexdigest() == str(g["logits_sha"][-1]),
-            "last_logits_max_rel_err": err}
+            "last_logits_sample_max_rel_err": err,
+            "sample": "the golden's top-64 ids and every 293rd id of the last step (0.4 % of "
+                      "the vocabulary); the whole vector is compared by its SHA-256"}
 
 
 def gpu_decode(M, CF):
@@ -250,14 +252,17 @@ def gpu_decode(M, CF):
             dec.close()
     finally:
         M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
-    head = out["exact_gemv_split_attention"]
-    out["headline"] = {"mode": "exact_gemv_split_attention", "tok_s": head["tok_s"],
+    head = out["exact"]
+    out["headline"] = {"mode": "exact", "tok_s": head["tok_s"],
                        "target_tok_s": 1000.0, "meets_target": head["tok_s"] > 1000.0,
                        "tokens_match_reference": head["tokens_match_reference"],
-                       "note": "every GEMV bit-identical to the reference kernels; attention "
-                               "softmax taken per 32-position chunk and combined (f32 rounding "
-                               "only); the 'exact' mode's logits are bit-identical to the "
-                               "compiled reference's (teacher_forced.last_logits_bit_identical)"}
+                       "logits_bit_identical": head["teacher_forced"]["last_logits_bit_identical"],
+                       "note": "every GEMV and the attention in the reference's operation order: "
+                               "logits bit-identical to the compiled reference's (SHA-256 of the "
+                               "whole vector). The split-attention modes take the softmax per "
+                               "32-position chunk: outside the 1e-4 per-element bar on whole "
+                               "vectors (up to 1.8e-4 at configs[2], 2.9e-4 at configs[4] in "
+                               "tests/test_decode_forced_gpu.py), reported for comparison only"}
     return out
 
 
@@ -366,20 +371,21 @@ def gpu_qwen3_4b(M, CF):
 
 
 def gpu_decode_4b(M, CF, steps: int):
-    """configs[4]'s decode alone in the headline mode (exact GEMV + split
-    attention): the 2048-token prompt prefilled in batches, then `steps`
-    greedy steps; one warm-up prompt first (graph captures)."""
+    """configs[4]'s decode alone in the headline mode (exact: logits
+    bit-identical to the reference's): the 2048-token prompt prefilled in
+    batches, then `steps` greedy steps; one warm-up prompt first (graph
+    captures)."""
     shape = CF.QWEN3_4B
     model = M.SynthQwen3(shape, 0)
     prompt = CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)
     dec = M.Qwen3Decoder(model, int(prompt.size) + steps + 1)
-    dec.set_attention(M.ATTN_SPLIT)
+    dec.set_attention(M.ATTN_EXACT)
     dec.prompt(prompt[:4], 4)
     dec.reset()
     toks, pre_ms, dec_ms = dec.prompt(prompt, steps)
     dec.close()
     want = c5_golden_ids()
-    return {"model": "Qwen3-4B random-init Q4_K_M mix", "mode": "exact_gemv_split_attention",
+    return {"model": "Qwen3-4B random-init Q4_K_M mix", "mode": "exact",
             "prompt": int(prompt.size), "steps": steps, "decode_ms": round(dec_ms, 2),
             "decode_tok_s": round(steps / (dec_ms * 1e-3), 1), "first_tokens": toks[:4],
             "tokens_match_reference": None if want is None else

@@ -203,3 +203,76 @@ def test_qwen3_4b_configs4_against_reference(M, mode):
         assert ids == got[done:stop + 1]
         check_step(last, g, j, exact=mode == "exact")
         done = stop + 1
+
+
+# Split attention against the whole logit vector. The split mode rounds its
+# per-chunk exponentials and sums differently from the reference (a few 1e-7
+# of an attention output, tests/test_attention_gpu.py); 28 to 36 random-init
+# layers amplify that. Measured whole-vector maxima of |gpu - ref| /
+# max(1, |ref|) on one MI355X: configs[2], 64 teacher-forced steps, 1.79e-4
+# (29 of the 64 steps above 1e-4, median 9.9e-5); configs[4], eight steps
+# after the 2048-token prompt, 1.33e-4 rising to 2.90e-4. The bounds below
+# are twice those: they hold the mode to what it does. It is outside the
+# north star's 1e-4 per element, which the exact mode meets bit for bit.
+TOL_SPLIT_C2 = 3.6e-4
+TOL_SPLIT_C5 = 6e-4
+
+
+def test_06b_split_whole_logits_against_oracle(M, m06, g06):
+    """configs[2], split attention: every one of the 64 teacher-forced
+    steps' whole logits vector against the oracle's (whose vectors are the
+    compiled reference's: each step's SHA-256 is checked against the
+    golden), and every greedy id."""
+    print("[case] 0.6B split attention, whole logits vs oracle, 64 steps", flush=True)
+    inputs = [int(t) for t in g06["inputs"]]
+    k, v = O.kv_prefill(O.substream, CF.QWEN3_06B, 0, CF.C3_PREFILL)
+    n_ctx = CF.C3_PREFILL + len(inputs) + 1
+    O.orc.orc_threads_init(0)
+    orc = O.OracleQwen3(O.SynthModel(CF.QWEN3_06B, 0), n_ctx)
+    orc.prefill_kv(k, v, CF.C3_PREFILL)
+    dec = decoder_06b(M, m06, MODES["split"])
+    errs = []
+    for i, tok in enumerate(inputs):
+        a, b = dec.forward(tok), orc.forward(tok)
+        assert hashlib.sha256(np.ascontiguousarray(b).tobytes()).hexdigest() == \
+            str(g06["logits_sha"][i]), f"oracle step {i}"
+        errs.append(rel_err(a, b))
+        assert int(np.argmax(a)) == int(np.argmax(b)), f"step {i}"
+    print(f"0.6B split: whole-vector max rel err per step: max {max(errs):.3e}, "
+          f"median {float(np.median(errs)):.3e}, steps above 1e-4: "
+          f"{sum(e > 1e-4 for e in errs)} of {len(errs)}")
+    assert max(errs) <= TOL_SPLIT_C2
+
+
+def test_4b_split_whole_logits_after_prompt(M):
+    """configs[4], split attention: the exact mode's cache after the
+    2048-token prompt (bit-identical to the reference's: the batched prefill
+    equals stepwise decode, and the stepwise decode's logits the compiled
+    reference's) seeds both the oracle and the split decoder; eight
+    teacher-forced steps then compare whole logit vectors and greedy ids."""
+    print("[case] 4B split attention, whole logits vs oracle after the prompt", flush=True)
+    shape, steps = CF.QWEN3_4B, 8
+    model = M.SynthQwen3(shape, 0)
+    prompt = [int(t) for t in CF.c5_prompt(M.synth_uniform, M.substream, shape.vocab)]
+    n = len(prompt) - 1
+    inputs = [prompt[-1]] + [int(t) for t in CF.forced_inputs(M.synth_uniform, M.substream,
+                                                              shape.vocab, steps - 1)]
+    n_ctx = n + steps + 1
+    ex = M.Qwen3Decoder(model, n_ctx)
+    ex.prefill(prompt[:-1])
+    k, v = ex.get_kv(n)
+    ex.close()
+    O.orc.orc_threads_init(0)
+    orc = O.OracleQwen3(O.SynthModel(shape, 0), n_ctx)
+    orc.prefill_kv(k, v, n)
+    dec = M.Qwen3Decoder(model, n_ctx)
+    dec.set_attention(MODES["split"])
+    dec.set_kv(k, v, n)
+    errs = []
+    for i, tok in enumerate(inputs):
+        a, b = dec.forward(tok), orc.forward(tok)
+        errs.append(rel_err(a, b))
+        assert int(np.argmax(a)) == int(np.argmax(b)), f"step {i}"
+    dec.close()
+    print(f"4B split after the prompt: whole-vector max rel err per step {['%.2e' % e for e in errs]}")
+    assert max(errs) <= TOL_SPLIT_C5

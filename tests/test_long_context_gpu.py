@@ -5,17 +5,21 @@ server/main.c:426).
 Qwen3-0.6B and Qwen3-4B with n_ctx 8192 and 8000 cache positions of N(0, 1)
 (the configs' KV prefill generator), then teacher-forced steps: every step's
 logits against the oracle decoder (the restated reference, bit-identical to
-it) and the same greedy id, in both attention modes. The exact mode's score
-rows no longer fit the LDS there, so it runs its two-launch form (softmax
-through memory, then the ordered PV chains with the probabilities staged per
-chunk) and must stay within |gpu - ref| / max(1, |ref|) <= 1e-4 (it is bit
-for bit equal on these inputs: its exponential is the C library's). The
-split mode (250 chunks combined) computes the same scores bit for bit but
-rounds its per-chunk exponentials and sums differently (about 1e-5 of the
-attention output); a random-init network amplifies that to 1e-4 .. 1e-2 of
-the logits over 28-36 layers (even one layer shows 2e-3), so split mode is
-held to its greedy id wherever the reference's top-two margin exceeds the
-observed error, and to a 5e-2 bound that catches a broken chunk.
+it) and the same greedy id. The exact mode's PV kernel reads the
+probabilities from memory there (a softmax launch normalises the scores rows
+in place) and must stay within |gpu - ref| / max(1, |ref|) <= 1e-4; it is
+bit for bit equal on these inputs.
+
+The split mode (250 chunks combined) computes the same scores bit for bit
+but rounds its per-chunk exponentials and sums differently; its attention
+output is within 2.3e-7 of the reference's at n_kv 8003
+(tests/test_attention_gpu.py). The network then amplifies any rounding
+difference at some inputs: measured on one MI355X, the 0.6B's third step
+moves to 1.32e-2 in split mode, and to 4.35e-2 with the exact attention and
+only the GEMV summation order changed (the control run below, which is
+printed, not bounded); at 4B split mode stays within 3.94e-4. TOL_SPLIT is
+twice the split mode's measured maximum, and the greedy id is held wherever
+the reference's top-two margin exceeds twice the observed error.
 
 The batched prefill past 4096 positions (its softmax rows through memory)
 against one decode step per token: K/V and the next logits bit-identical.
@@ -30,7 +34,7 @@ import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4          # exact attention
-TOL_SPLIT = 5e-2    # split attention: f32 rounding of the chunked softmax, amplified
+TOL_SPLIT = 2.7e-2  # split attention: twice the measured 1.32e-2 (the docstring above)
 N_CTX, N_PRE, STEPS = 8192, 8000, 3
 
 
@@ -59,20 +63,29 @@ def test_long_context_against_oracle(M, name):
     orc.prefill_kv(k, v, N_PRE)
     want = [orc.forward(t) for t in inputs]
     del orc
-    for mode in (M.ATTN_EXACT, M.ATTN_SPLIT):
+    # (attention mode, GEMV order): the exact mode, the split mode, and a
+    # control that keeps the exact attention but sums the GEMVs in another
+    # f32 order (MYNAH_GEMV_REORDERED) - a perturbation of the same size as
+    # the split softmax's, which shows how far the network alone carries one.
+    errs = {}
+    for mode, order in ((M.ATTN_EXACT, 0), (M.ATTN_SPLIT, 0), (M.ATTN_EXACT, 1)):
+        M.check(M.lib.mynah_hip_set_gemv_order(order), "order")
         dec = M.Qwen3Decoder(model, N_CTX)
         dec.set_attention(mode)
         dec.set_kv(k, v, N_PRE)
         for i, tok in enumerate(inputs):
             lg = dec.forward(tok)
             err = rel_err(lg, want[i])
-            print(f"{name} attention {mode} step {i}: max rel err {err:.2e}")
-            assert err <= (TOL if mode == M.ATTN_EXACT else TOL_SPLIT)
+            errs[(mode, order, i)] = err
+            print(f"{name} attention {mode} gemv order {order} step {i}: max rel err {err:.2e}")
+            if order == 0:
+                assert err <= (TOL if mode == M.ATTN_EXACT else TOL_SPLIT)
             top2 = np.sort(want[i].astype(np.float64))[-2:]
             margin = (top2[1] - top2[0]) / max(1.0, abs(top2[1]))
-            if mode == M.ATTN_EXACT or margin > 2 * err:
+            if (mode == M.ATTN_EXACT and order == 0) or margin > 2 * err:
                 assert int(np.argmax(lg)) == int(np.argmax(want[i]))
         dec.close()
+    M.check(M.lib.mynah_hip_set_gemv_order(0), "order")
 
 
 def test_prefill_past_4096_equals_stepwise(M):
