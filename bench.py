@@ -13,7 +13,11 @@ inside the timed region. `traffic` is the HBM bytes per launch measured by
 rocprofv3 PMC counters (profiles/traffic.json), when present.
 `cpu_baseline` times the CPU oracle (the C11 restatement of the reference's
 as-built kernels with the reference's 4*nth row-chunk threading, bit-identical
-to it) on the same sweep on this host's cores.
+to it) on the same sweep on this host's cores, the median of five runs; beside
+it the same sweep in the f32 lanes of an AVX2 + FMA ingot build (restated,
+pinned to such a build by golden vectors), configs[0], the configs[2] and
+configs[4] decode (tok/s, ids checked against the compiled reference's) and
+configs[3]'s batched products, each the median of five runs.
 
 Beside the metric line's value: `decode` (configs[2], Qwen3-0.6B greedy
 decode tok/s in three numerics modes, tokens checked against the compiled
@@ -447,8 +451,10 @@ def host_cpus() -> dict:
             "cgroup_quota_cpus": quota, "omp_num_threads": omp or None, "threads": threads}
 
 
-def _timed_passes(fn, seconds: float, min_reps: int = 2):
-    fn()                                       # warm-up pass
+RUNS = 5   # every CPU leg is measured this many times and reports the median
+
+
+def _timed_passes(fn, seconds: float, min_reps: int = 1):
     reps, t0 = 0, time.perf_counter()
     while True:
         fn()
@@ -458,96 +464,156 @@ def _timed_passes(fn, seconds: float, min_reps: int = 2):
             return reps, el
 
 
-def cpu_sweep(O, CF, mats, seconds: float):
+def _runs(rates):
+    """The median of a leg's runs, with the spread beside it."""
+    import statistics
+    r = sorted(rates)
+    return {"median": round(statistics.median(r), 2), "min": round(r[0], 2),
+            "max": round(r[-1], 2), "runs": len(r)}
+
+
+def cpu_sweep(O, CF, mats, seconds: float, avx2: bool = False):
     """GB/s of the oracle's threaded projection (4*nth row chunks, serial
-    below 64 rows: src/arch_qwen3.c:52-83) over the matrices of a config."""
+    below 64 rows: src/arch_qwen3.c:52-83) over the matrices of a config:
+    RUNS runs of about `seconds` each after one warm-up pass. avx2 takes the
+    restated f32 lanes of an AVX2 + FMA ingot build instead of the as-built
+    scalar ones."""
     data = []
     for i, m in enumerate(mats):
         ws, xs = CF.matrix_seeds(O.substream, 0, i)
         data.append((m, O.blocks(m.qtype, ws, m.rows, m.cols), O.normal(xs, m.cols)))
     step_bytes = sum(algorithmic_bytes(m) for m in mats)
+    proj = O.project_avx2 if avx2 else O.project
 
     def one():
         for m, w, x in data:
-            O.project(m.qtype, w, m.rows, m.cols, x)
-    reps, el = _timed_passes(one, seconds)
-    return step_bytes, reps, el
+            proj(m.qtype, w, m.rows, m.cols, x)
+    one()                                      # warm-up pass
+    rates, passes, total = [], 0, 0.0
+    for _ in range(RUNS):
+        reps, el = _timed_passes(one, seconds)
+        rates.append(step_bytes * reps / el / 1e9)
+        passes, total = passes + reps, total + el
+    return step_bytes, rates, passes, total
 
 
-def cpu_decode(O, CF, seconds: float):
+def _greedy_runs(O, orc, tok, steps_per_run):
+    """RUNS runs of `steps_per_run` greedy steps continuing one sequence
+    (first-index argmax, src/sampler.c:124-129); decode tok/s as
+    src/timing.c:52-54 defines it (generated ids / decode seconds)."""
+    toks, rates, total = [], [], 0.0
+    for _ in range(RUNS):
+        t0 = time.perf_counter()
+        for _ in range(steps_per_run):
+            lg = orc.forward(tok)
+            tok = int(O.orc.orc_argmax(O.ptr(lg), lg.size))
+            toks.append(tok)
+        el = time.perf_counter() - t0
+        rates.append(steps_per_run / el)
+        total += el
+    return toks, rates, total
+
+
+def cpu_decode(O, CF):
     """configs[2] on the CPU: the oracle decoder (the restated
     src/arch_qwen3.c:178-252 on the pool, bit-identical to the compiled
-    reference) with first-index greedy picks (src/sampler.c:124-129) from
-    the 512-position prefill, timed as src/timing.c:52-54 defines decode
-    tok/s (generated ids / decode seconds); stops after `seconds` (at least
-    4 steps) or the 64 steps of the golden run, whose ids it must match."""
+    reference) from the 512-position prefill, RUNS runs of 8 greedy steps;
+    the 40 ids must match the golden run's."""
     import numpy as np
-    shape = CF.QWEN3_06B
-    orc = O.OracleQwen3(O.SynthModel(shape, 0), CF.C3_PREFILL + CF.C3_STEPS + 1)
+    shape, per = CF.QWEN3_06B, 8
+    orc = O.OracleQwen3(O.SynthModel(shape, 0), CF.C3_PREFILL + RUNS * per + 1)
     k, v = O.kv_prefill(O.substream, shape, 0, CF.C3_PREFILL)
     orc.prefill_kv(k, v, CF.C3_PREFILL)
+    del k, v
     want = [int(t) for t in np.load(os.path.join(ROOT, "tests", "golden", "qwen3_06b.npz"),
                                     allow_pickle=False)["tokens"]]
-    tok, toks = O.first_token(0, shape.vocab), []
-    t0 = time.perf_counter()
-    while len(toks) < CF.C3_STEPS:
-        lg = orc.forward(tok)
-        tok = int(O.orc.orc_argmax(O.ptr(lg), lg.size))
-        toks.append(tok)
-        if time.perf_counter() - t0 >= seconds and len(toks) >= 4:
-            break
-    el = time.perf_counter() - t0
+    toks, rates, total = _greedy_runs(O, orc, O.first_token(0, shape.vocab), per)
     del orc
-    return {"tok_s": round(len(toks) / el, 2), "steps": len(toks), "seconds": round(el, 2),
+    return {"tok_s": _runs(rates), "steps": len(toks), "seconds": round(total, 2),
+            "context": f"{CF.C3_PREFILL}..{CF.C3_PREFILL + len(toks)}",
+            "tokens_match_reference": toks == want[:len(toks)]}
+
+
+def cpu_decode_4b(O, CF):
+    """configs[4]'s decode on the CPU: the oracle decoder over the Qwen3-4B
+    model with 2048 KV positions (filled with N(0, 1): a step's work depends
+    on the context length only), RUNS runs of 2 greedy steps; the ids must
+    match the compiled reference's on the same inputs."""
+    import numpy as np
+    shape, npre = CF.QWEN3_4B, CF.C5_CPU_KV
+    per = CF.C5_CPU_STEPS // RUNS
+    orc = O.OracleQwen3(O.SynthModel(shape, 0), npre + CF.C5_CPU_STEPS + 1)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    orc.prefill_kv(k, v, npre)
+    del k, v
+    want = [int(t) for t in np.load(os.path.join(ROOT, "tests", "golden", "qwen3_4b_kv2048.npz"),
+                                    allow_pickle=False)["tokens"]]
+    toks, rates, total = _greedy_runs(O, orc, O.first_token(0, shape.vocab), per)
+    del orc
+    return {"tok_s": _runs(rates), "steps": len(toks), "seconds": round(total, 2),
+            "context": f"{npre}..{npre + len(toks)}",
             "tokens_match_reference": toks == want[:len(toks)]}
 
 
 def cpu_prefill_gemm(O, CF):
-    """configs[3] on the CPU: one pass of the six exact batched products
-    (the reference's ingot matmat order) with the pool injected over 8-row
-    strips (third_party/ingot/src/cpu.c:217-230), 512 tokens."""
-    flop, el = 0, 0.0
-    per = {}
+    """configs[3] on the CPU: the six exact batched products (the reference's
+    ingot matmat order) with the pool injected over 8-row strips
+    (third_party/ingot/src/cpu.c:217-230), 512 tokens; RUNS passes over the
+    six, GFLOP/s of each pass."""
+    data = []
     for i, m in enumerate(CF.C4):
         wseed, _ = CF.matrix_seeds(O.substream, 0, i)
-        w = O.blocks(m.qtype, wseed, m.rows, m.cols)
-        x = O.normal(O.substream(0, CF.PREFILL_X_INDEX + i), CF.C4_TOKENS * m.cols)
+        data.append((m, O.blocks(m.qtype, wseed, m.rows, m.cols),
+                     O.normal(O.substream(0, CF.PREFILL_X_INDEX + i), CF.C4_TOKENS * m.cols)))
+    flop = sum(2 * m.rows * m.cols * CF.C4_TOKENS for m in CF.C4)
+    rates, total = [], 0.0
+    for _ in range(RUNS):
         t0 = time.perf_counter()
-        O.matmat(m.qtype, w, m.rows, m.cols, x, CF.C4_TOKENS, threaded=True)
-        dt = time.perf_counter() - t0
-        f = 2 * m.rows * m.cols * CF.C4_TOKENS
-        per[m.name] = round(f / dt / 1e9, 2)
-        flop += f
-        el += dt
-    return {"gflop_s": round(flop / el / 1e9, 2), "seconds": round(el, 2),
-            "per_matrix_gflop_s": per}
+        for m, w, x in data:
+            O.matmat(m.qtype, w, m.rows, m.cols, x, CF.C4_TOKENS, threaded=True)
+        el = time.perf_counter() - t0
+        rates.append(flop / el / 1e9)
+        total += el
+    return {"gflop_s": _runs(rates), "seconds": round(total, 2)}
 
 
 def cpu_baseline(CF, seconds: float = 10.0):
     """The CPU oracle (the C11 restatement of the reference's as-built
-    kernels and decoder, bit-identical to it) on this host's cores: the
-    configs[1] sweep (the metric's value), configs[0], configs[2] decode and
-    configs[3]'s batched products, each on a bounded sample."""
+    kernels and decoder, bit-identical to it) on this host's cores, each leg
+    the median of RUNS runs: the configs[1] sweep (the metric's value, about
+    `seconds` in all) and the same sweep in the AVX2 + FMA lanes' order,
+    configs[0], configs[2] and configs[4] decode, configs[3]'s batched
+    products."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     cpus = host_cpus()
     threads = O.orc.orc_threads_init(cpus["threads"])
     try:
-        step_bytes, reps, el = cpu_sweep(O, CF, CF.C2, seconds)
-        c1_bytes, c1_reps, c1_el = cpu_sweep(O, CF, CF.C1, max(1.0, seconds / 4))
-        decode = cpu_decode(O, CF, seconds)
+        step_bytes, rates, passes, el = cpu_sweep(O, CF, CF.C2, seconds / RUNS)
+        _, a_rates, a_passes, a_el = cpu_sweep(O, CF, CF.C2, seconds / (2 * RUNS), avx2=True)
+        c1_bytes, c1_rates, c1_passes, c1_el = cpu_sweep(O, CF, CF.C1, seconds / (4 * RUNS))
+        decode = cpu_decode(O, CF)
+        decode_4b = cpu_decode_4b(O, CF)
         gemm = cpu_prefill_gemm(O, CF)
     finally:
         O.orc.orc_threads_shutdown()
-    return {"value": round(step_bytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": threads,
+    sweep = _runs(rates)
+    return {"value": sweep["median"], "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"{reps} passes of the configs[1] sweep ({step_bytes / 1e6:.1f} MB each) "
-                      f"in {el:.1f} s, oracle restatement (bit-identical to the reference) with "
-                      f"4*nth row chunks on {threads} threads",
+            "sample": f"median of {RUNS} runs (GB/s {sweep['min']}..{sweep['max']}), "
+                      f"{passes} passes of the configs[1] sweep ({step_bytes / 1e6:.1f} MB "
+                      f"each) in {el:.1f} s, oracle restatement (bit-identical to the "
+                      f"as-built reference: ingot's scalar lanes) with 4*nth row chunks on "
+                      f"{threads} threads",
             "host": cpus,
-            "configs0_gbs": round(c1_bytes * c1_reps / c1_el / 1e9, 2),
-            "configs0_sample": f"{c1_reps} matvecs of Q4_K 1024x3072 in {c1_el:.1f} s",
+            "configs1_avx2_order_gbs": _runs(a_rates),
+            "configs1_avx2_order_sample": f"{a_passes} passes in {a_el:.1f} s of the same sweep "
+                                          "in the f32 lanes of an AVX2 + FMA ingot build "
+                                          "(restated, bit-identical to such a build)",
+            "configs0_gbs": _runs(c1_rates),
+            "configs0_sample": f"{c1_passes} matvecs of Q4_K 1024x3072 in {c1_el:.1f} s",
             "configs2_decode": decode,
+            "configs4_decode": decode_4b,
             "configs3_prefill_gemm": gemm}
 
 

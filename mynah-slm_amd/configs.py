@@ -91,6 +91,11 @@ C5_PROMPT = 2048      # prompt tokens, uniform over the vocabulary
 C5_STEPS = 256        # greedy steps after the prompt
 C5_GOLDEN_PROMPT = 8  # the prefix the compiled reference's golden run covers
 C5_GOLDEN_STEPS = 8
+# configs[4]'s decode at context 2048 on the CPU baseline: the 4B model with
+# 2048 KV positions prefilled with N(0, 1) (the work of one step depends on
+# the context length, not on the cached values), then greedy steps.
+C5_CPU_KV = 2048
+C5_CPU_STEPS = 10
 
 MATRIX_SEED_STRIDE = 2
 KV_SEED_INDEX = 1 << 20

@@ -9,6 +9,7 @@
  * SPDX-License-Identifier: MIT */
 #include "oracle.h"
 
+#include <math.h>
 #include <string.h>
 
 #define QK 256
@@ -378,7 +379,101 @@ int orc_matmat(int type, const void *w, size_t rows, size_t cols,
 }
 
 /* ── the CPU-baseline threading ───────────────────────────────────────────── */
+/* ── the AVX2 + FMA lanes (the secondary CPU baseline) ─────────────────────
+ * What an ingot build with -mavx2 -mfma takes (INGOT_SDOT unset):
+ *   Q4_K kernels.c:455-506 (q4_k_dot_block_avx2): eight lane accumulators;
+ *        per 64-weight group and 8-weight step, lane j adds fma(low weight,
+ *        x, acc[j]) then fma(high weight, x + 32, acc[j]); the weight is
+ *        q * (d sc) - dmin m with both steps rounded (the reference builds
+ *        with -std=c11, so no contraction); the eight lanes are then summed
+ *        in order from 0, and the row sum adds the block sums in order;
+ *   Q6_K kernels.c:2062-2081 (qk_dot_avx2) over the decoded block: four
+ *        8-lane accumulators over steps of 32, the lanes (acc0 + acc1) +
+ *        (acc2 + acc3), the 128-bit halves added, then (s0 + s2) + (s1 + s3);
+ *   Q8_0 the same dot over each 32-value block.
+ * Compiled for AVX2 + FMA (the loops over the eight lanes vectorise, fmaf is
+ * one instruction) so the timing is an AVX2 build's; operation order per lane
+ * is as written (no contraction, no reassociation). */
+#define AVX2_LANES __attribute__((target("avx2,fma"), optimize("O3")))
+
+AVX2_LANES static float q4_k_block_dot_avx2(const unsigned char *blk, const float *x) {
+    const float d = orc_f16_to_f32(le16(blk));
+    const float dmin = orc_f16_to_f32(le16(blk + 2));
+    const unsigned char *qs = blk + 16;
+    float acc[8] = {0};
+    for (int g = 0; g < 4; g++) {
+        unsigned char sa, ma, sb, mb;
+        orc_scale_min(blk + 4, 2 * g, &sa, &ma);
+        orc_scale_min(blk + 4, 2 * g + 1, &sb, &mb);
+        const float d0 = d * (float)sa, d1 = d * (float)sb;
+        const float m0 = dmin * (float)ma, m1 = dmin * (float)mb;
+        for (int i = 0; i < 32; i += 8)
+            for (int j = 0; j < 8; j++) {
+                const unsigned q = qs[32 * g + i + j];
+                const float lo = (float)(q & 15u) * d0 - m0;
+                const float hi = (float)(q >> 4) * d1 - m1;
+                acc[j] = fmaf(lo, x[64 * g + i + j], acc[j]);
+                acc[j] = fmaf(hi, x[64 * g + i + j + 32], acc[j]);
+            }
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < 8; j++) sum = sum + acc[j];
+    return sum;
+}
+
+AVX2_LANES static float dot_avx2_order(const float *a, const float *b, size_t n) {
+    float c[4][8] = {{0}};
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int k = 0; k < 4; k++)
+            for (int j = 0; j < 8; j++)
+                c[k][j] = fmaf(a[i + 8 * k + j], b[i + 8 * k + j], c[k][j]);
+    float acc[8], s[4];
+    for (int j = 0; j < 8; j++) acc[j] = (c[0][j] + c[1][j]) + (c[2][j] + c[3][j]);
+    for (int j = 0; j < 4; j++) s[j] = acc[j] + acc[j + 4];
+    float sum = (s[0] + s[2]) + (s[1] + s[3]);
+    for (; i < n; i++) sum = sum + a[i] * b[i];
+    return sum;
+}
+
+AVX2_LANES static void matvec_avx2_rows(int type, const unsigned char *base, size_t rb,
+                                        size_t rows, size_t cols, const float *x, float *y) {
+    float tmp[QK];
+    for (size_t r = 0; r < rows; r++) {
+        const unsigned char *row = base + r * rb;
+        float sum = 0.0f;
+        if (type == ORC_Q4_K) {
+            for (size_t b = 0; b < cols / QK; b++)
+                sum = sum + q4_k_block_dot_avx2(row + 144 * b, x + QK * b);
+        } else if (type == ORC_Q6_K) {
+            for (size_t b = 0; b < cols / QK; b++) {
+                q6_k_block_decode(row + 210 * b, tmp);
+                sum = sum + dot_avx2_order(tmp, x + QK * b, QK);
+            }
+        } else {
+            for (size_t b = 0; b < cols / 32; b++) {
+                q8_0_block_decode(row + 34 * b, tmp);
+                sum = sum + dot_avx2_order(tmp, x + 32 * b, 32);
+            }
+        }
+        y[r] = sum;
+    }
+}
+
+int orc_matvec_avx2(int type, const void *w, size_t rows, size_t cols,
+                    const float *x, float *y) {
+    size_t rb;
+    if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma")) return -1;
+    if (w == NULL || x == NULL || y == NULL || row_bytes_of(type, rows, cols, &rb) != 0 ||
+        (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0))
+        return -1;
+    matvec_avx2_rows(type, (const unsigned char *)w, rb, rows, cols, x, y);
+    return 0;
+}
+
 void orc_pool_run(int n, void (*fn)(void *, int), void *ctx);
+
+typedef int (*matvec_fn)(int, const void *, size_t, size_t, const float *, float *);
 
 typedef struct {
     int type;
@@ -387,6 +482,7 @@ typedef struct {
     const float *x;
     float *y;
     int rc;
+    matvec_fn mv;
 } project_job;
 
 static void project_chunk(void *ctx, int i) {
@@ -395,24 +491,34 @@ static void project_chunk(void *ctx, int i) {
     if (first >= j->rows) return;
     size_t n = j->per;
     if (first + n > j->rows) n = j->rows - first;
-    if (orc_matvec(j->type, j->base + first * j->rb, n, j->cols, j->x, j->y + first) != 0)
+    if (j->mv(j->type, j->base + first * j->rb, n, j->cols, j->x, j->y + first) != 0)
         j->rc = -1;
 }
 
 /* src/arch_qwen3.c:52-83: 4*nth contiguous chunks of output rows, each an
  * independent matvec; serial when nth <= 1 or rows < 64. */
-int orc_project(int type, const void *w, size_t rows, size_t cols,
-                const float *x, float *y) {
+static int project_with(matvec_fn mv, int type, const void *w, size_t rows, size_t cols,
+                        const float *x, float *y) {
     const int nth = orc_threads_count();
     size_t rb;
     if (nth <= 1 || rows < 64 || row_bytes_of(type, rows, cols, &rb) != 0)
-        return orc_matvec(type, w, rows, cols, x, y);
+        return mv(type, w, rows, cols, x, y);
     int chunks = nth * 4;
     if ((size_t)chunks > rows) chunks = (int)rows;
     project_job j = { type, (const unsigned char *)w, rb, rows, cols,
-                      (rows + (size_t)chunks - 1) / (size_t)chunks, x, y, 0 };
+                      (rows + (size_t)chunks - 1) / (size_t)chunks, x, y, 0, mv };
     orc_pool_run(chunks, project_chunk, &j);
     return j.rc;
+}
+
+int orc_project(int type, const void *w, size_t rows, size_t cols,
+                const float *x, float *y) {
+    return project_with(orc_matvec, type, w, rows, cols, x, y);
+}
+
+int orc_project_avx2(int type, const void *w, size_t rows, size_t cols,
+                     const float *x, float *y) {
+    return project_with(orc_matvec_avx2, type, w, rows, cols, x, y);
 }
 
 typedef struct {

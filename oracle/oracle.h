@@ -47,6 +47,12 @@ int  orc_threads_count(void);
 /* project(): 4*nth contiguous row chunks, serial below 64 rows. */
 int  orc_project(int type, const void *w, size_t rows, size_t cols,
                  const float *x, float *y);
+/* The AVX2 + FMA lanes of an ingot build with -mavx2 -mfma (Q4_K, Q6_K,
+ * Q8_0; the secondary CPU baseline), alone and as project(). */
+int  orc_matvec_avx2(int type, const void *w, size_t rows, size_t cols,
+                     const float *x, float *y);
+int  orc_project_avx2(int type, const void *w, size_t rows, size_t cols,
+                      const float *x, float *y);
 /* The batched exact matmat with the pool injected over 8-row strips
  * (ingot_set_parallel_for, third_party/ingot/src/cpu.c:217-230). */
 int  orc_matmat_mt(int type, const void *w, size_t rows, size_t cols,

@@ -26,6 +26,9 @@ records a SHA-256 of the input bytes so generator drift is detected):
                      steps): every step's greedy id, the top-64 logits of
                      seven snapshot steps (`--only c5full`; not part of the
                      default run: about ten minutes of CPU)
+  qwen3_4b_kv2048.npz  configs[4]'s model with 2048 N(0, 1) KV positions, the
+                     greedy ids of 10 steps (the CPU baseline's 4B decode
+                     leg checks its ids against them; `--only c5kv`)
   qwen3_4b_prompt.npz  configs[4]'s model (Qwen3-4B): the first 8 prompt ids,
                      prefill + 8 greedy steps, the first step's logits' top 64
                      (`--only c5` writes just this file)
@@ -38,12 +41,17 @@ records a SHA-256 of the input bytes so generator drift is detected):
                      all-zero block and token counts around the token tile,
                      and Q5_K batched outputs
                      (`--only int8` writes just this file)
+  avx2.npz           the f32 AVX2 + FMA lanes of the same build (INGOT_SDOT=0,
+                     in a process of its own): Q4_K, Q6_K and Q8_0 matvec on
+                     small shapes, and configs[1]'s sweep as a SHA-256 of each
+                     output plus every 97th row (`--only avx2`)
 """
 from __future__ import annotations
 
 import hashlib
 import os
 import shutil
+import subprocess
 import sys
 
 import numpy as np
@@ -91,6 +99,19 @@ def golden_c5(ref) -> None:
     np.savez_compressed(os.path.join(HERE, "qwen3_4b_prompt.npz"), prompt=prompt.astype(np.uint32),
                         tokens=np.array(toks, np.uint32), top_ids=top.astype(np.uint32),
                         top_vals=lg[top], logits0_sha=np.array(sha(lg)),
+                        blob_sha=np.array(sha(model.blob)))
+
+
+def golden_c5_kv(ref) -> None:
+    """configs[4]'s model with 2048 N(0, 1) KV positions, then the greedy ids
+    of C5_CPU_STEPS steps: the check of the CPU baseline's 4B decode leg."""
+    shape, npre, steps = CF.QWEN3_4B, CF.C5_CPU_KV, CF.C5_CPU_STEPS
+    model = O.SynthModel(shape, 0)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    first = O.first_token(0, shape.vocab)
+    toks, lg = O.ref_greedy(ref, model, k, v, npre, first, steps, npre + steps + 1)
+    np.savez_compressed(os.path.join(HERE, "qwen3_4b_kv2048.npz"), tokens=np.array(toks, np.uint32),
+                        first=np.array(first), logits0_sha=np.array(sha(lg)),
                         blob_sha=np.array(sha(model.blob)))
 
 
@@ -215,6 +236,30 @@ def golden_int8(ref8) -> None:
     np.savez_compressed(os.path.join(HERE, "int8.npz"), **out)
 
 
+AVX2_SHAPES = ((CF.Q4_K, 37, 512), (CF.Q4_K, 64, 2048), (CF.Q6_K, 37, 512),
+               (CF.Q6_K, 16, 3072), (CF.Q8_0, 37, 96), (CF.Q8_0, 37, 512))
+
+
+def golden_avx2(ref8) -> None:
+    out = {}
+    for t, rows, cols in AVX2_SHAPES:
+        key = f"{CF.TYPE_NAME[t]}_{rows}x{cols}"
+        w, x = O.blocks(t, 1300 + t, rows, cols), O.normal(1400 + t, cols)
+        y = np.empty(rows, np.float32)
+        assert ref8.ingot_matvec(t, O.ptr(w), rows, cols, O.ptr(x), O.ptr(y)) == 0
+        out[f"{key}_y"] = y
+        out[f"{key}_w_sha"] = np.array(sha(w))
+        out[f"{key}_x_sha"] = np.array(sha(x))
+    for i, m in enumerate(CF.C2):
+        ws, xs = CF.matrix_seeds(O.substream, 0, i)
+        w, x = O.blocks(m.qtype, ws, m.rows, m.cols), O.normal(xs, m.cols)
+        y = np.empty(m.rows, np.float32)
+        assert ref8.ingot_matvec(m.qtype, O.ptr(w), m.rows, m.cols, O.ptr(x), O.ptr(y)) == 0
+        out[f"{m.name}_y_sha"] = np.array(sha(y))
+        out[f"{m.name}_y_every97"] = y[::97].copy()
+    np.savez_compressed(os.path.join(HERE, "avx2.npz"), **out)
+
+
 def main() -> int:
     ref = O.load_ref()
     if ref is None:
@@ -310,11 +355,18 @@ def main() -> int:
     r8 = O.load_ref_int8()
     if r8 is not None:
         golden_int8(r8)
+        # INGOT_SDOT is read once per process: the f32 lanes get their own.
+        subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "avx2"], check=True)
     print("golden vectors written to", HERE)
     return 0
 
 
 if __name__ == "__main__":
+    if sys.argv[1:] == ["--only", "avx2"]:
+        r8 = O.load_ref_int8(sdot="0")
+        assert r8 is not None, "oracle/_ref/libref_int8.so is missing: run make -C oracle"
+        golden_avx2(r8)
+        sys.exit(0)
     if sys.argv[1:] == ["--only", "int8"]:
         r8 = O.load_ref_int8()
         assert r8 is not None, "oracle/_ref/libref_int8.so is missing: run make -C oracle"
@@ -334,6 +386,11 @@ if __name__ == "__main__":
         r = O.load_ref()
         assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
         golden_c5_full(r)
+        sys.exit(0)
+    if sys.argv[1:] == ["--only", "c5kv"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_c5_kv(r)
         sys.exit(0)
     if sys.argv[1:] == ["--only", "c5"]:
         r = O.load_ref()

@@ -88,6 +88,8 @@ def _load_oracle() -> C.CDLL:
         "orc_matmat": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
         "orc_matmat_mt": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P, _SZ]),
         "orc_project": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "orc_matvec_avx2": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
+        "orc_project_avx2": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
         "orc_threads_init": (C.c_int, [C.c_int]),
         "orc_threads_count": (C.c_int, []),
         "orc_threads_shutdown": (None, []),
@@ -184,13 +186,14 @@ def load_ref():
     return lib
 
 
-def load_ref_int8():
+def load_ref_int8(sdot: str = "1"):
     """ingot's kernels from an AVX2 + FMA build of the reference sources, with
     the int8 lane switched on for the matvec too (INGOT_SDOT=1, read once by
-    the library on its first call); None when not built on this machine."""
+    the library on its first call; sdot="0" keeps the matvec on its f32 AVX2
+    lanes); None when not built on this machine."""
     if not os.path.exists(REF_INT8_SO):
         return None
-    os.environ["INGOT_SDOT"] = "1"
+    os.environ["INGOT_SDOT"] = sdot
     lib = C.CDLL(REF_INT8_SO)
     sig = {
         "ingot_q4_k_matvec": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
@@ -199,6 +202,7 @@ def load_ref_int8():
         "ingot_q4_k_matmat_exact": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_q5_k_matmat": (C.c_int, [_P, _SZ, _SZ, _P, _P, _SZ]),
         "ingot_matmat_is_exact": (C.c_int, [_SZ]),
+        "ingot_matvec": (C.c_int, [C.c_int, _P, _SZ, _SZ, _P, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -271,6 +275,18 @@ def normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray
 def matvec(qtype, w, rows, cols, x) -> np.ndarray:
     y = np.empty(rows, np.float32)
     assert orc.orc_matvec(qtype, ptr(w), rows, cols, ptr(x), ptr(y)) == 0
+    return y
+
+
+def matvec_avx2(qtype, w, rows, cols, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    assert orc.orc_matvec_avx2(qtype, ptr(w), rows, cols, ptr(x), ptr(y)) == 0
+    return y
+
+
+def project_avx2(qtype, w, rows, cols, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    assert orc.orc_project_avx2(qtype, ptr(w), rows, cols, ptr(x), ptr(y)) == 0
     return y
 
 

@@ -286,3 +286,23 @@ def test_qwen3_4b_prompt_golden():
         out.append(tok)
         tok = int(np.argmax(orc.forward(tok)))
     assert out == [int(t) for t in g["tokens"]]
+
+
+def test_qwen3_4b_kv2048_golden():
+    """The oracle's forward at configs[4]'s context (2048 cached positions, the
+    CPU baseline's 4B decode leg) against the compiled reference on the same
+    inputs: the first step's logits by SHA-256, its greedy id."""
+    g = np.load(os.path.join(GOLDEN, "qwen3_4b_kv2048.npz"), allow_pickle=False)
+    O.orc.orc_threads_init(0)
+    shape, npre = CF.QWEN3_4B, CF.C5_CPU_KV
+    model = O.SynthModel(shape, 0)
+    assert sha(model.blob) == str(g["blob_sha"])
+    orc = O.OracleQwen3(model, npre + 2)
+    k, v = O.kv_prefill(O.substream, shape, 0, npre)
+    orc.prefill_kv(k, v, npre)
+    del k, v
+    first = O.first_token(0, shape.vocab)
+    assert first == int(g["first"])
+    lg = orc.forward(first)
+    assert sha(lg) == str(g["logits0_sha"])
+    assert int(O.orc.orc_argmax(O.ptr(lg), lg.size)) == int(g["tokens"][0])
