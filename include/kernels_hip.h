@@ -238,6 +238,14 @@ int   mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream
  * product in the exact summation orders; *simds (optional) gets the
  * device's SIMD count. Synchronous; allocates 4 bytes. */
 int   mynah_hip_valu_add_rate(uint32_t iters, float *ns_per_instr, uint32_t *simds);
+/* The products of the exact GEMM's matrix-core instruction (no reference
+ * counterpart; a test hook): per wave w < waves, a[64 w + l] and b[64 w + l]
+ * feed lane l, c the accumulator; prod (zero accumulator), acc (c), mul (the
+ * VALU's a * b) and fused (fmaf(a, b, c)) get 1024 w + 16 l + r for lane l,
+ * register r: block r / 4, row 4 (l / 16) + r % 4, column l % 16. Device
+ * buffers: a, b 64 * waves floats, the rest 1024 * waves. */
+int   mynah_hip_mfma_probe(const float *a, const float *b, const float *c, float *prod,
+                           float *acc, float *mul, float *fused, uint32_t waves, void *stream);
 void *mynah_hip_stream(void);           /* the library's own stream */
 
 /* y[i] = expf(x[i]) for i < n with the bits of the reference's C library

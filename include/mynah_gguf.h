@@ -98,9 +98,9 @@ const void *mynah_gguf_data(const mynah_gguf *g, uint64_t *bytes);
 /* mynah_slm_load + mynah_slm_state_init (src/model.c:177-228,
  * src/arch_qwen3.c:89-131) for the GPU: open `path` (split-aware, as
  * src/model.c:183 opens it), read the config and
- * tensors, build the resident decoder for n_ctx positions (0: the file's
- * context_length, as the reference's server asks, server/main.c:426; the KV
- * cache takes n_layers * n_ctx * kv_dim * 8 bytes of HBM, 12 GB for a 4B
+ * tensors, build the resident decoder for n_ctx positions (0 or above the
+ * file's context_length: context_length, as src/arch_qwen3.c:94 sets it; the
+ * KV cache takes n_layers * n_ctx * kv_dim * 8 bytes of HBM, 12 GB for a 4B
  * model at 40960), unmap. NULL with the reason in err. */
 mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *err, size_t errsz);
 

@@ -246,3 +246,35 @@ mynah_gemm_fold(const float *__restrict__ part, const float *res, float *y, uint
     for (; u < units; u++) acc = acc + part[(size_t)u * n + i];
     y[i] = res ? res[i] + acc : acc;
 }
+
+// Test hook for the product claim at the top of this file (no reference
+// counterpart). Per workgroup (one wave): 64 values of a and of b, lane l
+// feeding A and B of block l / 16 at row / column l % 16, and 1024 of c.
+// prod = the instruction with a zero accumulator, acc = the same with c as
+// the accumulator; mul and fused = the VALU's a * b and fmaf(a, b, c) of the
+// same operand pairs. Every output is in the instruction's layout: lane l,
+// register r holds block r / 4, row 4 (l / 16) + r % 4, column l % 16, at
+// index 1024 blockIdx + 16 l + r.
+extern "C" __global__ void __launch_bounds__(64)
+mynah_mfma_probe(const float *__restrict__ a, const float *__restrict__ b,
+                 const float *__restrict__ c, float *__restrict__ prod,
+                 float *__restrict__ acc, float *__restrict__ mul, float *__restrict__ fused) {
+#pragma clang fp contract(off)
+    const uint32_t l = threadIdx.x;
+    const size_t base = 64u * (size_t)blockIdx.x, out = 16u * (base + l);
+    const gf_f32x16 zero = {};
+    gf_f32x16 cv;
+#pragma unroll
+    for (int r = 0; r < 16; r++) cv[r] = c[out + r];
+    const gf_f32x16 p = __builtin_amdgcn_mfma_f32_16x16x1f32(a[base + l], b[base + l], zero, 0, 0, 0);
+    const gf_f32x16 q = __builtin_amdgcn_mfma_f32_16x16x1f32(a[base + l], b[base + l], cv, 0, 0, 0);
+#pragma unroll
+    for (uint32_t r = 0; r < 16; r++) {
+        const uint32_t blk = r / 4u, row = 4u * (l / 16u) + r % 4u, col = l % 16u;
+        const float x = a[base + 16u * blk + row], y = b[base + 16u * blk + col];
+        prod[out + r] = p[r];
+        acc[out + r] = q[r];
+        mul[out + r] = x * y;
+        fused[out + r] = __builtin_fmaf(x, y, cv[r]);
+    }
+}

@@ -19,6 +19,7 @@
 #include "mynah_gguf.h"
 #include "runtime_internal.h"
 
+#include <ctype.h>
 #include <fcntl.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -525,26 +526,34 @@ mynah_gguf *mynah_gguf_open(const char *path, char *err, size_t errsz) {
     return open_paths(&one, 1, err, errsz);
 }
 
-/* <prefix>-NNNNN-of-MMMMM.gguf with 1 <= NNNNN <= MMMMM <= 999 and MMMMM >= 2
- * (llama.cpp's split naming, read as third_party/ingot/src/gguf.c:466-509
- * reads it): the number of shards and the length of the prefix, else 0. */
+/* Shard names end in "-NNNNN-of-MMMMM.gguf": shard NNNNN of MMMMM, both
+ * zero-padded five-digit decimals, shards counted from 1, at most 999 of them
+ * (llama.cpp's gguf-split naming, which third_party/ingot/src/gguf.c:466-509
+ * accepts). A name that is not of this form, or names one shard of one, is a
+ * plain single file. Returns the shard count and the prefix length, else 0. */
+static int five_digits(const char *s, unsigned *v) {
+    unsigned x = 0;
+    for (int i = 0; i < 5; i++) {
+        if (!isdigit((unsigned char)s[i])) return 0;
+        x = 10u * x + (unsigned)(s[i] - '0');
+    }
+    *v = x;
+    return 1;
+}
+
 static uint32_t split_name(const char *path, size_t *prefix) {
-    const size_t len = strlen(path), tl = 15, sl = 5;      /* "-NNNNN-of-MMMMM", ".gguf" */
-    if (len < tl + sl || strcmp(path + len - sl, ".gguf") != 0) return 0;
-    const char *t = path + len - sl - tl;
-    if (t[0] != '-' || t[6] != '-' || t[7] != 'o' || t[8] != 'f' || t[9] != '-') return 0;
-    unsigned no = 0, total = 0;
-    for (int i = 1; i <= 5; i++) {
-        if (t[i] < '0' || t[i] > '9') return 0;
-        no = no * 10u + (unsigned)(t[i] - '0');
-    }
-    for (int i = 10; i <= 14; i++) {
-        if (t[i] < '0' || t[i] > '9') return 0;
-        total = total * 10u + (unsigned)(t[i] - '0');
-    }
-    if (total < 2 || total > 999 || no < 1 || no > total) return 0;
-    *prefix = (size_t)(t - path);
-    return total;
+    static const char of[] = "-of-", ext[] = ".gguf";
+    enum { OF = sizeof of - 1, EXT = sizeof ext - 1, TAIL = 1 + 5 + OF + 5 + EXT };
+    const size_t len = strlen(path);
+    if (len < TAIL) return 0;
+    const char *p = path + len - TAIL;        /* '-' NNNNN "-of-" MMMMM ".gguf" */
+    unsigned shard, count;
+    if (*p != '-' || !five_digits(p + 1, &shard) || memcmp(p + 6, of, OF) != 0 ||
+        !five_digits(p + 6 + OF, &count) || memcmp(p + 11 + OF, ext, EXT) != 0)
+        return 0;
+    if (count < 2 || count > 999 || shard < 1 || shard > count) return 0;
+    *prefix = len - TAIL;
+    return count;
 }
 
 mynah_gguf *mynah_gguf_open_split(const char *path, char *err, size_t errsz) {
@@ -556,7 +565,7 @@ mynah_gguf *mynah_gguf_open_split(const char *path, char *err, size_t errsz) {
     const uint32_t n = split_name(path, &prefix);
     if (n == 0) return mynah_gguf_open(path, err, errsz);
     char **paths = (char **)calloc(n, sizeof *paths);
-    const size_t plen = prefix + 15 + 5 + 1;
+    const size_t plen = strlen(path) + 1;     /* every shard name is as long */
     mynah_gguf *g = NULL;
     if (paths == NULL) goto oom;
     for (uint32_t i = 0; i < n; i++) {
@@ -776,10 +785,11 @@ mynah_qwen3 *mynah_hip_qwen3_from_gguf(const char *path, uint32_t n_ctx, char *e
             mynah_gguf_tensor_table(g, table, count, &count);
             for (uint32_t i = 0; i < g->n_sh; i++)
                 parts[i] = mynah_gguf_shard_data(g, i, &bytes[i], &at[i]);
-            /* The reference's server asks for the model's own context
-             * (server/main.c:426); a zero context_length means one position
-             * here, which the decoder refuses like any empty context. */
-            if (n_ctx == 0) n_ctx = n_train;
+            /* The state's context as src/arch_qwen3.c:94 sets it: 0 or more
+             * than the file's context_length takes context_length (a zero
+             * context_length leaves no position, which the decoder refuses
+             * like any empty context). */
+            if (n_ctx == 0 || n_ctx > n_train) n_ctx = n_train;
             s = mynah_qwen3_new_parts(&shape, table, count, parts, bytes, at, g->n_sh,
                                       g->concat_bytes, n_ctx, err, errsz);
         }

@@ -1183,6 +1183,20 @@ int mynah_hip_read_dev(const void *src, size_t bytes, void *sink, void *stream) 
                         args);
 }
 
+int mynah_hip_mfma_probe(const float *a, const float *b, const float *c, float *prod,
+                         float *acc, float *mul, float *fused, uint32_t waves, void *stream) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL) return -1;
+    if (a == NULL || b == NULL || c == NULL || prod == NULL || acc == NULL || mul == NULL ||
+        fused == NULL || waves == 0 || waves > 65535u) {
+        mynah_set_error("mfma probe: null buffer or waves outside 1..65535");
+        return -1;
+    }
+    void *args[] = {&a, &b, &c, &prod, &acc, &mul, &fused};
+    return mynah_launch(d, MYNAH_K_MFMA_PROBE, waves, 1, 64, 0,
+                        mynah_stream_or_default(d, stream), args);
+}
+
 int mynah_hip_valu_add_rate(uint32_t iters, float *ns_per_instr, uint32_t *simds) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;

@@ -69,6 +69,7 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_COPY16, "mynah_copy16")                  \
     X(MYNAH_K_READ16, "mynah_read16")                  \
     X(MYNAH_K_VALU_ADD_RATE, "mynah_valu_add_rate")  \
+    X(MYNAH_K_MFMA_PROBE, "mynah_mfma_probe")          \
     X(MYNAH_K_EXPF, "mynah_expf_map")                  \
     X(MYNAH_K_Q8_QUANTIZE, "mynah_q8_quantize")        \
     X(MYNAH_K_Q4K_GEMV_INT8, "mynah_q4k_gemv_int8")    \

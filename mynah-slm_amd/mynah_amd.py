@@ -103,6 +103,7 @@ def _load() -> C.CDLL:
         "mynah_hip_event_destroy": (C.c_int, [_P]),
         "mynah_hip_copy_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_read_dev": (C.c_int, [_P, _SZ, _P, _P]),
+        "mynah_hip_mfma_probe": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, C.c_uint32, _P]),
         "mynah_hip_valu_add_rate": (C.c_int, [C.c_uint32, C.POINTER(C.c_float),
                                               C.POINTER(C.c_uint32)]),
         "mynah_hip_expf_dev": (C.c_int, [_P, _P, _SZ, _P]),
@@ -595,7 +596,8 @@ class Qwen3Decoder:
     @classmethod
     def from_gguf(cls, path: str, n_ctx: int = 0) -> "Qwen3Decoder":
         """The decoder over a GGUF checkpoint (mynah_slm_load, src/model.c:177):
-        n_ctx 0 takes the file's context_length."""
+        n_ctx 0, or above the file's context_length, takes context_length
+        (src/arch_qwen3.c:94)."""
         with GgufFile(path, split=True) as g:
             shape, _ = g.qwen3_shape()
         self = cls.__new__(cls)

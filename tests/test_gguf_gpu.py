@@ -76,6 +76,21 @@ def test_tiny_gguf_decodes_the_golden_tokens(M, tiny, tmp_path):
     assert M.lib.mynah_hip_qwen3_forward(dec.h, 1, None) == -1
 
 
+@pytest.mark.parametrize("ask,have", [(10 * N_CTX, N_CTX), (N_PRE + 3, N_PRE + 3)])
+def test_context_clamped_to_context_length(M, tiny, tmp_path, ask, have):
+    """src/arch_qwen3.c:94: a context above the file's context_length is cut
+    to it, a smaller one is kept; the step after the last position fails."""
+    print(f"[case] from_gguf n_ctx {ask} on context_length {N_CTX}", flush=True)
+    model, k, v, first = tiny
+    dec = M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model)), ask)
+    dec.set_kv(k, v, N_PRE)
+    tok = first
+    for _ in range(have - N_PRE):
+        tok = int(np.argmax(dec.forward(tok)))
+    assert dec.n_past == have
+    assert M.lib.mynah_hip_qwen3_forward(dec.h, tok, None) == -1
+
+
 def test_file_and_table_decoders_bit_identical(M, tiny, tmp_path):
     print("[case] GGUF decoder vs synthetic-table decoder, 6 steps", flush=True)
     model, k, v, first = tiny
@@ -131,9 +146,10 @@ def test_refusals(M, tiny, tmp_path):
     w.tensors.insert(0, ("pad.weight", 0, [2], bytes(8)))
     with pytest.raises(M.HipError, match="16-byte aligned"):
         M.Qwen3Decoder.from_gguf(write(tmp_path, "align8", w))
-    # Any context up to 2^20 positions is taken; beyond it the shape is refused.
+    # A context up to 2^20 positions is taken; a file whose context_length
+    # asks for more is refused.
     with pytest.raises(M.HipError, match="unsupported shape"):
-        M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model)), (1 << 20) + 1)
+        M.Qwen3Decoder.from_gguf(write(tmp_path, "ctx", tiny_writer(model, (1 << 20) + 1)))
     with pytest.raises(M.HipError):
         M.Qwen3Decoder.from_gguf(str(tmp_path / "absent.gguf"))
 
