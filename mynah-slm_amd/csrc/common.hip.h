@@ -77,8 +77,8 @@ MYNAH_DEV double readlane_d(double v, int lane) {
     return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
 }
 
-// Positions per workgroup of the split decode attention (= MYNAH_AS_CH in
-// runtime_internal.h).
+// Positions per workgroup of the generic split decode attention (= MYNAH_AS_CH
+// in runtime_internal.h).
 #define AS_CH 32
 
 // Wave-wide float max (all lanes get the result).

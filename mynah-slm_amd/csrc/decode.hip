@@ -764,41 +764,50 @@ DPV_KERNEL(true, 1, mynah_attn_pv_m)
 
 // ── attention with the positions split across workgroups ───────────────────
 // The same operations as mynah_attn_scores + mynah_attn_out, except that the
-// softmax is taken per chunk of AS_CH positions and the chunks are combined
+// softmax is taken per chunk of CH positions and the chunks are combined
 // afterwards (the split form of src/kernels.c:228-250). mynah_attn_split:
-// workgroup (kvh, c) computes the scores of positions c * AS_CH .. for the
+// workgroup (kvh, c) computes the scores of positions c * CH .. for the
 // group's query heads (same lane order as the reference dot), its chunk max
 // m_c, e_t = expf(s_t - m_c), the double sum l_c of the e_t and the partial
 // o_c = sum e_t v_t (fma chain in t order), and stores (m_c, l_c, o_c).
 // mynah_attn_combine: M = max m_c, w_c = expf(m_c - M), inv = (float)(1 /
 // sum_c w_c l_c), o = sum_c (w_c * inv) o_c in chunk order. Differences from
 // the reference are f32 rounding of the exponentials and of the order of the
-// weighted sum. Split: grid (n_kv_heads, ceil(n_ctx / AS_CH)), block 128 *
+// weighted sum. Split: grid (n_kv_heads, ceil(n_ctx / CH)), block 128 *
 // group; group <= 8, hd == 128. Partials: pm, pl [n_kv][nch_max][group], po
 // [n_kv][nch_max][group][128].
-#define AS_PASS ((AS_CH + 15) / 16)                 // K passes of 16 positions (group >= 2)
-extern "C" __global__ void __launch_bounds__(1024)
-mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
-                 const float *__restrict__ v_layer, const float *__restrict__ q_norm,
-                 const float *__restrict__ k_norm, const float *__restrict__ rope_now,
-                 const uint32_t *__restrict__ pos_ptr,
-                 float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po,
-                 uint32_t nch_max, uint32_t kv_dim, uint32_t group, float eps, float scale,
-                 uint32_t n_ctx, uint32_t spec_chunks) {
+// CH positions per workgroup; G query heads per key head fixed at compile
+// time (block 128 G, K rows loaded in CH / (8 G) passes of 8 G rows), or
+// G = 0: the group given at run time (2 .. 8, block 128 group, CH = 32).
+template <uint32_t CH, uint32_t G>
+MYNAH_DEV void attn_split_body(const float *__restrict__ q, float *__restrict__ k_layer,
+                               const float *__restrict__ v_layer, const float *__restrict__ q_norm,
+                               const float *__restrict__ k_norm, const float *__restrict__ rope_now,
+                               const uint32_t *__restrict__ pos_ptr,
+                               float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po,
+                               uint32_t nch_max, uint32_t kv_dim, uint32_t group_rt, float eps,
+                               float scale, uint32_t n_ctx, uint32_t spec_chunks) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float qn[8][128];
+    constexpr uint32_t GM = G ? G : 8u;                       // most query heads per key head
+    constexpr uint32_t G1 = G ? G : 1u;
+    constexpr uint32_t PASSES = G ? CH / (8u * G1) : (CH + 15u) / 16u;
+    constexpr uint32_t VR = G ? CH / (4u * G1) : (CH * 32u + 255u) / 256u;
+    static_assert(G == 0 || (CH % (8u * G1) == 0 && CH % (4u * G1) == 0), "chunk and group");
+    __shared__ __attribute__((aligned(16))) float qn[GM][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
-    __shared__ __attribute__((aligned(16))) float vs[AS_CH][128];
-    __shared__ __attribute__((aligned(16))) float es[8][AS_CH];
-    __shared__ __attribute__((aligned(16))) float ee[8][AS_CH];
+    __shared__ __attribute__((aligned(16))) float vs[CH][128];
+    __shared__ __attribute__((aligned(16))) float es[GM][CH];
+    __shared__ __attribute__((aligned(16))) float ee[GM][CH];
+    const uint32_t group = G ? G : group_rt;
     const uint32_t pos = pos_ptr[0], n_kv = pos + 1u;
-    const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * AS_CH;
+    const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * CH;
     // Chunks below spec_chunks were live when the launch was enqueued and the
     // position only grows, so their K/V loads go out before the position
     // arrives; the others first learn whether they hold any position at all.
     const bool spec = c < spec_chunks;
     if (!spec && t0 >= n_kv) return;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nthr = blockDim.x;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t nthr = G ? 128u * G : blockDim.x;
     const uint32_t nw = nthr >> 6;                  // 2 * group waves
     // The K rows of the dot lanes and the V rows of the chunk are loaded
     // first (rows clamped into the cache; positions at or past pos are
@@ -807,22 +816,22 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     // holds pos) and the rotation of position pos.
     const uint32_t r = lane >> 4, l = lane & 15u;
     const uint32_t ppp = 4u * nw;                   // positions per pass
-    float kv[AS_PASS][8];
+    float kv[PASSES][8];
 #pragma unroll
-    for (int ps = 0; ps < AS_PASS; ps++) {
-        const uint32_t t = t0 + ppp * (uint32_t)ps + 4u * wave + r;
+    for (uint32_t ps = 0; ps < PASSES; ps++) {
+        const uint32_t t = t0 + ppp * ps + 4u * wave + r;
         const uint32_t row = t < n_ctx ? t : n_ctx - 1u;
         const float *krow = k_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + l;
 #pragma unroll
         for (int j = 0; j < 8; j++) kv[ps][j] = krow[16 * j];
     }
-    float4 vr[(AS_CH * 32 + 255) / 256];
+    float4 vr[VR];
 #pragma unroll
-    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
-        const uint32_t i = tid + nthr * (uint32_t)k;
+    for (uint32_t k = 0; k < VR; k++) {
+        const uint32_t i = tid + nthr * k;
         const uint32_t tr = i >> 5, q4 = i & 31u, t = t0 + tr;
         const uint32_t row = t < n_ctx ? t : n_ctx - 1u;
-        vr[k] = i < AS_CH * 32u
+        vr[k] = (G || i < CH * 32u)
                     ? *(const float4 *)(v_layer + (size_t)row * kv_dim + (size_t)kvh * 128u + 4u * q4)
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
@@ -843,10 +852,10 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         sn = rope_now[64u + lane];
     }
     if (t0 >= n_kv) return;       // a speculative chunk past the position (after a reset)
-    const bool has_pos = pos < t0 + AS_CH;
+    const bool has_pos = pos < t0 + CH;
 #pragma unroll
-    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
-        const uint32_t t = t0 + ((tid + nthr * (uint32_t)k) >> 5);
+    for (uint32_t k = 0; k < VR; k++) {
+        const uint32_t t = t0 + ((tid + nthr * k) >> 5);
         if (t >= n_kv) vr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     const bool kwave = wave == group && has_pos;
@@ -858,9 +867,9 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         w1 = k_norm[lane + 64u];
     }
 #pragma unroll
-    for (int k = 0; k < (AS_CH * 32 + 255) / 256; k++) {
-        const uint32_t i = tid + nthr * (uint32_t)k;
-        if (i < AS_CH * 32u) *(float4 *)(&vs[i >> 5][4u * (i & 31u)]) = vr[k];
+    for (uint32_t k = 0; k < VR; k++) {
+        const uint32_t i = tid + nthr * k;
+        if (G || i < CH * 32u) *(float4 *)(&vs[i >> 5][4u * (i & 31u)]) = vr[k];
     }
     if (qwave || kwave) {
         float y0, y1;
@@ -876,13 +885,15 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
     __syncthreads();
     // Scores, reference dot order, into es[h][t - t0].
 #pragma unroll
-    for (int ps = 0; ps < AS_PASS; ps++) {
-        const uint32_t tl = ppp * (uint32_t)ps + 4u * wave + r, t = t0 + tl;
-        if (tl < AS_CH && t < n_kv) {
+    for (uint32_t ps = 0; ps < PASSES; ps++) {
+        const uint32_t tl = ppp * ps + 4u * wave + r, t = t0 + tl;
+        if ((G || tl < CH) && t < n_kv) {
             float kk[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) kk[j] = t < pos ? kv[ps][j] : kn[16 * j + l];
-            for (uint32_t h = 0; h < group; h++) {
+#pragma unroll
+            for (uint32_t h = 0; h < GM; h++) {
+                if (G == 0 && h >= group) break;
                 float acc = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kk[j], acc);
@@ -892,40 +903,37 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         }
     }
     __syncthreads();
-    // Chunk softmax: thread (h, d) with d < AS_CH turns position d into e.
+    // Chunk softmax: thread (h, d) with d < CH turns position d into e.
     const uint32_t h = tid >> 7, d = tid & 127u;
-    const uint32_t tn = n_kv - t0 < AS_CH ? n_kv - t0 : AS_CH;
+    const uint32_t tn = n_kv - t0 < CH ? n_kv - t0 : CH;
     float m = -__builtin_inff();
     if (h < group) {
 #pragma unroll
-        for (int k = 0; k < AS_CH / 4; k++) {
+        for (uint32_t k = 0; k < CH / 4; k++) {
             const float4 v = *(const float4 *)(&es[h][4 * k]);
-            if ((uint32_t)(4 * k) < tn) m = fmaxf(m, v.x);
-            if ((uint32_t)(4 * k + 1) < tn) m = fmaxf(m, v.y);
-            if ((uint32_t)(4 * k + 2) < tn) m = fmaxf(m, v.z);
-            if ((uint32_t)(4 * k + 3) < tn) m = fmaxf(m, v.w);
+            if (4u * k < tn) m = fmaxf(m, v.x);
+            if (4u * k + 1u < tn) m = fmaxf(m, v.y);
+            if (4u * k + 2u < tn) m = fmaxf(m, v.z);
+            if (4u * k + 3u < tn) m = fmaxf(m, v.w);
         }
-        if (d < AS_CH) ee[h][d] = d < tn ? mynah_expf(es[h][d] - m) : 0.0f;
+        if (d < CH) ee[h][d] = d < tn ? mynah_expf(es[h][d] - m) : 0.0f;
     }
     __syncthreads();
     // Partial weighted sum (fma chain in t order) and the chunk's exp sum.
+    // Positions past n_kv have e = 0 and v = 0, so they leave both sums
+    // unchanged; the exp sum runs as four interleaved double chains.
     if (h < group) {
-        float e[AS_CH], vv[AS_CH];
-#pragma unroll
-        for (int k = 0; k < AS_CH / 4; k++) {
-            const float4 v = *(const float4 *)(&ee[h][4 * k]);
-            e[4 * k] = v.x; e[4 * k + 1] = v.y; e[4 * k + 2] = v.z; e[4 * k + 3] = v.w;
-        }
-#pragma unroll
-        for (int t = 0; t < AS_CH; t++) vv[t] = vs[t][d];
-        // Positions past n_kv have e = 0 and v = 0, so they leave both sums
-        // unchanged; the exp sum runs as four interleaved double chains.
         float o = 0.0f;
         double l4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int t = 0; t < AS_CH; t++) {
-            o = __builtin_fmaf(vv[t], e[t], o);
-            l4[t & 3] += (double)e[t];
+        for (uint32_t k = 0; k < CH / 4; k++) {
+            const float4 e = *(const float4 *)(&ee[h][4 * k]);
+            const float ev[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                o = __builtin_fmaf(vs[4 * k + u][d], ev[u], o);
+                l4[u] += (double)ev[u];
+            }
         }
         const double lsum = (l4[0] + l4[1]) + (l4[2] + l4[3]);
         const size_t slot = ((size_t)kvh * nch_max + c) * group + h;
@@ -936,6 +944,30 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
         }
     }
 }
+
+#define AS_ARGS                                                                                    \
+    const float *__restrict__ q, float *__restrict__ k_layer, const float *__restrict__ v_layer,   \
+        const float *__restrict__ q_norm, const float *__restrict__ k_norm,                        \
+        const float *__restrict__ rope_now, const uint32_t *__restrict__ pos_ptr,                  \
+        float *__restrict__ pm, double *__restrict__ pl, float *__restrict__ po, uint32_t nch_max, \
+        uint32_t kv_dim, uint32_t group, float eps, float scale, uint32_t n_ctx,                   \
+        uint32_t spec_chunks
+#define AS_PASS_ARGS q, k_layer, v_layer, q_norm, k_norm, rope_now, pos_ptr, pm, pl, po, nch_max, \
+                     kv_dim, group, eps, scale, n_ctx, spec_chunks
+
+extern "C" __global__ void __launch_bounds__(1024) mynah_attn_split(AS_ARGS) {
+    attn_split_body<AS_CH, 0>(AS_PASS_ARGS);
+}
+#define AS_KERNEL(G, CH)                                                                           \
+    extern "C" __global__ void __launch_bounds__(128 * G) mynah_attn_split_g##G##_##CH(AS_ARGS) { \
+        attn_split_body<CH, G>(AS_PASS_ARGS);                                                      \
+    }
+AS_KERNEL(2, 32)
+AS_KERNEL(2, 64)
+AS_KERNEL(2, 128)
+AS_KERNEL(4, 32)
+AS_KERNEL(4, 64)
+AS_KERNEL(4, 128)
 
 // Grid n_heads, block 256: four waves combine the chunks of one query head.
 // Thread c (and c + 256, ...) takes chunk c's max and exp sum: M = max m_c,
@@ -954,7 +986,8 @@ mynah_attn_split(const float *__restrict__ q, float *__restrict__ k_layer,
 extern "C" __global__ void __launch_bounds__(256)
 mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                    const double *__restrict__ pl, const float *__restrict__ po,
-                   float *__restrict__ out, uint32_t nch_max, uint32_t group, uint32_t wave0_max) {
+                   float *__restrict__ out, uint32_t nch_max, uint32_t group, uint32_t wave0_max,
+                   uint32_t ch) {
 #pragma clang fp contract(off)
     extern __shared__ float wsc[];
     __shared__ float smax[AC_WAVES];
@@ -980,7 +1013,7 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
     const uint32_t c1 = 64u + lane;
     const float pm1 = wave == 0u && c1 < nch_max ? pm[base + (size_t)c1 * group] : 0.0f;
     const double pl1 = wave == 0u && c1 < nch_max ? pl[base + (size_t)c1 * group] : 0.0;
-    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + ch - 1u) / ch;
     float inv;
     if (nch <= wave0_max) {          // wave0_max <= 128
         // Wave 0 alone finds M and L: lane l holds chunks l and 64 + l, whose
@@ -1090,7 +1123,8 @@ mynah_attn_combine(const uint32_t *__restrict__ pos_ptr, const float *__restrict
 template <int MAXC, int DPL>
 MYNAH_DEV void attn_combine_waves(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                                   const double *__restrict__ pl, const float *__restrict__ po,
-                                  float *__restrict__ out, uint32_t nch_max, uint32_t group) {
+                                  float *__restrict__ out, uint32_t nch_max, uint32_t group,
+                                  uint32_t ch) {
 #pragma clang fp contract(off)
     constexpr uint32_t SETS = (MAXC + 63) / 64;
     const uint32_t head = blockIdx.x, kvh = head / group, h = head - kvh * group;
@@ -1114,7 +1148,7 @@ MYNAH_DEV void attn_combine_waves(const uint32_t *__restrict__ pos_ptr, const fl
         pmv[k] = c < nch_max ? pm[base + (size_t)c * group] : 0.0f;
         plv[k] = c < nch_max ? pl[base + (size_t)c * group] : 0.0;
     });
-    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + AS_CH - 1u) / AS_CH;
+    const uint32_t n_kv = pos_ptr[0] + 1u, nch = (n_kv + ch - 1u) / ch;
     float m = -__builtin_inff();
     static_for<SETS>([&](auto K) {
         constexpr uint32_t k = decltype(K)::value;
@@ -1164,8 +1198,8 @@ MYNAH_DEV void attn_combine_waves(const uint32_t *__restrict__ pos_ptr, const fl
 extern "C" __global__ void __launch_bounds__(64)
 mynah_attn_combine1(const uint32_t *__restrict__ pos_ptr, const float *__restrict__ pm,
                     const double *__restrict__ pl, const float *__restrict__ po,
-                    float *__restrict__ out, uint32_t nch_max, uint32_t group) {
-    attn_combine_waves<AC1_MAX, 2>(pos_ptr, pm, pl, po, out, nch_max, group);
+                    float *__restrict__ out, uint32_t nch_max, uint32_t group, uint32_t ch) {
+    attn_combine_waves<AC1_MAX, 2>(pos_ptr, pm, pl, po, out, nch_max, group, ch);
 }
 
 // src/kernels.c:118-128 (the final norm before the head,

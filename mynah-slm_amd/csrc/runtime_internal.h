@@ -54,6 +54,12 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_ATTN_PV_4, "mynah_attn_pv_4")            \
     X(MYNAH_K_ATTN_PV_M, "mynah_attn_pv_m")            \
     X(MYNAH_K_ATTN_SPLIT, "mynah_attn_split")          \
+    X(MYNAH_K_ATTN_SPLIT_G2_32, "mynah_attn_split_g2_32") \
+    X(MYNAH_K_ATTN_SPLIT_G2_64, "mynah_attn_split_g2_64") \
+    X(MYNAH_K_ATTN_SPLIT_G2_128, "mynah_attn_split_g2_128") \
+    X(MYNAH_K_ATTN_SPLIT_G4_32, "mynah_attn_split_g4_32") \
+    X(MYNAH_K_ATTN_SPLIT_G4_64, "mynah_attn_split_g4_64") \
+    X(MYNAH_K_ATTN_SPLIT_G4_128, "mynah_attn_split_g4_128") \
     X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
     X(MYNAH_K_ATTN_COMBINE1, "mynah_attn_combine1")    \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
@@ -88,7 +94,9 @@ enum {
 
 #define MYNAH_MAX_DEVICES 16
 
-/* Positions per workgroup of the split attention (decode.hip AS_CH). */
+/* Positions per workgroup of the generic split attention kernel (decode.hip
+ * AS_CH); the kernels for 2 and 4 query heads per key head take 32, 64 or
+ * 128, chosen by the context length. */
 /* Dimensions per workgroup of the exact attention's PV kernel (= PV_SW in
  * decode.hip). */
 #define MYNAH_PV_SW 16

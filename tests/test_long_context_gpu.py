@@ -113,16 +113,27 @@ def test_prefill_past_4096_equals_stepwise(M):
     assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
 
 
-def test_split_attention_refused_past_its_combine_limit(M):
-    """n_ctx 524,289 needs 16,385 chunks, one more than the combine's 64 KiB
-    of per-chunk weights: the split mode is refused before any launch and
-    the exact mode (the default) still decodes."""
+def test_split_attention_refused_past_its_combine_limit(M, monkeypatch):
+    """The combine keeps one weight per chunk in 64 KiB of LDS: 16,384 chunks.
+    Forced to 32-position chunks (MYNAH_AS_CH=32, read when the decoder is
+    made), n_ctx 524,289 needs one chunk more: the split mode is refused
+    before any launch and the exact mode (the default) still decodes. By
+    default a context that long takes 128-position chunks (4,097 of them),
+    and the split mode decodes."""
     shape = CF.QWEN3_TINY
-    print("[case] tiny decoder at n_ctx 524289: split attention refused", flush=True)
+    print("[case] tiny decoder at n_ctx 524289: split refused with 32-position chunks", flush=True)
     model = M.SynthQwen3(shape, 0)
+    monkeypatch.setenv("MYNAH_AS_CH", "32")
     dec = M.Qwen3Decoder(model, 524289)
     with pytest.raises(M.HipError, match="split attention holds at most 524288"):
         dec.set_attention(M.ATTN_SPLIT)
+    lg = dec.forward(O.first_token(0, shape.vocab))
+    assert np.isfinite(lg).all() and dec.n_past == 1
+    dec.close()
+    monkeypatch.delenv("MYNAH_AS_CH")
+    print("[case] tiny decoder at n_ctx 524289: split with 128-position chunks", flush=True)
+    dec = M.Qwen3Decoder(model, 524289)
+    dec.set_attention(M.ATTN_SPLIT)
     lg = dec.forward(O.first_token(0, shape.vocab))
     assert np.isfinite(lg).all() and dec.n_past == 1
     dec.close()
