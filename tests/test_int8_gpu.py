@@ -187,6 +187,24 @@ def test_matmat_int8_against_oracle(M, rows, cols, tokens):
     np.testing.assert_array_equal(bits(got), bits(orc_matmat_int8(w, rows, cols, x, tokens)))
 
 
+@pytest.mark.parametrize("i", [i for i, m in enumerate(CF.C4) if m.qtype == CF.Q4_K])
+def test_matmat_int8_configs3_against_oracle(M, i):
+    """The five Q4_K products of configs[3] at 512 tokens, on the inputs
+    bench.py times (weights and activations from the config's seeds)."""
+    m = CF.C4[i]
+    say("matmat int8 configs[3]", m.rows, m.cols, CF.C4_TOKENS)
+    wseed, _ = CF.matrix_seeds(M.substream, 0, i)
+    w = M.synth_blocks(m.qtype, wseed, m.rows, m.cols)
+    x = M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i), CF.C4_TOKENS * m.cols)
+    M.set_int8(M.INT8_BATCHED)
+    try:
+        got = M.matmat(CF.Q4_K, w, m.rows, m.cols, x, CF.C4_TOKENS)
+    finally:
+        M.set_int8(M.INT8_OFF)
+    np.testing.assert_array_equal(bits(got),
+                                  bits(orc_matmat_int8(w, m.rows, m.cols, x, CF.C4_TOKENS)))
+
+
 @pytest.mark.parametrize("rows,cols,tokens", [(100, 2048, 70), (2048, 2048, 512), (77, 9728, 213),
                                               (1027, 4096, 33)])
 def test_q5k_matmat_int8_against_oracle(M, rows, cols, tokens):
