@@ -106,10 +106,12 @@ int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s);
  *   MYNAH_ATTN_EXACT (default): the reference's operations in its order — the
  *     full softmax over all positions, then o = fma(v_t, p_t, o) for t in
  *     order; two launches per layer;
- *   MYNAH_ATTN_SPLIT: positions split across workgroups, per-chunk softmax
- *     partials combined by a second small launch; short FMA chains; differs
- *     from the reference by f32 rounding only; refused (-1) for n_ctx above
- *     524,288 (the combine's per-chunk weights fill 64 KiB of LDS there). */
+ *   MYNAH_ATTN_SPLIT: positions split across workgroups (32-position chunks
+ *     up to n_ctx 32,768, 64 up to 65,536, 128 beyond; MYNAH_AS_CH forces
+ *     one when the decoder is made), per-chunk softmax partials combined by
+ *     a second small launch; short FMA chains; differs from the reference by
+ *     f32 rounding only; refused (-1) past 16,384 chunks (the combine's
+ *     per-chunk weights fill 64 KiB of LDS there). */
 enum { MYNAH_ATTN_EXACT = 0, MYNAH_ATTN_SPLIT = 1 };
 int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode);
 
