@@ -502,9 +502,12 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // dependent v_fmac_f32 costs about 8.7 cycles on gfx950). A workgroup takes
 // one query head and a slice of DPV_SW = 16 of its dimensions: lane l of wave
 // 0 carries the chain of dimension l % DPV_SW (lanes DPV_SW and up repeat the
-// first ones and are not stored), reading V (rows of DPV_SW floats in LDS)
-// and four probabilities per ds_read_b128 (every lane the same address),
-// eight groups of four positions ahead. V of the slice streams through a
+// first ones and are not stored), reading four positions of its dimension
+// (V in LDS dimension-major, rows padded by four floats so the loaders'
+// transposing stores and the chain's reads hit 64 distinct banks) and their
+// four probabilities (every lane the same address) with one ds_read_b128
+// each, eight groups of four positions ahead: the chain's wave issues two LDS
+// reads per four FMAs, whose issue cycles add to the chain. V of the slice streams through a
 // ring of three LDS chunks of DPV_CH positions, filled by four loader waves
 // that keep up to DPV_WIN chunks in flight in registers, one barrier per
 // chunk; narrow slices keep each CU's share of V (and its load issue) small
@@ -537,7 +540,8 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
 #pragma clang fp contract(off)
     constexpr uint32_t RQ = DPV_SW / 4u;                    // float4 per row of the slice
     constexpr uint32_t NV = DPV_CH * DPV_SW / 4u / 256u;     // float4 of V per loader thread per chunk
-    __shared__ __attribute__((aligned(16))) v4f vbuf[DPV_NBUF][DPV_CH * RQ];   // [t][DPV_SW]
+    constexpr uint32_t VST = DPV_CH + 4u;                   // floats per dimension row
+    __shared__ __attribute__((aligned(16))) float vbuf[DPV_NBUF][DPV_SW * VST];   // [dim][t]
     __shared__ __attribute__((aligned(16))) float pl[PMEM ? DPV_NBUF * DPV_CH : 1024 * KS];
     __shared__ uint64_t etab[4][32];
     __shared__ float wmax[4];
@@ -560,8 +564,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         // Group m of chunk c: positions DPV_CH c + 4 m .. + 3 of this lane's
         // dimension and their probabilities.
         auto vsrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
-            const float *vc = (const float *)vbuf[c % DPV_NBUF] + 4u * DPV_SW * m + d;
-            return make_float4(vc[0], vc[DPV_SW], vc[2u * DPV_SW], vc[3u * DPV_SW]);
+            return *(const float4 *)(vbuf[c % DPV_NBUF] + d * VST + 4u * m);
         };
         auto psrc = [&](uint32_t c, uint32_t m) __attribute__((always_inline)) {
             return *(const float4 *)(PMEM ? pl + (c % DPV_NBUF) * DPV_CH + 4u * m
@@ -600,9 +603,9 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
                 __builtin_amdgcn_sched_barrier(0);
             } else {
                 // The last chunk, partial: straight from LDS.
-                const float *vc = (const float *)vbuf[c % DPV_NBUF] + d;
+                const float *vc = vbuf[c % DPV_NBUF] + d * VST;
                 const float *pc = PMEM ? pl + (c % DPV_NBUF) * DPV_CH : pl + c * DPV_CH;
-                for (uint32_t t = 0; t < tn; t++) acc = __builtin_fmaf(vc[DPV_SW * t], pc[t], acc);
+                for (uint32_t t = 0; t < tn; t++) acc = __builtin_fmaf(vc[t], pc[t], acc);
             }
             __syncthreads();
         }
@@ -632,7 +635,14 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     };
     auto store = [&](const v4f *v4, const v4f &p4, uint32_t c) __attribute__((always_inline)) {
 #pragma unroll
-        for (uint32_t q = 0; q < NV; q++) vbuf[c % DPV_NBUF][lt + 256u * q] = v4[q];
+        for (uint32_t q = 0; q < NV; q++) {
+            const uint32_t i = lt + 256u * q, t = i / RQ, d0 = 4u * (i % RQ);
+            float *dst = vbuf[c % DPV_NBUF] + d0 * VST + t;
+            dst[0] = v4[q].x;
+            dst[VST] = v4[q].y;
+            dst[2u * VST] = v4[q].z;
+            dst[3u * VST] = v4[q].w;
+        }
         if constexpr (PMEM) {
             if (lt < DPV_CH / 4u) *(v4f *)(pl + (c % DPV_NBUF) * DPV_CH + 4u * lt) = p4;
         }
