@@ -437,11 +437,6 @@ static uint32_t prefetch_wgs(void) {
     return v > 0 && v <= 4096 ? (uint32_t)(v & ~7L) : 0u;
 }
 
-/* The exact attention's PV kernel for this state, or -1 for the eight-lane
- * kernels (MYNAH_ATTN_PV=0, or head_dim other than 128). Up to 4096
- * positions the softmax runs inside it, with 1024 scores per float4 column
- * of its four loader waves (1 to 4 columns by n_ctx); longer contexts read
- * the probabilities from the scores rows, normalised in place first. */
 /* Chunk size of the split attention: the kernels for 2 and 4 query heads per
  * key head take 32 positions up to a 32768-position context (1,024 chunks),
  * 64 up to 65536 and 128 beyond (MYNAH_AS_CH=32|64|128 forces one); other
@@ -466,12 +461,18 @@ static void split_plan(mynah_qwen3 *s, const mynah_qwen3_shape *c, uint32_t n_ct
     }
 }
 
+/* The exact attention's PV kernel for this state, or -1 for the eight-lane
+ * kernels (MYNAH_ATTN_PV=0, or head_dim other than 128). Up to 4 columns of
+ * 256 * MYNAH_PV_LW scores (one float4 per loader thread and column) the
+ * softmax runs inside it; longer contexts read the probabilities from the
+ * scores rows, normalised in place first. */
 static int pv_kernel(const mynah_qwen3 *s) {
+    const uint32_t col = 256u * MYNAH_PV_LW;
     if (env_or("MYNAH_ATTN_PV", 1) == 0 || s->c.head_dim != 128) return -1;
-    if (s->n_ctx > 4096) return MYNAH_K_ATTN_PV_M;
+    if (s->n_ctx > 4u * col) return MYNAH_K_ATTN_PV_M;
     static const int by_cols[4] = {MYNAH_K_ATTN_PV_1, MYNAH_K_ATTN_PV_2, MYNAH_K_ATTN_PV_3,
                                    MYNAH_K_ATTN_PV_4};
-    return by_cols[(s->n_ctx - 1u) / 1024u];
+    return by_cols[(s->n_ctx - 1u) / col];
 }
 
 static uint32_t prefetch_step(void) {
@@ -597,7 +598,8 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
                     void *args1[] = {&sc, &pos, &sstride};
                     rc = mynah_launch(d, MYNAH_K_ATTN_SOFTMAX, c->n_heads, 1, 64, 0, st, args1);
                 }
-                rc = rc ? rc : mynah_launch(d, pv, c->n_heads * (128u / MYNAH_PV_SW), 1, 320, 0,
+                rc = rc ? rc : mynah_launch(d, pv, c->n_heads * (128u / MYNAH_PV_SW), 1,
+                                            64u * (1u + MYNAH_PV_LW), 0,
                                             st, args3);
             } else if ((size_t)group * sstride * 4 <= EXACT_LDS_SCORES) {
                 rc = mynah_launch(d, MYNAH_K_ATTN_OUT, c->n_kv_heads, c->head_dim / 8, 64 * group,

@@ -512,7 +512,7 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // that keep up to DPV_WIN chunks in flight in registers, one barrier per
 // chunk; narrow slices keep each CU's share of V (and its load issue) small
 // beside the chain. The probabilities are either computed by the loader
-// waves into LDS (PMEM = false, n_kv <= 1024 KS: the softmax of
+// waves into LDS (PMEM = false, n_kv <= 256 DPV_LW KS: the softmax of
 // src/kernels.c:207-220 over the four waves — f32 max, expf, a double sum
 // per lane, per wave (wave_sum_d) and then of the four waves in order,
 // product with the f32 reciprocal) or read, normalised by
@@ -521,9 +521,12 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // key head kvh = b % n_kv_heads, query head kvh * group + (b / n_kv_heads) %
 // group and slice b / (n_kv_heads * group), so every workgroup of a key head
 // runs on the XCD b % 8 names when n_kv_heads is 8 and shares its V rows in
-// that L2; block 320; hd == 128.
+// that L2; block 64 (1 + DPV_LW); hd == 128.
 #define DPV_SW 16
 #define DPV_CH (4096 / DPV_SW)
+#ifndef DPV_LW
+#define DPV_LW 4                                          // loader waves (= MYNAH_PV_LW)
+#endif
 #define DPV_NBUF 3
 #define DPV_WIN 4
 // A native 4-float vector: arrays of it stay in registers (copies of the
@@ -539,13 +542,14 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
                             uint32_t n_kv_heads, uint32_t group) {
 #pragma clang fp contract(off)
     constexpr uint32_t RQ = DPV_SW / 4u;                    // float4 per row of the slice
-    constexpr uint32_t NV = DPV_CH * DPV_SW / 4u / 256u;     // float4 of V per loader thread per chunk
+    constexpr uint32_t NL = 64u * DPV_LW;                    // loader threads
+    constexpr uint32_t NV = DPV_CH * DPV_SW / 4u / NL;      // float4 of V per loader thread per chunk
     constexpr uint32_t VST = DPV_CH + 4u;                   // floats per dimension row
     __shared__ __attribute__((aligned(16))) float vbuf[DPV_NBUF][DPV_SW * VST];   // [dim][t]
-    __shared__ __attribute__((aligned(16))) float pl[PMEM ? DPV_NBUF * DPV_CH : 1024 * KS];
-    __shared__ uint64_t etab[4][32];
-    __shared__ float wmax[4];
-    __shared__ double wsum[4];
+    __shared__ __attribute__((aligned(16))) float pl[PMEM ? DPV_NBUF * DPV_CH : 4u * NL * KS];
+    __shared__ uint64_t etab[DPV_LW][32];
+    __shared__ float wmax[DPV_LW];
+    __shared__ double wsum[DPV_LW];
     const uint32_t n_kv = pos + 1u;
     const uint32_t b = blockIdx.x, kvh = b % n_kv_heads, rest = b / n_kv_heads;
     const uint32_t head = kvh * group + rest % group, slice = rest / group;
@@ -613,7 +617,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         return;
     }
 
-    // Loader waves 1 .. 4: chunk c is fetched into register slot c % DPV_WIN
+    // Loader waves 1 .. DPV_LW: chunk c is fetched into register slot c % DPV_WIN
     // DPV_WIN chunks before it is stored into buffer c % DPV_NBUF (two
     // iterations before the chain reads it). Rows past the position read the
     // last row, whose copies the chain never reads, so the loads have no
@@ -624,7 +628,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     auto fetch = [&](v4f *v4, v4f &p4, uint32_t c) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t q = 0; q < NV; q++) {
-            const uint32_t i = lt + 256u * q, t = c * DPV_CH + i / RQ;
+            const uint32_t i = lt + NL * q, t = c * DPV_CH + i / RQ;
             const uint32_t tt = t < n_kv ? t : n_kv - 1u;
             v4[q] = *(const v4f *)(vcol + (size_t)tt * kv_dim + 4u * (i % RQ));
         }
@@ -636,7 +640,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     auto store = [&](const v4f *v4, const v4f &p4, uint32_t c) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t q = 0; q < NV; q++) {
-            const uint32_t i = lt + 256u * q, t = i / RQ, d0 = 4u * (i % RQ);
+            const uint32_t i = lt + NL * q, t = i / RQ, d0 = 4u * (i % RQ);
             float *dst = vbuf[c % DPV_NBUF] + d0 * VST + t;
             dst[0] = v4[q].x;
             dst[VST] = v4[q].y;
@@ -648,7 +652,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         }
     };
     if constexpr (!PMEM) {
-        // The expf table, the scores (float4 lt + 256 k of the row, index
+        // The expf table, the scores (float4 lt + NL k of the row, index
         // clamped into the row's positions) and the first two chunks of V go
         // out first; the rest of V once the scores are in.
         const float4 *sc = (const float4 *)prow;
@@ -658,7 +662,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         const uint64_t tv = mynah_exp2_tab[lane & 31u];
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            const uint32_t i = lt + 256u * (uint32_t)k;
+            const uint32_t i = lt + NL * (uint32_t)k;
             sv[k] = sc[i < n4 ? i : n4 - 1u];
         }
         fetch(vr[0], pr[0], 0);
@@ -669,7 +673,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         float m = ninf;
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            const uint32_t t = 4u * (lt + 256u * (uint32_t)k);
+            const uint32_t t = 4u * (lt + NL * (uint32_t)k);
             float4 v = sv[k];
             v.x = t < n_kv ? v.x : ninf;
             v.y = t + 1u < n_kv ? v.y : ninf;
@@ -685,7 +689,9 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
             constexpr uint32_t W = decltype(w)::value + 2u;
             fetch(vr[W], pr[W], W);
         });
-        m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        m = wmax[0];
+#pragma unroll
+        for (uint32_t w = 1; w < DPV_LW; w++) m = fmaxf(m, wmax[w]);
         double acc = 0.0;
 #pragma unroll
         for (int k = 0; k < KS; k++) {
@@ -706,10 +712,13 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         acc = wave_sum_d(acc);
         if (lane == 0) wsum[lw] = acc;
         __syncthreads();
-        const float inv = (float)(1.0 / (((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]));
+        double lsum = wsum[0];
+#pragma unroll
+        for (uint32_t w = 1; w < DPV_LW; w++) lsum = lsum + wsum[w];
+        const float inv = (float)(1.0 / lsum);
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            const uint32_t i = lt + 256u * (uint32_t)k;
+            const uint32_t i = lt + NL * (uint32_t)k;
             if (i < n4) {
                 const float4 e = sv[k];
                 *(float4 *)(pl + 4u * i) = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
@@ -739,7 +748,7 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         __syncthreads();
     };
     if constexpr (!PMEM) {
-        steps_until<0, 1024u * KS / DPV_CH>(nc, [&](auto ci) __attribute__((always_inline)) {
+        steps_until<0, 4u * NL * KS / DPV_CH>(nc, [&](auto ci) __attribute__((always_inline)) {
             constexpr uint32_t c = decltype(ci)::value;
             step(Index<c % DPV_WIN>{}, c);
         });
@@ -757,14 +766,14 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
 }
 
 #define DPV_KERNEL(PMEM, KS, NAME)                                                             \
-    extern "C" __global__ void __launch_bounds__(320)                                         \
+    extern "C" __global__ void __launch_bounds__(64 * (1 + DPV_LW))                           \
     NAME(const float *v_layer, const float *sp, const uint32_t *__restrict__ pos_ptr,         \
          float *__restrict__ out, uint32_t sstride, uint32_t kv_dim, uint32_t n_kv_heads,     \
          uint32_t group) {                                                                    \
         attn_pv_body<PMEM, KS>(v_layer, sp, pos_ptr[0], out, sstride, kv_dim, n_kv_heads,     \
                                group);                                                        \
     }
-// Probabilities in LDS: KS float4 of scores per loader thread cover n_ctx <= 1024 KS.
+// Probabilities in LDS: KS float4 of scores per loader thread cover n_ctx <= 256 DPV_LW KS.
 DPV_KERNEL(false, 1, mynah_attn_pv_1)
 DPV_KERNEL(false, 2, mynah_attn_pv_2)
 DPV_KERNEL(false, 3, mynah_attn_pv_3)

@@ -100,6 +100,10 @@ enum {
 /* Dimensions per workgroup of the exact attention's PV kernel (= PV_SW in
  * decode.hip). */
 #define MYNAH_PV_SW 16
+/* Loader waves of the exact attention's PV kernel (= DPV_LW in decode.hip). */
+#ifndef MYNAH_PV_LW
+#define MYNAH_PV_LW 4
+#endif
 #define MYNAH_AS_CH 32
 /* Most chunks mynah_attn_combine1 (one wave per query head) takes. */
 #define MYNAH_AC1_MAX 32
