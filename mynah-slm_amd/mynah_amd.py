@@ -663,21 +663,23 @@ class Qwen3Decoder:
         return [int(t) for t in out], logits
 
     def generate_tokens(self, prompt, max_new: int, eos=(), sampler=None, chunk: int = 0,
-                        stop_after=None):
+                        stop_after=None, on_token=None):
         """The generation loop (include/mynah_generate.h). `sampler`: None for
         greedy on the device, else an object with a C handle `h` and
         `fn_addresses()` -> (sample, accept). The token callback stops after
-        `stop_after` ids. Returns (ids the callback saw, count the loop
-        returned, timing)."""
+        `stop_after` ids, or when `on_token(id)` (if given) returns true.
+        Returns (ids the callback saw, count the loop returned, timing)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         e = np.ascontiguousarray(list(eos) or [0], dtype=np.uint32)
         seen = []
 
-        def on_token(_ctx, tok):
+        def token_cb(_ctx, tok):
             seen.append(int(tok))
+            if on_token is not None:
+                return 1 if on_token(int(tok)) else 0
             return 1 if stop_after is not None and len(seen) >= stop_after else 0
 
-        cb = TOKEN_FN(on_token)
+        cb = TOKEN_FN(token_cb)
         gp = GenParams()
         gp.prompt, gp.n_prompt, gp.max_new = ptr(p), p.size, max_new
         gp.eos, gp.n_eos = ptr(e), len(eos)

@@ -18,10 +18,13 @@
 #include "ingot/write.h"
 
 #include "arch_qwen3.h"
+#include "generate.h"
 #include "model.h"
 #include "mynah_slm.h"
 #include "sampler.h"
 #include "threads.h"
+#include "timing.h"
+#include "tokenizer.h"
 
 #include "mynah_synth.h"
 
@@ -62,12 +65,30 @@ int ref_has_kernel(int type) { return ingot_has_kernel(type); }
 
 /* Write a random-init Qwen3 (tensor table + blob from mynah_synth_qwen3_*)
  * as a GGUF the reference loader accepts. */
-int ref_write_qwen3_gguf(const char *path, const mynah_qwen3_shape *s,
-                         const mynah_synth_tensor *table, size_t count, const void *blob,
-                         uint32_t n_ctx, char *err, size_t errsz) {
+static int write_qwen3(const char *path, const mynah_qwen3_shape *s,
+                       const mynah_synth_tensor *table, size_t count, const void *blob,
+                       uint32_t n_ctx, int with_vocab, char *err, size_t errsz) {
     ingot_gguf_writer *w = ingot_gguf_writer_new();
     if (w == NULL) { snprintf(err, errsz, "writer alloc"); return -1; }
     int rc = 0;
+    if (with_vocab) {
+        /* A vocabulary for src/tokenizer.c's loader and detokenizer: token i
+         * is the text "t<i>", one merge. */
+        char **tok = (char **)calloc(s->vocab, sizeof *tok);
+        rc = tok ? 0 : -1;
+        for (uint32_t i = 0; i < s->vocab && rc == 0; i++) {
+            tok[i] = (char *)malloc(16);
+            if (tok[i] == NULL) rc = -1;
+            else snprintf(tok[i], 16, "t%u", i);
+        }
+        const char *merges[1] = {"t 0"};
+        if (rc == 0)
+            rc |= ingot_gguf_kv_array_string(w, "tokenizer.ggml.tokens",
+                                             (const char *const *)tok, s->vocab);
+        rc |= ingot_gguf_kv_array_string(w, "tokenizer.ggml.merges", merges, 1);
+        for (uint32_t i = 0; tok && i < s->vocab; i++) free(tok[i]);
+        free(tok);
+    }
     rc |= ingot_gguf_kv_string(w, "general.architecture", "qwen3");
     rc |= ingot_gguf_kv_u32(w, "qwen3.block_count", s->n_layers);
     rc |= ingot_gguf_kv_u32(w, "qwen3.embedding_length", s->d_model);
@@ -92,6 +113,105 @@ int ref_write_qwen3_gguf(const char *path, const mynah_qwen3_shape *s,
     }
     rc = ingot_gguf_writer_save(w, path, err, errsz);
     ingot_gguf_writer_free(w);
+    return rc;
+}
+
+int ref_write_qwen3_gguf(const char *path, const mynah_qwen3_shape *s,
+                         const mynah_synth_tensor *table, size_t count, const void *blob,
+                         uint32_t n_ctx, char *err, size_t errsz) {
+    return write_qwen3(path, s, table, count, blob, n_ctx, 0, err, errsz);
+}
+
+/* The same checkpoint with a vocabulary, for the generation loop. */
+int ref_write_qwen3_gguf_vocab(const char *path, const mynah_qwen3_shape *s,
+                               const mynah_synth_tensor *table, size_t count, const void *blob,
+                               uint32_t n_ctx, char *err, size_t errsz) {
+    return write_qwen3(path, s, table, count, blob, n_ctx, 1, err, errsz);
+}
+
+/* A token callback that records the ids it sees and asks to stop once it
+ * has seen stop_after of them (0: never). */
+typedef struct {
+    uint32_t *ids;
+    size_t cap, n, stop_after;
+} ref_rec;
+
+static int ref_rec_cb(void *ctx, uint32_t id, const char *text, size_t len) {
+    (void)text;
+    (void)len;
+    ref_rec *r = (ref_rec *)ctx;
+    if (r->n < r->cap) r->ids[r->n] = id;
+    r->n++;
+    return r->stop_after != 0 && r->n >= r->stop_after;
+}
+
+/* src/generate.c:13-86 itself, on the checkpoint at `path` (written with a
+ * vocabulary) with a fresh state of n_ctx positions and the reference's
+ * sampler (`sp`; NULL: greedy). The answer channel's callback records into
+ * answer (stopping after stop_after ids when non-zero), the thinking
+ * channel's into think; think_open / think_close -1 disables the split.
+ * Reports the loop's return value, the timing's generated count and the
+ * state's position afterwards. */
+int ref_generate_record(const char *path, uint32_t n_ctx, const uint32_t *prompt,
+                        size_t n_prompt, uint32_t max_new, const uint32_t *eos, size_t n_eos,
+                        long think_open, long think_close, size_t stop_after,
+                        const mynah_slm_sampler_params *sp, uint32_t *answer, size_t answer_cap,
+                        size_t *n_answer, uint32_t *think, size_t think_cap, size_t *n_think,
+                        long *produced, uint32_t *n_gen, uint32_t *n_past, char *err,
+                        size_t errsz) {
+    mynah_slm_threads_init(0);
+    mynah_slm_model_t *m = mynah_slm_load(path, err, errsz);
+    if (m == NULL) return -1;
+    mynah_slm_tokenizer *tok = mynah_slm_tokenizer_load(m->gguf, err, errsz);
+    if (tok == NULL) {
+        mynah_slm_free(m);
+        return -1;
+    }
+    mynah_slm_state st;
+    if (mynah_slm_state_init(&st, m, n_ctx, err, errsz) != 0) {
+        mynah_slm_tokenizer_free(tok);
+        mynah_slm_free(m);
+        return -1;
+    }
+    const mynah_slm_config *c = mynah_slm_model_config(m);
+    mynah_slm_sampler_params greedy;
+    memset(&greedy, 0, sizeof greedy);
+    greedy.temp = 0.0f;
+    greedy.top_p = 1.0f;
+    greedy.repeat_penalty = 1.0f;
+    mynah_slm_sampler *sam = mynah_slm_sampler_new(sp ? sp : &greedy, c->vocab_size);
+    ref_rec ra = {answer, answer_cap, 0, stop_after}, rt = {think, think_cap, 0, 0};
+    mynah_slm_gen_params gp;
+    memset(&gp, 0, sizeof gp);
+    gp.prompt = prompt;
+    gp.n_prompt = n_prompt;
+    gp.max_new = max_new;
+    gp.eos = eos;
+    gp.n_eos = n_eos;
+    gp.cb = ref_rec_cb;
+    gp.cb_ctx = &ra;
+    gp.cb_think = ref_rec_cb;
+    gp.cb_think_ctx = &rt;
+    gp.think_open = think_open;
+    gp.think_close = think_close;
+    mynah_slm_timing tm;
+    mynah_slm_timing_reset(&tm);
+    mynah_slm_timing_start(&tm);
+    int rc = 0;
+    if (sam == NULL) {
+        snprintf(err, errsz, "sampler alloc");
+        rc = -1;
+    } else {
+        *produced = mynah_slm_generate(&st, tok, sam, &gp, &tm);
+        *n_answer = ra.n;
+        *n_think = rt.n;
+        *n_gen = tm.n_gen;
+        *n_past = st.n_past;
+    }
+    if (sam) mynah_slm_sampler_free(sam);
+    mynah_slm_state_free(&st);
+    mynah_slm_tokenizer_free(tok);
+    mynah_slm_free(m);
     return rc;
 }
 

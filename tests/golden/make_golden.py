@@ -41,6 +41,13 @@ records a SHA-256 of the input bytes so generator drift is detected):
                      all-zero block and token counts around the token tile,
                      and Q5_K batched outputs
                      (`--only int8` writes just this file)
+  generate_cases.json  the reference's generation loop (src/generate.c:13-86,
+                     compiled, on the tiny model with a vocabulary): for each
+                     case its prompt, limits, EOS ids, think markers, callback
+                     stop and sampler, and what the loop did — the ids each
+                     channel's callback saw, the count it returned, the
+                     timing's generated count, the state's position
+                     (`--only generate`)
   avx2.npz           the f32 AVX2 + FMA lanes of the same build (INGOT_SDOT=0,
                      in a process of its own): Q4_K, Q6_K and Q8_0 matvec on
                      small shapes, and configs[1]'s sweep as a SHA-256 of each
@@ -236,6 +243,46 @@ def golden_int8(ref8) -> None:
     np.savez_compressed(os.path.join(HERE, "int8.npz"), **out)
 
 
+def generate_cases(ref):
+    """The cases of generate_cases.json, each run through the compiled loop."""
+    shape = CF.QWEN3_TINY
+    model = O.SynthModel(shape, 0)
+    prompt = [int(t) for t in O.uniform(O.substream(6, 1), 9, shape.vocab)]
+    pen = dict(repeat_penalty=1.5, penalty_window=16)
+    temp = dict(temp=0.6, top_k=20, top_p=0.95, seed=7)
+    base = dict(prompt=prompt, n_ctx=64, max_new=20, eos=[], think=[-1, -1], stop_after=0,
+                sampler=None)
+    cases = {"greedy": {}, "context_end": dict(n_ctx=16, max_new=30),
+             "stop_after": dict(stop_after=7), "temperature": dict(sampler=temp),
+             "penalty": dict(max_new=24, sampler=pen)}
+    first = O.ref_generate(ref, model, 64, prompt, 1)["answer"][0]
+    cases["eos_first"] = dict(eos=[5, first])
+    seq = O.ref_generate(ref, model, 64, prompt, 24, sampler=pen)["answer"]
+    k = next(i for i, t in enumerate(seq) if i >= 5 and t not in seq[:i])
+    cases["penalty_eos"] = dict(max_new=24, sampler=pen, eos=[seq[k]])
+    # Think markers: the first occurrences of two ids of the penalised run.
+    a = next(i for i, t in enumerate(seq) if i >= 3 and t not in seq[:i])
+    b = next(i for i, t in enumerate(seq) if i > a + 3 and t not in seq[:i] and t != seq[a])
+    cases["think"] = dict(max_new=24, sampler=pen, think=[seq[a], seq[b]])
+    # The answer callback stops on the first answer id after the block.
+    cases["think_stop"] = dict(max_new=24, sampler=pen, think=[seq[a], seq[b]], stop_after=a + 1)
+    out = {}
+    for name, over in cases.items():
+        c = dict(base, **over)
+        got = O.ref_generate(ref, model, c["n_ctx"], c["prompt"], c["max_new"], eos=c["eos"],
+                             think=tuple(c["think"]), stop_after=c["stop_after"],
+                             sampler=c["sampler"])
+        out[name] = dict(c, want=got)
+    return out
+
+
+def golden_generate(ref) -> None:
+    import json
+    with open(os.path.join(HERE, "generate_cases.json"), "w") as f:
+        json.dump(generate_cases(ref), f, indent=1, sort_keys=True)
+        f.write("\n")
+
+
 AVX2_SHAPES = ((CF.Q4_K, 37, 512), (CF.Q4_K, 64, 2048), (CF.Q6_K, 37, 512),
                (CF.Q6_K, 16, 3072), (CF.Q8_0, 37, 96), (CF.Q8_0, 37, 512))
 
@@ -352,6 +399,7 @@ def main() -> int:
                         blob_sha=np.array(sha(model.blob)))
     golden_forced(ref)
     golden_adjacent(ref)
+    golden_generate(ref)
     r8 = O.load_ref_int8()
     if r8 is not None:
         golden_int8(r8)
@@ -386,6 +434,11 @@ if __name__ == "__main__":
         r = O.load_ref()
         assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
         golden_c5_full(r)
+        sys.exit(0)
+    if sys.argv[1:] == ["--only", "generate"]:
+        r = O.load_ref()
+        assert r is not None, "oracle/_ref/libref.so is missing: run make -C oracle"
+        golden_generate(r)
         sys.exit(0)
     if sys.argv[1:] == ["--only", "c5kv"]:
         r = O.load_ref()

@@ -155,6 +155,14 @@ def load_ref():
         "ref_qwen3_run": (C.c_int, [C.c_char_p, _P, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32,
                                     _P, C.c_uint32, C.c_uint32, C.c_int, _P, _P, C.c_char_p,
                                     _SZ]),
+        "ref_write_qwen3_gguf_vocab": (C.c_int, [C.c_char_p, C.POINTER(SynthShape),
+                                                 C.POINTER(SynthTensor), _SZ, _P, C.c_uint32,
+                                                 C.c_char_p, _SZ]),
+        "ref_generate_record": (C.c_int, [C.c_char_p, C.c_uint32, _P, _SZ, C.c_uint32, _P, _SZ,
+                                          C.c_long, C.c_long, _SZ, _P, _P, _SZ, C.POINTER(_SZ),
+                                          _P, _SZ, C.POINTER(_SZ), C.POINTER(C.c_long),
+                                          C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                          C.c_char_p, _SZ]),
         # ingot's GGUF reader (third_party/ingot/include/ingot/gguf.h:60-130)
         "ingot_gguf_open": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
         "ingot_gguf_open_split": (C.c_int, [C.POINTER(_P), C.c_char_p, C.c_char_p, _SZ]),
@@ -429,12 +437,13 @@ class OracleSampler:
 
 
 def oracle_generate(orc_model: "OracleQwen3", prompt, max_new: int, eos=(), sampler=None,
-                    stop_after=None):
+                    stop_after=None, on_token=None):
     """src/generate.c:13-86 restated over the oracle decoder: the prompt's
     tokens but the last fill the cache, each step forwards the current
     token, picks (greedy, or `sampler`), accepts, stops on an EOS id (which
-    counts) or when `stop_after` ids have reached the token callback, and
-    ends early when the context is full. Returns the generated ids."""
+    counts) or when the token callback asks to (`on_token(id)` true; without
+    one, once `stop_after` ids have reached it), and ends early when the
+    context is full. Returns the generated ids."""
     for t in prompt[:-1]:
         orc_model.forward(t)
         if sampler:
@@ -454,10 +463,41 @@ def oracle_generate(orc_model: "OracleQwen3", prompt, max_new: int, eos=(), samp
         if tok in eos:
             break
         shown += 1
-        if stop_after is not None and shown >= stop_after:
+        if on_token is not None:
+            if on_token(tok):
+                break
+        elif stop_after is not None and shown >= stop_after:
             break
         nxt = tok
     return out
+
+
+class ChannelRouter:
+    """The token callback a front end binds around the generation loop
+    (src/generate.c:60-77; INTEGRATION.md section 2's glue): the think
+    markers switch channels and reach neither, answer ids go to `answer`
+    (asking to stop once `stop_after` of them arrived, 0: never), ids between
+    the markers to `think`. Called with each generated non-EOS id; returns
+    whether to stop."""
+
+    def __init__(self, think_open=-1, think_close=-1, stop_after=0):
+        self.open, self.close, self.stop_after = think_open, think_close, stop_after
+        self.split = think_open >= 0 and think_close >= 0
+        self.in_think = False
+        self.answer, self.think = [], []
+
+    def __call__(self, tok: int) -> bool:
+        if self.split and tok == self.open:
+            self.in_think = True
+            return False
+        if self.split and tok == self.close:
+            self.in_think = False
+            return False
+        if self.in_think:
+            self.think.append(tok)
+            return False
+        self.answer.append(tok)
+        return self.stop_after != 0 and len(self.answer) >= self.stop_after
 
 
 def kv_prefill(substream_fn, shape, config_seed: int, n: int):
@@ -526,6 +566,39 @@ def ref_run(ref, model: SynthModel, n_ctx, steps, k=None, v=None, n_prefill=0, p
                                ptr(greedy), ptr(logits) if want_logits else None, err, 512)
         assert rc == 0, err.value
     return [int(t) for t in greedy], logits
+
+
+def ref_generate(ref, model: SynthModel, n_ctx, prompt, max_new, eos=(), think=(-1, -1),
+                 stop_after=0, sampler=None):
+    """src/generate.c:13-86 compiled (ref_harness.c ref_generate_record) on
+    the model written with a vocabulary: the ids its answer and thinking
+    callbacks saw, the count it returned, the timing's generated count and
+    the state's position afterwards. `sampler`: None for greedy, else the
+    sampler_params keyword arguments."""
+    p = np.ascontiguousarray(prompt, np.uint32)
+    e = np.ascontiguousarray(list(eos) or [0], np.uint32)
+    ans = np.zeros(max_new + 1, np.uint32)
+    thk = np.zeros(max_new + 1, np.uint32)
+    n_ans, n_thk = _SZ(0), _SZ(0)
+    produced, n_gen, n_past = C.c_long(0), C.c_uint32(0), C.c_uint32(0)
+    sp = sampler_params(**sampler) if sampler is not None else None
+    err = C.create_string_buffer(512)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf").encode()
+        rc = ref.ref_write_qwen3_gguf_vocab(path, C.byref(model.c_shape), model.table,
+                                            model.count, ptr(model.blob), n_ctx, err, 512)
+        assert rc == 0, err.value
+        rc = ref.ref_generate_record(path, n_ctx, ptr(p), p.size, max_new, ptr(e), len(eos),
+                                     think[0], think[1], stop_after,
+                                     C.cast(C.byref(sp), C.c_void_p) if sp is not None else None,
+                                     ptr(ans), ans.size, C.byref(n_ans), ptr(thk), thk.size,
+                                     C.byref(n_thk), C.byref(produced), C.byref(n_gen),
+                                     C.byref(n_past), err, 512)
+        assert rc == 0, err.value
+    return {"answer": [int(t) for t in ans[:n_ans.value]],
+            "think": [int(t) for t in thk[:n_thk.value]],
+            "produced": int(produced.value), "n_gen": int(n_gen.value),
+            "n_past": int(n_past.value)}
 
 
 def ref_gguf_read(ref, path: str, keys=(), split: bool = False):

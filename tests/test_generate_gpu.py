@@ -12,9 +12,15 @@ request in the middle of a device-side chunk (the position rewinds to just
 after the stopping step, so the next step equals a fresh decoder's), the
 end of the context, the host-sampling mode with penalties and with a
 seeded temperature sampler, and the timing fields (src/timing.c:30-62).
+Beside it, the record of the compiled reference's own loop
+(tests/golden/generate_cases.json, written by tests/golden/make_golden.py
+from src/generate.c built from its sources) is replayed through the GPU
+loop with the channel-routing callback of a front end (think markers,
+answer-callback stop).
 """
 from __future__ import annotations
 
+import json
 import os
 
 import numpy as np
@@ -153,3 +159,27 @@ def test_qwen3_06b_generate_matches_golden(M):
     assert n == 32 and seen == want
     print(f"0.6B generate: prefill {t.prefill_s * 1e3:.2f} ms, TTFT {t.ttft_s * 1e3:.2f} ms, "
           f"{t.n_gen / t.decode_s:.0f} tok/s")
+
+
+GEN_CASES = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                        "generate_cases.json")))
+
+
+@pytest.mark.parametrize("name", sorted(GEN_CASES))
+def test_loop_against_the_compiled_reference_loop(M, tiny, name):
+    """The compiled src/generate.c:13-86's record (tests/golden/
+    generate_cases.json) replayed through mynah_hip_qwen3_generate_tokens
+    with the channel-routing callback a front end binds (think markers,
+    answer-callback stop): each channel's ids, the count returned, the
+    timing's generated count and the position afterwards."""
+    c, want = GEN_CASES[name], GEN_CASES[name]["want"]
+    print(f"[case] generate vs compiled loop: {name}", flush=True)
+    model, _ = tiny
+    router = O.ChannelRouter(c["think"][0], c["think"][1], c["stop_after"])
+    sampler = O.OracleSampler(CF.QWEN3_TINY.vocab, **c["sampler"]) if c["sampler"] else None
+    dec = M.Qwen3Decoder(model, c["n_ctx"])
+    _, n, t = dec.generate_tokens(c["prompt"], c["max_new"], eos=tuple(c["eos"]),
+                                  sampler=sampler, on_token=router)
+    assert router.answer == want["answer"] and router.think == want["think"]
+    assert n == want["produced"] and t.n_gen == want["n_gen"]
+    assert dec.n_past == want["n_past"]

@@ -12,7 +12,11 @@ archive like the reference's libingot.a, against libmynah_hip.so with
   * no object or archive member linked defines a symbol the library exports
     (no duplicate definitions);
   * the executable exports ingot_gguf_data, which the library's
-    ingot_gguf_matvec uses to locate a tensor's bytes.
+    ingot_gguf_matvec uses to locate a tensor's bytes;
+  * the front-end binding of the generation loop (oracle/generate_hip.c, the
+    code INTEGRATION.md shows) compiles against the reference's headers and
+    links: mynah_slm_generate_hip is defined and its loop,
+    mynah_hip_qwen3_generate_tokens, comes from the library.
 """
 from __future__ import annotations
 
@@ -72,3 +76,10 @@ def test_no_linked_object_redefines_a_library_symbol(linked):
     for m in members:
         defined |= {s for t, s in nm(["--defined-only", m]) if t.isupper()}
     assert not (defined & ours), sorted(defined & ours)
+
+
+def test_generate_binding_links(linked):
+    ours = {s for t, s in nm(["-D", "--defined-only", LIB]) if t in "TWiDBR"}
+    imported = {s for t, s in nm(["-D", linked]) if t == "U" and s.startswith("mynah_hip_")}
+    assert imported == {"mynah_hip_qwen3_generate_tokens"} and imported <= ours
+    assert ("T", "mynah_slm_generate_hip") in set(nm([linked]))
