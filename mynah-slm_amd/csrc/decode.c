@@ -41,6 +41,20 @@ typedef struct {
     const unsigned char *dev;
 } dtensor;
 
+/* STEP_MULTI + v: STEP_BATCH consecutive steps of variant v in one graph
+ * (the counters live on the device, so the steps are identical launches);
+ * it saves the per-launch gap between graphs. */
+enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_MULTI = 2 };
+#define STEP_BATCH 8u
+
+/* Context buckets: a launch whose last step attends n_kv positions runs the
+ * graph of the first bucket holding n_kv (its capacity clamped to n_ctx),
+ * whose attention grids (16- or 32-position chunks) and exact PV kernel
+ * (probabilities in LDS up to 4096 positions) are sized for that capacity,
+ * not for the whole context. Capacities 256, 512, 1024, 2048, 3072, 4096,
+ * then doubling to 2^20. */
+#define N_BUCKETS 14u
+
 typedef struct {
     dtensor attn_norm, wq, wk, wv, q_norm, k_norm, wo, ffn_norm, gate, up, down;
 } dlayer;
@@ -62,16 +76,18 @@ struct mynah_qwen3 {
     uint32_t sstride;               /* floats between the score rows of two heads */
     uint32_t *tokens;               /* [n_ctx] generated ids */
     /* Captured steps: [STEP_FULL] with the head and argmax, [STEP_PREFILL]
-     * without the head (a prompt token whose logits nobody reads). */
-    hipGraph_t graph[4];
-    hipGraphExec_t exec[4];
-    int graph_state[4];             /* 0 not tried, 1 ready, -1 unavailable */
-    int graph_order[4];             /* GEMV order the graph was captured with */
-    int graph_attn[4];              /* attention mode the graph was captured with */
+     * without the head (a prompt token whose logits nobody reads); one per
+     * context bucket (the attention launches sized for the positions the
+     * step reaches). */
+    hipGraph_t graph[4][N_BUCKETS];
+    hipGraphExec_t exec[4][N_BUCKETS];
+    int graph_state[4][N_BUCKETS];  /* 0 not tried, 1 ready, -1 unavailable */
+    int graph_order[4][N_BUCKETS];  /* GEMV order the graph was captured with */
+    int graph_attn[4][N_BUCKETS];   /* attention mode the graph was captured with */
+    int buckets;                    /* 0: every step sized for the whole context */
     int attn_mode;                  /* MYNAH_ATTN_EXACT or MYNAH_ATTN_SPLIT */
-    uint32_t nch_max;               /* position chunks of the split attention */
-    uint32_t as_ch;                 /* positions per chunk */
-    int as_kernel;                  /* its kernel */
+    uint32_t nch_max;               /* split-attention partial slots per key head and group */
+    uint32_t as_ch;                 /* positions per chunk at the whole context */
     float *pm, *po;                 /* split-attention partials: chunk max, weighted V */
     double *pl;                     /* split-attention partials: chunk exp sums */
     /* Batched prompt prefill (allocated on first use for pf_cap tokens):
@@ -89,11 +105,6 @@ struct mynah_qwen3 {
 #define STEP(s) ((s)->counters + 2)
 #define NFORCED(s) ((s)->counters + 3)
 
-/* STEP_MULTI + v: STEP_BATCH consecutive steps of variant v in one graph
- * (the counters live on the device, so the steps are identical launches);
- * it saves the per-launch gap between graphs. */
-enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_MULTI = 2 };
-#define STEP_BATCH 8u
 
 /* The largest context (positions) a state takes: 2^20, far beyond any Qwen3
  * (40960), small enough that every offset fits 32 bits. */
@@ -167,10 +178,11 @@ static int head_group(const mynah_qwen3 *s, mynah_gemv_group *g) {
 
 void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
-    for (int v = 0; v < 4; v++) {
-        if (s->exec[v]) (void)hipGraphExecDestroy(s->exec[v]);
-        if (s->graph[v]) (void)hipGraphDestroy(s->graph[v]);
-    }
+    for (int v = 0; v < 4; v++)
+        for (uint32_t b = 0; b < N_BUCKETS; b++) {
+            if (s->exec[v][b]) (void)hipGraphExecDestroy(s->exec[v][b]);
+            if (s->graph[v][b]) (void)hipGraphDestroy(s->graph[v][b]);
+        }
     void *bufs[] = {s->keys, s->blob, s->k_cache, s->v_cache, s->rope_cos, s->rope_sin, s->rope_now,
                     s->x, s->q,
                     s->attn, s->act, s->logits, s->scores, s->counters, s->tokens, s->forced, s->pm, s->pl,
@@ -183,7 +195,8 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     free(s);
 }
 
-static void split_plan(mynah_qwen3 *s, const mynah_qwen3_shape *c, uint32_t n_ctx);
+static uint32_t split_chunk(const mynah_qwen3 *s, uint32_t cap, int *kernel);
+static uint32_t bucket_cap(uint32_t b);
 
 mynah_qwen3 *mynah_hip_qwen3_new(const mynah_qwen3_shape *c, const mynah_synth_tensor *table,
                                  size_t count, const void *blob, uint64_t blob_bytes,
@@ -303,9 +316,16 @@ mynah_qwen3 *mynah_qwen3_new_parts(const mynah_qwen3_shape *c, const mynah_synth
     s->scores = (float *)dalloc((size_t)c->n_heads * s->sstride * 4, &ok);
     s->counters = (uint32_t *)dalloc(16, &ok);
     s->forced = (uint32_t *)dalloc((size_t)n_ctx * 4, &ok);
+    s->buckets = getenv("MYNAH_CTX_BUCKETS") == NULL || atoi(getenv("MYNAH_CTX_BUCKETS")) != 0;
     {
-        split_plan(s, c, n_ctx);
+        /* Partial slots for the bucket with the most chunks. */
+        s->as_ch = split_chunk(s, n_ctx, NULL);
         s->nch_max = (n_ctx + s->as_ch - 1) / s->as_ch;
+        for (uint32_t b = 0; s->buckets && b < N_BUCKETS && bucket_cap(b) < n_ctx; b++) {
+            const uint32_t ch = split_chunk(s, bucket_cap(b), NULL);
+            const uint32_t n = (bucket_cap(b) + ch - 1) / ch;
+            if (n > s->nch_max) s->nch_max = n;
+        }
         const size_t parts = (size_t)c->n_kv_heads * s->nch_max * (c->n_heads / c->n_kv_heads);
         s->pm = (float *)dalloc(parts * 4, &ok);
         s->pl = (double *)dalloc(parts * 8, &ok);
@@ -437,42 +457,61 @@ static uint32_t prefetch_wgs(void) {
     return v > 0 && v <= 4096 ? (uint32_t)(v & ~7L) : 0u;
 }
 
-/* Chunk size of the split attention: the kernels for 2 and 4 query heads per
- * key head take 32 positions up to a 32768-position context (1,024 chunks),
- * 64 up to 65536 and 128 beyond (MYNAH_AS_CH=32|64|128 forces one); other
- * groups take the generic kernel's 32. More, smaller chunks run faster while
- * the combine stays small: Qwen3-4B decode at context 2048, split mode,
- * 467.6 tok/s with 32 positions, 456.7 with 64, 446.8 with 128. */
-static void split_plan(mynah_qwen3 *s, const mynah_qwen3_shape *c, uint32_t n_ctx) {
-    const uint32_t group = c->n_heads / c->n_kv_heads;
-    uint32_t ch = n_ctx <= 32768u ? 32u : n_ctx <= 65536u ? 64u : 128u;
+/* Chunk size of the split attention for a launch sized for `cap`
+ * positions, and its kernel: the kernels for 2 and 4 query heads per key
+ * head take 32 positions up to 32768 (1,024 chunks), 64 up to 65536 and 128
+ * beyond (MYNAH_AS_CH=32|64|128 forces one); other groups take the generic
+ * kernel's 32. More, smaller chunks run faster while the combine stays
+ * small: Qwen3-4B decode at context 2048, split mode, 467.6 tok/s with 32
+ * positions, 456.7 with 64, 446.8 with 128. */
+static uint32_t split_chunk(const mynah_qwen3 *s, uint32_t cap, int *kernel) {
+    const uint32_t group = s->c.n_heads / s->c.n_kv_heads;
+    uint32_t ch = cap <= 32768u ? 32u : cap <= 65536u ? 64u : 128u;
     const uint32_t want = (uint32_t)env_or("MYNAH_AS_CH", 0);
     if (want == 32u || want == 64u || want == 128u) ch = want;
-    s->as_ch = MYNAH_AS_CH;
-    s->as_kernel = MYNAH_K_ATTN_SPLIT;
-    if (group == 2u || group == 4u) {
-        static const int k2[3] = {MYNAH_K_ATTN_SPLIT_G2_32, MYNAH_K_ATTN_SPLIT_G2_64,
-                                  MYNAH_K_ATTN_SPLIT_G2_128};
-        static const int k4[3] = {MYNAH_K_ATTN_SPLIT_G4_32, MYNAH_K_ATTN_SPLIT_G4_64,
-                                  MYNAH_K_ATTN_SPLIT_G4_128};
-        const int i = ch == 32u ? 0 : ch == 64u ? 1 : 2;
-        s->as_ch = ch;
-        s->as_kernel = group == 2u ? k2[i] : k4[i];
+    if (group != 2u && group != 4u) {
+        if (kernel) *kernel = MYNAH_K_ATTN_SPLIT;
+        return MYNAH_AS_CH;
     }
+    static const int k2[3] = {MYNAH_K_ATTN_SPLIT_G2_32, MYNAH_K_ATTN_SPLIT_G2_64,
+                              MYNAH_K_ATTN_SPLIT_G2_128};
+    static const int k4[3] = {MYNAH_K_ATTN_SPLIT_G4_32, MYNAH_K_ATTN_SPLIT_G4_64,
+                              MYNAH_K_ATTN_SPLIT_G4_128};
+    const int i = ch == 32u ? 0 : ch == 64u ? 1 : 2;
+    if (kernel) *kernel = group == 2u ? k2[i] : k4[i];
+    return ch;
 }
 
-/* The exact attention's PV kernel for this state, or -1 for the eight-lane
- * kernels (MYNAH_ATTN_PV=0, or head_dim other than 128). Up to 4 columns of
- * 256 * MYNAH_PV_LW scores (one float4 per loader thread and column) the
- * softmax runs inside it; longer contexts read the probabilities from the
- * scores rows, normalised in place first. */
-static int pv_kernel(const mynah_qwen3 *s) {
+static uint32_t bucket_cap(uint32_t b) {
+    static const uint32_t caps[6] = {256u, 512u, 1024u, 2048u, 3072u, 4096u};
+    return b < 6u ? caps[b] : 8192u << (b - 6u);
+}
+
+/* The bucket of a launch whose last step attends n_kv positions, and its
+ * capacity (MYNAH_CTX_BUCKETS=0: one bucket, the whole context). */
+static uint32_t ctx_bucket(const mynah_qwen3 *s, uint32_t n_kv, uint32_t *cap) {
+    uint32_t b = 0;
+    if (!s->buckets) {
+        *cap = s->n_ctx;
+        return 0;
+    }
+    while (bucket_cap(b) < n_kv && bucket_cap(b) < s->n_ctx) b++;
+    *cap = bucket_cap(b) < s->n_ctx ? bucket_cap(b) : s->n_ctx;
+    return b;
+}
+
+/* The exact attention's PV kernel for a launch sized for `cap` positions,
+ * or -1 for the eight-lane kernels (MYNAH_ATTN_PV=0, or head_dim other than
+ * 128). Up to 4 columns of 256 * MYNAH_PV_LW scores (one float4 per loader
+ * thread and column) the softmax runs inside it; longer contexts read the
+ * probabilities from the scores rows, normalised in place first. */
+static int pv_kernel(const mynah_qwen3 *s, uint32_t cap) {
     const uint32_t col = 256u * MYNAH_PV_LW;
     if (env_or("MYNAH_ATTN_PV", 1) == 0 || s->c.head_dim != 128) return -1;
-    if (s->n_ctx > 4u * col) return MYNAH_K_ATTN_PV_M;
+    if (cap > 4u * col) return MYNAH_K_ATTN_PV_M;
     static const int by_cols[4] = {MYNAH_K_ATTN_PV_1, MYNAH_K_ATTN_PV_2, MYNAH_K_ATTN_PV_3,
                                    MYNAH_K_ATTN_PV_4};
-    return by_cols[(s->n_ctx - 1u) / col];
+    return by_cols[(cap - 1u) / col];
 }
 
 static uint32_t prefetch_step(void) {
@@ -480,7 +519,10 @@ static uint32_t prefetch_step(void) {
     return v >= 2 && v <= 12 ? (uint32_t)v : 7u;
 }
 
-static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int variant) {
+/* One step of variant `variant` whose attention launches are sized for
+ * `cap` positions; p0 is the first position the launch (its graph) runs at. */
+static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int variant,
+                        uint32_t p0, uint32_t cap) {
     const mynah_qwen3_shape *c = &s->c;
     const size_t per_layer = (size_t)s->n_ctx * s->kv_dim;
     uint32_t *tok = TOKEN(s), *pos = POS(s), *step = STEP(s);
@@ -538,19 +580,25 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             const float *rnow = s->rope_now;
             float *pm = s->pm, *po = s->po, *out = s->attn;
             double *pl = s->pl;
-            uint32_t nchm = s->nch_max, kvd = s->kv_dim;
+            int kernel = 0;
+            uint32_t ch = split_chunk(s, cap, &kernel);
+            uint32_t nchm = (cap + ch - 1) / ch, kvd = s->kv_dim;
             uint32_t group = c->n_heads / c->n_kv_heads;
             float eps = c->rms_eps, scale = s->scale;
-            /* Chunks live at this step's position stay live in every later
-             * step (the graphs replay forward), so they load K/V before the
-             * position arrives. */
-            uint32_t nctx = s->n_ctx;
-            uint32_t spec = (s->n_past + s->as_ch) / s->as_ch, ch = s->as_ch;
+            /* Chunks live at the launch's first position stay live in every
+             * later step (the graphs replay forward), so they load K/V
+             * before the position arrives. */
+            uint32_t nctx = cap;
+            uint32_t spec = (p0 + ch) / ch;
             if (spec > nchm) spec = nchm;
+            if (nchm > s->nch_max) {
+                mynah_set_error("split launch of %u chunks exceeds the partials", nchm);
+                rc = -1;
+                break;
+            }
             void *args[] = {&q, &kl, &vl, &qn, &kn, &rnow, &pos, &pm, &pl, &po, &nchm, &kvd,
                             &group, &eps, &scale, &nctx, &spec};
-            rc = mynah_launch(d, s->as_kernel, c->n_kv_heads, s->nch_max, 128 * group, 0, st,
-                              args);
+            rc = mynah_launch(d, kernel, c->n_kv_heads, nchm, 128 * group, 0, st, args);
             if (rc) break;
             const float *cpm = pm, *cpo = po;
             const double *cpl = pl;
@@ -562,24 +610,24 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             /* Up to MYNAH_AC1_MAX chunks one wave per query head combines
              * (no barrier), past that four (MYNAH_ATTN_COMBINE1=0: always
              * four); same bits. */
-            if (s->nch_max <= MYNAH_AC1_MAX && env_or("MYNAH_ATTN_COMBINE1", 1) != 0)
+            if (nchm <= MYNAH_AC1_MAX && env_or("MYNAH_ATTN_COMBINE1", 1) != 0)
                 rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE1, c->n_heads, 1, 64, 0, st, args2w);
             else
                 rc = mynah_launch(d, MYNAH_K_ATTN_COMBINE, c->n_heads, 1, 256,
-                                  (size_t)s->nch_max * sizeof(float), st, args2);
+                                  (size_t)nchm * sizeof(float), st, args2);
         } else {
             const float *q = s->q, *qn = (const float *)L->q_norm.dev;
             const float *kn = (const float *)L->k_norm.dev;
             const float *rnow = s->rope_now;
             float *sc = s->scores;
-            uint32_t nctx = s->n_ctx, kvd = s->kv_dim, sstride = s->sstride;
+            uint32_t nctx = cap, kvd = s->kv_dim, sstride = s->sstride;
             uint32_t group = c->n_heads / c->n_kv_heads;
             float eps = c->rms_eps, scale = s->scale;
-            /* 16-position chunks live at this step's position stay live in
-             * every later step (the graphs replay forward), so they load
-             * their key rows before the position arrives. */
-            const uint32_t nsc = (s->n_ctx + 15) / 16;
-            uint32_t spec = (s->n_past + 16) / 16;
+            /* 16-position chunks live at the launch's first position stay
+             * live in every later step (the graphs replay forward), so they
+             * load their key rows before the position arrives. */
+            const uint32_t nsc = (cap + 15) / 16;
+            uint32_t spec = (p0 + 16) / 16;
             if (spec > nsc) spec = nsc;
             void *args[] = {&q, &kl, &qn, &kn, &rnow, &pos, &sc, &nctx, &sstride, &kvd,
                             &group, &eps, &scale, &spec};
@@ -588,7 +636,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
             float *out = s->attn;
             const float *scc = s->scores;
             void *args2[] = {&vl, &scc, &pos, &out, &sstride, &kvd, &group};
-            const int pv = pv_kernel(s);
+            const int pv = pv_kernel(s, cap);
             if (pv >= 0) {
                 /* A PV chain in every lane (MYNAH_ATTN_PV=0: the eight-lane
                  * kernels below; same bits). */
@@ -666,64 +714,84 @@ static int embed_current(mynah_qwen3 *s, mynah_device *d) {
     return mynah_launch(d, MYNAH_K_EMBED, (dm / 32 + 255) / 256, 1, 256, 0, d->stream, args);
 }
 
-/* Capture step variant v once (or again after the GEMV order or attention
- * mode changed); leaves graph_state[v] = -1 when capture is unavailable. */
-static void ensure_graph(mynah_qwen3 *s, mynah_device *d, int v) {
+/* Steps in one launch of variant v. */
+static uint32_t launch_steps(int v) { return v >= STEP_MULTI ? STEP_BATCH : 1u; }
+
+/* Capture variant v for the bucket of a launch starting at position p0 once
+ * (or again after the GEMV order or attention mode changed); leaves its
+ * state -1 when capture is unavailable. Returns the bucket. */
+static uint32_t ensure_graph(mynah_qwen3 *s, mynah_device *d, int v, uint32_t p0) {
     hipStream_t st = d->stream;
-    if (s->graph_state[v] == 1 &&
-        (s->graph_order[v] != mynah_hip_gemv_order() || s->graph_attn[v] != s->attn_mode)) {
-        (void)hipGraphExecDestroy(s->exec[v]);
-        (void)hipGraphDestroy(s->graph[v]);
-        s->exec[v] = NULL;
-        s->graph[v] = NULL;
-        s->graph_state[v] = 0;
+    uint32_t cap = 0;
+    const uint32_t b = ctx_bucket(s, p0 + launch_steps(v), &cap);
+    if (s->graph_state[v][b] == 1 && (s->graph_order[v][b] != mynah_hip_gemv_order() ||
+                                      s->graph_attn[v][b] != s->attn_mode)) {
+        (void)hipGraphExecDestroy(s->exec[v][b]);
+        (void)hipGraphDestroy(s->graph[v][b]);
+        s->exec[v][b] = NULL;
+        s->graph[v][b] = NULL;
+        s->graph_state[v][b] = 0;
     }
-    if (s->graph_state[v] == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
-        s->graph_state[v] = -1;
+    if (s->graph_state[v][b] == 0 && getenv("MYNAH_HIP_NO_GRAPH") == NULL) {
+        s->graph_state[v][b] = -1;
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-            int rc = enqueue_step(s, d, st, v % STEP_MULTI);
-            for (uint32_t r = 1; v >= STEP_MULTI && r < STEP_BATCH && rc == 0; r++)
-                rc = enqueue_step(s, d, st, v % STEP_MULTI);
+            int rc = 0;
+            for (uint32_t r = 0; r < launch_steps(v) && rc == 0; r++)
+                rc = enqueue_step(s, d, st, v % STEP_MULTI, p0, cap);
             hipGraph_t g = NULL;
             const hipError_t e = hipStreamEndCapture(st, &g);
             if (rc == 0 && e == hipSuccess && g != NULL &&
-                hipGraphInstantiate(&s->exec[v], g, NULL, NULL, 0) == hipSuccess) {
-                s->graph[v] = g;
-                s->graph_state[v] = 1;
-                s->graph_order[v] = mynah_hip_gemv_order();
-                s->graph_attn[v] = s->attn_mode;
+                hipGraphInstantiate(&s->exec[v][b], g, NULL, NULL, 0) == hipSuccess) {
+                s->graph[v][b] = g;
+                s->graph_state[v][b] = 1;
+                s->graph_order[v][b] = mynah_hip_gemv_order();
+                s->graph_attn[v][b] = s->attn_mode;
             } else if (g != NULL) {
                 (void)hipGraphDestroy(g);
             }
         }
         (void)hipGetLastError();
     }
+    return b;
 }
 
-/* One launch of variant v: its graph, or direct launches without one. */
-static int run_step(mynah_qwen3 *s, mynah_device *d, int v) {
+/* One launch of variant v starting at position p0: its bucket's graph, or
+ * direct launches without one. */
+static int run_step(mynah_qwen3 *s, mynah_device *d, int v, uint32_t p0) {
     hipStream_t st = d->stream;
-    ensure_graph(s, d, v);
-    if (s->graph_state[v] == 1) {
-        if (hipGraphLaunch(s->exec[v], st) != hipSuccess) {
+    const uint32_t b = ensure_graph(s, d, v, p0);
+    if (s->graph_state[v][b] == 1) {
+        if (hipGraphLaunch(s->exec[v][b], st) != hipSuccess) {
             mynah_set_error("hipGraphLaunch failed");
             return -1;
         }
         return 0;
     }
-    int rc = enqueue_step(s, d, st, v % STEP_MULTI);
-    for (uint32_t r = 1; v >= STEP_MULTI && r < STEP_BATCH && rc == 0; r++)
-        rc = enqueue_step(s, d, st, v % STEP_MULTI);
+    uint32_t cap = 0;
+    (void)ctx_bucket(s, p0 + launch_steps(v), &cap);
+    int rc = 0;
+    for (uint32_t r = 0; r < launch_steps(v) && rc == 0; r++)
+        rc = enqueue_step(s, d, st, v % STEP_MULTI, p0, cap);
     return rc;
 }
 
-/* n steps of variant v: batches of STEP_BATCH, then single steps. */
-static int run_steps(mynah_qwen3 *s, mynah_device *d, int v, uint32_t n) {
+/* n steps of variant v from position p0: batches of STEP_BATCH, then single
+ * steps. */
+static int run_steps(mynah_qwen3 *s, mynah_device *d, int v, uint32_t p0, uint32_t n) {
     int rc = 0;
     uint32_t i = 0;
-    for (; i + STEP_BATCH <= n && rc == 0; i += STEP_BATCH) rc = run_step(s, d, STEP_MULTI + v);
-    for (; i < n && rc == 0; i++) rc = run_step(s, d, v);
+    for (; i + STEP_BATCH <= n && rc == 0; i += STEP_BATCH)
+        rc = run_step(s, d, STEP_MULTI + v, p0 + i);
+    for (; i < n && rc == 0; i++) rc = run_step(s, d, v, p0 + i);
     return rc;
+}
+
+/* Capture every graph run_steps(v, p0, n) replays (a capture leaves the
+ * device idle, so callers do it before their clock starts). */
+static void prepare_steps(mynah_qwen3 *s, mynah_device *d, int v, uint32_t p0, uint32_t n) {
+    uint32_t i = 0;
+    for (; i + STEP_BATCH <= n; i += STEP_BATCH) (void)ensure_graph(s, d, STEP_MULTI + v, p0 + i);
+    for (; i < n; i++) (void)ensure_graph(s, d, v, p0 + i);
 }
 
 static int set_counters(mynah_qwen3 *s, mynah_device *d, uint32_t token, uint32_t step,
@@ -749,7 +817,7 @@ int mynah_hip_qwen3_forward(mynah_qwen3 *s, uint32_t token, float *logits) {
         return -1;
     }
     if (set_counters(s, d, token, 0, 0) != 0 || embed_current(s, d) != 0 ||
-        run_step(s, d, STEP_FULL) != 0)
+        run_step(s, d, STEP_FULL, s->n_past) != 0)
         return -1;
     s->n_past++;
     if (logits && hipMemcpyAsync(logits, s->logits, (size_t)s->c.vocab * 4,
@@ -991,8 +1059,8 @@ static int prompt_batched(mynah_qwen3 *s, mynah_device *d, const uint32_t *promp
                           float *prefill_ms, float *decode_ms) {
     const uint32_t cap = prefill_chunk_cap();
     if (prefill_alloc(s, n_prompt - 1u < cap ? n_prompt - 1u : cap) != 0) return -1;
-    ensure_graph(s, d, n_steps >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
-    if (n_steps % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
+    const uint32_t start = s->n_past;
+    prepare_steps(s, d, STEP_FULL, start + (n_prompt - 1u), n_steps);
     hipEvent_t ev[4] = {NULL, NULL, NULL, NULL};
     for (int i = 0; i < 4; i++)
         if (hipEventCreate(&ev[i]) != hipSuccess) {
@@ -1000,14 +1068,13 @@ static int prompt_batched(mynah_qwen3 *s, mynah_device *d, const uint32_t *promp
             for (int j = 0; j < i; j++) (void)hipEventDestroy(ev[j]);
             return -1;
         }
-    const uint32_t start = s->n_past;
     (void)hipEventRecord(ev[0], d->stream);
     int rc = mynah_hip_qwen3_prefill(s, prompt, n_prompt - 1u);
     (void)hipEventRecord(ev[1], d->stream);
     if (rc == 0) rc = set_counters(s, d, prompt[n_prompt - 1u], 0, 0);
     (void)hipEventRecord(ev[2], d->stream);
     if (rc == 0) rc = embed_current(s, d);
-    if (rc == 0) rc = run_steps(s, d, STEP_FULL, n_steps);
+    if (rc == 0) rc = run_steps(s, d, STEP_FULL, start + (n_prompt - 1u), n_steps);
     (void)hipEventRecord(ev[3], d->stream);
     if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("decode failed");
@@ -1061,19 +1128,16 @@ int mynah_hip_qwen3_prompt(mynah_qwen3 *s, const uint32_t *prompt, uint32_t n_pr
         return -1;
     }
     /* Capture before the clock starts: a capture leaves the device idle. */
-    if (n_prompt > 1) {
-        ensure_graph(s, d, n_prompt - 1u >= STEP_BATCH ? STEP_MULTI + STEP_PREFILL : STEP_PREFILL);
-        if ((n_prompt - 1u) % STEP_BATCH) ensure_graph(s, d, STEP_PREFILL);
-    }
-    ensure_graph(s, d, n_steps >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
-    if (n_steps % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
+    const uint32_t p_first = s->n_past + (n_prompt - 1u);
+    if (n_prompt > 1) prepare_steps(s, d, STEP_PREFILL, s->n_past, n_prompt - 1u);
+    prepare_steps(s, d, STEP_FULL, p_first, n_steps);
     (void)hipEventRecord(a, d->stream);
     int rc = embed_current(s, d);
     /* src/generate.c:33-36: every prompt token but the last only fills the
      * cache; its logits are never produced. */
-    if (rc == 0 && n_prompt > 1) rc = run_steps(s, d, STEP_PREFILL, n_prompt - 1u);
+    if (rc == 0 && n_prompt > 1) rc = run_steps(s, d, STEP_PREFILL, s->n_past, n_prompt - 1u);
     (void)hipEventRecord(m, d->stream);
-    if (rc == 0) rc = run_steps(s, d, STEP_FULL, n_steps);
+    if (rc == 0) rc = run_steps(s, d, STEP_FULL, p_first, n_steps);
     (void)hipEventRecord(b, d->stream);
     if (rc == 0 && hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("decode failed");
@@ -1124,9 +1188,8 @@ int mynah_hip_qwen3_forced(mynah_qwen3 *s, const uint32_t *inputs, uint32_t n,
         return -1;
     }
     if (set_counters(s, d, inputs[0], 0, n) != 0) return -1;
-    ensure_graph(s, d, n >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
-    if (n % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
-    if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, n) != 0) return -1;
+    prepare_steps(s, d, STEP_FULL, s->n_past, n);
+    if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, s->n_past, n) != 0) return -1;
     if (hipStreamSynchronize(d->stream) != hipSuccess) {
         mynah_set_error("forced decode failed");
         return -1;
@@ -1248,9 +1311,9 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
             if (c > p->max_new - done) c = p->max_new - done;
             if (c > s->n_ctx - s->n_past) c = s->n_ctx - s->n_past;
             if (set_counters(s, d, next, 0, 0) != 0) return -1;
-            ensure_graph(s, d, c >= STEP_BATCH ? STEP_MULTI + STEP_FULL : STEP_FULL);
-            if (c % STEP_BATCH) ensure_graph(s, d, STEP_FULL);
-            if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, c) != 0) return -1;
+            prepare_steps(s, d, STEP_FULL, s->n_past, c);
+            if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, s->n_past, c) != 0)
+                return -1;
             uint32_t ids[64];
             uint32_t *buf = c <= 64u ? ids : (uint32_t *)malloc((size_t)c * 4);
             if (buf == NULL ||
@@ -1337,7 +1400,11 @@ void mynah_hip_qwen3_reset(mynah_qwen3 *s) {
 }
 
 int mynah_hip_qwen3_uses_graph(const mynah_qwen3 *s) {
-    return s ? (s->graph_state[STEP_FULL] == 1 || s->graph_state[STEP_MULTI + STEP_FULL] == 1) : 0;
+    if (s == NULL) return 0;
+    for (uint32_t b = 0; b < N_BUCKETS; b++)
+        if (s->graph_state[STEP_FULL][b] == 1 || s->graph_state[STEP_MULTI + STEP_FULL][b] == 1)
+            return 1;
+    return 0;
 }
 
 int mynah_hip_qwen3_set_attention(mynah_qwen3 *s, int mode) {
