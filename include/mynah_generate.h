@@ -25,6 +25,11 @@
  *     sample(sampler, logits) picks (the reference's mynah_slm_sample, which
  *     may modify the logits in place, fits as is); accept(sampler, id), when
  *     set, is called where the reference calls mynah_slm_sampler_accept.
+ *   - device_sampler != NULL (sample, accept and sampler are then unused):
+ *     the reference's sampler on the device (below), inside the captured
+ *     steps like greedy, so the logits never leave HBM; the prompt tokens
+ *     and every generated id enter its window, and its rng advances once
+ *     per sampled id, exactly as the reference's sampler object would.
  *
  * Detokenisation and the thinking channel (src/generate.c:38-77) stay with
  * the caller: on_token receives the id, and the reference's binding feeds
@@ -66,7 +71,8 @@ typedef struct {
     mynah_hip_sample_fn sample;     /* NULL: greedy on the device */
     mynah_hip_accept_fn accept;     /* optional */
     void *sampler;
-    uint32_t chunk;                 /* device-greedy steps per round trip, 0 = 8 */
+    uint32_t chunk;                 /* device steps per round trip, 0 = 8 */
+    struct mynah_hip_sampler *device_sampler; /* NULL: as above */
 } mynah_hip_gen_params;
 
 /* src/timing.h:14-28 (mynah_slm_timing), the fields the loop fills. */
@@ -75,6 +81,41 @@ typedef struct {
     uint32_t n_prompt, n_gen;
     int ttft_done;
 } mynah_hip_timing;
+
+/* ── the reference's sampler on the device ─────────────────────────────────
+ * src/sampler.h:16-30 (mynah_slm_sampler_params), field for field. */
+typedef struct {
+    float temp;                     /* <= 0: greedy */
+    uint32_t top_k;                 /* 0 = off (host sampler only when temp > 0) */
+    float top_p, min_p;
+    float repeat_penalty, freq_penalty, presence_penalty;
+    uint32_t penalty_window;
+    uint64_t seed;
+} mynah_hip_sampler_params;
+
+/* A sampler object like the reference's (src/sampler.c:16-25): parameters,
+ * splitmix64 state and penalty window, kept in device memory. Every id it
+ * returns is the one mynah_slm_sample returns for the same logits and
+ * history (the same penalties, f32 exponentials, double sum, f32
+ * probabilities, candidate order, draw and walk). It takes what the
+ * reference's defaults use: with temp > 0, 1 <= top_k <= 128 (and below the
+ * vocabulary; the reference's top_k = 0 sorts the whole vocabulary, which
+ * this sampler does not), a penalty window of at most 4096; otherwise
+ * mynah_hip_sampler_new returns NULL (mynah_hip_last_error says why) and
+ * the caller keeps the reference's sampler on the host. */
+typedef struct mynah_hip_sampler mynah_hip_sampler;
+
+/* src/sampler.c:48-64 (mynah_slm_sampler_new); seed 0 takes the same
+ * fixed default state. */
+mynah_hip_sampler *mynah_hip_sampler_new(const mynah_hip_sampler_params *p, uint32_t vocab);
+/* src/sampler.c:66-71 (mynah_slm_sampler_free). */
+void mynah_hip_sampler_free(mynah_hip_sampler *s);
+/* src/sampler.c:73-78 (mynah_slm_sampler_accept). 0, or -1. */
+int mynah_hip_sampler_accept(mynah_hip_sampler *s, uint32_t token);
+/* src/sampler.c:116-187 (mynah_slm_sample) over host logits, modified in
+ * place like the reference's (the penalties): *id is the picked token. The
+ * generation loop samples on the device without this host copy. 0, or -1. */
+int mynah_hip_sample(mynah_hip_sampler *s, float *logits, uint32_t *id);
 
 /* src/generate.h:47-52 (mynah_slm_generate). t may be NULL. */
 long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params *p,

@@ -118,6 +118,39 @@ MYNAH_DEV float wave_max_dpp(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// A 64-bit key moved across lanes by one DPP control (both halves).
+template <int CTRL>
+MYNAH_DEV unsigned long long dpp_u64(unsigned long long v) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)v, CTRL, 0xf, 0xf, false);
+    const unsigned hi =
+        (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+MYNAH_DEV unsigned long long readlane_u64(unsigned long long v, int lane) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, lane);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), lane);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// Wave-wide 64-bit max of a fully active wave, every lane receiving it: DPP
+// within quads and rows, then the four row maxima read as scalars (no LDS
+// round trip, unlike wave_max_u64's shuffles).
+MYNAH_DEV unsigned long long wave_max_u64_dpp(unsigned long long v) {
+    unsigned long long o = dpp_u64<0xB1>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<0x4E>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<0x124>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<0x128>(v);
+    v = o > v ? o : v;
+    const unsigned long long a = readlane_u64(v, 0), b = readlane_u64(v, 16);
+    const unsigned long long c = readlane_u64(v, 32), d = readlane_u64(v, 48);
+    const unsigned long long ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
+}
+
 // Sum over the 64 lanes of a (fully active) wave in double, every lane
 // receiving the total: DPP within quads (xor 1, xor 2) and rows (rotate by
 // 4, 8), then the four row sums read as scalars.

@@ -28,6 +28,7 @@
 #include "mynah_decode.h"
 #include "mynah_generate.h"
 #include "runtime_internal.h"
+#include "sample.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -43,9 +44,20 @@ typedef struct {
 
 /* STEP_MULTI + v: STEP_BATCH consecutive steps of variant v in one graph
  * (the counters live on the device, so the steps are identical launches);
- * it saves the per-launch gap between graphs. */
-enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_MULTI = 2 };
+ * it saves the per-launch gap between graphs. STEP_SAMPLE is STEP_FULL with
+ * the device sampler between the head and the advance. */
+enum { STEP_FULL = 0, STEP_PREFILL = 1, STEP_SAMPLE = 2, STEP_MULTI = 3, STEP_VARIANTS = 6 };
 #define STEP_BATCH 8u
+
+/* Scratch of the device sampler (sample.hip) for one vocabulary: the
+ * exponentials, each workgroup's first-maximum key, double-double sum and
+ * top_k keys, the picked id's key, and (standalone sampling) the logits. */
+typedef struct {
+    float *e, *logits;
+    unsigned long long *wkey, *cand, *key;
+    double *wsum;
+    uint32_t nwg;
+} samp_scratch;
 
 /* Context buckets: a launch whose last step attends n_kv positions runs the
  * graph of the first bucket holding n_kv (its capacity clamped to n_ctx),
@@ -79,11 +91,11 @@ struct mynah_qwen3 {
      * without the head (a prompt token whose logits nobody reads); one per
      * context bucket (the attention launches sized for the positions the
      * step reaches). */
-    hipGraph_t graph[4][N_BUCKETS];
-    hipGraphExec_t exec[4][N_BUCKETS];
-    int graph_state[4][N_BUCKETS];  /* 0 not tried, 1 ready, -1 unavailable */
-    int graph_order[4][N_BUCKETS];  /* GEMV order the graph was captured with */
-    int graph_attn[4][N_BUCKETS];   /* attention mode the graph was captured with */
+    hipGraph_t graph[STEP_VARIANTS][N_BUCKETS];
+    hipGraphExec_t exec[STEP_VARIANTS][N_BUCKETS];
+    int graph_state[STEP_VARIANTS][N_BUCKETS];  /* 0 not tried, 1 ready, -1 unavailable */
+    int graph_order[STEP_VARIANTS][N_BUCKETS];  /* GEMV order the graph was captured with */
+    int graph_attn[STEP_VARIANTS][N_BUCKETS];   /* attention mode the graph was captured with */
     int buckets;                    /* 0: every step sized for the whole context */
     int attn_mode;                  /* MYNAH_ATTN_EXACT or MYNAH_ATTN_SPLIT */
     uint32_t nch_max;               /* split-attention partial slots per key head and group */
@@ -98,6 +110,10 @@ struct mynah_qwen3 {
     float *pf_x, *pf_xn, *pf_q, *pf_att, *pf_g, *pf_u, *pf_s;
     uint32_t *pf_tok;
     float *host_logits;             /* pinned: logits for a host-side sampler */
+    /* The device sampler's state for sampled steps (a copy of the caller's
+     * sampler for the length of a generation) and its scratch. */
+    SampState *samp_st;
+    samp_scratch samp_sc;
 };
 
 #define TOKEN(s) ((s)->counters + 0)
@@ -176,9 +192,13 @@ static int head_group(const mynah_qwen3 *s, mynah_gemv_group *g) {
     return 0;
 }
 
+static void samp_scratch_free(samp_scratch *sc);
+static int samp_enqueue(mynah_device *d, hipStream_t st, SampState *state, const samp_scratch *sc,
+                        float *logits, uint32_t vocab, uint32_t accept);
+
 void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     if (s == NULL) return;
-    for (int v = 0; v < 4; v++)
+    for (int v = 0; v < STEP_VARIANTS; v++)
         for (uint32_t b = 0; b < N_BUCKETS; b++) {
             if (s->exec[v][b]) (void)hipGraphExecDestroy(s->exec[v][b]);
             if (s->graph[v][b]) (void)hipGraphDestroy(s->graph[v][b]);
@@ -191,6 +211,8 @@ void mynah_hip_qwen3_free(mynah_qwen3 *s) {
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++)
         if (bufs[i]) (void)hipFree(bufs[i]);
     if (s->host_logits) (void)hipHostFree(s->host_logits);
+    samp_scratch_free(&s->samp_sc);
+    if (s->samp_st) (void)hipFree(s->samp_st);
     free(s->layers);
     free(s);
 }
@@ -665,7 +687,7 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
         rc = rc ? rc : mynah_gemv_group_launch(d, &lg[LG_FFN], st, NULL, -1);
         rc = rc ? rc : mynah_gemv_group_launch(d, &lg[LG_DOWN], st, NULL, -1);
     }
-    if (rc == 0 && variant == STEP_FULL) {
+    if (rc == 0 && (variant == STEP_FULL || variant == STEP_SAMPLE)) {
         /* The final norm (src/arch_qwen3.c:239) runs inside the head GEMV. */
         mynah_gemv_group g;
         /* The exact kernel is also the faster one for the head (its fused
@@ -681,9 +703,17 @@ static int enqueue_step(mynah_qwen3 *s, mynah_device *d, hipStream_t st, int var
         }
         rc = rc ? rc : mynah_gemv_group_launch(d, &g, st, &head_tiles, MYNAH_GEMV_EXACT);
     }
+    const unsigned long long *keys = s->keys;
+    uint32_t n = head_tiles;
+    if (rc == 0 && variant == STEP_SAMPLE) {
+        /* src/sampler.c:116-187 on the head's logits; the advance then takes
+         * the sampled id as its only key. */
+        rc = samp_enqueue(d, st, s->samp_st, &s->samp_sc, s->logits, c->vocab, 1u);
+        keys = s->samp_sc.key;
+        n = 1;
+    }
     if (rc == 0) {
-        const unsigned long long *keys = s->keys;
-        uint32_t n = head_tiles, maxs = s->n_ctx;
+        uint32_t maxs = s->n_ctx;
         uint32_t *toks = s->tokens;
         const unsigned char *tab = s->embed.dev;
         float *x = s->x;
@@ -1204,6 +1234,185 @@ int mynah_hip_qwen3_forced(mynah_qwen3 *s, const uint32_t *inputs, uint32_t n,
     return 0;
 }
 
+/* ── the reference's sampler on the device (sample.hip) ──────────────────── */
+
+struct mynah_hip_sampler {
+    uint32_t vocab;
+    SampState *st;                  /* device: what the kernels read and update */
+    SampState h;                    /* host mirror */
+    samp_scratch sc;                /* for mynah_hip_sample */
+};
+
+static uint32_t samp_nwg(uint32_t vocab) { return (vocab + SP_CH - 1u) / SP_CH; }
+static uint32_t samp_nwg_tk(uint32_t vocab) { return (vocab + SP_TK_CH - 1u) / SP_TK_CH; }
+
+static void samp_scratch_free(samp_scratch *sc) {
+    void *b[] = {sc->e, sc->logits, sc->wkey, sc->cand, sc->key, sc->wsum};
+    for (size_t i = 0; i < sizeof b / sizeof b[0]; i++)
+        if (b[i]) (void)hipFree(b[i]);
+    memset(sc, 0, sizeof *sc);
+}
+
+static int samp_scratch_alloc(samp_scratch *sc, uint32_t vocab, int with_logits) {
+    if (sc->e != NULL && (!with_logits || sc->logits != NULL)) return 0;
+    samp_scratch_free(sc);
+    const uint32_t nwg = samp_nwg(vocab);
+    int ok = 1;
+    sc->nwg = nwg;
+    sc->e = (float *)dalloc((size_t)vocab * 4, &ok);
+    if (with_logits) sc->logits = (float *)dalloc((size_t)vocab * 4, &ok);
+    sc->wkey = (unsigned long long *)dalloc((size_t)nwg * 8, &ok);
+    sc->cand = (unsigned long long *)dalloc((size_t)SP_TK_MAXWG * SP_KMAX * 8, &ok);
+    sc->key = (unsigned long long *)dalloc(8, &ok);
+    sc->wsum = (double *)dalloc((size_t)nwg * 16, &ok);
+    if (!ok) {
+        samp_scratch_free(sc);
+        mynah_set_error("out of device memory for the sampler");
+        return -1;
+    }
+    return 0;
+}
+
+/* The four launches of one draw over `logits` (device), state `state`;
+ * `accept`: the id also enters the window. */
+static int samp_enqueue(mynah_device *d, hipStream_t st, SampState *state, const samp_scratch *sc,
+                        float *logits, uint32_t vocab, uint32_t accept) {
+    const float *clogits = logits, *ce = sc->e;
+    const SampState *cstate = state;
+    float *e = sc->e;
+    unsigned long long *wkey = sc->wkey, *cand = sc->cand, *key = sc->key;
+    const unsigned long long *cwkey = wkey, *ccand = cand;
+    double *wsum = sc->wsum;
+    const double *cwsum = wsum;
+    uint32_t nwg = sc->nwg, nwg_tk = samp_nwg_tk(vocab);
+    void *a1[] = {&logits, &vocab, &cstate, &wkey};
+    void *a2[] = {&clogits, &vocab, &cstate, &cwkey, &nwg, &e, &wsum};
+    void *a3[] = {&ce, &vocab, &cstate, &cwsum, &nwg, &cand};
+    void *a4[] = {&state, &vocab, &cwkey, &ccand, &nwg, &nwg_tk, &key, &accept};
+    int rc = mynah_launch(d, MYNAH_K_SAMP_PENALIZE, nwg, 1, SP_T, 0, st, a1);
+    rc = rc ? rc : mynah_launch(d, MYNAH_K_SAMP_EXP, nwg, 1, SP_T, 0, st, a2);
+    rc = rc ? rc : mynah_launch(d, MYNAH_K_SAMP_TOPK, nwg_tk, 1, SP_TK_T, 0, st, a3);
+    rc = rc ? rc : mynah_launch(d, MYNAH_K_SAMP_PICK, 1, 1, 64, 0, st, a4);
+    return rc;
+}
+
+/* What the device sampler takes (include/mynah_generate.h). */
+static int samp_check(const mynah_hip_sampler_params *p, uint32_t vocab) {
+    if (p == NULL || vocab == 0) {
+        mynah_set_error("sampler: null parameters or empty vocabulary");
+        return -1;
+    }
+    if (samp_nwg_tk(vocab) > SP_TK_MAXWG) {
+        mynah_set_error("sampler: vocabulary of %u exceeds %u", vocab, SP_TK_MAXWG * SP_TK_CH);
+        return -1;
+    }
+    if (p->penalty_window > SP_WMAX) {
+        mynah_set_error("sampler: penalty window %u exceeds %u", p->penalty_window, SP_WMAX);
+        return -1;
+    }
+    if (p->temp > 0.0f && (p->top_k == 0 || p->top_k > SP_KMAX || p->top_k >= vocab)) {
+        mynah_set_error("sampler: with temp > 0 the device sampler takes 1 <= top_k <= %u "
+                        "(below the vocabulary), not %u; sample on the host instead",
+                        SP_KMAX, p->top_k);
+        return -1;
+    }
+    return 0;
+}
+
+/* src/sampler.c:73-78. */
+static void samp_push(SampState *h, uint32_t token) {
+    if (h->window == 0) return;
+    h->ring[h->head] = token;
+    h->head = (h->head + 1u) % h->window;
+    if (h->n_recent < h->window) h->n_recent++;
+}
+
+/* Bytes of the state that matter: everything before the window, and the
+ * window's slots. */
+static size_t samp_bytes(const SampState *h) {
+    return offsetof(SampState, ring) + (size_t)h->window * sizeof(uint32_t);
+}
+
+mynah_hip_sampler *mynah_hip_sampler_new(const mynah_hip_sampler_params *p, uint32_t vocab) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || samp_check(p, vocab) != 0) return NULL;
+    mynah_hip_sampler *s = (mynah_hip_sampler *)calloc(1, sizeof *s);
+    if (s == NULL) {
+        mynah_set_error("out of host memory");
+        return NULL;
+    }
+    s->vocab = vocab;
+    SampState *h = &s->h;
+    h->temp = p->temp;
+    h->top_k = p->top_k;
+    h->top_p = p->top_p;
+    h->min_p = p->min_p;
+    h->repeat_penalty = p->repeat_penalty;
+    h->freq_penalty = p->freq_penalty;
+    h->presence_penalty = p->presence_penalty;
+    h->window = p->penalty_window;
+    h->seed = p->seed;
+    h->rng = p->seed ? p->seed : 0x853C49E6748FEA9Bull;       /* src/sampler.c:55 */
+    /* MYNAH_SAMPLE_SEQ_SUM=1: always the index-order double sum (tests). */
+    h->flags = env_or("MYNAH_SAMPLE_SEQ_SUM", 0) != 0 ? SP_FLAG_SEQ_SUM : 0u;
+    int ok = 1;
+    s->st = (SampState *)dalloc(sizeof(SampState), &ok);
+    if (!ok || hipMemcpy(s->st, h, samp_bytes(h), hipMemcpyHostToDevice) != hipSuccess) {
+        mynah_set_error("sampler state upload failed");
+        mynah_hip_sampler_free(s);
+        return NULL;
+    }
+    return s;
+}
+
+void mynah_hip_sampler_free(mynah_hip_sampler *s) {
+    if (s == NULL) return;
+    samp_scratch_free(&s->sc);
+    if (s->st) (void)hipFree(s->st);
+    free(s);
+}
+
+/* The host mirror into the device state. */
+static int samp_upload(mynah_hip_sampler *s) {
+    if (hipMemcpy(s->st, &s->h, samp_bytes(&s->h), hipMemcpyHostToDevice) != hipSuccess) {
+        mynah_set_error("sampler state upload failed");
+        return -1;
+    }
+    return 0;
+}
+
+int mynah_hip_sampler_accept(mynah_hip_sampler *s, uint32_t token) {
+    if (s == NULL) {
+        mynah_set_error("null sampler");
+        return -1;
+    }
+    samp_push(&s->h, token);
+    return s->h.window ? samp_upload(s) : 0;
+}
+
+int mynah_hip_sample(mynah_hip_sampler *s, float *logits, uint32_t *id) {
+    mynah_device *d = mynah_dev();
+    if (d == NULL || s == NULL || logits == NULL || id == NULL) {
+        mynah_set_error("bad sample arguments");
+        return -1;
+    }
+    if (samp_scratch_alloc(&s->sc, s->vocab, 1) != 0) return -1;
+    const size_t bytes = (size_t)s->vocab * 4;
+    unsigned long long key = 0;
+    if (hipMemcpyAsync(s->sc.logits, logits, bytes, hipMemcpyHostToDevice, d->stream) != hipSuccess ||
+        samp_enqueue(d, d->stream, s->st, &s->sc, s->sc.logits, s->vocab, 0u) != 0 ||
+        hipMemcpyAsync(logits, s->sc.logits, bytes, hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
+        hipMemcpyAsync(&key, s->sc.key, 8, hipMemcpyDeviceToHost, d->stream) != hipSuccess ||
+        hipMemcpyAsync(&s->h, s->st, samp_bytes(&s->h), hipMemcpyDeviceToHost, d->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(d->stream) != hipSuccess) {
+        mynah_set_error("device sampling failed");
+        return -1;
+    }
+    *id = ~(uint32_t)(key & 0xffffffffull);
+    return 0;
+}
+
 /* ── the generation loop (src/generate.c:13-86) ──────────────────────────── */
 
 static double now_s(void) {
@@ -1240,17 +1449,29 @@ static int take_token(const mynah_hip_gen_params *p, mynah_hip_timing *t, double
     return 1;
 }
 
-long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params *p,
+long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params *pp,
                                      mynah_hip_timing *t) {
     mynah_device *d = mynah_dev();
     mynah_hip_timing scratch_t;
     if (t == NULL) t = &scratch_t;
     memset(t, 0, sizeof *t);
-    if (d == NULL || s == NULL || p == NULL || p->prompt == NULL || p->n_prompt == 0 ||
-        (p->n_eos > 0 && p->eos == NULL) || p->n_prompt > 0xffffffffu) {
+    if (d == NULL || s == NULL || pp == NULL || pp->prompt == NULL || pp->n_prompt == 0 ||
+        (pp->n_eos > 0 && pp->eos == NULL) || pp->n_prompt > 0xffffffffu) {
         mynah_set_error("bad generation arguments");
         return -1;
     }
+    /* With the device sampler the host sampler's hooks are not used. */
+    mynah_hip_gen_params q = *pp;
+    mynah_hip_sampler *sm = q.device_sampler;
+    if (sm != NULL) {
+        q.sample = NULL;
+        q.accept = NULL;
+        if (sm->vocab != s->c.vocab) {
+            mynah_set_error("sampler vocabulary %u, model %u", sm->vocab, s->c.vocab);
+            return -1;
+        }
+    }
+    const mynah_hip_gen_params *p = &q;
     for (size_t i = 0; i < p->n_prompt; i++)
         if (p->prompt[i] >= s->c.vocab) {
             mynah_set_error("token %u out of range", p->prompt[i]);
@@ -1270,6 +1491,8 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
     }
     if (p->accept)
         for (uint32_t i = 0; i + 1 < n_prompt; i++) p->accept(p->sampler, p->prompt[i]);
+    if (sm != NULL)
+        for (uint32_t i = 0; i + 1 < n_prompt; i++) samp_push(&sm->h, p->prompt[i]);
     {   /* src/timing.c:30-35 */
         const double now = now_s();
         t->prefill_s = now - t0;
@@ -1278,6 +1501,7 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
     }
     uint32_t next = p->prompt[n_prompt - 1u];
     if (p->accept) p->accept(p->sampler, next);
+    if (sm != NULL) samp_push(&sm->h, next);
     long produced = 0;
     if (p->sample != NULL) {
         /* Host sampling: every step's logits come back to the host and the
@@ -1297,12 +1521,30 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
             next = id;
         }
     } else {
-        /* Greedy on the device: up to `chunk` steps replay as graphs per
-         * host round trip (the first step alone, so TTFT is one step), then
-         * the ids come back and run through the loop's checks in order. A
-         * stop inside a chunk rewinds the position to just after the
-         * stopping step: the cache slots past it are rewritten before any
-         * later step reads them. */
+        /* Greedy, or the device sampler, on the device: up to `chunk` steps
+         * replay as graphs per host round trip (the first step alone, so
+         * TTFT is one step), then the ids come back and run through the
+         * loop's checks in order. A stop inside a chunk rewinds the position
+         * to just after the stopping step: the cache slots past it are
+         * rewritten before any later step reads them. The sampler's device
+         * copy may run ahead of the stop; the caller's sampler is brought to
+         * exactly the ids taken, below. Greedy without penalties is the
+         * reference's sampler at temp <= 0 and takes the plain greedy steps. */
+        int variant = STEP_FULL;
+        if (sm != NULL) {
+            const SampState *h = &sm->h;
+            if (h->temp > 0.0f || h->repeat_penalty != 1.0f || h->freq_penalty != 0.0f ||
+                h->presence_penalty != 0.0f) {
+                int ok = 1;
+                if (s->samp_st == NULL) s->samp_st = (SampState *)dalloc(sizeof(SampState), &ok);
+                if (!ok || samp_scratch_alloc(&s->samp_sc, s->c.vocab, 0) != 0 ||
+                    hipMemcpy(s->samp_st, h, samp_bytes(h), hipMemcpyHostToDevice) != hipSuccess) {
+                    mynah_set_error("device sampler set-up failed");
+                    return -1;
+                }
+                variant = STEP_SAMPLE;
+            }
+        }
         const uint32_t chunk = p->chunk ? p->chunk : STEP_BATCH;
         uint32_t done = 0;
         int go = 1;
@@ -1311,8 +1553,8 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
             if (c > p->max_new - done) c = p->max_new - done;
             if (c > s->n_ctx - s->n_past) c = s->n_ctx - s->n_past;
             if (set_counters(s, d, next, 0, 0) != 0) return -1;
-            prepare_steps(s, d, STEP_FULL, s->n_past, c);
-            if (embed_current(s, d) != 0 || run_steps(s, d, STEP_FULL, s->n_past, c) != 0)
+            prepare_steps(s, d, variant, s->n_past, c);
+            if (embed_current(s, d) != 0 || run_steps(s, d, variant, s->n_past, c) != 0)
                 return -1;
             uint32_t ids[64];
             uint32_t *buf = c <= 64u ? ids : (uint32_t *)malloc((size_t)c * 4);
@@ -1329,12 +1571,19 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
                 const uint32_t id = buf[used++];
                 go = take_token(p, t, t0, id, &produced);
                 next = id;
+                if (sm != NULL) {
+                    /* src/generate.c:51-52: the id entered the window and,
+                     * at temp > 0, took one splitmix64 draw. */
+                    samp_push(&sm->h, id);
+                    if (sm->h.temp > 0.0f) sm->h.rng += 0x9E3779B97F4A7C15ull;
+                }
             }
             if (buf != ids) free(buf);
             s->n_past += used;
             done += used;
         }
     }
+    if (sm != NULL && samp_upload(sm) != 0) return -1;
     t->decode_s = now_s() - t0;        /* src/timing.c:57-59 */
     return produced;
 }

@@ -11,5 +11,6 @@
 #include "gemm_exact.hip"
 #include "gemm_mfma.hip"
 #include "decode.hip"
+#include "sample.hip"
 #include "copy.hip"
 #include "int8.hip"

@@ -63,6 +63,10 @@ enum { MYNAH_Q4_0 = 2, MYNAH_Q8_0 = 8, MYNAH_Q4_K = 12, MYNAH_Q5_K = 13, MYNAH_Q
     X(MYNAH_K_ATTN_COMBINE, "mynah_attn_combine")      \
     X(MYNAH_K_ATTN_COMBINE1, "mynah_attn_combine1")    \
     X(MYNAH_K_ARGMAX, "mynah_argmax_advance")          \
+    X(MYNAH_K_SAMP_PENALIZE, "mynah_samp_penalize")    \
+    X(MYNAH_K_SAMP_EXP, "mynah_samp_exp")              \
+    X(MYNAH_K_SAMP_TOPK, "mynah_samp_topk")            \
+    X(MYNAH_K_SAMP_PICK, "mynah_samp_pick")            \
     X(MYNAH_K_RMSNORM, "mynah_rmsnorm")                \
     X(MYNAH_K_EMBED, "mynah_embed_row")                \
     X(MYNAH_K_RMSNORM_ROWS, "mynah_rmsnorm_rows")      \

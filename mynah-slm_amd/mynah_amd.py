@@ -41,7 +41,16 @@ class GenParams(C.Structure):
     _fields_ = [("prompt", C.c_void_p), ("n_prompt", C.c_size_t), ("max_new", C.c_uint32),
                 ("eos", C.c_void_p), ("n_eos", C.c_size_t), ("on_token", C.c_void_p),
                 ("token_ctx", C.c_void_p), ("sample", C.c_void_p), ("accept", C.c_void_p),
-                ("sampler", C.c_void_p), ("chunk", C.c_uint32)]
+                ("sampler", C.c_void_p), ("chunk", C.c_uint32), ("device_sampler", C.c_void_p)]
+
+
+class SamplerParams(C.Structure):
+    """mynah_hip_sampler_params (include/mynah_generate.h) = the reference's
+    mynah_slm_sampler_params (src/sampler.h:16-30)."""
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("min_p", C.c_float), ("repeat_penalty", C.c_float), ("freq_penalty", C.c_float),
+                ("presence_penalty", C.c_float), ("penalty_window", C.c_uint32),
+                ("seed", C.c_uint64)]
 
 
 class GenTiming(C.Structure):
@@ -128,6 +137,10 @@ def _load() -> C.CDLL:
         "mynah_hip_qwen3_generate": (C.c_int, [_P, C.c_uint32, C.c_uint32, _P,
                                                C.POINTER(C.c_float)]),
         "mynah_hip_qwen3_forced": (C.c_int, [_P, _P, C.c_uint32, _P, _P]),
+        "mynah_hip_sampler_new": (_P, [C.POINTER(SamplerParams), C.c_uint32]),
+        "mynah_hip_sampler_free": (None, [_P]),
+        "mynah_hip_sampler_accept": (C.c_int, [_P, C.c_uint32]),
+        "mynah_hip_sample": (C.c_int, [_P, _P, C.POINTER(C.c_uint32)]),
         "mynah_hip_qwen3_generate_tokens": (C.c_long, [_P, C.POINTER(GenParams),
                                                        C.POINTER(GenTiming)]),
         "mynah_hip_qwen3_set_kv": (C.c_int, [_P, _P, _P, C.c_uint32]),
@@ -582,6 +595,44 @@ ATTN_EXACT, ATTN_SPLIT = 0, 1
 PREFILL_BATCHED, PREFILL_STEPS = 0, 1
 
 
+def sampler_params(temp=0.0, top_k=0, top_p=1.0, min_p=0.0, repeat_penalty=1.0,
+                   freq_penalty=0.0, presence_penalty=0.0, penalty_window=64, seed=0):
+    return SamplerParams(temp, top_k, top_p, min_p, repeat_penalty, freq_penalty,
+                         presence_penalty, penalty_window, seed)
+
+
+class DeviceSampler:
+    """The reference's sampler on the device (mynah_hip_sampler_*): `sample`
+    picks from host logits (modified in place like the reference's), and
+    Qwen3Decoder.generate_tokens(device_sampler=...) samples inside the
+    captured steps."""
+
+    def __init__(self, vocab: int, **params):
+        self.params = sampler_params(**params)
+        self.h = lib.mynah_hip_sampler_new(C.byref(self.params), vocab)
+        if not self.h:
+            raise HipError(f"sampler_new: {lib.mynah_hip_last_error().decode()}")
+
+    def sample(self, logits: np.ndarray) -> int:
+        out = C.c_uint32(0)
+        check(lib.mynah_hip_sample(self.h, ptr(logits), C.byref(out)), "sample")
+        return int(out.value)
+
+    def accept(self, token: int) -> None:
+        check(lib.mynah_hip_sampler_accept(self.h, token), "sampler_accept")
+
+    def close(self) -> None:
+        if self.h:
+            lib.mynah_hip_sampler_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Qwen3Decoder:
     """The GPU decode state (include/mynah_decode.h) over a SynthQwen3."""
 
@@ -663,10 +714,12 @@ class Qwen3Decoder:
         return [int(t) for t in out], logits
 
     def generate_tokens(self, prompt, max_new: int, eos=(), sampler=None, chunk: int = 0,
-                        stop_after=None, on_token=None):
+                        stop_after=None, on_token=None, device_sampler=None):
         """The generation loop (include/mynah_generate.h). `sampler`: None for
         greedy on the device, else an object with a C handle `h` and
-        `fn_addresses()` -> (sample, accept). The token callback stops after
+        `fn_addresses()` -> (sample, accept); `device_sampler`: a
+        DeviceSampler, sampling inside the device steps instead (then
+        `sampler` is unused). The token callback stops after
         `stop_after` ids, or when `on_token(id)` (if given) returns true.
         Returns (ids the callback saw, count the loop returned, timing)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
@@ -685,6 +738,8 @@ class Qwen3Decoder:
         gp.eos, gp.n_eos = ptr(e), len(eos)
         gp.on_token = C.cast(cb, C.c_void_p).value
         gp.chunk = chunk
+        if device_sampler is not None:
+            gp.device_sampler = device_sampler.h
         if sampler is not None:
             gp.sample, gp.accept = sampler.fn_addresses()
             gp.sampler = sampler.h

@@ -15,6 +15,10 @@
  * switch the channel and reach neither callback, each channel has its own
  * detokenizer and callback — and afterwards the answer detokenizer is
  * flushed (src/generate.c:80-83) and the timing copied.
+ * mynah_slm_generate_hip_dev is the same with the sampler on the device: a
+ * front end makes it from its mynah_slm_sampler_params (same fields, same
+ * order) with mynah_hip_sampler_new and keeps the reference's sampler for
+ * the settings that returns NULL for.
  *
  * SPDX-License-Identifier: MIT */
 #include "generate.h"
@@ -48,14 +52,13 @@ static int token_cb(void *c_, uint32_t id) {
     return cb ? cb(c->in_think ? p->cb_think_ctx : p->cb_ctx, id, piece, (size_t)w) : 0;
 }
 
-long mynah_slm_generate_hip(mynah_qwen3 *gpu, const mynah_slm_tokenizer *tok,
-                            mynah_slm_sampler *sam, const mynah_slm_gen_params *p,
-                            mynah_slm_timing *t) {
+static long generate(mynah_qwen3 *gpu, const mynah_slm_tokenizer *tok, mynah_slm_sampler *sam,
+                     mynah_hip_sampler *dev, const mynah_slm_gen_params *p, mynah_slm_timing *t) {
     struct chan c = {.p = p};
     mynah_slm_detok_init(&c.d_answer, tok);
     mynah_slm_detok_init(&c.d_think, tok);
     mynah_hip_gen_params g = {p->prompt, p->n_prompt, p->max_new, p->eos, p->n_eos,
-                              token_cb, &c, sample_cb, accept_cb, sam, 0};
+                              token_cb, &c, sample_cb, accept_cb, sam, 0, dev};
     mynah_hip_timing ht;
     const long n = mynah_hip_qwen3_generate_tokens(gpu, &g, &ht);
     char piece[512];
@@ -70,4 +73,16 @@ long mynah_slm_generate_hip(mynah_qwen3 *gpu, const mynah_slm_tokenizer *tok,
         t->n_gen = ht.n_gen;
     }
     return n;
+}
+
+long mynah_slm_generate_hip(mynah_qwen3 *gpu, const mynah_slm_tokenizer *tok,
+                            mynah_slm_sampler *sam, const mynah_slm_gen_params *p,
+                            mynah_slm_timing *t) {
+    return generate(gpu, tok, sam, NULL, p, t);
+}
+
+long mynah_slm_generate_hip_dev(mynah_qwen3 *gpu, const mynah_slm_tokenizer *tok,
+                                mynah_hip_sampler *dev, const mynah_slm_gen_params *p,
+                                mynah_slm_timing *t) {
+    return generate(gpu, tok, NULL, dev, p, t);
 }

@@ -15,7 +15,8 @@ archive like the reference's libingot.a, against libmynah_hip.so with
     ingot_gguf_matvec uses to locate a tensor's bytes;
   * the front-end binding of the generation loop (oracle/generate_hip.c, the
     code INTEGRATION.md shows) compiles against the reference's headers and
-    links: mynah_slm_generate_hip is defined and its loop,
+    links: mynah_slm_generate_hip and mynah_slm_generate_hip_dev are defined
+    and their loop,
     mynah_hip_qwen3_generate_tokens, comes from the library.
 """
 from __future__ import annotations
@@ -83,3 +84,4 @@ def test_generate_binding_links(linked):
     imported = {s for t, s in nm(["-D", linked]) if t == "U" and s.startswith("mynah_hip_")}
     assert imported == {"mynah_hip_qwen3_generate_tokens"} and imported <= ours
     assert ("T", "mynah_slm_generate_hip") in set(nm([linked]))
+    assert ("T", "mynah_slm_generate_hip_dev") in set(nm([linked]))
