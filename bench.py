@@ -254,6 +254,7 @@ def gpu_decode(M, CF):
                          "tokens_match_reference": toks == want, "graph": dec.uses_graph,
                          "teacher_forced": forced_check(dec, forced, k, v, npre)}
             dec.close()
+        out["sampled"] = sampled_decode(M, model, k, v, npre, first, steps)
     finally:
         M.check(M.lib.mynah_hip_set_gemv_order(old), "order")
     head = out["exact"]
@@ -268,6 +269,29 @@ def gpu_decode(M, CF):
                                "vectors (up to 1.8e-4 at configs[2], 2.9e-4 at configs[4] in "
                                "tests/test_decode_forced_gpu.py), reported for comparison only"}
     return out
+
+
+def sampled_decode(M, model, k, v, npre, first, steps):
+    """The same workload through the generation loop (exact mode, chunks of
+    eight steps per host round trip) with the front ends' default sampler
+    (Qwen3's temp 0.6, top_k 20, top_p 0.95; src/sampler.c:27-36) on the
+    device, beside greedy through the same loop. Its ids are the reference
+    sampler's (tests/test_sampler_gpu.py); here only the rate."""
+    params = dict(temp=0.6, top_k=20, top_p=0.95, seed=0)
+    res = {"sampler": "temp 0.6, top_k 20, top_p 0.95, seed 0, on the device"}
+    for name in ("greedy", "sampled"):
+        dec = M.Qwen3Decoder(model, npre + steps + 1)
+        dec.set_attention(M.ATTN_EXACT)
+        for rep in range(2):                             # the first captures the graphs
+            smp = M.DeviceSampler(model.shape.vocab, **params) if name == "sampled" else None
+            dec.reset()
+            dec.set_kv(k, v, npre)
+            _, n, t = dec.generate_tokens([first], steps, device_sampler=smp)
+            if smp is not None:
+                smp.close()
+        res[name + "_tok_s"] = round(n / t.decode_s, 1)
+        dec.close()
+    return res
 
 
 def gpu_prefill_gemm(M, CF, reps: int = 20, int8: bool = False):
