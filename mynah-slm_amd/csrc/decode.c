@@ -1449,6 +1449,12 @@ static int take_token(const mynah_hip_gen_params *p, mynah_hip_timing *t, double
     return 1;
 }
 
+/* A failed call still leaves the caller's sampler with the ids it took. */
+static long gen_fail(mynah_hip_sampler *sm) {
+    if (sm != NULL) (void)samp_upload(sm);
+    return -1;
+}
+
 long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params *pp,
                                      mynah_hip_timing *t) {
     mynah_device *d = mynah_dev();
@@ -1540,7 +1546,7 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
                 if (!ok || samp_scratch_alloc(&s->samp_sc, s->c.vocab, 0) != 0 ||
                     hipMemcpy(s->samp_st, h, samp_bytes(h), hipMemcpyHostToDevice) != hipSuccess) {
                     mynah_set_error("device sampler set-up failed");
-                    return -1;
+                    return gen_fail(sm);
                 }
                 variant = STEP_SAMPLE;
             }
@@ -1552,10 +1558,10 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
             uint32_t c = done == 0 ? 1u : chunk;
             if (c > p->max_new - done) c = p->max_new - done;
             if (c > s->n_ctx - s->n_past) c = s->n_ctx - s->n_past;
-            if (set_counters(s, d, next, 0, 0) != 0) return -1;
+            if (set_counters(s, d, next, 0, 0) != 0) return gen_fail(sm);
             prepare_steps(s, d, variant, s->n_past, c);
             if (embed_current(s, d) != 0 || run_steps(s, d, variant, s->n_past, c) != 0)
-                return -1;
+                return gen_fail(sm);
             uint32_t ids[64];
             uint32_t *buf = c <= 64u ? ids : (uint32_t *)malloc((size_t)c * 4);
             if (buf == NULL ||
@@ -1564,7 +1570,7 @@ long mynah_hip_qwen3_generate_tokens(mynah_qwen3 *s, const mynah_hip_gen_params 
                 hipStreamSynchronize(d->stream) != hipSuccess) {
                 if (buf != ids) free(buf);
                 mynah_set_error("greedy decode failed");
-                return -1;
+                return gen_fail(sm);
             }
             uint32_t used = 0;
             while (used < c && go) {
