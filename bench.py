@@ -7,7 +7,9 @@ in HBM. Each step reads a different one of several device copies of every
 matrix (together > 2x the 256 MB MALL), so every launch streams from HBM.
 
 `value` = algorithmic bytes per step (weights + x + y) / time per step.
-`roofline` is the dominant kernel (the Q6_K head GEMV): algorithmic bytes per
+`sweep` gives beside it the median and spread of 20 shorter trials of the
+same sweep and the hot-cache figure (one weight copy, mostly held by the
+MALL). `roofline` is the dominant kernel (the Q6_K head GEMV): algorithmic bytes per
 launch over its average duration, timed with HIP events on the launch stream
 inside the timed region. `traffic` is the HBM bytes per launch measured by
 rocprofv3 PMC counters (profiles/traffic.json), when present.
@@ -21,7 +23,8 @@ configs[3]'s batched products, each the median of five runs.
 
 Beside the metric line's value: `decode` (configs[2], Qwen3-0.6B greedy
 decode tok/s in three numerics modes, tokens checked against the compiled
-reference's), `prefill_gemm` (configs[3], the exact batched GEMM at 512
+reference's, and `decode.sampled`: the generation loop with the front ends'
+default sampler on the device), `prefill_gemm` (configs[3], the exact batched GEMM at 512
 tokens), `prefill_gemm_int8` (the same with Q4_K on the int8 activation
 lane, the batched default of the reference's AVX2 build),
 `qwen3_4b_end_to_end` (configs[4]: 2048-token prompt prefill and 256
@@ -83,6 +86,20 @@ def gpu_sweep(M, CF, steps: int, warmup: int):
     M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, max(1, warmup), -1)
     total_ms, head_total = M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, steps, head)
     head_ms = head_total / steps
+    # Beside the timed block: 20 trials of the same sweep (median, spread),
+    # and the hot-cache figure over one weight copy (144 MB: the MALL holds
+    # most of it).
+    trial_steps = max(1, steps // 20)
+    trials = sorted(step_bytes * trial_steps / (M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs,
+                                                             trial_steps, -1)[0] * 1e-3) / 1e9
+                    for _ in range(20))
+    one = [ws[i][0].ptr for i in range(len(mats))]
+    M.time_sweep(mats, one, 1, x_ptrs, y_ptrs, max(1, warmup), -1)
+    hot_ms = M.time_sweep(mats, one, 1, x_ptrs, y_ptrs, steps, -1)[0] / steps
+    extra = {"trials": {"count": 20, "steps_each": trial_steps,
+                        "median_gbs": round(trials[10], 1), "min_gbs": round(trials[0], 1),
+                        "max_gbs": round(trials[-1], 1)},
+             "hot_cache_gbs": round(step_bytes / (hot_ms * 1e-3) / 1e9, 1)}
 
     # Per-matrix averages, each matrix alone over its rotating copies.
     per = {}
@@ -93,7 +110,7 @@ def gpu_sweep(M, CF, steps: int, warmup: int):
         per[m.name] = round(algorithmic_bytes(m) / (ms * 1e-3) / 1e9, 1)
     for b in [b for c in ws for b in c] + xs + ys:
         b.free()
-    return step_bytes, copies, total_ms, head_ms, algorithmic_bytes(mats[head]), per
+    return step_bytes, copies, total_ms, head_ms, algorithmic_bytes(mats[head]), per, extra
 
 
 def gpu_c1(M, CF, launches: int = 256):
@@ -745,8 +762,8 @@ def main() -> int:
         return 0
 
     log("[bench] configs[1] sweep")
-    step_bytes, copies, total_ms, head_ms, head_bytes, per = gpu_sweep(M, CF, args.steps,
-                                                                       args.warmup)
+    step_bytes, copies, total_ms, head_ms, head_bytes, per, sweep_extra = gpu_sweep(
+        M, CF, args.steps, args.warmup)
     ms_per_step = total_ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = head_bytes / (head_ms * 1e-3) / 1e9
@@ -821,6 +838,7 @@ def main() -> int:
         "prefill_gemm": prefill,
         "prefill_gemm_int8": prefill_int8,
         "qwen3_4b_end_to_end": e2e_4b,
+        "sweep": sweep_extra,
         "per_matrix_gbs": per,
         "qwen3_4b_gemv_gbs": extra_4b,
         "qwen3_4b_copy_ceiling_gbs": ceiling_4b,
