@@ -8,8 +8,10 @@ place, over streams of logits with exact ties at the top (the lower id must
 win) and extra window entries between draws, at a 3,000-entry vocabulary
 (two workgroups) and Qwen3's 151,936 (75), for greedy with penalties, the
 Qwen3 defaults, min_p, top_p with frequency and presence penalties, top_k 1
-and 128, a hot temperature and seed 0's fixed state; the index-order double
-sum forced on (MYNAH_SAMPLE_SEQ_SUM=1) gives the same ids. Then the
+and 128, a hot temperature, seed 0's fixed state, temperatures 0.01 and 100,
+a top_p below the best candidate's probability, min_p 1 and a window of 4096
+entries; the index-order double sum forced on (MYNAH_SAMPLE_SEQ_SUM=1) gives
+the same ids. Then the
 generation loop with the device sampler against the same loop with the
 oracle sampler on the host (the decoder's logits are bit-identical, so the
 sampler is the only difference): ids, count, a stop in the middle of a
@@ -36,6 +38,12 @@ CASES = [
     dict(temp=1.5, top_k=128, seed=0),                                        # the fixed default state
     dict(temp=0.7, top_k=1, seed=5),
     dict(temp=3.0, top_k=100, top_p=0.99, repeat_penalty=0.9, penalty_window=64, seed=9),
+    dict(temp=0.01, top_k=20, top_p=0.95, seed=2),                          # nearly greedy
+    dict(temp=100.0, top_k=128, min_p=0.5, seed=4),                          # nearly flat
+    dict(temp=0.6, top_k=20, top_p=0.01, seed=6),                            # top_p below the best
+    dict(temp=1.0, top_k=64, min_p=1.0, seed=8),                             # min_p keeps the best
+    dict(temp=0.9, top_k=30, repeat_penalty=1.1, freq_penalty=0.05, presence_penalty=0.2,
+         penalty_window=4096, seed=10),                                      # the largest window
 ]
 
 
