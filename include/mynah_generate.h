@@ -19,8 +19,8 @@
  *     index of the largest logit), with the logits never leaving HBM; steps
  *     run as captured graphs, up to `chunk` per host round trip (0: 8), the
  *     first step alone so TTFT is one step. This is the reference's sampler
- *     at temp <= 0 with every penalty off; with penalties on, pass the
- *     reference's sampler as below.
+ *     at temp <= 0 with every penalty off; with penalties on, pass a
+ *     device sampler or the reference's sampler as below.
  *   - sample != NULL: every step's logits are copied to a host buffer and
  *     sample(sampler, logits) picks (the reference's mynah_slm_sample, which
  *     may modify the logits in place, fits as is); accept(sampler, id), when
