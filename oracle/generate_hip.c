@@ -5,8 +5,9 @@
  * TEST INFRASTRUCTURE HERE: oracle/Makefile's `linkcheck` compiles it
  * against the reference's headers under /root/reference and links it, with
  * the reference's decoder and CLI, against libmynah_hip.so with
- * --no-undefined (tests/test_integration_link.py). INTEGRATION.md shows the
- * same code. Nothing of it is part of the library or runs on the GPU box.
+ * --no-undefined (tests/test_integration_link.py); the integration notes
+ * show the same code. Nothing of it is part of the library or runs on the
+ * GPU box.
  *
  * mynah_slm_generate_hip has mynah_slm_generate's contract
  * (src/generate.h:47-52) over the resident decoder: the loop itself is

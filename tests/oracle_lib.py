@@ -474,7 +474,7 @@ def oracle_generate(orc_model: "OracleQwen3", prompt, max_new: int, eos=(), samp
 
 class ChannelRouter:
     """The token callback a front end binds around the generation loop
-    (src/generate.c:60-77; INTEGRATION.md section 2's glue): the think
+    (src/generate.c:60-77; oracle/generate_hip.c's token_cb): the think
     markers switch channels and reach neither, answer ids go to `answer`
     (asking to stop once `stop_after` of them arrived, 0: never), ids between
     the markers to `think`. Called with each generated non-EOS id; returns

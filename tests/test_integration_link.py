@@ -14,9 +14,9 @@ archive like the reference's libingot.a, against libmynah_hip.so with
   * the executable exports ingot_gguf_data, which the library's
     ingot_gguf_matvec uses to locate a tensor's bytes;
   * the front-end binding of the generation loop (oracle/generate_hip.c, the
-    code INTEGRATION.md shows) compiles against the reference's headers and
-    links: mynah_slm_generate_hip and mynah_slm_generate_hip_dev are defined
-    and their loop,
+    code a maintainer adds beside src/generate.c) compiles against the
+    reference's headers and links: mynah_slm_generate_hip and
+    mynah_slm_generate_hip_dev are defined and their loop,
     mynah_hip_qwen3_generate_tokens, comes from the library.
 """
 from __future__ import annotations
