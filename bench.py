@@ -53,6 +53,7 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3
 PEAK_INT8_TOPS = 5000.0
 MALL_BYTES = 256 << 20
+HEAD_EVERY = 10   # the roofline kernel's launch is timed in every tenth pass
 
 
 def log(msg: str) -> None:
@@ -84,8 +85,11 @@ def gpu_sweep(M, CF, steps: int, warmup: int):
     w_ptrs = [b.ptr for copies_of in ws for b in copies_of]
     x_ptrs, y_ptrs = [b.ptr for b in xs], [b.ptr for b in ys]
     M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, max(1, warmup), -1)
-    total_ms, head_total = M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, steps, head)
-    head_ms = head_total / steps
+    # The head's launch is bracketed by HIP events in every tenth pass of
+    # the timed region (an event pair lengthens a pass by ~5.6 µs, so they
+    # sample the passes rather than mark all of them).
+    total_ms, head_ms = M.time_sweep(mats, w_ptrs, copies, x_ptrs, y_ptrs, steps, head,
+                                     HEAD_EVERY)
     # Beside the timed block: 20 trials of the same sweep (median, spread),
     # and the hot-cache figure over one weight copy (144 MB: the MALL holds
     # most of it).

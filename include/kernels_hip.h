@@ -264,11 +264,13 @@ int   mynah_hip_event_destroy(void *event);
 /* Benchmark helper for a sweep of n matrices: `steps` passes, pass i
  * launching matrix m on weight copy w[m * copies + i % copies] (all copies of
  * one matrix share x[m] and y[m]). Launched from C on the library stream and
- * timed with HIP events: *ms_total for all passes, and *ms_timed the summed
- * duration of matrix `timed`'s launches (events around each). */
+ * timed with HIP events: *ms_total for all passes, and *ms_timed the average
+ * duration of matrix `timed`'s launch in every `every`-th pass (an event pair
+ * around each of those: the markers lengthen a pass by a few µs, so a sample
+ * of the passes carries them; every = 1: all). timed < 0: none. */
 int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copies,
                          const size_t *rows, const size_t *cols, const float *const *x,
-                         float *const *y, int steps, int timed, float *ms_total,
+                         float *const *y, int steps, int timed, int every, float *ms_total,
                          float *ms_timed);
 
 /* Benchmark helper: `iters` launches of the matvec, cycling through the

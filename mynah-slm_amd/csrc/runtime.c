@@ -1323,13 +1323,13 @@ int mynah_hip_event_destroy(void *event) {
 
 int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copies,
                          const size_t *rows, const size_t *cols, const float *const *x,
-                         float *const *y, int steps, int timed, float *ms_total,
+                         float *const *y, int steps, int timed, int every, float *ms_total,
                          float *ms_timed) {
     mynah_device *d = mynah_dev();
     if (d == NULL) return -1;
     if (n <= 0 || copies <= 0 || steps <= 0 || types == NULL || w == NULL || rows == NULL ||
         cols == NULL || x == NULL || y == NULL || ms_total == NULL || ms_timed == NULL ||
-        timed >= n) {
+        timed >= n || every <= 0) {
         mynah_set_error("bad sweep arguments");
         return -1;
     }
@@ -1341,11 +1341,12 @@ int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copi
         if (hipEventCreate(&ev[i]) != hipSuccess) rc = -1;
     if (rc == 0 && hipEventRecord(a, d->stream) != hipSuccess) rc = -1;
     for (int i = 0; rc == 0 && i < steps; i++) {
+        const int mark = i % every == 0;
         for (int m = 0; rc == 0 && m < n; m++) {
-            if (m == timed) (void)hipEventRecord(ev[2 * i], d->stream);
+            if (m == timed && mark) (void)hipEventRecord(ev[2 * i], d->stream);
             rc = mynah_gemv_launch(d, types[m], w[(size_t)m * copies + (size_t)(i % copies)],
                                    rows[m], cols[m], x[m], y[m], d->stream);
-            if (m == timed) (void)hipEventRecord(ev[2 * i + 1], d->stream);
+            if (m == timed && mark) (void)hipEventRecord(ev[2 * i + 1], d->stream);
         }
     }
     if (rc == 0 && (hipEventRecord(b, d->stream) != hipSuccess ||
@@ -1353,11 +1354,14 @@ int mynah_hip_time_sweep(int n, const int *types, const void *const *w, int copi
                     hipEventElapsedTime(ms_total, a, b) != hipSuccess))
         rc = -1;
     *ms_timed = 0.0f;
-    for (int i = 0; rc == 0 && timed >= 0 && i < steps; i++) {
+    int marked = 0;
+    for (int i = 0; rc == 0 && timed >= 0 && i < steps; i += every) {
         float t = 0.0f;
         if (hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = -1;
         *ms_timed += t;
+        marked++;
     }
+    if (marked > 0) *ms_timed /= (float)marked;
     if (rc != 0 && mynah_hip_last_error()[0] == 0) mynah_set_error("sweep timing failed");
     for (int i = 0; ev && timed >= 0 && i < 2 * steps; i++)
         if (ev[i]) (void)hipEventDestroy(ev[i]);

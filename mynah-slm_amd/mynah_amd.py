@@ -117,7 +117,8 @@ def _load() -> C.CDLL:
                                               C.POINTER(C.c_uint32)]),
         "mynah_hip_expf_dev": (C.c_int, [_P, _P, _SZ, _P]),
         "mynah_hip_time_sweep": (C.c_int, [C.c_int, _P, _P, C.c_int, _P, _P, _P, _P, C.c_int,
-                                           C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+                                           C.c_int, C.c_int, C.POINTER(C.c_float),
+                                           C.POINTER(C.c_float)]),
         "mynah_hip_time_matvec": (C.c_int, [C.c_int, _P, C.c_int, _SZ, _SZ, _P, _P, C.c_int,
                                             C.POINTER(C.c_float)]),
         "mynah_synth_blocks": (C.c_int, [C.c_int, C.c_uint64, _SZ, _SZ, _SZ, _P, C.c_int]),
@@ -379,9 +380,11 @@ def valu_add_rate(iters: int = 20000):
     return float(ns.value), int(simds.value)
 
 
-def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int):
+def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int,
+               every: int = 1):
     """Time `steps` passes over mats (launched from C); returns (total ms,
-    summed ms of matrix `timed`). w_ptrs is [matrix][copy] flattened."""
+    average ms of matrix `timed`'s launch over every `every`-th pass). w_ptrs
+    is [matrix][copy] flattened."""
     n = len(mats)
     types = (C.c_int * n)(*[m.qtype for m in mats])
     rows = (C.c_size_t * n)(*[m.rows for m in mats])
@@ -390,7 +393,7 @@ def time_sweep(mats, w_ptrs, copies: int, x_ptrs, y_ptrs, steps: int, timed: int
     x = (C.c_void_p * n)(*x_ptrs)
     y = (C.c_void_p * n)(*y_ptrs)
     tot, tim = C.c_float(0.0), C.c_float(0.0)
-    check(lib.mynah_hip_time_sweep(n, types, w, copies, rows, cols, x, y, steps, timed,
+    check(lib.mynah_hip_time_sweep(n, types, w, copies, rows, cols, x, y, steps, timed, every,
                                    C.byref(tot), C.byref(tim)), "time_sweep")
     return float(tot.value), float(tim.value)
 
