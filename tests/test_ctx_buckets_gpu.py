@@ -12,9 +12,11 @@ sides), decoded with n_ctx 40960 by buckets, with n_ctx 40960 as one bucket
 the probabilities from memory) and with n_ctx 1101. Exact attention: every
 piece's greedy ids and last logits bit for bit equal across the three, and
 the last logits against the oracle decoder (the restated reference) within
-|gpu - ref| / max(1, |ref|) <= 1e-4. Split attention: the buckets below
-32768 positions take 32-position chunks at both context sizes, so n_ctx
-40960 and 1101 agree bit for bit.
+|gpu - ref| / max(1, |ref|) <= 1e-4. The same across the largest buckets
+(32,760 cached positions, steps past 32,768, where the probabilities come
+from memory). Split attention: the buckets below 32768 positions take
+32-position chunks at both context sizes, so n_ctx 40960 and 1101 agree bit
+for bit.
 """
 from __future__ import annotations
 
@@ -88,6 +90,41 @@ def test_exact_attention_independent_of_buckets(M, inputs, monkeypatch):
         orc.forward(tok)
     want = orc.forward(inputs[-1]).astype(np.float64)
     got = by_bucket[-1][1].astype(np.float64)
+    err = float((np.abs(got - want) / np.maximum(1.0, np.abs(want))).max())
+    print(f"last step against the oracle: max rel err {err:.2e}")
+    assert err <= TOL
+
+
+def test_exact_attention_across_the_top_buckets(M, monkeypatch):
+    """Past 4096 positions the exact PV kernel reads the probabilities from
+    memory and the grids grow with the bucket: the tiny model with n_ctx
+    33,000 and 32,760 cached positions of N(0, 1), then 12 forced steps
+    across the 32,768-position boundary (the last bucket is the context
+    itself), by buckets and as one bucket: ids and last logits bit for bit
+    equal, and the last logits against the oracle within 1e-4."""
+    shape, n_ctx, n_pre, steps = CF.QWEN3_TINY, 33000, 32760, 12
+    print(f"[case] tiny exact attention, n_ctx {n_ctx}, {n_pre} cached, {steps} steps "
+          f"across 32768", flush=True)
+    k, v = O.kv_prefill(O.substream, shape, 0, n_pre)
+    inputs = [int(t) for t in CF.forced_inputs(M.synth_uniform, M.substream, shape.vocab, steps)]
+    model = M.SynthQwen3(shape, 0)
+    out = []
+    for buckets in ("1", "0"):
+        monkeypatch.setenv("MYNAH_CTX_BUCKETS", buckets)
+        dec = M.Qwen3Decoder(model, n_ctx)
+        monkeypatch.delenv("MYNAH_CTX_BUCKETS")
+        dec.set_kv(k, v, n_pre)
+        out.append(dec.forced(inputs))
+        dec.close()
+    assert out[0][0] == out[1][0]
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    O.orc.orc_threads_init(0)
+    orc = O.OracleQwen3(O.SynthModel(shape, 0), n_ctx)
+    orc.prefill_kv(k, v, n_pre)
+    for tok in inputs[:-1]:
+        orc.forward(tok)
+    want = orc.forward(inputs[-1]).astype(np.float64)
+    got = out[0][1].astype(np.float64)
     err = float((np.abs(got - want) / np.maximum(1.0, np.abs(want))).max())
     print(f"last step against the oracle: max rel err {err:.2e}")
     assert err <= TOL
