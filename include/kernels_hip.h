@@ -169,6 +169,20 @@ int mynah_hip_matmat_mv_dev(int type, const void *w, size_t rows, size_t cols,
 enum { MYNAH_GEMV_EXACT = 0, MYNAH_GEMV_REORDERED = 1 };
 int mynah_hip_set_gemv_order(int order);
 int mynah_hip_gemv_order(void);
+/* The reference's double sums (RMSNorm's squares, src/kernels.c:118-121;
+ * the softmax's exponentials, :213-218) are taken in a parallel order. Any
+ * order lies within γ(n−1) of the exact sum, as does the reference's index
+ * order, so where the f32 result (RMS scale, softmax reciprocal) is the same
+ * over that whole interval it is the reference's (csrc/sum_settle.h);
+ * otherwise the softmax and norm kernels add the terms again in index
+ * order. The GEMV kernels' fused RMSNorm keeps its parallel sum unchecked
+ * (by a rounding estimate its scale differs from the reference's about
+ * once in 10^7 sums), as do the split attention's query/key norms.
+ * on = 1 sends every checked sum through the index-order path (both paths
+ * give the same bits; a test switch), 0 (default) restores the check. Takes
+ * effect for launches after the call, on every initialised device. No
+ * reference counterpart. */
+int mynah_hip_set_index_order_sums(int on);
 /* The code-object name of the kernel one matvec of this type and shape
  * launches in the given order (-1: the current one), from the same plan the
  * launch makes; NULL (reason in mynah_hip_last_error) when it cannot run.

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "mynah_expf.h"
+#include "sum_settle.h"
 
 #define MYNAH_DEV static __device__ __forceinline__
 
@@ -174,6 +175,66 @@ MYNAH_DEV double block_sum_d(double v, double *sh) {
     const uint32_t nw = (blockDim.x + 63u) >> 6;
     for (uint32_t k = 0; k < nw; k++) t += sh[k];
     return t;
+}
+
+// ── the reference's double sums, from a parallel order ─────────────────────
+// The test that keeps a parallel-order double sum, and when it holds, is in
+// sum_settle.h. mynah_index_sums != 0 makes every such sum take the
+// index-order path (a test switch: mynah_hip_set_index_order_sums).
+// The hot kernels read it once, early, beside their other first loads
+// (index_sums_forced), and hand it to every test; protected visibility
+// addresses it directly, without a load of its address first.
+extern "C" {
+__device__ __attribute__((used, visibility("protected"))) uint32_t mynah_index_sums;
+}
+
+MYNAH_DEV uint32_t index_sums_forced() { return mynah_index_sums; }
+
+// The test on r's bits (every lane holds the same r), in the vector unit.
+MYNAH_DEV bool sum_settled(double r, uint32_t n, uint32_t k2, uint32_t forced) {
+    const uint64_t bits = (uint64_t)__double_as_longlong(r);
+    return (forced == 0u) & (mynah_sum_settled((uint32_t)(bits >> 32), (uint32_t)bits, n, k2) != 0);
+}
+
+// The branch to a sum's index-order path, marked unlikely so that the path
+// is laid out after the kernel's main path, which stays one straight run of
+// code (a taken branch over it would start a new instruction fetch).
+#define MYNAH_UNSETTLED(r, n, k2, forced) __builtin_expect(!sum_settled((r), (n), (k2), (forced)), 0)
+
+// src/kernels.c:119-120 itself: the squares of x[0 .. n) added in index
+// order. Every calling lane computes the whole sum (the addresses are the
+// same across the wave, so each load is one broadcast).
+MYNAH_DEV double seq_sumsq(const float *x, uint32_t n) {
+#pragma clang fp contract(off)
+    double acc = 0.0;
+#pragma nounroll
+    for (uint32_t i = 0; i < n; i++) acc += (double)x[i] * (double)x[i];
+    return acc;
+}
+
+// src/kernels.c:213-217's sum itself: e[0 .. n) added in index order, by
+// every calling lane.
+MYNAH_DEV double seq_sum(const float *e, uint32_t n) {
+#pragma clang fp contract(off)
+    double acc = 0.0;
+#pragma nounroll
+    for (uint32_t i = 0; i < n; i++) acc += (double)e[i];
+    return acc;
+}
+
+// src/kernels.c:121 before its conversion to f32.
+MYNAH_DEV double rms_inv(double sum, uint32_t n, float eps) {
+#pragma clang fp contract(off)
+    return 1.0 / sqrt(sum / (double)n + (double)eps);
+}
+
+// The RMS scale (float)(1 / sqrt(sum / n + eps)) of x[0 .. n) as the
+// reference computes it, from the sum of squares `sum` in a parallel order;
+// x is read again only when that sum cannot settle it.
+MYNAH_DEV float rms_scale_settled(double sum, const float *x, uint32_t n, float eps) {
+    double r = rms_inv(sum, n, eps);
+    if (MYNAH_UNSETTLED(r, n, 1u, index_sums_forced())) r = rms_inv(seq_sumsq(x, n), n, eps);
+    return (float)r;
 }
 
 MYNAH_DEV unsigned long long wave_max_u64(unsigned long long v) {

@@ -4,8 +4,11 @@
 // (src/kernels.c, src/arch_qwen3.c, src/sampler.c) operation for operation:
 // same products and sums, no contraction, double accumulators where the
 // reference keeps them. Parallel reductions change only the order of
-// double-precision sums (of exactly representable terms) and of
-// order-independent maxima; expf is the GPU's.
+// order-independent maxima and of double-precision sums of exactly
+// representable terms, whose f32 results (the softmax reciprocal, the RMS
+// scale) are kept only where sum_settled (sum_settle.h) shows that the
+// reference's index order gives the same; elsewhere the terms are added
+// again in index order. expf is the C library's (mynah_expf.h).
 //
 // The step position lives in device memory (`pos`, the reference's n_past),
 // so one captured launch sequence advances itself when replayed.
@@ -43,8 +46,7 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
     const uint32_t lane = threadIdx.x & 63u;
     double acc = 0.0;
     for (uint32_t i = lane; i < hd; i += 64) acc += (double)src[i] * (double)src[i];
-    const double sum = wave_sum_d(acc);
-    const float s = (float)(1.0 / sqrt(sum / (double)hd + (double)eps));
+    const float s = rms_scale_settled(wave_sum_d(acc), src, hd, eps);
     for (uint32_t i = lane; i < hd; i += 64) tmp[i] = src[i] * (s * w[i]);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -58,15 +60,35 @@ MYNAH_DEV void head_norm_rope(const float *src, float *dst, const float *__restr
 
 // Per-head RMSNorm + RoPE of a 128-vector held by one wave, lane i holding
 // x[i] and x[i + 64] (src/kernels.c:130-137, 173-189): the same operations as
-// head_norm_rope, with the pair (i, i + 64) rotated in registers.
-MYNAH_DEV void norm_rope_reg(float x0, float x1, float w0, float w1, float c, float sn, float eps,
-                             float &y0, float &y1) {
+// head_norm_rope, with the pair (i, i + 64) rotated in registers. The sum of
+// squares is the wave's (seq = false) or the reference's index order
+// (seq = true: x[0 .. 63] from the lanes' x0, then x[64 .. 127]); returns
+// the double scale r, s = (float)r, for the caller's check (sum_settled).
+MYNAH_DEV double norm_rope_reg(float x0, float x1, float w0, float w1, float c, float sn,
+                               float eps, bool seq, float &y0, float &y1) {
 #pragma clang fp contract(off)
-    const double sum = wave_sum_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
-    const float s = (float)(1.0 / sqrt(sum / 128.0 + (double)eps));
+    double sum;
+    if (!seq) {
+        sum = wave_sum_d((double)x0 * (double)x0 + (double)x1 * (double)x1);
+    } else {
+        sum = 0.0;
+#pragma nounroll
+        for (int j = 0; j < 64; j++) {
+            const double v = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x0), j));
+            sum += v * v;
+        }
+#pragma nounroll
+        for (int j = 0; j < 64; j++) {
+            const double v = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(x1), j));
+            sum += v * v;
+        }
+    }
+    const double r = rms_inv(sum, 128u, eps);
+    const float s = (float)r;
     const float a = x0 * (s * w0), b = x1 * (s * w1);
     y0 = a * c - b * sn;
     y1 = b * c + a * sn;
+    return r;
 }
 
 // Attention scores for one key head and a chunk of SC_POS positions
@@ -98,6 +120,8 @@ MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) float qn[8][128];
     __shared__ __attribute__((aligned(16))) float kn[128];
+    __shared__ double nr[9];
+    const uint32_t forced = index_sums_forced();
     const uint32_t kvh = blockIdx.x, c = blockIdx.y, t0 = c * SC_POS;
     if (c >= spec_chunks && t0 >= pos_ptr[0] + 1u) return;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -133,37 +157,60 @@ MYNAH_DEV void attn_scores_body(const float *__restrict__ q, float *__restrict__
         kw0 = k_norm[lane];
         kw1 = k_norm[lane + 64u];
     }
+    // The norms, then the scores; each norm's double scale goes to nr (the
+    // query heads' at h, the key's at 8) for the check after the scores.
+    auto norms = [&](bool seq) __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
-        const uint32_t h = wave + 4u * (uint32_t)e;
-        if (h < group) {
+        for (int e = 0; e < 2; e++) {
+            const uint32_t h = wave + 4u * (uint32_t)e;
+            if (h < group) {
+                float y0, y1;
+                const double rs = norm_rope_reg(x0[e], x1[e], w0, w1, cs, sn, eps, seq, y0, y1);
+                qn[h][lane] = y0;
+                qn[h][lane + 64u] = y1;
+                if (lane == 0) nr[h] = rs;
+            }
+        }
+        if (has_pos && wave == kw) {
             float y0, y1;
-            norm_rope_reg(x0[e], x1[e], w0, w1, cs, sn, eps, y0, y1);
-            qn[h][lane] = y0;
-            qn[h][lane + 64u] = y1;
+            const double rs = norm_rope_reg(k0, k1, kw0, kw1, cs, sn, eps, seq, y0, y1);
+            kn[lane] = y0;
+            kn[lane + 64u] = y1;
+            kpos[lane] = y0;
+            kpos[lane + 64u] = y1;
+            if (lane == 0) nr[8] = rs;
         }
-    }
-    if (has_pos && wave == kw) {
-        float y0, y1;
-        norm_rope_reg(k0, k1, kw0, kw1, cs, sn, eps, y0, y1);
-        kn[lane] = y0;
-        kn[lane + 64u] = y1;
-        kpos[lane] = y0;
-        kpos[lane + 64u] = y1;
-    }
+    };
+    auto dots = [&]() __attribute__((always_inline)) {
+        if (t < n_kv) {
+            if (t >= pos) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
+            }
+            for (uint32_t h = 0; h < group; h++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kv[j], acc);
+                const float dot = row16_dot(acc);
+                if (l == 0) scores[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
+            }
+        }
+    };
+    norms(false);
     __syncthreads();
-    if (t < n_kv) {
-        if (t >= pos) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) kv[j] = kn[16 * j + l];
-        }
-        for (uint32_t h = 0; h < group; h++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc = __builtin_fmaf(qn[h][16 * j + l], kv[j], acc);
-            const float dot = row16_dot(acc);
-            if (l == 0) scores[(size_t)(kvh * group + h) * sstride + t] = dot * scale;
-        }
+    dots();
+    // The check, after the scores are out (off the path to them): lane h <
+    // group tests query head h's scale, lane 8 the key's; every wave reads
+    // the same nr, so the workgroup decides as one. Where a scale does not
+    // settle (or under the test switch), the norms are taken again in index
+    // order and the scores (and the cache slot) written again.
+    bool bad = false;
+    if (lane < group || (lane == 8u && has_pos)) bad = !sum_settled(nr[lane], 128u, 1u, 0u);
+    if (forced != 0u || __ballot(bad) != 0ull) {
+        __syncthreads();
+        norms(true);
+        __syncthreads();
+        dots();
     }
 }
 
@@ -281,8 +328,19 @@ MYNAH_DEV void softmax_finish(float4 *sv, uint32_t n_kv, float *p, const uint64_
             sv[k] = e;
         }
     }
-    const double sum = wave_sum_d(acc);
-    const float inv = (float)(1.0 / sum);
+    double r = 1.0 / wave_sum_d(acc);
+    if (MYNAH_UNSETTLED(r, n_kv, 2u, index_sums_forced())) {
+        // The exponentials into p, then every lane adds them in index order.
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const uint32_t i = lane + 64u * (uint32_t)k;
+            if ((uint32_t)k < kmax && i < n4) *(float4 *)(p + 4u * i) = sv[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        r = 1.0 / seq_sum(p, n_kv);
+    }
+    const float inv = (float)r;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int k = 0; k < KS; k++) {
@@ -344,8 +402,13 @@ MYNAH_DEV void softmax_row_long(const float *sc_row, uint32_t n_kv, float *p) {
         acc += (double)e.w;
         p4[i] = e;
     }
-    const double sum = wave_sum_d(acc);
-    const float inv = (float)(1.0 / sum);
+    double r = 1.0 / wave_sum_d(acc);
+    if (MYNAH_UNSETTLED(r, n_kv, 2u, index_sums_forced())) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        r = 1.0 / seq_sum(p, n_kv);
+    }
+    const float inv = (float)r;
     for (uint32_t i = lane; i < n4; i += 64u) {
         const float4 e = p4[i];
         p4[i] = make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv);
@@ -514,8 +577,10 @@ MYNAH_DEV void steps_until(uint32_t n, F &&f) {
 // beside the chain. The probabilities are either computed by the loader
 // waves into LDS (PMEM = false, n_kv <= 256 DPV_LW KS: the softmax of
 // src/kernels.c:207-220 over the four waves — f32 max, expf, a double sum
-// per lane, per wave (wave_sum_d) and then of the four waves in order,
-// product with the f32 reciprocal) or read, normalised by
+// per lane, per wave (wave_sum_d) and then of the four waves in order, kept
+// where sum_settled shows the reference's index order gives the same f32
+// reciprocal and otherwise taken again in index order, product with the
+// f32 reciprocal) or read, normalised by
 // mynah_attn_softmax, from the scores rows and staged per chunk beside V
 // (PMEM = true, any length). Grid n_heads * 128 / DPV_SW: workgroup b takes
 // key head kvh = b % n_kv_heads, query head kvh * group + (b / n_kv_heads) %
@@ -550,19 +615,57 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
     __shared__ uint64_t etab[DPV_LW][32];
     __shared__ float wmax[DPV_LW];
     __shared__ double wsum[DPV_LW];
+    const uint32_t forced = index_sums_forced();
     const uint32_t n_kv = pos + 1u;
     const uint32_t b = blockIdx.x, kvh = b % n_kv_heads, rest = b / n_kv_heads;
     const uint32_t head = kvh * group + rest % group, slice = rest / group;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t nc = (n_kv + DPV_CH - 1u) / DPV_CH;
     const float *prow = sp + (size_t)head * sstride;
-
     if (wave == 0) {
+        bool refix = false;
+        float fix = 0.0f, mx = 0.0f;
         if constexpr (!PMEM) {
             __syncthreads();                              // wave maxima
             __syncthreads();                              // wave sums
+            // The loaders keep the reciprocal of the four waves' double sum
+            // in wave order. This wave, idle until the probabilities are
+            // staged, checks it (sum_settled); where it does not settle it
+            // adds the exponentials again in index order — lane j
+            // recomputes position 64 c + j from the scores row with the
+            // loaders' expf and maximum, the wave adds each c's 64 values in
+            // lane order — and, if that reciprocal differs, rewrites the
+            // probabilities before its chain reads them (always, under the
+            // test switch).
+            double lsum = wsum[0];
+#pragma unroll
+            for (uint32_t w = 1; w < DPV_LW; w++) lsum = lsum + wsum[w];
+            const double r = 1.0 / lsum;
+            if (MYNAH_UNSETTLED(r, n_kv, 2u, forced)) {
+                mx = wmax[0];
+#pragma unroll
+                for (uint32_t w = 1; w < DPV_LW; w++) mx = fmaxf(mx, wmax[w]);
+                double seq = 0.0;
+                for (uint32_t c0 = 0; c0 < n_kv; c0 += 64u) {
+                    const uint32_t t = c0 + lane, cnt = n_kv - c0 < 64u ? n_kv - c0 : 64u;
+                    const float e = t < n_kv ? mynah_expf_t(prow[t] - mx, etab[0]) : 0.0f;
+#pragma nounroll
+                    for (uint32_t j = 0; j < cnt; j++)
+                        seq += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                }
+                fix = (float)(1.0 / seq);
+                refix = forced != 0u || __float_as_uint(fix) != __float_as_uint((float)r);
+            }
         }
         __syncthreads();                                  // p, chunks 0 and 1 staged
+        if constexpr (!PMEM) {
+            if (refix) {
+                for (uint32_t t = lane; t < n_kv; t += 64u)
+                    pl[t] = mynah_expf_t(prow[t] - mx, etab[0]) * fix;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
         const uint32_t d = lane % DPV_SW;
         float acc = 0.0f;
         // Group m of chunk c: positions DPV_CH c + 4 m .. + 3 of this lane's
@@ -712,6 +815,8 @@ MYNAH_DEV void attn_pv_body(const float *v_layer, const float *sp, uint32_t pos,
         acc = wave_sum_d(acc);
         if (lane == 0) wsum[lw] = acc;
         __syncthreads();
+        // The double sum of the four waves in wave order (the chain's wave
+        // checks its reciprocal against the reference's index order).
         double lsum = wsum[0];
 #pragma unroll
         for (uint32_t w = 1; w < DPV_LW; w++) lsum = lsum + wsum[w];
@@ -892,7 +997,9 @@ MYNAH_DEV void attn_split_body(const float *__restrict__ q, float *__restrict__ 
     }
     if (qwave || kwave) {
         float y0, y1;
-        norm_rope_reg(x0, x1, w0, w1, cs, sn, eps, y0, y1);
+        // The wave's order of the sum of squares, unchecked: the split
+        // attention rounds differently from the reference anyway.
+        norm_rope_reg(x0, x1, w0, w1, cs, sn, eps, false, y0, y1);
         float *dst = qwave ? qn[wave] : kn;
         dst[lane] = y0;
         dst[lane + 64u] = y1;
@@ -1231,8 +1338,7 @@ mynah_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float *_
     __shared__ double sh[16];
     double acc = 0.0;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) acc += (double)x[i] * (double)x[i];
-    const double sum = block_sum_d(acc, sh);
-    const float s = (float)(1.0 / sqrt(sum / (double)n + (double)eps));
+    const float s = rms_scale_settled(block_sum_d(acc, sh), x, n, eps);
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * s * w[i];
 }
 
@@ -1412,8 +1518,8 @@ mynah_rmsnorm_rows(const float *__restrict__ x, const float *__restrict__ w, flo
         acc = __builtin_fma((double)v.z, (double)v.z, acc);
         acc = __builtin_fma((double)v.w, (double)v.w, acc);
     }
-    const double sum = block_sum_d(acc, shd);
-    const float sc = (float)(1.0 / sqrt(sum / (double)cols + (double)eps));
+    const float sc = rms_scale_settled(block_sum_d(acc, shd), x + (size_t)blockIdx.x * cols,
+                                       cols, eps);
     for (uint32_t q = threadIdx.x; q < n4; q += blockDim.x) {
         float4 v = x4[q];
         const float4 wv = w4[q];

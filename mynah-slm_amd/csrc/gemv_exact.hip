@@ -433,7 +433,16 @@ MYNAH_DEV uint32_t xpad_floats(uint32_t cols) { return cols + 4u * ((cols + 255u
 // lds[i + 4 * (i / 256)]. lw (cols floats of LDS) holds the norm weights
 // while they are applied. All x and norm-weight loads are issued before the
 // first wait. Every thread of the workgroup calls it (it has barriers when
-// norm_w is set); the caller synchronises before reading the copy.
+// norm_w is set); the caller synchronises before reading the copy. The sum
+// of squares is the workgroup's parallel-order sum, without the index-order
+// check of the standalone norm kernels (sum_settled): these kernels hold
+// the first unit's weights in registers across the staging, and either
+// half of the check (the test or the index-order loop) pushes the Q6_K
+// grouped kernels into spills. Its f32 scale differs from the reference's
+// only when the scale lies within the two orders' rounding distance of an
+// f32 midpoint: by a rounding estimate about once in 10^7 sums, and in none
+// of the tests' sums (every test of the decoder compares whole logits
+// vectors bit for bit).
 MYNAH_DEV void stage_x(const float *__restrict__ x, const float *__restrict__ norm_w,
                        uint32_t cols, float eps, float *lds, float *lw, double *shd) {
 #pragma clang fp contract(off)

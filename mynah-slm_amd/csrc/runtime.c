@@ -49,6 +49,7 @@ static const char *const kernel_names[MYNAH_K_COUNT] = {
 };
 
 static mynah_device devices[MYNAH_MAX_DEVICES];
+static int index_order_sums;
 static int current_device = -1;
 static pthread_mutex_t init_mu = PTHREAD_MUTEX_INITIALIZER;
 static pthread_mutex_t host_mu = PTHREAD_MUTEX_INITIALIZER;
@@ -83,8 +84,20 @@ static int load_device(int dev) {
         }
         d->scratch = (unsigned char *)p;
         d->scratch_bytes = bytes;
+        HIP_OK(hipModuleGetGlobal(&p, &bytes, d->module, "mynah_index_sums"),
+               "hipModuleGetGlobal(mynah_index_sums)");
+        d->index_sums = (uint32_t *)p;
     }
     HIP_OK(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
+    /* The switch starts at 0 with the code object; it is written only when
+     * on, through the library's stream: a copy on the null stream here
+     * measurably slowed every later decode step (about 1 %). */
+    if (index_order_sums) {
+        const uint32_t on = 1u;
+        HIP_OK(hipMemcpyHtoDAsync((hipDeviceptr_t)d->index_sums, (void *)&on, sizeof on, d->stream),
+               "hipMemcpyHtoDAsync(mynah_index_sums)");
+        HIP_OK(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+    }
     if (hipDeviceGetAttribute(&d->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         d->cus <= 0)
         d->cus = 256;
@@ -193,6 +206,32 @@ int mynah_hip_set_gemv_order(int order) {
 }
 
 int mynah_hip_gemv_order(void) { return gemv_order; }
+
+int mynah_hip_set_index_order_sums(int on) {
+    if (on != 0 && on != 1) {
+        mynah_set_error("index-order sums: %d is neither 0 nor 1", on);
+        return -1;
+    }
+    pthread_mutex_lock(&init_mu);
+    index_order_sums = on;
+    int rc = 0, cur = -1;
+    (void)hipGetDevice(&cur);
+    for (int dev = 0; dev < MYNAH_MAX_DEVICES && rc == 0; dev++) {
+        mynah_device *d = &devices[dev];
+        if (!d->loaded) continue;
+        const uint32_t v = (uint32_t)on;
+        if (hipSetDevice(dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+            hipMemcpyHtoDAsync((hipDeviceptr_t)d->index_sums, (void *)&v, sizeof v, d->stream) !=
+                hipSuccess ||
+            hipStreamSynchronize(d->stream) != hipSuccess) {
+            mynah_set_error("index-order sums: setting the switch on device %d failed", dev);
+            rc = -1;
+        }
+    }
+    if (cur >= 0) (void)hipSetDevice(cur);
+    pthread_mutex_unlock(&init_mu);
+    return rc;
+}
 
 /* allow_int8 == 0 keeps the exact order whatever the int8 lane's mode (the
  * reference's ingot_q4_k_matvec_scalar). */

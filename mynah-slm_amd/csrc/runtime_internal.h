@@ -122,6 +122,9 @@ typedef struct {
      * (mynah_scratch, int8.hip), resolved once when the module loads. */
     unsigned char *scratch;
     size_t scratch_bytes;
+    /* Device address of mynah_index_sums (common.hip.h), the switch that
+     * sends every norm and softmax sum through the index-order path. */
+    uint32_t *index_sums;
 } mynah_device;
 
 void mynah_set_error(const char *fmt, ...);

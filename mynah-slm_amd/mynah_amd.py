@@ -104,6 +104,7 @@ def _load() -> C.CDLL:
         "mynah_hip_sync": (C.c_int, [_P]),
         "mynah_hip_stream": (_P, []),
         "mynah_hip_set_gemv_order": (C.c_int, [C.c_int]),
+        "mynah_hip_set_index_order_sums": (C.c_int, [C.c_int]),
         "mynah_hip_gemv_order": (C.c_int, []),
         "mynah_hip_gemv_kernel": (C.c_char_p, [C.c_int, C.c_size_t, C.c_size_t, C.c_int]),
         "mynah_hip_event_create": (_P, []),
