@@ -16,8 +16,11 @@ generation loop with the device sampler against the same loop with the
 oracle sampler on the host (the decoder's logits are bit-identical, so the
 sampler is the only difference): ids, count, a stop in the middle of a
 device chunk, and the sampler's state after the call (its next draw). The
-settings the device sampler does not take (temp > 0 with top_k 0 or above
-128, a window over 4096) are refused when the sampler is made.
+settings the device sampler does not take (temp > 0 with top_k 0, above
+128 or not below the vocabulary, a window over 4096, an empty vocabulary or
+one above 32 x 8192) are refused when the sampler is made; the largest
+vocabulary taken (32 x 8192, the most lists the merge takes) draws as the
+oracle does.
 """
 from __future__ import annotations
 
@@ -114,6 +117,29 @@ def test_index_order_sum_gives_the_same_draws(M, monkeypatch):
 def test_unsupported_settings_are_refused(M, params, error):
     with pytest.raises(M.HipError, match=error):
         M.DeviceSampler(3000, **params)
+
+
+@pytest.mark.parametrize("vocab,params,error", [
+    (0, dict(), "empty vocabulary"),
+    (32 * 8192 + 1, dict(), "exceeds"),          # more top-k workgroups than the merge takes
+    (100, dict(temp=0.6, top_k=100), "top_k"),   # top_k not below the vocabulary
+])
+def test_unsupported_vocabularies_are_refused(M, vocab, params, error):
+    with pytest.raises(M.HipError, match=error):
+        M.DeviceSampler(vocab, **params)
+
+
+def test_largest_vocabulary_taken(M):
+    """32 top-k workgroups of 8,192 probabilities: the largest vocabulary the
+    merge takes, against the oracle sampler."""
+    vocab, params = 32 * 8192, CASES[1]
+    print(f"[case] device sampler {params} vocab {vocab}", flush=True)
+    want = draws(O.OracleSampler(vocab, **params), vocab, steps=6)
+    dev = M.DeviceSampler(vocab, **params)
+    got = draws(dev, vocab, steps=6)
+    dev.close()
+    assert got[0] == want[0]
+    assert np.array_equal(got[1].view(np.uint32), want[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("params", CASES[:5], ids=[str(i) for i in range(5)])
