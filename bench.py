@@ -323,20 +323,39 @@ def gpu_prefill_gemm(M, CF, reps: int = 20, int8: bool = False):
     is), quantisation included in the time; Q6_K stays exact, as there."""
     out, tot_flop, tot_ms = {}, 0, 0.0
     M.set_int8(M.INT8_BATCHED if int8 else M.INT8_OFF)
+    bufs = []
     try:
+        # Every operand is made and resident before any GEMM runs, and the
+        # six products run back to back for about 100 ms before the first
+        # timed block: a prefill's GEMMs follow each other, and an idle gap
+        # before a short timed block (the host making the next matrix) left
+        # the GPU's clocks low for it (44 against 50 TFLOP/s measured).
         for i, m in enumerate(CF.C4):
             wseed, _ = CF.matrix_seeds(M.substream, 0, i)
             w = M.DeviceBuffer.from_array(M.synth_blocks(m.qtype, wseed, m.rows, m.cols))
             x = M.DeviceBuffer.from_array(M.synth_normal(M.substream(0, CF.PREFILL_X_INDEX + i),
                                                          CF.C4_TOKENS * m.cols))
             y = M.DeviceBuffer(4 * m.rows * CF.C4_TOKENS)
-            M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
+            bufs.append((m, w, x, y))
+        run = lambda m, w, x, y: M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr,
+                                               CF.C4_TOKENS)
+        a, b = M.Event(), M.Event()
+        a.record()
+        warm = 0
+        while True:
+            for args in bufs:
+                run(*args)
+            warm += 1
+            b.record()
             M.sync()
-            a, b = M.Event(), M.Event()
+            if a.elapsed_ms(b) >= 100.0 or warm >= 200:
+                break
+        for m, w, x, y in bufs:
             n = reps * (4 if int8 else 1)
+            a, b = M.Event(), M.Event()
             a.record()
             for _ in range(n):
-                M.matmat_dev(m.qtype, w.ptr, m.rows, m.cols, x.ptr, y.ptr, CF.C4_TOKENS)
+                run(m, w, x, y)
             b.record()
             M.sync()
             ms = a.elapsed_ms(b) / n
@@ -345,9 +364,10 @@ def gpu_prefill_gemm(M, CF, reps: int = 20, int8: bool = False):
             tot_ms += ms
             lane = "int8" if (int8 and m.qtype == CF.Q4_K) else "exact"
             out[m.name] = {"ms": round(ms, 4), "tflop_s": round(flop / ms / 1e9, 2), "lane": lane}
+    finally:
+        for _, w, x, y in bufs:
             for buf in (w, x, y):
                 buf.free()
-    finally:
         M.set_int8(M.INT8_OFF)
     res = {"workload": "configs[3]: Q4_K 4096/2048/2048/6144/6144 x 2048 and Q6_K 2048 x 6144, "
                        "512 tokens, " + ("Q4_K on the int8 activation lane" if int8
