@@ -69,6 +69,16 @@ def upload_copies(M, w, copies: int):
     return [M.DeviceBuffer.from_array(w) for _ in range(copies)]
 
 
+def warm_for(fn, ms: float = 100.0) -> None:
+    """Run fn() until about `ms` of wall time has passed. The GPU's clocks
+    rise under load; a short timed block right after an idle gap (the host
+    making the next matrix) runs partly on low clocks (the 4B head class:
+    4,131 GB/s so, 4,755 after 150 ms of launches)."""
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+
+
 def gpu_sweep(M, CF, steps: int, warmup: int):
     """configs[1] sweep launched from C (no Python between launches)."""
     mats = CF.C2
@@ -131,7 +141,7 @@ def gpu_c1(M, CF, launches: int = 256):
     y = M.DeviceBuffer(4 * m.rows)
     ptrs = [b.ptr for b in w]
     n = max(launches, 2 * copies)
-    M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies)
+    warm_for(lambda: M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies))
     ms = M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, n) / n
     for b in w + [x, y]:
         b.free()
@@ -155,8 +165,12 @@ def copy_ceiling(M, traffic: int, launches: int = 64) -> float:
     for b in src:
         M.check(M.lib.mynah_hip_memset(b.ptr, 1, half), "memset")
     n = max(launches, 4 * copies)
-    for i in range(copies):
-        M.copy_dev(dst.ptr, src[i].ptr, half)
+
+    def one_pass():
+        for i in range(copies):
+            M.copy_dev(dst.ptr, src[i].ptr, half)
+        M.sync()
+    warm_for(one_pass)
     a, e = M.Event(), M.Event()
     a.record()
     for i in range(n):
@@ -181,8 +195,12 @@ def read_ceiling(M, nbytes: int, launches: int = 64) -> float:
     for b in src:
         M.check(M.lib.mynah_hip_memset(b.ptr, 1, size), "memset")
     n = max(launches, 4 * copies)
-    for i in range(copies):
-        M.read_dev(src[i].ptr, size, sink.ptr)
+
+    def one_pass():
+        for i in range(copies):
+            M.read_dev(src[i].ptr, size, sink.ptr)
+        M.sync()
+    warm_for(one_pass)
     a, e = M.Event(), M.Event()
     a.record()
     for i in range(n):
@@ -209,7 +227,7 @@ def gpu_4b_classes(M, CF, launches: int = 64):
         y = M.DeviceBuffer(4 * m.rows)
         ptrs = [b.ptr for b in w]
         n = max(launches, 4 * copies)
-        M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies)
+        warm_for(lambda: M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, copies))
         ms = M.time_matvec(m.qtype, ptrs, m.rows, m.cols, x.ptr, y.ptr, n) / n
         out[m.name] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         for b in w + [x, y]:
